@@ -1,0 +1,141 @@
+"""Sampled rows/s of the fused sampling kernel on one MI355X.
+
+Workload: 256 rows x 129,280-token bf16 logits with a heavy tail (N(0,1) plus
+32 spikes of +U[8,15] per row), per-row temperature U[0.2,1.5], top-k
+U{1..1024}, top-p U[0.5,1], a packed allow bitmask disallowing 10% of
+tokens, one pre-drawn uniform per row.  Inputs are resident in HBM before
+the timed region; one step is one ``dsr_sample_rows`` launch over the batch.
+
+Prints one JSON line with rows/s, the roofline of the kernel (algorithmic
+HBM bytes / measured kernel time against 8 TB/s) and the CPU baseline: the
+float64 oracle (a restatement of the reference's NumPy sampler) timed on the
+host cores over all 256 rows of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import multiprocessing as mp
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_HBM_GBS = 8000.0
+
+
+_CPU_WORKLOAD = None
+
+
+def _cpu_rows(span):
+    from oracle import sampling_oracle as O
+    w = _CPU_WORKLOAD
+    lo, hi = span
+    t0 = time.perf_counter()
+    for r in range(lo, hi):
+        O.sample_row(w.logits[r], O.Policy(**w.policies[r]), float(w.uniforms[r]), allowed=w.allowed[r],
+                     keep_probs=False)
+    return hi - lo, time.perf_counter() - t0
+
+
+def cpu_baseline(w, passes=2):
+    """Oracle rows/s on the host cores: one forked worker per core, rows split
+    evenly; run before the GPU is initialised.  Only the mapped work is timed."""
+    global _CPU_WORKLOAD
+    _CPU_WORKLOAD = w
+    os.environ["OMP_NUM_THREADS"] = "1"
+    cores = min(16, os.cpu_count() or 1)
+    edges = np.linspace(0, w.rows, cores + 1).astype(int)
+    spans = [(int(a), int(b)) for a, b in zip(edges[:-1], edges[1:])] * passes
+    with mp.get_context("fork").Pool(cores) as pool:
+        pool.map(_cpu_rows, [(0, 1)] * cores)            # warm the workers
+        t0 = time.perf_counter()
+        done = pool.map(_cpu_rows, spans, chunksize=1)
+        wall = time.perf_counter() - t0
+    n = sum(d[0] for d in done)
+    busy = sum(d[1] for d in done)
+    return {"value": n / wall, "unit": "rows/s", "cores": cores, "kind": "port",
+            "sample": f"{passes} passes over all {w.rows} rows of the same workload ({n} rows, {busy:.1f} s of CPU "
+                      f"work) with the float64 NumPy oracle on {cores} worker processes; "
+                      f"{n / busy:.1f} rows/s per core"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (rows are independent, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from deepseekrpc_amd import workloads
+    w = workloads.c3()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(w)
+
+    import torch
+    from deepseekrpc_amd import _native as N
+    from deepseekrpc_amd import batch
+
+    N.load()
+    d = workloads.to_device(w)
+    prep = batch.PreparedSample(d.logits, d.policies, allow_bits=d.allow_bits, uniforms=d.uniforms)
+    torch.cuda.synchronize()
+    res = prep.result
+    status = res.status.cpu().numpy()
+    if (status != 0).any():
+        raise SystemExit(f"kernel reported row errors: {np.unique(status)}")
+
+    for _ in range(args.warmup):
+        prep.launch()
+    torch.cuda.synchronize()
+    # Whole-job throughput: K back-to-back steps on the stream.
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        prep.launch()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # Kernel duration: HIP events around each launch on the launch stream.
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for s, e in evs:
+        s.record(stream)
+        prep.launch()
+        e.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in evs]))
+    status = res.status.cpu().numpy()
+    if (status != 0).any():
+        raise SystemExit("kernel reported row errors in the timed region")
+
+    rows = w.rows
+    ms_per_step = wall * 1e3 / args.steps
+    alg_bytes = workloads.algorithmic_bytes(w)
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "c3_traffic.json")
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get("bytes_per_launch")
+    line = {
+        "metric": "sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline",
+        "value": rows / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "c3: 256 rows x 129280 bf16 heavy-tail logits, per-row T/top-k/top-p, 10% allow mask",
+                   "rows": rows, "vocab": int(w.logits.shape[1]), "fast_path_rows": None},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": alg_bytes},
+    }
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

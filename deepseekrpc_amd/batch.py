@@ -1,0 +1,383 @@
+"""Batched device API of the sampling hot path (rows already in HBM).
+
+This is the interface a serving loop uses: logits ``[rows, V]`` stay on the
+GPU, one launch samples every row, and the host only sees the compact
+decisions.  It replaces the reference's per-row device-to-host copy and
+NumPy pipeline (terminal_sampling.py:16-27,83-95; sampling.py:48-128) and
+its verifier (terminal_sampling.py:170-183; sampling.py:247-294).
+
+Uniforms are drawn on the host (the reference's PCG64 domains stay there)
+and passed in; each result reports which uniforms were consumed so the host
+streams advance exactly as the reference's would.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _native as N
+
+VOCAB = 129280
+POLICY_DTYPE = np.dtype(N.POLICY_DTYPE_FIELDS, align=True)
+assert POLICY_DTYPE.itemsize == ctypes.sizeof(N.Policy) == 56
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _require_cuda(t, name):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def policy_array(policies) -> np.ndarray:
+    """Pack policies (objects with the seven SamplingPolicy fields, or dicts) into ``dsr_policy_t`` rows."""
+    out = np.zeros(len(policies), POLICY_DTYPE)
+    for i, p in enumerate(policies):
+        get = p.get if isinstance(p, dict) else (lambda k, d=None, p=p: getattr(p, k, d))
+        out[i]["temperature"] = get("temperature", 1.0)
+        out[i]["top_p"] = get("top_p", 1.0)
+        out[i]["min_p"] = get("min_p", 0.0)
+        out[i]["repetition_penalty"] = get("repetition_penalty", 1.0)
+        out[i]["presence_penalty"] = get("presence_penalty", 0.0)
+        out[i]["frequency_penalty"] = get("frequency_penalty", 0.0)
+        out[i]["top_k"] = get("top_k", 0)
+    return out
+
+
+def policy_tensor(policies, device) -> torch.Tensor:
+    arr = policies if isinstance(policies, np.ndarray) and policies.dtype == POLICY_DTYPE else policy_array(policies)
+    return torch.from_numpy(arr.view(np.uint8).copy()).to(device)
+
+
+@dataclass
+class HistoryTable:
+    """Per-row sparse token-history counts in CSR form (device tensors).
+
+    Row ``r`` owns ``ids[off[r]:off[r+1]]`` (strictly increasing) with
+    ``counts`` (all history) and ``generated`` (output part only): the
+    reference's dense ``counts`` / ``generated_counts`` pair restricted to
+    ``counts > 0`` (sampling.py:54-66, history.py:46-47).
+    """
+    offsets: torch.Tensor
+    ids: torch.Tensor
+    counts: torch.Tensor
+    generated: torch.Tensor
+
+    @classmethod
+    def from_token_lists(cls, histories, generated_start=None, device="cuda"):
+        """Histories as token-id lists; ids before ``generated_start[r]`` are prompt tokens."""
+        offs, ids, cnt, gen = [0], [], [], []
+        for r, h in enumerate(histories):
+            h = np.asarray(h, np.int64)
+            s = 0 if generated_start is None else int(generated_start[r])
+            u, c = np.unique(h, return_counts=True)
+            if s > 0:
+                gu, gc = np.unique(h[s:], return_counts=True)
+                g = np.zeros(len(u), np.int64)
+                g[np.searchsorted(u, gu)] = gc
+            else:
+                g = c
+            ids.append(u)
+            cnt.append(c)
+            gen.append(g)
+            offs.append(offs[-1] + len(u))
+        return cls._upload(offs, ids, cnt, gen, device)
+
+    @classmethod
+    def from_dense(cls, counts, generated=None, device="cuda"):
+        """Dense ``[rows, V]`` count arrays (NumPy), as the reference's callers hold them."""
+        counts = np.atleast_2d(np.asarray(counts))
+        generated = counts if generated is None else np.atleast_2d(np.asarray(generated))
+        offs, ids, cnt, gen = [0], [], [], []
+        for r in range(counts.shape[0]):
+            nz = np.flatnonzero(counts[r] > 0)
+            ids.append(nz)
+            cnt.append(counts[r][nz])
+            gen.append(generated[r][nz])
+            offs.append(offs[-1] + len(nz))
+        return cls._upload(offs, ids, cnt, gen, device)
+
+    @classmethod
+    def _upload(cls, offs, ids, cnt, gen, device):
+        cat = lambda xs: np.concatenate(xs) if xs and sum(len(x) for x in xs) else np.zeros(0)
+        return cls(torch.tensor(np.asarray(offs, np.int64), device=device),
+                   torch.tensor(cat(ids).astype(np.int32), device=device),
+                   torch.tensor(cat(cnt).astype(np.int32), device=device),
+                   torch.tensor(cat(gen).astype(np.int32), device=device))
+
+
+@dataclass
+class BiasTable:
+    """Per-row sparse logit bias in CSR form (ids strictly increasing)."""
+    offsets: torch.Tensor
+    ids: torch.Tensor
+    values: torch.Tensor
+
+    @classmethod
+    def from_dicts(cls, biases, device="cuda"):
+        offs, ids, vals = [0], [], []
+        for b in biases:
+            items = sorted((b or {}).items())
+            ids.extend(int(t) for t, _ in items)
+            vals.extend(float(v) for _, v in items)
+            offs.append(len(ids))
+        return cls(torch.tensor(offs, dtype=torch.int64, device=device),
+                   torch.tensor(ids, dtype=torch.int32, device=device),
+                   torch.tensor(vals, dtype=torch.float64, device=device))
+
+
+def allow_words(vocab: int) -> int:
+    return (vocab + 31) // 32
+
+
+def pack_allow(allowed: np.ndarray) -> np.ndarray:
+    """bool ``[..., V]`` -> uint32 ``[..., ceil(V/32)]`` with bit ``i & 31`` of word ``i >> 5``."""
+    allowed = np.asarray(allowed, bool)
+    V = allowed.shape[-1]
+    pad = allow_words(V) * 32 - V
+    a = np.concatenate([allowed, np.zeros(allowed.shape[:-1] + (pad,), bool)], axis=-1)
+    return np.packbits(a.reshape(a.shape[:-1] + (-1, 32)), axis=-1, bitorder="little").view(np.uint32)[..., 0]
+
+
+def unpack_bits(words: np.ndarray, vocab: int) -> np.ndarray:
+    w = np.ascontiguousarray(words, np.uint32)
+    bits = np.unpackbits(w.view(np.uint8), bitorder="little").reshape(w.shape[:-1] + (-1,))
+    return bits[..., :vocab].astype(bool)
+
+
+_DTYPES = {torch.bfloat16: N.BF16, torch.float32: N.F32, torch.float64: N.F64}
+
+
+@dataclass
+class SampleResult:
+    tokens: torch.Tensor      # int32 [rows]
+    consumed: torch.Tensor    # uint8 [rows]
+    status: torch.Tensor      # int32 [rows]
+    flags: torch.Tensor       # uint8 [rows]
+    probs: torch.Tensor | None = None
+    kept_bits: torch.Tensor | None = None
+    args: object = None       # the marshalled dsr_sample_args_t of this call
+
+
+class Workspace:
+    """Caller-owned scratch for the library (it never allocates)."""
+
+    def __init__(self):
+        self._buf = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self._buf is None or self._buf.numel() < nbytes or self._buf.device != torch.device(device):
+            self._buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return self._buf
+
+
+_default_ws = Workspace()
+
+
+def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None = None, bias: BiasTable | None = None,
+                allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
+                probs: str | None = None, kept: bool = False, workspace: Workspace | None = None) -> SampleResult:
+    """Sample every row of ``logits [rows, V]`` on the current stream.
+
+    ``policies`` is a device tensor made by ``policy_tensor`` or a list of
+    policy objects/dicts.  ``uniforms`` (float64 ``[rows]``) are the pre-drawn
+    target-domain draws; without them only the distribution is computed.
+    ``probs`` may be ``"f32"`` or ``"f64"`` to return the final probabilities.
+    """
+    lib = N.load()
+    _require_cuda(logits, "logits")
+    if logits.dim() != 2 or logits.dtype not in _DTYPES:
+        raise ValueError("logits must be a [rows, V] bf16/f32/f64 tensor")
+    rows, V = logits.shape
+    dev = logits.device
+    if not isinstance(policies, torch.Tensor):
+        policies = policy_tensor(policies, dev)
+    if policies.numel() != rows * POLICY_DTYPE.itemsize:
+        raise ValueError("one policy per row is required")
+    res = SampleResult(torch.empty(rows, dtype=torch.int32, device=dev), torch.empty(rows, dtype=torch.uint8, device=dev),
+                       torch.empty(rows, dtype=torch.int32, device=dev), torch.empty(rows, dtype=torch.uint8, device=dev))
+    if probs == "f32":
+        res.probs = torch.empty(rows, V, dtype=torch.float32, device=dev)
+    elif probs == "f64":
+        res.probs = torch.empty(rows, V, dtype=torch.float64, device=dev)
+    elif probs is not None:
+        raise ValueError("probs must be None, 'f32' or 'f64'")
+    if kept:
+        res.kept_bits = torch.empty(rows, allow_words(V), dtype=torch.int32, device=dev)
+    if uniforms is not None:
+        _require_cuda(uniforms, "uniforms")
+        if uniforms.dtype != torch.float64 or uniforms.numel() != rows:
+            raise ValueError("uniforms must be float64 [rows]")
+    if allow_bits is not None:
+        _require_cuda(allow_bits, "allow_bits")
+        if allow_bits.dim() != 2 or allow_bits.shape[0] != rows or allow_bits.element_size() != 4:
+            raise ValueError("allow_bits must be [rows, words] 32-bit")
+    ws = (workspace or _default_ws).get(lib.dsr_sample_workspace_bytes(rows, V), dev)
+    a = N.SampleArgs()
+    a.logits = logits.data_ptr()
+    a.dtype = _DTYPES[logits.dtype]
+    a.rows, a.vocab, a.ld = rows, V, logits.stride(0)
+    a.policy = policies.data_ptr()
+    if history is not None:
+        a.pen_off, a.pen_ids = history.offsets.data_ptr(), history.ids.data_ptr()
+        a.pen_count, a.pen_gen = history.counts.data_ptr(), history.generated.data_ptr()
+    if bias is not None:
+        a.bias_off, a.bias_ids, a.bias_val = bias.offsets.data_ptr(), bias.ids.data_ptr(), bias.values.data_ptr()
+    if allow_bits is not None:
+        a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.stride(0)
+    if uniforms is not None:
+        a.uniforms = uniforms.data_ptr()
+    a.out_token, a.out_consumed = res.tokens.data_ptr(), res.consumed.data_ptr()
+    a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
+    if res.probs is not None:
+        if probs == "f32":
+            a.out_probs_f32 = res.probs.data_ptr()
+        else:
+            a.out_probs_f64 = res.probs.data_ptr()
+        a.probs_ld = V
+    if res.kept_bits is not None:
+        a.out_kept_bits, a.kept_ld = res.kept_bits.data_ptr(), res.kept_bits.stride(0)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    N.check(lib.dsr_sample_rows(ctypes.byref(a), _stream()), "dsr_sample_rows")
+    res.args = a
+    return res
+
+
+class PreparedSample:
+    """A ``dsr_sample_rows`` call whose arguments are marshalled once.
+
+    ``launch()`` re-issues the same launch on the current stream (outputs are
+    overwritten in place); a serving loop or a benchmark calls it per step.
+    """
+
+    def __init__(self, logits, policies, **kw):
+        self.workspace = kw.pop("workspace", None) or Workspace()
+        self.inputs = (logits, policies, kw)
+        self.result = sample_rows(logits, policies, workspace=self.workspace, **kw)
+        self.args = self.result.args
+        self._lib = N.load()
+
+    def launch(self):
+        rc = self._lib.dsr_sample_rows(ctypes.byref(self.args), _stream())
+        if rc != 0:
+            N.check(rc, "dsr_sample_rows")
+        return self.result
+
+
+@dataclass
+class VerifyResult:
+    accepted: torch.Tensor
+    ids: torch.Tensor
+    count: torch.Tensor
+    pending: torch.Tensor
+    stop: torch.Tensor
+    used_accept: torch.Tensor
+    used_target: torch.Tensor
+    status: torch.Tensor
+    flags: torch.Tensor
+
+
+def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, policies, u_accept: torch.Tensor,
+                  u_target: torch.Tensor, output_limit: torch.Tensor, *, history: HistoryTable | None = None,
+                  bias: BiasTable | None = None, allow_bits: torch.Tensor | None = None,
+                  eos_offsets: torch.Tensor | None = None, eos_ids: torch.Tensor | None = None,
+                  workspace: Workspace | None = None) -> VerifyResult:
+    """Exact sampled verification of ``rows`` requests with ``K`` drafts each.
+
+    ``target [rows, K+1, V]`` and ``draft [rows, K, V]`` are logits; row ``j``
+    of both is conditioned on the prefix ``draft_ids[:, :j]``.
+    """
+    lib = N.load()
+    _require_cuda(target, "target")
+    rows, K1, V = target.shape
+    K = K1 - 1
+    dev = target.device
+    if K > 0:
+        _require_cuda(draft, "draft")
+        if tuple(draft.shape) != (rows, K, V) or draft.dtype != target.dtype:
+            raise ValueError("draft must be [rows, K, V] of the target dtype")
+        _require_cuda(draft_ids, "draft_ids")
+        _require_cuda(u_accept, "u_accept")
+    if not isinstance(policies, torch.Tensor):
+        policies = policy_tensor(policies, dev)
+    i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
+    res = VerifyResult(i32(rows), i32(rows, K + 1), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows),
+                       torch.empty(rows, dtype=torch.uint8, device=dev))
+    ws = (workspace or _default_ws).get(lib.dsr_verify_workspace_bytes(rows, K, V), dev)
+    a = N.VerifyArgs()
+    a.target = target.data_ptr()
+    a.draft = draft.data_ptr() if K > 0 else None
+    a.dtype = _DTYPES[target.dtype]
+    a.K, a.rows, a.vocab, a.ld = K, rows, V, V
+    a.draft_ids = draft_ids.data_ptr() if K > 0 else None
+    a.policy = policies.data_ptr()
+    if history is not None:
+        a.pen_off, a.pen_ids = history.offsets.data_ptr(), history.ids.data_ptr()
+        a.pen_count, a.pen_gen = history.counts.data_ptr(), history.generated.data_ptr()
+    if bias is not None:
+        a.bias_off, a.bias_ids, a.bias_val = bias.offsets.data_ptr(), bias.ids.data_ptr(), bias.values.data_ptr()
+    if allow_bits is not None:
+        a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.shape[-1]
+    a.u_accept = u_accept.data_ptr() if K > 0 else None
+    a.u_target = u_target.data_ptr()
+    if eos_offsets is not None:
+        a.eos_off, a.eos_ids = eos_offsets.data_ptr(), eos_ids.data_ptr()
+    a.output_limit = output_limit.data_ptr()
+    a.out_accepted, a.out_ids, a.out_count = res.accepted.data_ptr(), res.ids.data_ptr(), res.count.data_ptr()
+    a.out_pending, a.out_stop = res.pending.data_ptr(), res.stop.data_ptr()
+    a.out_used_accept, a.out_used_target = res.used_accept.data_ptr(), res.used_target.data_ptr()
+    a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    N.check(lib.dsr_verify_drafts(ctypes.byref(a), _stream()), "dsr_verify_drafts")
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Probability-vector kernels used by the drop-in API.
+
+
+def prob_stats(p: torch.Tensor):
+    """(sum, valid, n_positive, first_positive, argmax) of a float64 device vector."""
+    lib = N.load()
+    out_sum = torch.empty(1, dtype=torch.float64, device=p.device)
+    out = torch.empty(4, dtype=torch.int32, device=p.device)
+    N.check(lib.dsr_prob_stats(_ptr(p), p.numel(), _ptr(out_sum), _ptr(out), _stream()), "dsr_prob_stats")
+    o = out.cpu().tolist()
+    return float(out_sum.item()), bool(o[0]), int(o[1]), int(o[2]), int(o[3])
+
+
+def prob_categorical(p: torch.Tensor, u: float):
+    lib = N.load()
+    out = torch.empty(2, dtype=torch.int32, device=p.device)
+    N.check(lib.dsr_prob_categorical(_ptr(p), p.numel(), float(u), _ptr(out), _stream()), "dsr_prob_categorical")
+    tok, flags = out.cpu().tolist()
+    return int(tok), int(flags)
+
+
+def prob_correction(p: torch.Tensor, q: torch.Tensor):
+    lib = N.load()
+    out = torch.empty_like(p)
+    st = torch.empty(1, dtype=torch.int32, device=p.device)
+    N.check(lib.dsr_prob_correction(_ptr(p), _ptr(q), p.numel(), _ptr(out), _ptr(st), _stream()),
+            "dsr_prob_correction")
+    return out, int(st.item())
+
+
+def prob_accept(p: torch.Tensor, q: torch.Tensor, x: int, u: float):
+    lib = N.load()
+    out = torch.empty(2, dtype=torch.int32, device=p.device)
+    N.check(lib.dsr_prob_accept(_ptr(p), _ptr(q), p.numel(), int(x), float(u), _ptr(out), _stream()),
+            "dsr_prob_accept")
+    q_pos, ok = out.cpu().tolist()
+    return bool(q_pos), bool(ok)

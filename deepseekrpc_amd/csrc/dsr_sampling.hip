@@ -1,0 +1,596 @@
+// Kernels and C ABI of the token-sampling hot path (gfx950).
+//
+//   dsr_sample_rows    -> SamplingPolicy.probabilities + categorical
+//                         (sampling.py:48-128), one workgroup per row.
+//   dsr_verify_drafts  -> SamplingWork.verify -> verify_drafts
+//                         (terminal_sampling.py:170-183, sampling.py:247-294):
+//                         one workgroup per conditional distribution, then
+//                         one per request for the sequential accept chain.
+//   dsr_prob_*         -> categorical / correction_distribution / the accept
+//                         test on float64 probability vectors.
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "dsr_fast.h"
+#include "dsr_general.h"
+
+namespace dsr {
+
+__host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(int64_t)31; }
+
+// ---------------------------------------------------------------------------
+// dsr_sample_rows: general path.
+
+__device__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int st, unsigned flags,
+                           GenShared& sh) {
+  const int64_t V = a.vocab;
+  int64_t token = -1;
+  int consumed = 0;
+  if (st == DSR_OK) {
+    if (a.out_probs_f32) {
+      float* o = a.out_probs_f32 + row * a.probs_ld;
+      DSR_FOR_ROW(i, V) o[i] = (float)W[i];
+    }
+    if (a.out_probs_f64) {
+      double* o = a.out_probs_f64 + row * a.probs_ld;
+      DSR_FOR_ROW(i, V) o[i] = W[i];
+    }
+    if (a.uniforms) {
+      long long npos, first;
+      positive_support(W, V, sh, npos, first);
+      if (npos == 1) {
+        token = first;  // sampling.py:120-122: no uniform is drawn
+      } else {
+        const double u = a.uniforms[row];
+        if (!(u >= 0.0 && u < 1.0)) {
+          st = DSR_E_UNIFORM;
+        } else {
+          token = cdf_search(W, V, u, npos, sh, flags);
+          consumed = 1;
+        }
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.out_token[row] = st == DSR_OK ? (int32_t)token : -1;
+    a.out_consumed[row] = (uint8_t)(st == DSR_OK ? consumed : 0);
+    a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = (uint8_t)flags;
+  }
+}
+
+__device__ RowSpec sample_row_spec(const dsr_sample_args_t& a, int64_t row, double* W) {
+  RowSpec r;
+  r.V = a.vocab;
+  r.dtype = a.dtype;
+  const size_t esz = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
+  r.logits = (const char*)a.logits + (size_t)row * (size_t)a.ld * esz;
+  r.pol = a.policy[row];
+  r.pen_n = 0;
+  r.pen_ids = r.pen_count = r.pen_gen = nullptr;
+  if (a.pen_off) {
+    int64_t o = a.pen_off[row];
+    r.pen_n = a.pen_off[row + 1] - o;
+    r.pen_ids = a.pen_ids + o;
+    r.pen_count = a.pen_count + o;
+    r.pen_gen = a.pen_gen + o;
+  }
+  r.prefix = nullptr;
+  r.prefix_n = 0;
+  r.bias_n = 0;
+  r.bias_ids = nullptr;
+  r.bias_val = nullptr;
+  if (a.bias_off) {
+    int64_t o = a.bias_off[row];
+    r.bias_n = a.bias_off[row + 1] - o;
+    r.bias_ids = a.bias_ids + o;
+    r.bias_val = a.bias_val + o;
+  }
+  r.allow = a.allow_bits ? a.allow_bits + row * a.allow_ld : nullptr;
+  r.W = W;
+  r.kept_bits = a.out_kept_bits ? a.out_kept_bits + row * a.kept_ld : nullptr;
+  r.kept_words = (a.vocab + 31) >> 5;
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x;
+  double* W = (double*)a.workspace + row * ws_stride(a.vocab);
+  RowSpec r = sample_row_spec(a, row, W);
+  unsigned flags = 0;
+  int64_t onehot;
+  int st = general_distribution(r, sh, flags, onehot);
+  finish_row(a, row, W, st, flags, sh);
+}
+
+// Fast path for bf16 rows; rows it does not take are redone by the general
+// path inside the same workgroup.
+__global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t a) {
+  __shared__ FastShared sh;
+  const int64_t row = blockIdx.x;
+  if (fast_sample_row(a, row, sh)) return;
+  __syncthreads();
+  GenShared& gs = *reinterpret_cast<GenShared*>(&sh);
+  double* W = (double*)a.workspace + row * ws_stride(a.vocab);
+  RowSpec r = sample_row_spec(a, row, W);
+  unsigned flags = 0;
+  int64_t onehot;
+  int st = general_distribution(r, gs, flags, onehot);
+  finish_row(a, row, W, st, flags, gs);
+}
+
+// ---------------------------------------------------------------------------
+// dsr_verify_drafts.
+
+struct VerifyLayout {
+  int64_t slots;   // 2K+1 distributions per request: targets 0..K, drafts K+1..2K
+  int64_t stride;  // doubles per workspace row
+  double* W;       // [rows * slots * stride]
+  int32_t* info;   // [rows * slots * 4]: status, onehot, flags, unused
+};
+
+__device__ __forceinline__ bool in_eos(const dsr_verify_args_t& a, int64_t row, int32_t t) {
+  if (!a.eos_off) return false;
+  for (int64_t e = a.eos_off[row]; e < a.eos_off[row + 1]; ++e)
+    if (a.eos_ids[e] == t) return true;
+  return false;
+}
+
+__global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x / L.slots;
+  const int slot = (int)(blockIdx.x % L.slots);
+  const int K = a.K;
+  const bool is_target = slot <= K;
+  const int j = is_target ? slot : slot - (K + 1);
+  const size_t esz = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
+  RowSpec r;
+  r.V = a.vocab;
+  r.dtype = a.dtype;
+  r.logits = is_target ? (const char*)a.target + ((size_t)row * (K + 1) + j) * (size_t)a.ld * esz
+                       : (const char*)a.draft + ((size_t)row * K + j) * (size_t)a.ld * esz;
+  r.pol = a.policy[row];
+  r.pen_n = 0;
+  r.pen_ids = r.pen_count = r.pen_gen = nullptr;
+  if (a.pen_off) {
+    int64_t o = a.pen_off[row];
+    r.pen_n = a.pen_off[row + 1] - o;
+    r.pen_ids = a.pen_ids + o;
+    r.pen_count = a.pen_count + o;
+    r.pen_gen = a.pen_gen + o;
+  }
+  r.prefix = a.draft_ids + row * K;
+  r.prefix_n = j;
+  r.bias_n = 0;
+  r.bias_ids = nullptr;
+  r.bias_val = nullptr;
+  if (a.bias_off) {
+    int64_t o = a.bias_off[row];
+    r.bias_n = a.bias_off[row + 1] - o;
+    r.bias_ids = a.bias_ids + o;
+    r.bias_val = a.bias_val + o;
+  }
+  r.allow = a.allow_bits ? a.allow_bits + (row * (K + 1) + j) * a.allow_ld : nullptr;
+  r.W = L.W + (row * L.slots + slot) * L.stride;
+  r.kept_bits = nullptr;
+  r.kept_words = 0;
+  unsigned flags = 0;
+  int64_t onehot;
+  int st = general_distribution(r, sh, flags, onehot);
+  if (threadIdx.x == 0) {
+    int32_t* info = L.info + (row * L.slots + slot) * 4;
+    info[0] = st;
+    info[1] = (int32_t)onehot;
+    info[2] = (int32_t)flags;
+  }
+}
+
+// Categorical draw over max(p - q, 0) / sum (correction_distribution,
+// sampling.py:131-139, then categorical :118-128); q == nullptr draws from p.
+__device__ int draw_from(const double* P, const double* Q, int64_t V, double u, GenShared& sh, int64_t& token,
+                         int& used, unsigned& flags) {
+  double acc = 0.0;
+  long long n = 0, f = LLONG_MAX;
+  DSR_FOR_ROW(i, V) {
+    double x = Q ? fmax(P[i] - Q[i], 0.0) : P[i];
+    acc += x;
+    if (x > 0.0) {
+      ++n;
+      if (i < f) f = i;
+    }
+  }
+  const double total = block_sum(acc, sh.b);
+  n = block_sum_i64(n, sh.b);
+  f = block_min_i64(f, sh.b);
+  if (Q && (!(total > 0.0) || !isfinite(total))) return DSR_E_CORRECTION;
+  used = 0;
+  if (n == 1) {
+    token = f;
+    return DSR_OK;
+  }
+  if (!(u >= 0.0 && u < 1.0)) return DSR_E_UNIFORM;
+  used = 1;
+  // CDF of the normalised residual, computed on the fly in index order.
+  int64_t lo, hi;
+  thread_slice(V, lo, hi);
+  double part = 0.0;
+  for (int64_t i = lo; i < hi; ++i) part += Q ? fmax(P[i] - Q[i], 0.0) / total : P[i];
+  double ctot;
+  const double base = block_exclusive_scan_f64(part, sh.b, ctot);
+  const double thr = u * ctot;
+  long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
+  const long long owner = block_max_i64(cand, sh.b);
+  if ((long long)threadIdx.x == owner) {
+    double c = base, before = base;
+    int64_t tok = -1, last = -1;
+    for (int64_t i = lo; i < hi; ++i) {
+      double w = Q ? fmax(P[i] - Q[i], 0.0) / total : P[i];
+      if (w > 0.0) {
+        before = c;
+        c += w;
+        last = i;
+        if (c > thr) {
+          tok = i;
+          break;
+        }
+      }
+    }
+    const double tol = ((double)n + 16.0) * 0x1p-51 * ctot;
+    int margin = 0;
+    if (tok < 0) {
+      tok = last;
+      margin = 1;
+    } else if (c - thr <= tol || (before > 0.0 && thr - before <= tol)) {
+      margin = 1;
+    }
+    sh.b.bcast_i[0] = tok;
+    sh.b.bcast_i[1] = margin;
+  }
+  __syncthreads();
+  token = sh.b.bcast_i[0];
+  if (sh.b.bcast_i[1]) flags |= DSR_FLAG_MARGIN;
+  __syncthreads();
+  return DSR_OK;
+}
+
+__global__ __launch_bounds__(kThreads) void k_verify_decide(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  __shared__ int s_status, s_accepted, s_count, s_pending, s_stop, s_ua, s_ut, s_next;
+  __shared__ double s_u;
+  const int64_t row = blockIdx.x;
+  const int K = a.K;
+  const int64_t V = a.vocab;
+  const int32_t* info = L.info + row * L.slots * 4;
+  auto Prow = [&](int slot) { return L.W + (row * L.slots + slot) * L.stride; };
+  const bool greedy = a.policy[row].temperature == 0.0;
+  unsigned flags = 0;
+  int32_t* out_ids = a.out_ids + row * (K + 1);
+  if (threadIdx.x == 0) {
+    for (int j = 0; j <= K; ++j) out_ids[j] = -1;
+    s_status = DSR_OK;
+    s_accepted = 0;
+    s_count = 0;
+    s_pending = -1;
+    s_stop = DSR_STOP_NONE;
+    s_ua = 0;
+    s_ut = 0;
+    s_next = 0;
+    for (int j = 0; j < K; ++j) flags |= (unsigned)info[(K + 1 + j) * 4 + 2] & DSR_FLAG_MARGIN;
+    // Order of the reference's checks (sampling.py:255-272): proposals, the
+    // first target, then token ids.
+    const int limit = a.output_limit[row];
+    if (limit < 1 || limit > DSR_MAX_COUNT) s_status = DSR_E_COUNTS;
+    for (int j = 0; j < K && s_status == DSR_OK; ++j) s_status = info[(K + 1 + j) * 4];
+    if (s_status == DSR_OK) s_status = info[0];
+    if (s_status == DSR_OK) {
+      for (int j = 0; j < K; ++j) {
+        int32_t t = a.draft_ids[row * K + j];
+        if (t < 0 || t >= V) s_status = DSR_E_TOKEN;
+      }
+      if (a.eos_off) {
+        for (int64_t e = a.eos_off[row]; e < a.eos_off[row + 1]; ++e)
+          if (a.eos_ids[e] < 0 || a.eos_ids[e] >= V) s_status = DSR_E_TOKEN;
+      }
+    }
+  }
+  __syncthreads();
+  // Sequential accept chain; thread 0 decides, the block joins for residual draws.
+  for (int j = 0; j < K; ++j) {
+    if (threadIdx.x == 0 && s_status == DSR_OK && s_next == 0) {
+      const int32_t x = a.draft_ids[row * K + j];
+      if (j > 0 && info[j * 4] != DSR_OK) {
+        s_status = info[j * 4];  // the lazily built target j fails only when reached
+      } else {
+        flags |= (unsigned)info[j * 4 + 2] & DSR_FLAG_MARGIN;
+        const double* P = Prow(j);
+        const double* Q = Prow(K + 1 + j);
+        if (!(Q[x] > 0.0)) {
+          s_status = DSR_E_PROPOSAL_ZERO;
+        } else {
+          bool ok;
+          if (greedy) {
+            ok = x == info[j * 4 + 1];
+          } else {
+            const double u = a.u_accept[row * K + j];
+            ++s_ua;
+            if (!(u >= 0.0 && u < 1.0)) {
+              s_status = DSR_E_UNIFORM;
+              ok = false;
+            } else {
+              double ratio = P[x] / Q[x];
+              ratio = ratio < 1.0 ? ratio : 1.0;
+              if (fabs(u - ratio) <= 0x1p-48 * ratio) flags |= DSR_FLAG_MARGIN;
+              ok = u < ratio;
+            }
+          }
+          if (s_status == DSR_OK) {
+            if (!ok) {
+              s_accepted = j;
+              s_next = 1;  // reject: replacement below
+            } else {
+              out_ids[s_count++] = x;
+              if (in_eos(a, row, x) || s_count >= a.output_limit[row]) {
+                s_accepted = j + 1;
+                s_stop = in_eos(a, row, x) ? DSR_STOP_EOS : DSR_STOP_LENGTH;
+                s_next = 3;  // finished inside the drafts: no bonus
+              }
+            }
+          }
+        }
+      }
+      if (s_status == DSR_OK && s_next == 0 && j == K - 1) s_next = 2;  // all accepted: bonus
+    }
+    __syncthreads();
+    if (s_status != DSR_OK || s_next != 0) break;
+  }
+  if (K == 0 && threadIdx.x == 0 && s_status == DSR_OK) s_next = 2;
+  __syncthreads();
+  if (s_status == DSR_OK && (s_next == 1 || s_next == 2)) {
+    const int j = s_next == 1 ? s_accepted : K;
+    if (s_next == 2 && j > 0 && info[j * 4] != DSR_OK) {
+      if (threadIdx.x == 0) s_status = info[j * 4];
+    } else {
+      if (s_next == 2) flags |= (unsigned)info[j * 4 + 2] & DSR_FLAG_MARGIN;
+      int64_t rep = -1;
+      int used = 0;
+      int st = DSR_OK;
+      if (greedy) {
+        rep = info[j * 4 + 1];
+      } else {
+        const double u = a.u_target[row];
+        st = draw_from(Prow(j), s_next == 1 ? Prow(K + 1 + j) : nullptr, V, u, sh, rep, used, flags);
+      }
+      if (threadIdx.x == 0) {
+        if (st != DSR_OK) {
+          s_status = st;
+        } else {
+          s_ut += used;
+          if (s_next == 2) s_accepted = K;
+          const int before = s_count;
+          out_ids[s_count++] = (int32_t)rep;
+          s_pending = (int)rep;
+          s_stop = in_eos(a, row, (int32_t)rep) ? DSR_STOP_EOS
+                   : (before + 1 >= a.output_limit[row] ? DSR_STOP_LENGTH : DSR_STOP_NONE);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool ok = s_status == DSR_OK;
+    a.out_status[row] = s_status;
+    a.out_accepted[row] = ok ? s_accepted : 0;
+    a.out_count[row] = ok ? s_count : 0;
+    a.out_pending[row] = ok ? s_pending : -1;
+    a.out_stop[row] = ok ? s_stop : DSR_STOP_NONE;
+    a.out_used_accept[row] = ok ? s_ua : 0;
+    a.out_used_target[row] = ok ? s_ut : 0;
+    if (!ok)
+      for (int j = 0; j <= K; ++j) out_ids[j] = -1;
+    if (a.out_flags) a.out_flags[row] = (uint8_t)flags;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Probability-vector kernels (single workgroup).
+
+__global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_t n, double* out_sum,
+                                                         int32_t* out) {
+  __shared__ GenShared sh;
+  double acc = 0.0, mx = -INFINITY;
+  int bad = 0;
+  long long npos = 0, first = LLONG_MAX;
+  DSR_FOR_ROW(i, n) {
+    double x = p[i];
+    if (!isfinite(x) || x < 0.0) bad = 1;
+    acc += x;
+    if (x > 0.0) {
+      ++npos;
+      if (i < first) first = i;
+    }
+    mx = x > mx ? x : mx;
+  }
+  const double s = block_sum(acc, sh.b);
+  bad = block_or(bad, sh.b);
+  npos = block_sum_i64(npos, sh.b);
+  first = block_min_i64(first, sh.b);
+  const double M = block_max(mx, sh.b);
+  long long am = LLONG_MAX;
+  DSR_FOR_ROW(i, n) if (p[i] == M && i < am) am = i;
+  am = block_min_i64(am, sh.b);
+  if (threadIdx.x == 0) {
+    out_sum[0] = s;
+    out[0] = bad ? 0 : 1;
+    out[1] = (int32_t)npos;
+    out[2] = first == LLONG_MAX ? -1 : (int32_t)first;
+    out[3] = am == LLONG_MAX ? -1 : (int32_t)am;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, int64_t n, double u, int32_t* out) {
+  __shared__ GenShared sh;
+  long long npos, first;
+  positive_support(p, n, sh, npos, first);
+  unsigned flags = 0;
+  int64_t tok = cdf_search(p, n, u, npos, sh, flags);
+  if (threadIdx.x == 0) {
+    out[0] = (int32_t)tok;
+    out[1] = (int32_t)flags;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void k_prob_correction(const double* p, const double* q, int64_t n,
+                                                              double* out, int32_t* st) {
+  __shared__ GenShared sh;
+  double acc = 0.0;
+  DSR_FOR_ROW(i, n) {
+    double r = fmax(p[i] - q[i], 0.0);
+    out[i] = r;
+    acc += r;
+  }
+  const double total = block_sum(acc, sh.b);
+  const bool ok = total > 0.0 && isfinite(total);
+  if (ok) DSR_FOR_ROW(i, n) out[i] = out[i] / total;
+  if (threadIdx.x == 0) st[0] = ok ? DSR_OK : DSR_E_CORRECTION;
+}
+
+__global__ void k_prob_accept(const double* p, const double* q, int32_t x, double u, int32_t* out) {
+  if (threadIdx.x == 0) {
+    const double qx = q[x];
+    out[0] = qx > 0.0 ? 1 : 0;
+    double ratio = p[x] / qx;
+    ratio = ratio < 1.0 ? ratio : 1.0;
+    out[1] = (qx > 0.0 && u < ratio) ? 1 : 0;
+  }
+}
+
+}  // namespace dsr
+
+// ---------------------------------------------------------------------------
+// C ABI.
+
+using namespace dsr;
+
+static int32_t launched() { return hipGetLastError() == hipSuccess ? 0 : DSR_ERR_LAUNCH; }
+
+extern "C" {
+
+int32_t dsr_abi_version(void) { return DSR_ABI_VERSION; }
+
+const char* dsr_status_message(int32_t code) {
+  switch (code) {
+    case DSR_OK: return "ok";
+    case DSR_E_LOGITS: return "sampling needs one bounded finite-or-masked floating logit vector";
+    case DSR_E_MASKED: return "sampling controls masked every vocabulary token";
+    case DSR_E_NO_MASS: return "sampling controls produced no positive probability";
+    case DSR_E_UNIFORM: return "sampling uniform must lie in [0,1)";
+    case DSR_E_COUNTS: return "sampling frequency counts do not match the vocabulary";
+    case DSR_E_BIAS: return "invalid logit bias mapping";
+    case DSR_E_PROPOSAL_ZERO: return "a proposed token has zero probability under its claimed conditional proposal";
+    case DSR_E_CORRECTION: return "a rejected proposal has no positive correction distribution";
+    case DSR_E_TOKEN: return "verification token must be an integer in the vocabulary";
+    case DSR_E_DISTRIBUTION: return "verifier requires a normalized complete FP64 probability vector";
+    case DSR_E_POLICY: return "invalid sampling policy";
+    case DSR_E_GENERATED: return "generated token counts must be a subset of complete sampling history";
+    default: return "unknown sampling status";
+  }
+}
+
+size_t dsr_sample_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows < 0 || vocab < 1) return 0;
+  return (size_t)rows * (size_t)ws_stride(vocab) * sizeof(double);
+}
+
+size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab) {
+  if (rows < 0 || vocab < 1 || K < 0) return 0;
+  const size_t slots = (size_t)(2 * K + 1);
+  return (size_t)rows * slots * (size_t)ws_stride(vocab) * sizeof(double) + (size_t)rows * slots * 4 * sizeof(int32_t);
+}
+
+static bool dtype_ok(int32_t d) { return d == DSR_BF16 || d == DSR_F32 || d == DSR_F64; }
+
+int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  const dsr_sample_args_t& a = *args;
+  const int64_t words = (a.vocab + 31) / 32;
+  if (!a.logits || !a.policy || !a.out_token || !a.out_consumed || !a.out_status || !dtype_ok(a.dtype) ||
+      a.rows < 0 || a.rows > INT_MAX || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab)
+    return DSR_ERR_ARG;
+  if (a.pen_off && (!a.pen_ids || !a.pen_count || !a.pen_gen)) return DSR_ERR_ARG;
+  if (a.bias_off && (!a.bias_ids || !a.bias_val)) return DSR_ERR_ARG;
+  if (a.allow_bits && a.allow_ld < words) return DSR_ERR_ARG;
+  if ((a.out_probs_f32 || a.out_probs_f64) && a.probs_ld < a.vocab) return DSR_ERR_ARG;
+  if (a.out_kept_bits && a.kept_ld < words) return DSR_ERR_ARG;
+  if (!a.workspace || a.workspace_bytes < dsr_sample_workspace_bytes(a.rows, a.vocab) ||
+      ((uintptr_t)a.workspace & 7u))
+    return DSR_ERR_WORKSPACE;
+  if (a.rows == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (fast_path_eligible(a)) {
+    hipLaunchKernelGGL(k_sample_bf16_fast, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(k_sample_general, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+  }
+  return launched();
+}
+
+int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  const dsr_verify_args_t& a = *args;
+  if (!a.target || (a.K > 0 && (!a.draft || !a.draft_ids || !a.u_accept)) || !a.policy || !a.u_target ||
+      !a.output_limit || !a.out_accepted || !a.out_ids || !a.out_count || !a.out_pending || !a.out_stop ||
+      !a.out_used_accept || !a.out_used_target || !a.out_status || !dtype_ok(a.dtype) || a.K < 0 ||
+      a.K > DSR_MAX_DRAFTS || a.rows < 0 || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab)
+    return DSR_ERR_ARG;
+  if (a.pen_off && (!a.pen_ids || !a.pen_count || !a.pen_gen)) return DSR_ERR_ARG;
+  if (a.bias_off && (!a.bias_ids || !a.bias_val)) return DSR_ERR_ARG;
+  if (a.eos_off && !a.eos_ids) return DSR_ERR_ARG;
+  if (a.allow_bits && a.allow_ld < (a.vocab + 31) / 32) return DSR_ERR_ARG;
+  const int64_t slots = 2 * (int64_t)a.K + 1;
+  if ((int64_t)a.rows * slots > INT_MAX) return DSR_ERR_ARG;
+  if (!a.workspace || a.workspace_bytes < dsr_verify_workspace_bytes(a.rows, a.K, a.vocab) ||
+      ((uintptr_t)a.workspace & 7u))
+    return DSR_ERR_WORKSPACE;
+  if (a.rows == 0) return 0;
+  VerifyLayout L;
+  L.slots = slots;
+  L.stride = ws_stride(a.vocab);
+  L.W = (double*)a.workspace;
+  L.info = (int32_t*)(L.W + (size_t)a.rows * slots * L.stride);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_verify_dists, dim3((unsigned)(a.rows * slots)), dim3(kThreads), 0, s, a, L);
+  if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  hipLaunchKernelGGL(k_verify_decide, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
+  return launched();
+}
+
+int32_t dsr_prob_stats(const double* p, int64_t n, double* out_sum, int32_t* out_i32, void* stream) {
+  if (!p || !out_sum || !out_i32 || n < 1 || n > DSR_MAX_VOCAB) return DSR_ERR_ARG;
+  hipLaunchKernelGGL(k_prob_stats, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, p, n, out_sum, out_i32);
+  return launched();
+}
+
+int32_t dsr_prob_categorical(const double* p, int64_t n, double u, int32_t* out_i32, void* stream) {
+  if (!p || !out_i32 || n < 1 || n > DSR_MAX_VOCAB || !(u >= 0.0 && u < 1.0)) return DSR_ERR_ARG;
+  hipLaunchKernelGGL(k_prob_categorical, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, p, n, u, out_i32);
+  return launched();
+}
+
+int32_t dsr_prob_correction(const double* p, const double* q, int64_t n, double* out, int32_t* out_i32,
+                            void* stream) {
+  if (!p || !q || !out || !out_i32 || n < 1 || n > DSR_MAX_VOCAB) return DSR_ERR_ARG;
+  hipLaunchKernelGGL(k_prob_correction, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, p, q, n, out, out_i32);
+  return launched();
+}
+
+int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, double u, int32_t* out_i32,
+                        void* stream) {
+  if (!p || !q || !out_i32 || n < 1 || n > DSR_MAX_VOCAB || x < 0 || x >= n) return DSR_ERR_ARG;
+  hipLaunchKernelGGL(k_prob_accept, dim3(1), dim3(64), 0, (hipStream_t)stream, p, q, x, u, out_i32);
+  return launched();
+}
+
+}  // extern "C"

@@ -1,0 +1,366 @@
+"""Drop-in replacement of the reference's sampling API, computed on the GPU.
+
+Same names, signatures, validation and error messages as the reference's
+src/deepseekrpc/sampling.py:
+
+* ``SamplingPolicy`` (:28-46) and ``probabilities`` (:48-106): validated on the
+  host exactly as the reference does, then computed by ``dsr_sample_rows``;
+* ``categorical`` (:118-128), ``correction_distribution`` (:131-139) and
+  ``verify_drafts`` (:247-294): control flow on the host (lazy targets, one
+  uniform per tested position, drawn only when needed), arithmetic by the
+  ``dsr_prob_*`` kernels;
+* ``RandomStreams`` / ``RandomTransaction`` (:142-231): three NumPy PCG64
+  domains on the host with transactional begin/commit/abort and the same
+  snapshot format.
+
+Arrays may be NumPy arrays (uploaded; results come back as NumPy) or CUDA
+tensors (kept on the device; results stay device tensors).  There is no CPU
+arithmetic path: without the HIP library every computing call raises.
+"""
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+import hashlib
+import math
+
+import numpy as np
+import torch
+
+from . import _native as N
+from . import batch
+from .jsonutil import ValidationError, hex_id, integer
+
+DOMAINS = ("target", "draft", "accept")
+VOCAB = 129280
+MAX_COUNT = 1048576
+
+_MESSAGES = {
+    N.E_LOGITS: "sampling needs one bounded finite-or-masked floating logit vector",
+    N.E_MASKED: "sampling controls masked every vocabulary token",
+    N.E_NO_MASS: "sampling controls produced no positive probability",
+    N.E_COUNTS: "sampling frequency counts do not match the vocabulary",
+    N.E_GENERATED: "generated token counts must be a subset of complete sampling history",
+    N.E_BIAS: "invalid logit bias mapping",
+    N.E_UNIFORM: "sampling uniform must lie in [0,1)",
+    N.E_CORRECTION: "a rejected proposal has no positive correction distribution",
+    N.E_POLICY: "invalid sampling policy",
+}
+
+
+def _real(value, name, low, high):
+    if isinstance(value, bool) or not isinstance(value, (int, float)) or not math.isfinite(value) \
+            or not low <= value <= high:
+        raise ValidationError(f"invalid {name}")
+    return float(value)
+
+
+def _device():
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _on_device(values, dtype=None):
+    """(device tensor, was_numpy) for a NumPy array or a CUDA tensor."""
+    if isinstance(values, torch.Tensor):
+        if not values.is_cuda:
+            raise ValidationError("sampling tensors must live on the GPU")
+        t = values.detach()
+        return (t if dtype is None else t.to(dtype)).contiguous(), False
+    arr = np.ascontiguousarray(values)
+    return torch.from_numpy(arr).to(_device(), non_blocking=False), True
+
+
+def _raise_status(code):
+    raise ValidationError(_MESSAGES.get(int(code), N.status_message(int(code))))
+
+
+@dataclass(frozen=True)
+class SamplingPolicy:
+    temperature: float = 1.0
+    top_p: float = 1.0
+    top_k: int = 0
+    min_p: float = 0.0
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+
+    def __post_init__(self):
+        for name, low, high in (("temperature", 0, 100), ("top_p", 0, 1), ("min_p", 0, 1),
+                                ("repetition_penalty", 0.01, 100), ("presence_penalty", -2, 2),
+                                ("frequency_penalty", -2, 2)):
+            object.__setattr__(self, name, _real(getattr(self, name), name, low, high))
+        integer(self.top_k, "top-k", 0, VOCAB)
+
+    def as_dict(self):
+        return asdict(self)
+
+    def probabilities(self, logits, *, counts=None, generated_counts=None, logit_bias=None, allowed=None):
+        """Adjusted, filtered and normalised float64 probabilities (sampling.py:48-106)."""
+        device_input = isinstance(logits, torch.Tensor)
+        if device_input:
+            if logits.dim() != 1 or not 1 <= logits.numel() <= VOCAB or \
+                    logits.dtype not in (torch.float32, torch.float64, torch.bfloat16):
+                raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
+            n = logits.numel()
+        else:
+            values = np.asarray(logits)
+            if (values.ndim != 1 or not 1 <= len(values) <= VOCAB or values.dtype not in (np.float32, np.float64)
+                    or np.isnan(values).any() or np.isposinf(values).any()):
+                raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
+            n = len(values)
+        table = None
+        if counts is not None:
+            counts = np.asarray(counts.cpu() if isinstance(counts, torch.Tensor) else counts)
+            if (counts.shape != (n,) or counts.dtype not in (np.int32, np.int64) or (counts < 0).any()
+                    or (counts > MAX_COUNT).any() or int(counts.sum(dtype=np.int64)) > MAX_COUNT):
+                raise ValidationError("sampling frequency counts do not match the vocabulary")
+            gen = counts if generated_counts is None else np.asarray(
+                generated_counts.cpu() if isinstance(generated_counts, torch.Tensor) else generated_counts)
+            if (gen.shape != counts.shape or gen.dtype not in (np.int32, np.int64) or (gen < 0).any()
+                    or (gen > counts).any()):
+                raise ValidationError("generated token counts must be a subset of complete sampling history")
+            table = batch.HistoryTable.from_dense(counts[None], gen[None], device=_device())
+        elif generated_counts is not None:
+            raise ValidationError("generated counts require complete repetition-penalty history")
+        bias = None
+        if logit_bias is not None:
+            if not isinstance(logit_bias, dict) or len(logit_bias) > n:
+                raise ValidationError("invalid logit bias mapping")
+            checked = {}
+            for token, value in logit_bias.items():
+                integer(token, "biased token", 0, n - 1)
+                checked[token] = _real(value, "logit bias", -100, 100)
+            bias = batch.BiasTable.from_dicts([checked], device=_device())
+        allow = None
+        if allowed is not None:
+            mask = np.asarray(allowed.cpu() if isinstance(allowed, torch.Tensor) else allowed)
+            if mask.shape != (n,) or mask.dtype != np.bool_:
+                raise ValidationError("sampling grammar/token mask does not match the vocabulary")
+            allow = torch.from_numpy(batch.pack_allow(mask[None]).astype(np.int32)).to(_device())
+        x, _ = _on_device(logits)
+        res = batch.sample_rows(x.reshape(1, n), [self], history=table, bias=bias, allow_bits=allow, probs="f64")
+        status = int(res.status.item())
+        if status != N.OK:
+            _raise_status(status)
+        out = res.probs[0]
+        return out if device_input else out.cpu().numpy()
+
+
+def _distribution(values):
+    """Validated float64 probability vector on the device (sampling.py:109-115)."""
+    if isinstance(values, torch.Tensor):
+        ok = values.dim() == 1 and 1 <= values.numel() <= VOCAB and values.dtype == torch.float64
+    else:
+        values = np.asarray(values)
+        ok = values.ndim == 1 and 1 <= len(values) <= VOCAB and values.dtype == np.float64
+    if not ok:
+        raise ValidationError("verifier requires a normalized complete FP64 probability vector")
+    t, _ = _on_device(values)
+    total, valid, npos, first, argmax = batch.prob_stats(t)
+    if not valid or not math.isclose(total, 1.0, rel_tol=0, abs_tol=1e-10):
+        raise ValidationError("verifier requires a normalized complete FP64 probability vector")
+    return _Dist(t, npos, first, argmax)
+
+
+@dataclass
+class _Dist:
+    tensor: torch.Tensor
+    positive: int
+    first: int
+    argmax: int
+
+    def __len__(self):
+        return self.tensor.numel()
+
+
+def _as_dist(values):
+    return values if isinstance(values, _Dist) else _distribution(values)
+
+
+def categorical(probabilities, uniform):
+    """Index drawn from ``probabilities``; the uniform is requested only if needed (sampling.py:118-128)."""
+    d = _as_dist(probabilities)
+    if d.positive == 1:
+        return d.first
+    value = uniform()
+    if not isinstance(value, float) or not 0 <= value < 1:
+        raise ValidationError("sampling uniform must lie in [0,1)")
+    token, _flags = batch.prob_categorical(d.tensor, value)
+    return token
+
+
+def _correction(target, proposal):
+    if len(target) != len(proposal):
+        raise ValidationError("target and proposal vocabulary sizes differ")
+    out, status = batch.prob_correction(target.tensor, proposal.tensor)
+    if status != N.OK:
+        raise ValidationError("a rejected proposal has no positive correction distribution")
+    return out
+
+
+def correction_distribution(target, proposal):
+    """Normalised positive part of ``target - proposal`` (sampling.py:131-139)."""
+    numpy_out = not isinstance(target, torch.Tensor)
+    out = _correction(_as_dist(target), _as_dist(proposal))
+    return out.cpu().numpy() if numpy_out else out
+
+
+def _export(generator):
+    state = generator.bit_generator.state
+    return {"state": f"{state['state']['state']:032x}", "increment": f"{state['state']['inc']:032x}",
+            "has_uint32": state["has_uint32"], "uinteger": state["uinteger"]}
+
+
+def _import(state):
+    if not isinstance(state, dict) or set(state) != {"state", "increment", "has_uint32", "uinteger"}:
+        raise ValidationError("invalid PCG64 snapshot fields")
+    for key in ("state", "increment"):
+        hex_id(state[key], 32, f"PCG64 {key}")
+    integer(state["has_uint32"], "PCG64 cached half-word flag", 0, 1)
+    integer(state["uinteger"], "PCG64 cached word", 0, (1 << 32) - 1)
+    increment = int(state["increment"], 16)
+    if increment % 2 != 1:
+        raise ValidationError("PCG64 increment must be odd")
+    generator = np.random.Generator(np.random.PCG64(0))
+    generator.bit_generator.state = {"bit_generator": "PCG64",
+                                     "state": {"state": int(state["state"], 16), "inc": increment},
+                                     "has_uint32": state["has_uint32"], "uinteger": state["uinteger"]}
+    return generator
+
+
+class RandomStreams:
+    """Three independent PCG64 domains seeded from SHA-256 (sampling.py:166-202)."""
+
+    def __init__(self, seed: int):
+        integer(seed, "sampling seed", 0, (1 << 64) - 1)
+        self._streams = {}
+        for domain in DOMAINS:
+            digest = hashlib.sha256(b"DeepSeekRPC/PCG64/v1/" + seed.to_bytes(8, "little") + domain.encode()).digest()
+            self._streams[domain] = np.random.Generator(np.random.PCG64(int.from_bytes(digest[:16], "little")))
+        self.active = False
+
+    def snapshot(self):
+        if self.active:
+            raise ValidationError("terminal RNG snapshot requires a committed idle boundary")
+        return self._snapshot()
+
+    def _snapshot(self):
+        return {"algorithm": "PCG64-domains-v1", "domains": {name: _export(g) for name, g in self._streams.items()}}
+
+    def restore(self, state):
+        if self.active:
+            raise ValidationError("RNG restore requires an idle terminal sampler")
+        self._restore(state)
+
+    def _restore(self, state):
+        if (not isinstance(state, dict) or set(state) != {"algorithm", "domains"}
+                or state["algorithm"] != "PCG64-domains-v1" or not isinstance(state["domains"], dict)
+                or set(state["domains"]) != set(DOMAINS)):
+            raise ValidationError("incompatible terminal RNG snapshot")
+        # Every domain is validated before any live state is replaced.
+        self._streams = {name: _import(state["domains"][name]) for name in DOMAINS}
+
+    def begin(self):
+        if self.active:
+            raise ValidationError("terminal RNG transaction is already active")
+        before = self.snapshot()
+        self.active = True
+        return RandomTransaction(self, before)
+
+
+class RandomTransaction:
+    """One bounded window of draws, committed or fully rolled back (sampling.py:205-231)."""
+
+    def __init__(self, owner, before):
+        self.owner, self.before, self.closed = owner, before, False
+        self.draws = dict.fromkeys(DOMAINS, 0)
+
+    def random(self, domain):
+        if self.closed or domain not in DOMAINS or self.draws[domain] >= 64:
+            raise ValidationError("terminal RNG domain is closed, invalid or exceeds its bounded window")
+        self.draws[domain] += 1
+        return float(self.owner._streams[domain].random())
+
+    def commit(self):
+        if self.closed:
+            raise ValidationError("terminal RNG transaction is already closed")
+        self.closed, self.owner.active = True, False
+        return self.owner.snapshot()
+
+    def prepared_state(self):
+        if self.closed:
+            raise ValidationError("terminal RNG transaction is already closed")
+        return self.owner._snapshot()
+
+    def abort(self):
+        if self.closed:
+            raise ValidationError("terminal RNG transaction is already closed")
+        self.owner._restore(self.before)
+        self.closed, self.owner.active = True, False
+
+
+@dataclass(frozen=True)
+class VerificationDecision:
+    accepted_drafts: int
+    output_ids: tuple[int, ...]
+    pending_token: int | None
+    stop_reason: str | None
+
+    @property
+    def accepted_target_rows(self):
+        # The first verification input was the already sampled seed token.
+        return 1 + self.accepted_drafts
+
+
+def verify_drafts(target_rows, proposal_rows, proposal_ids, transaction, *, greedy: bool, output_limit: int,
+                  eos_ids=frozenset()):
+    """Exact speculative verification: accept with min(1, p/q), else resample
+    from the normalised residual; one target bonus draw when all accept
+    (sampling.py:247-294).  Targets are evaluated lazily, in order."""
+    integer(len(proposal_ids), "proposal length", 0, 5)
+    integer(output_limit, "remaining output limit", 1, MAX_COUNT)
+    if type(greedy) is not bool or len(proposal_rows) != len(proposal_ids) or len(target_rows) != len(proposal_ids) + 1:
+        raise ValidationError("target/proposal verification row counts differ")
+    proposals = tuple(_as_dist(row) for row in proposal_rows)
+    first_target = _as_dist(target_rows[0])
+    vocabulary = len(first_target)
+    if any(len(row) != vocabulary for row in proposals):
+        raise ValidationError("verification probability vocabularies differ")
+
+    def target_at(index):
+        # A finished grammar never builds a later distribution: only used prefixes are evaluated.
+        result = first_target if index == 0 else _as_dist(target_rows[index])
+        if len(result) != vocabulary:
+            raise ValidationError("verification probability vocabularies differ")
+        return result
+
+    for token in (*proposal_ids, *eos_ids):
+        integer(token, "verification token", 0, vocabulary - 1)
+    output = []
+    for index, token in enumerate(proposal_ids):
+        target, proposal = target_at(index), proposals[index]
+        if greedy:
+            positive, _ = batch.prob_accept(target.tensor, proposal.tensor, token, 0.0)
+            if not positive:
+                raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")
+            accepted = token == target.argmax
+        else:
+            positive, _ = batch.prob_accept(target.tensor, proposal.tensor, token, 0.0)
+            if not positive:
+                raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")
+            u = transaction.random("accept")
+            _, accepted = batch.prob_accept(target.tensor, proposal.tensor, token, u)
+        if not accepted:
+            if greedy:
+                replacement = target.argmax
+            else:
+                residual = _distribution(_correction(target, proposal))
+                replacement = categorical(residual, lambda: transaction.random("target"))
+            stop = "eos" if replacement in eos_ids else "length" if len(output) + 1 >= output_limit else None
+            return VerificationDecision(index, tuple(output) + (replacement,), replacement, stop)
+        output.append(token)
+        if token in eos_ids or len(output) >= output_limit:
+            return VerificationDecision(index + 1, tuple(output), None, "eos" if token in eos_ids else "length")
+    bonus_target = target_at(len(proposal_ids))
+    bonus = bonus_target.argmax if greedy else categorical(bonus_target, lambda: transaction.random("target"))
+    stop = "eos" if bonus in eos_ids else "length" if len(output) + 1 >= output_limit else None
+    return VerificationDecision(len(proposal_ids), tuple(output) + (bonus,), bonus, stop)

@@ -1,0 +1,221 @@
+/*
+ * dsr_sampling.h - C ABI of the MI355X (gfx950) token-sampling hot path.
+ *
+ * The reference sampler (Protonburn35/DeepSeekRPC) is a Python/NumPy API with
+ * no native binding: src/deepseekrpc/sampling.py (SamplingPolicy.probabilities
+ * :48-106, categorical :118-128, correction_distribution :131-139,
+ * verify_drafts :247-294) driven by src/deepseekrpc/terminal_sampling.py
+ * (SamplingWork.distribution :127-136, verify :170-183).  Each entry point
+ * below replaces one of those functions for rows that already live in device
+ * memory; the reference copies them to the host first
+ * (terminal_sampling.py:16-27).
+ *
+ * Conventions (after the reference's native extension, native/operations.cu
+ * :12-15,165 and src/deepseekrpc/cuda_ops.py:11-34):
+ *   - every pointer is a device pointer owned by the caller;
+ *   - kernels are launched on the caller's stream; nothing synchronises;
+ *   - the library never allocates: scratch memory is the caller's workspace,
+ *     sized by the matching *_workspace_bytes query;
+ *   - the return value is 0 or a negative DSR_ERR_* launch/argument error;
+ *   - data errors are per-row status codes (DSR_E_*), one per reference
+ *     ValidationError, readable with dsr_status_message().
+ * Every decision-bearing quantity is computed in float64 with IEEE division
+ * and no FMA contraction.  A decision whose threshold lies inside the float64
+ * rounding band (where a different exp or summation order may legitimately
+ * pick the neighbouring token) is still made, and flagged DSR_FLAG_MARGIN.
+ */
+#ifndef DSR_SAMPLING_H
+#define DSR_SAMPLING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSR_ABI_VERSION 1
+#define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
+#define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
+#define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
+
+/* Logit element types. */
+#define DSR_BF16 1
+#define DSR_F32 2
+#define DSR_F64 3
+
+/* Per-row status codes: 0 or the reference ValidationError it stands for. */
+#define DSR_OK 0
+#define DSR_E_LOGITS 1          /* sampling.py:50-52: NaN / +inf logit */
+#define DSR_E_MASKED 2          /* sampling.py:80-81: every token masked */
+#define DSR_E_NO_MASS 3         /* sampling.py:103-105: no positive probability */
+#define DSR_E_UNIFORM 4         /* sampling.py:123-125: uniform outside [0,1) */
+#define DSR_E_COUNTS 5          /* sampling.py:55-58,62-65: bad history counts */
+#define DSR_E_BIAS 6            /* sampling.py:69-74: bad logit bias */
+#define DSR_E_PROPOSAL_ZERO 7   /* sampling.py:276-277: q[x] == 0 */
+#define DSR_E_CORRECTION 8      /* sampling.py:135-138: empty residual */
+#define DSR_E_TOKEN 9           /* sampling.py:271-272: token id out of range */
+#define DSR_E_DISTRIBUTION 10   /* sampling.py:109-115: not a distribution */
+#define DSR_E_POLICY 11         /* sampling.py:38-43: control outside its bounds */
+#define DSR_E_GENERATED 12      /* sampling.py:62-65: generated counts not within counts */
+
+/* Launch / argument errors (return values). */
+#define DSR_ERR_ARG (-1)
+#define DSR_ERR_LAUNCH (-2)
+#define DSR_ERR_WORKSPACE (-3)
+
+/* Per-row flags. */
+#define DSR_FLAG_MARGIN 1u      /* a threshold decision sat inside the rounding band */
+
+/* Verifier stop reasons (sampling.py:286,289,294). */
+#define DSR_STOP_NONE 0
+#define DSR_STOP_EOS 1
+#define DSR_STOP_LENGTH 2
+
+/* One row's sampling controls: SamplingPolicy (sampling.py:28-43).  A row
+ * whose controls are outside these bounds gets status DSR_E_POLICY. */
+typedef struct dsr_policy {
+  double temperature;          /* [0, 100]; 0 = greedy argmax */
+  double top_p;                /* [0, 1]; 1 = off */
+  double min_p;                /* [0, 1]; 0 = off */
+  double repetition_penalty;   /* [0.01, 100] */
+  double presence_penalty;     /* [-2, 2] */
+  double frequency_penalty;    /* [-2, 2] */
+  int32_t top_k;               /* [0, 129280]; 0 = off */
+  int32_t reserved;            /* must be 0 */
+} dsr_policy_t;
+
+/* Arguments of dsr_sample_rows.  Optional pointers may be NULL.
+ *
+ * History counts are a per-row sparse table in CSR form: row r owns entries
+ * [pen_off[r], pen_off[r+1]) of pen_ids / pen_count / pen_gen, with strictly
+ * increasing token ids, 1 <= count <= 1048576, 0 <= gen <= count and a row
+ * total <= 1048576.  It is exactly the reference's dense `counts` /
+ * `generated_counts` pair restricted to counts > 0 (sampling.py:54-66).
+ * Logit bias is a second per-row CSR table with strictly increasing ids and
+ * values in [-100, 100] (sampling.py:69-74).  allow_bits holds one bit per
+ * token, bit (i & 31) of word i >> 5, 1 = allowed (sampling.py:75-79). */
+typedef struct dsr_sample_args {
+  const void* logits;          /* [rows, ld] of dtype */
+  int32_t dtype;               /* DSR_BF16 | DSR_F32 | DSR_F64 */
+  int32_t reserved0;
+  int64_t rows;
+  int64_t vocab;               /* 1 .. 129280 */
+  int64_t ld;                  /* elements between rows, >= vocab */
+  const dsr_policy_t* policy;  /* [rows] */
+  const int64_t* pen_off;      /* [rows + 1] or NULL (no penalties) */
+  const int32_t* pen_ids;
+  const int32_t* pen_count;
+  const int32_t* pen_gen;
+  const int64_t* bias_off;     /* [rows + 1] or NULL (no bias) */
+  const int32_t* bias_ids;
+  const double* bias_val;
+  const uint32_t* allow_bits;  /* [rows, allow_ld] words or NULL */
+  int64_t allow_ld;
+  const double* uniforms;      /* [rows] pre-drawn u in [0,1), or NULL: no draw */
+  int32_t* out_token;          /* [rows] sampled id, -1 on error / no draw */
+  uint8_t* out_consumed;       /* [rows] 1 if the draw used its uniform */
+  int32_t* out_status;         /* [rows] DSR_OK or DSR_E_* */
+  uint8_t* out_flags;          /* [rows] DSR_FLAG_* or NULL */
+  float* out_probs_f32;        /* [rows, probs_ld] final probabilities or NULL */
+  double* out_probs_f64;       /* [rows, probs_ld] final probabilities or NULL */
+  int64_t probs_ld;
+  uint32_t* out_kept_bits;     /* [rows, kept_ld] tokens still finite after top-k, or NULL */
+  int64_t kept_ld;
+  void* workspace;             /* >= dsr_sample_workspace_bytes(rows, vocab) */
+  size_t workspace_bytes;
+} dsr_sample_args_t;
+
+/* Arguments of dsr_verify_drafts: the exact sampled speculative verifier for
+ * `rows` requests with K drafts each (SamplingWork.verify ->
+ * verify_drafts, terminal_sampling.py:170-183, sampling.py:247-294).
+ * Target row j and draft row j of a request are both conditioned on the
+ * accepted prefix draft_ids[:j] (each prefix token adds one to count and
+ * generated count, terminal_sampling.py:127-136) and on allow mask j. */
+typedef struct dsr_verify_args {
+  const void* target;          /* [rows, K+1, ld] logits */
+  const void* draft;           /* [rows, K, ld] logits */
+  int32_t dtype;
+  int32_t K;                   /* 0 .. 5 */
+  int64_t rows;
+  int64_t vocab;
+  int64_t ld;
+  const int32_t* draft_ids;    /* [rows, K] */
+  const dsr_policy_t* policy;  /* [rows] */
+  const int64_t* pen_off;      /* as dsr_sample_args_t, per request */
+  const int32_t* pen_ids;
+  const int32_t* pen_count;
+  const int32_t* pen_gen;
+  const int64_t* bias_off;
+  const int32_t* bias_ids;
+  const double* bias_val;
+  const uint32_t* allow_bits;  /* [rows, K+1, allow_ld] or NULL */
+  int64_t allow_ld;
+  const double* u_accept;      /* [rows, K] */
+  const double* u_target;      /* [rows] */
+  const int64_t* eos_off;      /* [rows + 1] CSR of EOS ids, or NULL */
+  const int32_t* eos_ids;
+  const int32_t* output_limit; /* [rows], 1 .. 1048576 */
+  int32_t* out_accepted;       /* [rows] accepted drafts */
+  int32_t* out_ids;            /* [rows, K+1] output ids, -1 padded */
+  int32_t* out_count;          /* [rows] number of output ids */
+  int32_t* out_pending;        /* [rows] pending token or -1 */
+  int32_t* out_stop;           /* [rows] DSR_STOP_* */
+  int32_t* out_used_accept;    /* [rows] accept-domain draws consumed */
+  int32_t* out_used_target;    /* [rows] target-domain draws consumed (0/1) */
+  int32_t* out_status;         /* [rows] */
+  uint8_t* out_flags;          /* [rows] or NULL */
+  void* workspace;             /* >= dsr_verify_workspace_bytes(rows, K, vocab) */
+  size_t workspace_bytes;
+} dsr_verify_args_t;
+
+/* ABI gate, after the reference's abi_version() (native/bindings.cpp:25). */
+int32_t dsr_abi_version(void);
+
+/* Message of a DSR_E_* status code (the reference's ValidationError text). */
+const char* dsr_status_message(int32_t code);
+
+/* Workspace queries. */
+size_t dsr_sample_workspace_bytes(int64_t rows, int64_t vocab);
+size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab);
+
+/* Fused penalties -> temperature -> top-k -> softmax -> min-p -> top-p ->
+ * categorical draw for `rows` independent rows.
+ * Replaces SamplingPolicy.probabilities + categorical (sampling.py:48-128),
+ * as called by TerminalSampler.begin_seed (terminal_sampling.py:83-95). */
+int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream);
+
+/* Exact sampled verifier; replaces SamplingWork.verify (terminal_sampling.py
+ * :170-183) with verify_drafts (sampling.py:247-294) and the lazy
+ * conditional targets (terminal_sampling.py:234-244). */
+int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream);
+
+/* Probability-vector kernels behind the drop-in categorical /
+ * correction_distribution / verify_drafts on float64 distributions.
+ * Each works on one vector p[n] (n <= 129280) and writes a small result.
+ *
+ * dsr_prob_stats (sampling.py:109-115,120-122): out_sum[0] = sum of p,
+ *   out_i32[0] = 1 if every entry is finite and >= 0, out_i32[1] = number of
+ *   positive entries, out_i32[2] = first positive index, out_i32[3] = first
+ *   index of the maximum (np.argmax). */
+int32_t dsr_prob_stats(const double* p, int64_t n, double* out_sum, int32_t* out_i32, void* stream);
+
+/* dsr_prob_categorical (sampling.py:126-128): first i with
+ * cumsum(p)[i] / sum(p) > u.  out_i32[0] = token, out_i32[1] = flags. */
+int32_t dsr_prob_categorical(const double* p, int64_t n, double u, int32_t* out_i32, void* stream);
+
+/* dsr_prob_correction (sampling.py:131-139): out = max(p - q, 0) / sum;
+ * out_i32[0] = status (DSR_OK or DSR_E_CORRECTION). */
+int32_t dsr_prob_correction(const double* p, const double* q, int64_t n, double* out, int32_t* out_i32,
+                            void* stream);
+
+/* dsr_prob_accept (sampling.py:276-281): out_i32[0] = 1 if q[x] > 0,
+ * out_i32[1] = 1 if u < min(1, p[x] / q[x]). */
+int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, double u, int32_t* out_i32,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSR_SAMPLING_H */

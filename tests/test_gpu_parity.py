@@ -1,0 +1,264 @@
+"""HIP path against the oracle on identical inputs and pre-drawn uniforms.
+
+Token ids, consumption flags, top-k index sets and statuses must be bit-exact;
+fp32 probabilities within 1e-5 relative (exactly zero where the oracle is
+zero).  The only tolerated token difference is a decision flagged as lying
+inside the float64 rounding band (by the GPU's DSR_FLAG_MARGIN or the
+oracle's own margin), and such rows must be rare.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from deepseekrpc_amd import _native as N
+from deepseekrpc_amd import batch, workloads
+from oracle import sampling_oracle as O
+from parity_util import compare, oracle_row, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def check(rep, max_margin_frac=0.01):
+    print(f"rows={rep.rows} exact={rep.exact} margin={rep.margin_rows} max_rel={rep.max_rel:.3g}", flush=True)
+    assert not rep.mismatches, rep.mismatches[:10]
+    assert len(rep.margin_rows) <= max(1, int(max_margin_frac * rep.rows))
+
+
+def test_c1_single_row_fp32():
+    w = workloads.c1()
+    gpu = run_gpu(w)
+    check(compare(w, gpu))
+
+
+def test_c2_penalised_rows():
+    w = workloads.c2()
+    gpu = run_gpu(w)
+    check(compare(w, gpu))
+
+
+def test_c3_metric_workload_all_rows():
+    w = workloads.c3()
+    gpu = run_gpu(w)
+    check(compare(w, gpu))
+
+
+def test_c5_stress_rows():
+    w = workloads.c5()
+    gpu = run_gpu(w, probs=None, kept=False)
+    # Every greedy row at full size: the first argmax of the adjusted logits.
+    V = w.logits.shape[1]
+    for r in range(0, w.rows, 2):
+        c = np.bincount(w.histories[r], minlength=V).astype(np.int32)
+        v = O.adjusted_logits(w.logits[r], O.Policy(**w.policies[r]), c, c)
+        assert gpu["tokens"][r] == int(np.argmax(v)) and gpu["consumed"][r] == 0 and gpu["status"][r] == 0
+    # Sampled rows from both families against the full oracle.
+    rows = [r for r in list(range(1, 96, 2)) + list(range(513, 608, 2))]
+    sub = workloads.select_rows(w, rows)
+    gpu_sub = {k: v[rows] for k, v in gpu.items()}
+    check(compare(sub, gpu_sub), max_margin_frac=0.05)
+
+
+def test_c5_near_tie_rows_with_probs_and_sets():
+    w = workloads.select_rows(workloads.c5(), list(range(512, 544)))
+    gpu = run_gpu(w)
+    check(compare(w, gpu), max_margin_frac=0.1)
+
+
+GOLD = np.load(os.path.join(HERE, "golden", "sampling_golden.npz"))
+META = json.load(open(os.path.join(HERE, "golden", "sampling_golden.json")))
+
+
+@pytest.mark.parametrize("case", META["probabilities"], ids=lambda c: c["name"])
+def test_golden_vectors_on_gpu(case):
+    from test_oracle_golden import golden_case
+    logits, counts, gen, bias, allowed = golden_case(case)
+    n = case["name"]
+    V = len(logits)
+    dev = "cuda"
+    x = torch.from_numpy(np.ascontiguousarray(logits)).to(dev).reshape(1, V)
+    hist = None if counts is None else batch.HistoryTable.from_dense(counts[None], gen[None], device=dev)
+    bt = None if bias is None else batch.BiasTable.from_dicts([bias], device=dev)
+    allow = None if allowed is None else torch.from_numpy(batch.pack_allow(allowed[None]).view(np.int32)).to(dev)
+    for u, want in zip(case["uniforms"], case["ids"]):
+        res = batch.sample_rows(x, [case["policy"]], history=hist, bias=bt, allow_bits=allow,
+                                uniforms=torch.tensor([u], dtype=torch.float64, device=dev), probs="f64")
+        assert int(res.status.item()) == 0
+        assert int(res.tokens.item()) == want or int(res.flags.item()) & 1
+        p = res.probs[0].cpu().numpy()
+        if f"{n}/probs" in GOLD:
+            ref = GOLD[f"{n}/probs"]
+            np.testing.assert_array_equal(p > 0, ref > 0)
+            np.testing.assert_allclose(p, ref, rtol=1e-12, atol=0)
+        else:
+            np.testing.assert_allclose(p[GOLD[f"{n}/probs_top_idx"]], GOLD[f"{n}/probs_top_val"], rtol=1e-12)
+            assert abs(p.sum() - 1) < 1e-12
+
+
+def _one(logits, policy, u=0.5, **kw):
+    x = torch.as_tensor(np.asarray(logits)).to("cuda").reshape(1, -1)
+    res = batch.sample_rows(x, [policy], uniforms=torch.tensor([u], dtype=torch.float64, device="cuda"),
+                            probs="f64", **kw)
+    return int(res.status.item()), int(res.tokens.item()), int(res.consumed.item()), res.probs[0].cpu().numpy()
+
+
+def test_edge_cases_against_oracle():
+    rng = np.random.default_rng(5)
+    cases = [
+        (np.array([0.5]), dict()),
+        (np.array([1.0, 1.0]), dict()),
+        (np.array([1.0, 1.0, 1.0]), dict(temperature=1e-320)),
+        (np.log(np.array([.5, .3, .2])), dict(top_p=0.0)),
+        (np.log(np.array([.5, .3, .2])), dict(min_p=1.0)),
+        (np.array([-np.inf, 2.0, -np.inf]), dict(top_k=1)),
+        (rng.normal(0, 1, 1000), dict(top_k=999, top_p=0.999999)),
+        (rng.normal(0, 1, 1000), dict(top_k=1000)),
+        (rng.normal(0, 1, 1000), dict(top_k=5000)),
+        (np.round(rng.normal(0, 1, 777), 1), dict(top_k=37, top_p=0.6, temperature=0.3)),
+        (rng.normal(0, 50, 4099), dict(temperature=100.0, min_p=0.9)),
+        (np.zeros(64), dict(top_p=0.5)),
+        (np.zeros(65), dict(top_k=3)),
+    ]
+    for logits, kw in cases:
+        for dtype in (np.float64, np.float32):
+            x = logits.astype(dtype)
+            for u in (0.0, 0.37, np.nextafter(1.0, 0.0)):
+                st, tok, used, p = _one(x, kw, float(u))
+                ref = O.sample_row(x, O.Policy(**kw), float(u))
+                assert st == ref.status, (kw, dtype)
+                assert tok == ref.token and bool(used) == ref.consumed, (kw, dtype, u, tok, ref.token)
+                np.testing.assert_allclose(p, ref.probs, rtol=1e-12, atol=1e-300)
+
+
+def test_status_codes():
+    assert _one(np.array([0.0, np.nan]), {})[0] == N.E_LOGITS
+    assert _one(np.array([0.0, np.inf]), {})[0] == N.E_LOGITS
+    assert _one(np.array([-np.inf, -np.inf]), {})[0] == N.E_MASKED
+    allow = torch.zeros(1, 1, dtype=torch.int32, device="cuda")
+    assert _one(np.array([1.0, 2.0]), {}, allow_bits=allow)[0] == N.E_MASKED
+    assert _one(np.array([1.0, 2.0]), {}, u=1.0)[0] == N.E_UNIFORM
+    assert _one(np.array([1.0, 2.0]), {}, u=-0.1)[0] == N.E_UNIFORM
+    assert _one(np.array([1.0, 9.0]), {"temperature": 0}, u=7.0)[0] == 0   # no draw: the uniform is not read
+    assert _one(np.array([1.0, 2.0]), {"temperature": -1.0})[0] == N.E_POLICY
+    assert _one(np.array([1.0, 2.0]), {"top_k": -2})[0] == N.E_POLICY
+    d = "cuda"
+    h = batch.HistoryTable(torch.tensor([0, 1], device=d), torch.tensor([1], dtype=torch.int32, device=d),
+                           torch.tensor([1], dtype=torch.int32, device=d), torch.tensor([2], dtype=torch.int32, device=d))
+    assert _one(np.array([1.0, 2.0]), {}, history=h)[0] == N.E_GENERATED
+    h.counts.fill_(2_000_000)
+    assert _one(np.array([1.0, 2.0]), {}, history=h)[0] == N.E_COUNTS
+    h = batch.HistoryTable(torch.tensor([0, 1], device=d), torch.tensor([5], dtype=torch.int32, device=d),
+                           torch.tensor([1], dtype=torch.int32, device=d), torch.tensor([1], dtype=torch.int32, device=d))
+    assert _one(np.array([1.0, 2.0]), {}, history=h)[0] == N.E_COUNTS
+    b = batch.BiasTable(torch.tensor([0, 1], device=d), torch.tensor([0], dtype=torch.int32, device=d),
+                        torch.tensor([101.0], dtype=torch.float64, device=d))
+    assert _one(np.array([1.0, 2.0]), {}, bias=b)[0] == N.E_BIAS
+
+
+def test_penalties_bias_mask_match_oracle_on_mixed_rows():
+    rng = np.random.default_rng(9)
+    V, B = 5000, 24
+    logits = workloads.bf16_round(rng.normal(0, 2, (B, V)))
+    dev = "cuda"
+    counts = np.zeros((B, V), np.int32)
+    gens = np.zeros((B, V), np.int32)
+    biases, pols = [], []
+    for r in range(B):
+        h = rng.integers(0, V, int(rng.integers(0, 400)))
+        counts[r] = np.bincount(h, minlength=V)
+        gens[r] = np.minimum(counts[r], np.bincount(h[len(h) // 3:], minlength=V))
+        ids = rng.choice(V, int(rng.integers(0, 20)), replace=False)
+        biases.append({int(t): float(rng.uniform(-100, 100)) for t in ids})
+        pols.append(dict(temperature=float(rng.choice([0.0, 0.5, 1.0, 1.7])), top_k=int(rng.choice([0, 1, 40, 4999])),
+                         top_p=float(rng.choice([1.0, 0.9, 0.3])), min_p=float(rng.choice([0.0, 0.02])),
+                         repetition_penalty=float(rng.uniform(0.5, 2)), presence_penalty=float(rng.uniform(-2, 2)),
+                         frequency_penalty=float(rng.uniform(-2, 2))))
+    allowed = rng.random((B, V)) < 0.8
+    u = rng.random(B)
+    x = torch.from_numpy(workloads.bf16_bits(logits).view(np.int16)).to(dev).view(torch.bfloat16)
+    res = batch.sample_rows(x, pols, history=batch.HistoryTable.from_dense(counts, gens, device=dev),
+                            bias=batch.BiasTable.from_dicts(biases, device=dev),
+                            allow_bits=torch.from_numpy(batch.pack_allow(allowed).view(np.int32)).to(dev),
+                            uniforms=torch.from_numpy(u).to(dev), probs="f64", kept=True)
+    kept = batch.unpack_bits(res.kept_bits.cpu().numpy().view(np.uint32), V)
+    probs = res.probs.cpu().numpy()
+    for r in range(B):
+        ref = O.sample_row(logits[r], O.Policy(**pols[r]), float(u[r]), counts[r], gens[r], biases[r], allowed[r])
+        assert int(res.status[r]) == ref.status
+        if ref.status:
+            continue
+        if not (int(res.flags[r]) & 1 or ref.margin < 1e-11):
+            assert int(res.tokens[r]) == ref.token and bool(res.consumed[r]) == ref.consumed, r
+        np.testing.assert_array_equal(kept[r], ref.topk_kept)
+        np.testing.assert_allclose(probs[r], ref.probs, rtol=1e-12, atol=1e-300)
+
+
+def test_strided_rows_and_odd_vocab():
+    rng = np.random.default_rng(2)
+    V, ld = 1001, 1040
+    base = rng.normal(0, 1, (6, ld)).astype(np.float32)
+    x = torch.from_numpy(base).to("cuda")[:, :V]
+    assert x.stride(0) == ld
+    pols = [dict(top_k=20, top_p=0.8, temperature=0.9)] * 6
+    u = rng.random(6)
+    res = batch.sample_rows(x, pols, uniforms=torch.from_numpy(u).to("cuda"))
+    for r in range(6):
+        ref = O.sample_row(base[r, :V], O.Policy(**pols[r]), float(u[r]))
+        assert int(res.tokens[r]) == ref.token
+
+
+def test_verify_c4_against_oracle():
+    w = workloads.c4()
+    e = w.extra
+    dev = "cuda"
+    R, K, V = e["target"].shape[0], e["K"], e["target"].shape[2]
+    tgt = torch.from_numpy(e["target"]).to(dev)
+    drf = torch.from_numpy(e["draft"]).to(dev)
+    # Proposal step on the GPU: draft ids drawn from each draft row.
+    draw = batch.sample_rows(drf.reshape(R * K, V), [dict()] * (R * K),
+                             uniforms=torch.from_numpy(e["u_draft"].reshape(-1)).to(dev))
+    ids = draw.tokens.reshape(R, K).contiguous()
+    res = batch.verify_drafts(tgt, drf, ids, [dict()] * R, torch.from_numpy(e["u_accept"]).to(dev),
+                              torch.from_numpy(e["u_target"]).to(dev), torch.from_numpy(e["limit"]).to(dev))
+    torch.cuda.synchronize()
+    ids_np = ids.cpu().numpy()
+    hits = 0
+    for r in range(R):
+        ref = O.verify(e["target"][r], e["draft"][r], list(ids_np[r]), O.Policy(), e["u_accept"][r],
+                       float(e["u_target"][r]), output_limit=10)
+        assert int(res.status[r]) == ref.status == 0
+        got = (int(res.accepted[r]), tuple(int(t) for t in res.ids[r, :int(res.count[r])].tolist()),
+               None if int(res.pending[r]) < 0 else int(res.pending[r]), int(res.used_accept[r]),
+               int(res.used_target[r]))
+        want = (ref.accepted, ref.output_ids, ref.pending, ref.used_accept, ref.used_target)
+        if got == want:
+            hits += 1
+        else:
+            assert int(res.flags[r]) & 1 or ref.margin < 1e-11, (r, got, want)
+    assert hits >= R - 1
+
+
+@pytest.mark.parametrize("case", META["verify"], ids=lambda c: c["name"])
+def test_verify_golden_on_gpu(case):
+    dev = "cuda"
+    tgt = torch.from_numpy(GOLD[f"{case['name']}/target"]).to(dev)[None]
+    drf = torch.from_numpy(GOLD[f"{case['name']}/draft"]).to(dev)[None]
+    ids = torch.tensor([case["ids"]], dtype=torch.int32, device=dev)
+    eos = case["eos"]
+    res = batch.verify_drafts(tgt, drf, ids, [case["policy"]], torch.tensor([case["u_accept"]], device=dev),
+                              torch.tensor([case["u_target"]], device=dev),
+                              torch.tensor([case["limit"]], dtype=torch.int32, device=dev),
+                              eos_offsets=torch.tensor([0, len(eos)], dtype=torch.int64, device=dev),
+                              eos_ids=torch.tensor(eos, dtype=torch.int32, device=dev))
+    assert int(res.status.item()) == 0
+    n = int(res.count.item())
+    stop = {0: None, 1: "eos", 2: "length"}[int(res.stop.item())]
+    pending = int(res.pending.item())
+    assert (int(res.accepted.item()), res.ids[0, :n].tolist(), None if pending < 0 else pending, stop) == (
+        case["accepted"], case["output_ids"], case["pending"], case["stop"])
+    assert int(res.used_accept.item()) == case["calls"].count("accept")
+    assert int(res.used_target.item()) == case["calls"].count("target")

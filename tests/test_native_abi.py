@@ -1,0 +1,96 @@
+"""The C-ABI library loads on the CPU and exports what include/dsr_sampling.h
+declares; struct layouts agree between the header and the ctypes binding.
+No compute call is made here (there is no GPU)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from deepseekrpc_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsr_sampling.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|size_t|const char\*)\s+(dsr_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exists_and_loads():
+    lib = N.load()
+    assert lib.dsr_abi_version() == N.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported():
+    lib = N.load()
+    names = declared_functions()
+    assert set(names) == set(N.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_status_messages_match_reference_texts():
+    assert N.status_message(N.E_MASKED) == "sampling controls masked every vocabulary token"
+    assert N.status_message(N.E_NO_MASS) == "sampling controls produced no positive probability"
+    assert N.status_message(N.E_UNIFORM) == "sampling uniform must lie in [0,1)"
+    assert "unknown" in N.status_message(999)
+
+
+def test_workspace_queries():
+    lib = N.load()
+    assert lib.dsr_sample_workspace_bytes(256, 129280) == 256 * 129280 * 8
+    assert lib.dsr_sample_workspace_bytes(1, 3) == 32 * 8
+    assert lib.dsr_verify_workspace_bytes(32, 4, 129280) == 32 * 9 * 129280 * 8 + 32 * 9 * 16
+
+
+def test_argument_errors_return_before_any_launch():
+    lib = N.load()
+    a = N.SampleArgs()  # all null
+    assert lib.dsr_sample_rows(ctypes.byref(a), None) == -1
+    assert lib.dsr_sample_rows(None, None) == -1
+    v = N.VerifyArgs()
+    assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1
+    assert lib.dsr_prob_stats(None, 3, None, None, None) == -1
+    assert lib.dsr_prob_categorical(None, 3, 0.5, None, None) == -1
+
+
+LAYOUT_C = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "dsr_sampling.h"
+#define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
+int main(void) {
+  printf("dsr_policy_t size %zu\n", sizeof(dsr_policy_t));
+  printf("dsr_sample_args_t size %zu\n", sizeof(dsr_sample_args_t));
+  printf("dsr_verify_args_t size %zu\n", sizeof(dsr_verify_args_t));
+  %FIELDS%
+  return 0;
+}
+"""
+
+
+def test_struct_layouts_match_header(tmp_path):
+    fields = []
+    for cname, cls in (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs),
+                       ("dsr_verify_args_t", N.VerifyArgs)):
+        fields += [f"F({cname}, {f})" for f, _ in cls._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(LAYOUT_C.replace("%FIELDS%", "\n  ".join(fields)))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {}
+    for line in out:
+        if line:
+            t, f, off = line.split()
+            got[(t, f)] = int(off)
+    assert got[("dsr_policy_t", "size")] == ctypes.sizeof(N.Policy)
+    assert got[("dsr_sample_args_t", "size")] == ctypes.sizeof(N.SampleArgs)
+    assert got[("dsr_verify_args_t", "size")] == ctypes.sizeof(N.VerifyArgs)
+    for cname, cls in (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs),
+                       ("dsr_verify_args_t", N.VerifyArgs)):
+        for f, _ in cls._fields_:
+            assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
