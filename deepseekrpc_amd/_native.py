@@ -31,6 +31,7 @@ E_POLICY = 11
 E_GENERATED = 12
 
 FLAG_MARGIN = 1
+FLAG_GENERAL = 2
 STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 
 EXPORTS = (

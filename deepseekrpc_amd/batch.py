@@ -33,11 +33,23 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _require_cuda(t, name):
+def _require_cuda(t, name, rows_strided=False):
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise TypeError(f"{name} must be a device tensor")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    ok = (t.dim() == 2 and t.stride(1) == 1 and t.stride(0) >= t.shape[1]) if rows_strided else t.is_contiguous()
+    if not ok:
+        raise ValueError(f"{name} must be contiguous" + (" within rows" if rows_strided else ""))
+
+
+def _require(t, name, dtype, numel=None):
+    _require_cuda(t, name)
+    if t.dtype != dtype or (numel is not None and t.numel() != numel):
+        raise ValueError(f"{name} must be {dtype} with {numel} elements")
+
+
+def _nonempty(table, field):
+    """Tables without entries are passed as absent (an empty tensor has no data pointer)."""
+    return table is not None and getattr(table, field).numel() > 0
 
 
 def policy_array(policies) -> np.ndarray:
@@ -196,7 +208,7 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     ``probs`` may be ``"f32"`` or ``"f64"`` to return the final probabilities.
     """
     lib = N.load()
-    _require_cuda(logits, "logits")
+    _require_cuda(logits, "logits", rows_strided=True)
     if logits.dim() != 2 or logits.dtype not in _DTYPES:
         raise ValueError("logits must be a [rows, V] bf16/f32/f64 tensor")
     rows, V = logits.shape
@@ -229,10 +241,10 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     a.dtype = _DTYPES[logits.dtype]
     a.rows, a.vocab, a.ld = rows, V, logits.stride(0)
     a.policy = policies.data_ptr()
-    if history is not None:
+    if _nonempty(history, "ids"):
         a.pen_off, a.pen_ids = history.offsets.data_ptr(), history.ids.data_ptr()
         a.pen_count, a.pen_gen = history.counts.data_ptr(), history.generated.data_ptr()
-    if bias is not None:
+    if _nonempty(bias, "ids"):
         a.bias_off, a.bias_ids, a.bias_val = bias.offsets.data_ptr(), bias.ids.data_ptr(), bias.values.data_ptr()
     if allow_bits is not None:
         a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.stride(0)
@@ -307,8 +319,12 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
         _require_cuda(draft, "draft")
         if tuple(draft.shape) != (rows, K, V) or draft.dtype != target.dtype:
             raise ValueError("draft must be [rows, K, V] of the target dtype")
-        _require_cuda(draft_ids, "draft_ids")
-        _require_cuda(u_accept, "u_accept")
+        _require(draft_ids, "draft_ids", torch.int32, rows * K)
+        _require(u_accept, "u_accept", torch.float64, rows * K)
+    _require(u_target, "u_target", torch.float64, rows)
+    _require(output_limit, "output_limit", torch.int32, rows)
+    if target.dtype not in _DTYPES:
+        raise ValueError("target must be bf16/f32/f64")
     if not isinstance(policies, torch.Tensor):
         policies = policy_tensor(policies, dev)
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
@@ -322,16 +338,19 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     a.K, a.rows, a.vocab, a.ld = K, rows, V, V
     a.draft_ids = draft_ids.data_ptr() if K > 0 else None
     a.policy = policies.data_ptr()
-    if history is not None:
+    if _nonempty(history, "ids"):
         a.pen_off, a.pen_ids = history.offsets.data_ptr(), history.ids.data_ptr()
         a.pen_count, a.pen_gen = history.counts.data_ptr(), history.generated.data_ptr()
-    if bias is not None:
+    if _nonempty(bias, "ids"):
         a.bias_off, a.bias_ids, a.bias_val = bias.offsets.data_ptr(), bias.ids.data_ptr(), bias.values.data_ptr()
     if allow_bits is not None:
+        _require_cuda(allow_bits, "allow_bits")
         a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.shape[-1]
     a.u_accept = u_accept.data_ptr() if K > 0 else None
     a.u_target = u_target.data_ptr()
-    if eos_offsets is not None:
+    if eos_offsets is not None and eos_ids is not None and eos_ids.numel() > 0:
+        _require(eos_offsets, "eos_offsets", torch.int64, rows + 1)
+        _require_cuda(eos_ids, "eos_ids")
         a.eos_off, a.eos_ids = eos_offsets.data_ptr(), eos_ids.data_ptr()
     a.output_limit = output_limit.data_ptr()
     a.out_accepted, a.out_ids, a.out_count = res.accepted.data_ptr(), res.ids.data_ptr(), res.count.data_ptr()

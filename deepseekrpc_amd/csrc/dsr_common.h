@@ -1,11 +1,15 @@
 // Device-side building blocks shared by the sampling kernels (gfx950, wave64).
 //
 // Every block-wide reduction here runs in a fixed order (xor butterflies
-// inside a wave, then the per-wave partials summed in wave order), so a
-// floating-point result is bit-reproducible from run to run.
+// inside a wave, then the 16 per-wave partials combined by a butterfly over
+// lanes 0..15), so a floating-point result is bit-reproducible from run to
+// run.  The cross-wave step reads one partial per lane, which keeps register
+// pressure low in kernels that hold a whole row in VGPRs.
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "dsr_sampling.h"
@@ -22,142 +26,123 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 // barriers, reads, and barriers again, so calls can follow each other freely.
 struct BlockScratch {
   double f64[kWaves];
-  unsigned long long u64[kWaves];
   long long i64[kWaves];
   double bcast_f[4];
   long long bcast_i[4];
 };
 
-template <class T>
-__device__ __forceinline__ T wave_sum(T x) {
+struct OpSum {
+  template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+  template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return b > a ? b : a; }
+};
+struct OpMin {
+  template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }
+};
+
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T x, Op op) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  for (int o = 32; o > 0; o >>= 1) x = op(x, __shfl_xor(x, o));
   return x;
 }
 
 template <class T>
-__device__ __forceinline__ T wave_max(T x) {
+__device__ __forceinline__ T wave_sum(T x) { return wave_reduce(x, OpSum()); }
+
+// Combines the per-wave partials slot[0..15]: lane l < 16 takes slot[l] and a
+// four-step butterfly leaves the result in every lane of every wave.
+template <class T, class Op>
+__device__ __forceinline__ T combine_waves(const T* slot, T identity, Op op) {
+  const int l = lane_id();
+  T y = l < kWaves ? slot[l] : identity;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T y = __shfl_xor(x, o);
-    x = y > x ? y : x;
-  }
-  return x;
+  for (int o = 8; o > 0; o >>= 1) y = op(y, __shfl_xor(y, o));
+  return __shfl(y, 0);
 }
 
-template <class T>
-__device__ __forceinline__ T wave_min(T x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T y = __shfl_xor(x, o);
-    x = y < x ? y : x;
-  }
-  return x;
+template <class T, class Op>
+__device__ __forceinline__ T block_reduce(T x, T* slot, T identity, Op op) {
+  x = wave_reduce(x, op);
+  if (lane_id() == 0) slot[wave_id()] = x;
+  __syncthreads();
+  const T r = combine_waves(slot, identity, op);
+  __syncthreads();
+  return r;
 }
 
 __device__ __forceinline__ double block_sum(double x, BlockScratch& s) {
-  x = wave_sum(x);
-  if (lane_id() == 0) s.f64[wave_id()] = x;
-  __syncthreads();
-  double r = 0.0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) r += s.f64[w];
-  __syncthreads();
-  return r;
+  return block_reduce(x, s.f64, 0.0, OpSum());
 }
 
 __device__ __forceinline__ double block_max(double x, BlockScratch& s) {
-  x = wave_max(x);
-  if (lane_id() == 0) s.f64[wave_id()] = x;
-  __syncthreads();
-  double r = s.f64[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = s.f64[w] > r ? s.f64[w] : r;
-  __syncthreads();
-  return r;
+  return block_reduce(x, s.f64, -(double)INFINITY, OpMax());
 }
 
 __device__ __forceinline__ long long block_sum_i64(long long x, BlockScratch& s) {
-  x = wave_sum(x);
-  if (lane_id() == 0) s.i64[wave_id()] = x;
-  __syncthreads();
-  long long r = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) r += s.i64[w];
-  __syncthreads();
-  return r;
+  return block_reduce(x, s.i64, 0ll, OpSum());
 }
 
 __device__ __forceinline__ long long block_min_i64(long long x, BlockScratch& s) {
-  x = wave_min(x);
-  if (lane_id() == 0) s.i64[wave_id()] = x;
-  __syncthreads();
-  long long r = s.i64[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = s.i64[w] < r ? s.i64[w] : r;
-  __syncthreads();
-  return r;
+  return block_reduce(x, s.i64, LLONG_MAX, OpMin());
 }
 
 __device__ __forceinline__ long long block_max_i64(long long x, BlockScratch& s) {
-  x = wave_max(x);
-  if (lane_id() == 0) s.i64[wave_id()] = x;
-  __syncthreads();
-  long long r = s.i64[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) r = s.i64[w] > r ? s.i64[w] : r;
-  __syncthreads();
-  return r;
+  return block_reduce(x, s.i64, LLONG_MIN, OpMax());
 }
 
 __device__ __forceinline__ int block_or(int x, BlockScratch& s) {
   return block_max_i64(x ? 1 : 0, s) != 0;
 }
 
-// Exclusive prefix sum over threads in thread order; `total` gets the sum.
-__device__ __forceinline__ long long block_exclusive_scan_i64(long long x, BlockScratch& s, long long& total) {
-  long long v = x;
+// Inclusive prefix over the lanes of a wave (fixed association order).
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    long long y = __shfl_up(v, o);
+    T y = __shfl_up(v, o);
     if (lane_id() >= o) v += y;
   }
+  return v;
+}
+
+// Prefix of the 16 per-wave totals: exclusive base of this wave, and the total.
+template <class T>
+__device__ __forceinline__ void wave_bases(const T* slot, T& base, T& total) {
+  const int l = lane_id();
+  T y = l < kWaves ? slot[l] : (T)0;
+  T incl = y;
+#pragma unroll
+  for (int o = 1; o < kWaves; o <<= 1) {
+    T z = __shfl_up(incl, o);
+    if (l >= o) incl += z;
+  }
+  base = __shfl(incl - y, wave_id());
+  total = __shfl(incl, kWaves - 1);
+}
+
+// Exclusive prefix sum over threads in thread order; `total` gets the sum.
+__device__ __forceinline__ long long block_exclusive_scan_i64(long long x, BlockScratch& s, long long& total) {
+  const long long v = wave_incl_scan(x);
   if (lane_id() == 63) s.i64[wave_id()] = v;
   __syncthreads();
-  long long base = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    long long t = s.i64[w];
-    base += w < wave_id() ? t : 0;
-    tot += t;
-  }
+  long long base;
+  wave_bases(s.i64, base, total);
   __syncthreads();
-  total = tot;
   return base + v - x;
 }
 
 // Exclusive prefix sum of doubles in thread order (fixed association order).
 __device__ __forceinline__ double block_exclusive_scan_f64(double x, BlockScratch& s, double& total) {
-  double v = x;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    double y = __shfl_up(v, o);
-    if (lane_id() >= o) v += y;
-  }
+  const double v = wave_incl_scan(x);
   if (lane_id() == 63) s.f64[wave_id()] = v;
   __syncthreads();
-  double base = 0.0, tot = 0.0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    double t = s.f64[w];
-    if (w < wave_id()) base += t;
-    tot += t;
-  }
+  double base;
+  wave_bases(s.f64, base, total);
   __syncthreads();
-  total = tot;
   // v is the inclusive prefix inside the wave; drop this thread's own term.
-  double incl = base + v;
-  return incl - x;
+  return (base + v) - x;
 }
 
 // Order-preserving 64-bit key of a double: larger value -> larger key,
@@ -165,11 +150,6 @@ __device__ __forceinline__ double block_exclusive_scan_f64(double x, BlockScratc
 __device__ __forceinline__ uint64_t order_key(double x) {
   uint64_t b = (x == 0.0) ? 0ull : (uint64_t)__double_as_longlong(x);
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-}
-
-__device__ __forceinline__ double key_value(uint64_t k) {
-  uint64_t b = (k >> 63) ? (k & 0x7FFFFFFFFFFFFFFFull) : ~k;
-  return __longlong_as_double((long long)b);
 }
 
 __device__ __forceinline__ double load_logit(const void* base, int dtype, int64_t off) {

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
   const int64_t row = blockIdx.x;
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
   RowSpec r = sample_row_spec(a, row, W);
-  unsigned flags = 0;
+  unsigned flags = DSR_FLAG_GENERAL;
   int64_t onehot;
   int st = general_distribution(r, sh, flags, onehot);
   finish_row(a, row, W, st, flags, sh);
@@ -111,12 +111,13 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
 __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t a) {
   __shared__ FastShared sh;
   const int64_t row = blockIdx.x;
-  if (fast_sample_row(a, row, sh)) return;
+  const int why = fast_sample_row(a, row, sh);
+  if (why == 0) return;
   __syncthreads();
   GenShared& gs = *reinterpret_cast<GenShared*>(&sh);
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
   RowSpec r = sample_row_spec(a, row, W);
-  unsigned flags = 0;
+  unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
   int64_t onehot;
   int st = general_distribution(r, gs, flags, onehot);
   finish_row(a, row, W, st, flags, gs);

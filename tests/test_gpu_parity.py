@@ -249,8 +249,9 @@ def test_verify_golden_on_gpu(case):
     drf = torch.from_numpy(GOLD[f"{case['name']}/draft"]).to(dev)[None]
     ids = torch.tensor([case["ids"]], dtype=torch.int32, device=dev)
     eos = case["eos"]
-    res = batch.verify_drafts(tgt, drf, ids, [case["policy"]], torch.tensor([case["u_accept"]], device=dev),
-                              torch.tensor([case["u_target"]], device=dev),
+    f64 = torch.float64
+    res = batch.verify_drafts(tgt, drf, ids, [case["policy"]], torch.tensor([case["u_accept"]], dtype=f64, device=dev),
+                              torch.tensor([case["u_target"]], dtype=f64, device=dev),
                               torch.tensor([case["limit"]], dtype=torch.int32, device=dev),
                               eos_offsets=torch.tensor([0, len(eos)], dtype=torch.int64, device=dev),
                               eos_ids=torch.tensor(eos, dtype=torch.int32, device=dev))
