@@ -1,38 +1,47 @@
 // Register-resident fast path for bf16 rows (gfx950, wave64, no MFMA).
 //
 // One 1024-thread workgroup owns one row of up to 131,072 bf16 logits.  The
-// row is read from HBM exactly once, by raw buffer loads of 16 bytes issued
-// all up front, straight into VGPRs (16 x uint4 per thread: 256 KB per row
-// across the workgroup), and turned into order-preserving 16-bit keys with
-// the allow mask and the NaN/+inf check fused into that pass, which overlaps
-// the loads still in flight (the staging barrier orders LDS only).  Wave w
-// owns the contiguous chunk range [w*CW, (w+1)*CW) of 8-token chunks; lane l
-// of it takes chunk w*CW + 64*j + l at step j, so every load instruction
-// reads a contiguous 1 KB and the row's index order is (wave, j, lane, elem).
+// row is read from HBM exactly once: the allow bitmask is fetched first, then
+// every 16-byte load of the row is issued up front, as raw buffer loads
+// straight into VGPRs (16 x uint4 per thread, 256 KB per row across the
+// workgroup).  Pass 1 turns each chunk into order-preserving 16-bit keys as
+// it arrives, with the allow mask and the NaN/+inf check fused in, so it runs
+// under the loads still in flight (the staging barrier orders LDS only).
+// Wave w owns the contiguous chunk range [w*CW, (w+1)*CW) of 8-token chunks;
+// lane l of it takes chunk w*CW + 64*j + l at step j, so every load
+// instruction reads a contiguous 1 KB and the row's index order is
+// (wave, j, lane, element).
 //
-// Selection works on chunks first, so per-element work stays off the
-// 129k-token row:
-//   * a 12-bit radix histogram of the 16,160 chunk maxima gives tau, the low
-//     edge of the bin that holds the k-th largest chunk maximum: at least k
-//     chunks (hence k tokens) reach tau, and only about k more do;
-//   * those chunks are compacted, whole and in index order, into LDS with
-//     one ballot per register slot;
-//   * a 12-bit and a 4-bit radix pass over the tokens of that short list give
-//     the exact k-th key; its tie group is resolved by index (lowest first),
-//     as the reference's stable argsort does (sampling.py:89-91), and one
-//     packed scan gives both tie ranks and the kept tokens' positions;
+// The path is VALU-issue bound once the row is in registers, so everything
+// after pass 1 works on few tokens, few waves and few barriers:
+//   * keys are tracked as distances below the row maximum; a histogram of
+//     the 4,096 group maxima (a group is 4 chunks of one thread) over the
+//     4,096 keys below the maximum gives tau, the k-th largest group maximum:
+//     at least k tokens reach tau, and only the chunks whose maximum reaches
+//     it are compacted, whole and in index order, into LDS (one ballot per
+//     register slot);
+//   * an exact-key histogram of the listed tokens gives the k-th key; its
+//     tie group is resolved by index (lowest first), as the reference's
+//     stable argsort does (sampling.py:89-91), and one packed scan gives both
+//     tie ranks and the kept tokens' positions;
 //   * the k <= 1024 kept tokens then sit one per thread: float64
-//     (v - max) / T, exp, sums, min-p, top-p (radix passes over probability
-//     mass in fixed point, then exact float64 tie arithmetic) and the
-//     index-order CDF search of categorical (sampling.py:92-128).
-// Workgroup reductions use DPP inside waves and cost one barrier each.
+//     r = exp((v - max) / T) (sampling.py:86-92); min-p and top-p are decided
+//     on these unnormalised masses (the maximum is exp(0) = 1, so min-p keeps
+//     r >= min_p, and top-p compares prefix mass with top_p times the total);
+//     the top-p boundary key comes from a fixed-point mass histogram, its tie
+//     group is settled in exact float64 arithmetic;
+//   * one wave finishes with the index-order CDF search of categorical
+//     (sampling.py:103-128).
+// Histogram selects that fit in 1,024 bins run in one wave with DPP scans.
 //
 // The path is exact only where bf16 key order equals the reference's float64
 // order; each row checks that at its decision boundaries (no +-0 boundary,
-// neighbouring bf16 values keep distinct (v - max) / T and probabilities) and
+// neighbouring bf16 values keep distinct (v - max) / T and masses) and
 // otherwise hands the row to the general path in the same workgroup, as it
-// does for rows with penalties, bias, no top-k, k > 1024 or too many
-// boundary chunks.
+// does for rows with penalties, bias, no top-k, k > 1024, too many boundary
+// chunks or a k-th group maximum more than 4,095 keys below the maximum.
+// Decisions that the reference's own rounding could tip (min-p, top-p and
+// CDF comparisons within a few ulps) are reported with DSR_FLAG_MARGIN.
 #pragma once
 
 #include "dsr_general.h"
@@ -44,36 +53,36 @@ constexpr int kFastChunks = 16;                                         // 16-by
 constexpr int64_t kFastMaxVocab = (int64_t)kThreads * kFastChunks * 8;  // 131072
 constexpr int kChunkCap = 2048;                                         // compacted chunk list
 constexpr int kFastMaxK = kThreads;                                     // one kept token per thread
-constexpr int kBins = 4096;                                             // 12-bit radix digit
+constexpr uint32_t kWindow = 4096;                                      // keys tracked below the maximum
+constexpr int kWaveBins = 1024;                                         // bins one wave selects over
 
 // Why a row is handed to the general path (reported in out_flags bits 4-7).
 constexpr int kHandPolicy = 1;     // controls out of bounds (the general path reports it)
 constexpr int kHandTopK = 2;       // no top-k, or k > 1024, or k >= vocabulary
 constexpr int kHandZero = 3;       // a decision boundary sits at +-0
-constexpr int kHandCapacity = 4;   // more than kChunkCap chunks reach tau
+constexpr int kHandCapacity = 4;   // too many chunks reach tau, or tau lies outside the key window
 constexpr int kHandOrder = 5;      // bf16 key order may differ from float64 order at a boundary
+constexpr int kHandInvalid = 6;    // invalid or fully masked logits (reported in the reference's order)
 
 struct FastLists {
   union {
+    uint32_t lut[256][4];                  // allow byte -> four 2 x 16-bit "disallowed" masks (pass 1)
     struct {
-      uint32_t lut[256][4];                // allow byte -> four 2 x 16-bit lane masks
-      uint32_t allow[kFastMaxVocab / 32];  // the row's allow bitmask
-    } stage;                               // pass 1 only
-    struct {
-      uint4 keys[kChunkCap];               // chunks reaching tau, index order
+      uint4 raw[kChunkCap];                // chunks reaching tau (masked bf16 bits), index order
       uint32_t id[kChunkCap];
     } list;
   };
-  uint32_t hist[2][kBins];                 // 12-bit counts: chunk maxima, then list tokens
-  unsigned long long mass[kBins];          // 12-bit fixed-point probability mass
-  uint32_t sub[16];                        // 4-bit second digit
-  unsigned long long submass[16];
+  uint32_t cnt[2][kWindow];                // counts by distance below the maximum key
+  long long mass[kWindow];                 // fixed-point mass by distance below the maximum key
+  double kr[kFastMaxK];                    // final masses of the kept tokens, index order
   uint16_t kkey[kFastMaxK];                // kept tokens, index order
   uint32_t kidx[kFastMaxK];
-  int sel[4];
-  long long sel_mass;
-  double bcast_d;
-  int bcast_i[2];
+  uint32_t wn[kWaves];
+  uint32_t wflag[kWaves];
+  long long sel_above;
+  int sel;
+  int bc_i[2];
+  double bc_d[2];
   SyncSlots sync;
 };
 
@@ -121,9 +130,27 @@ __device__ __forceinline__ uint32_t key_at(const uint4& v, int e) {
   return (w >> (16 * (e & 1))) & 0xFFFFu;
 }
 
-__device__ __forceinline__ uint32_t lanes_below(unsigned long long b) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+typedef short dsr_i16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_max_i16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(dsr_i16x2, a),
+                                                                __builtin_bit_cast(dsr_i16x2, b)));
 }
+
+// Chunk maxima are held as signed 16-bit "levels": level = key - 0x8000, so a
+// positive bf16 value's level is its own bit pattern.
+__device__ __forceinline__ int chunk_level(const uint32_t* cmx, int j) {
+  return (int)(short)(uint16_t)(cmx[j >> 1] >> (16 * (j & 1)));
+}
+
+// All-allowed bitmask read in place of a row's allow bits when there are none.
+struct AllowAll {
+  uint8_t b[kFastMaxVocab / 8];
+  constexpr AllowAll() : b() {
+    for (int i = 0; i < kFastMaxVocab / 8; ++i) b[i] = 0xFF;
+  }
+};
+__device__ const AllowAll kAllowAll;
 
 static inline bool fast_path_eligible(const dsr_sample_args_t& a) {
   return a.dtype == DSR_BF16 && a.vocab >= 8 && a.vocab <= kFastMaxVocab && (a.vocab & 7) == 0 && (a.ld & 7) == 0 &&
@@ -164,179 +191,310 @@ __device__ __forceinline__ void fast_scatter(const dsr_sample_args_t& a, int64_t
   if (a.out_kept_bits) atomicOr(&a.out_kept_bits[row * a.kept_ld + (idx >> 5)], 1u << (idx & 31));
 }
 
-// Over 4096 counting bins held 4 per thread (scanned from the top), finds the
-// bin where the count first reaches `rem`: sel[0] = bin, sel[1] = count above.
-__device__ __forceinline__ void select_count_bin(const uint32_t* hist, uint32_t rem, FastLists& sh, BlockSync& bs) {
-  const int rt = kThreads - 1 - (int)threadIdx.x;
-  const uint4 c = *(const uint4*)(hist + 4 * rt);
-  uint32_t total;
-  uint32_t above = bs.scan(c.x + c.y + c.z + c.w, total);
-  const uint32_t cc[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-  for (int j = 3; j >= 0; --j) {
-    if (above < rem && rem <= above + cc[j]) {
-      sh.sel[0] = 4 * rt + j;
-      sh.sel[1] = (int)above;
-    }
-    above += cc[j];
-  }
+// Exclusive prefix of one wave-uniform count per wave, and the total.
+__device__ __forceinline__ uint32_t wave_offset(uint32_t wn, uint32_t* slot, uint32_t& total) {
+  if (lane_id() == 0) slot[wave_id()] = wn;
   lds_barrier();
+  const uint32_t y = lane_id() < kWaves ? slot[lane_id()] : 0u;
+  const uint32_t incl = row_scan_dpp(y);
+  total = lane_value(incl, kWaves - 1);
+  return lane_value(incl - y, wave_id());
 }
 
-// The same for fixed-point mass; sel[0] = -1 if the mass never reaches tgt.
-__device__ __forceinline__ void select_mass_bin(const unsigned long long* m, unsigned long long tgt, FastLists& sh,
-                                                BlockSync& bs) {
-  const int rt = kThreads - 1 - (int)threadIdx.x;
-  unsigned long long c[4];
+template <class T> struct Bins16;
+template <> struct Bins16<uint32_t> {
+  static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* c) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) c[j] = m[4 * rt + j];
-  if (threadIdx.x == 0) sh.sel[0] = -1;  // ordered before the writes below by the scan's barrier
-  long long total;
-  unsigned long long above = (unsigned long long)bs.scan((long long)(c[0] + c[1] + c[2] + c[3]), total);
-#pragma unroll
-  for (int j = 3; j >= 0; --j) {
-    if (above < tgt && tgt <= above + c[j]) {
-      sh.sel[0] = 4 * rt + j;
-      sh.sel_mass = (long long)above;
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = ((const uint4*)p)[q];
+      c[4 * q] = v.x; c[4 * q + 1] = v.y; c[4 * q + 2] = v.z; c[4 * q + 3] = v.w;
     }
-    above += c[j];
+  }
+};
+template <> struct Bins16<long long> {
+  static __device__ __forceinline__ void load(const long long* p, long long* c) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const longlong2 v = ((const longlong2*)p)[q];
+      c[2 * q] = v.x; c[2 * q + 1] = v.y;
+    }
+  }
+};
+
+// bins[0..kWindow) hold counts (or fixed-point mass) by distance below the
+// maximum key, largest key first.  Returns the first bin where the running
+// total reaches `rem` (-1 if the whole window stays below it) and the total
+// before that bin.  Wave 0 scans the first 1,024 bins with a DPP scan; the
+// workgroup scans the rest only when those fall short.  Every thread calls.
+template <class T>
+__device__ int select_bin(const T* bins, T rem, FastLists& sh, BlockSync& bs, T& above) {
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    T c[16];
+    Bins16<T>::load(bins + 16 * l, c);
+    T s = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += c[j];
+    const T incl = wave_scan_dpp(s);
+    const T ex = incl - s;
+    const unsigned long long hit = __ballot(ex < rem && rem <= incl);
+    if (hit == 0) {
+      if (l == 0) {
+        sh.sel = -1;
+        sh.sel_above = (long long)lane_value(incl, 63);
+      }
+    } else if (l == __ffsll((long long)hit) - 1) {
+      T run = ex, ab = 0;
+      int b = -1;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (b < 0 && run + c[j] >= rem) {
+          b = j;
+          ab = run;
+        }
+        run += c[j];
+      }
+      sh.sel = 16 * l + b;
+      sh.sel_above = (long long)ab;
+    }
   }
   lds_barrier();
+  int b = sh.sel;
+  above = (T)sh.sel_above;
+  if (b >= 0) return b;
+  // The first 1,024 bins hold less than rem: the workgroup scans the rest.
+  const T below = above;
+  const int t = threadIdx.x;
+  T c[4] = {0, 0, 0, 0};
+  if (t >= kWaveBins / 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = bins[4 * t + j];
+  }
+  T total;
+  T run = bs.scan(c[0] + c[1] + c[2] + c[3], total) + below;  // its barrier orders the reads of sel above
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (run < rem && rem <= run + c[j]) {
+      sh.sel = 4 * t + j;
+      sh.sel_above = (long long)run;
+    }
+    run += c[j];
+  }
+  lds_barrier();
+  b = sh.sel;
+  above = (T)sh.sel_above;
+  return b;
 }
 
 // Returns 0 if the row was decided here, else the reason it is handed to the
 // general path (kHand*).
 __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShared& shu) {
   FastLists& sh = shu.f;
-  const dsr_policy_t pol = a.policy[row];
-  const bool greedy = pol.temperature == 0.0;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int64_t V = a.vocab;
-  if (!policy_ok(pol)) return kHandPolicy;
-  if (!greedy && !(pol.top_k >= 1 && pol.top_k <= kFastMaxK && pol.top_k < V)) return kHandTopK;
-
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const uint32_t C = (uint32_t)(V >> 3);
   const uint32_t CW = (C + kWaves - 1) / kWaves;
-  const uint16_t* lrow = (const uint16_t*)a.logits + row * a.ld;
-  const uint32_t* mrow = a.allow_bits ? a.allow_bits + row * a.allow_ld : nullptr;
   BlockSync bs(sh.sync);
 
-  // ---- one HBM pass: every load of the row is issued up front, as raw
-  // buffer loads over the row (32-bit offsets; out-of-range reads return 0).
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)lrow, (short)0, (int)(V * 2), 0x00020000);
+  // ---- one HBM pass, every load issued up front in the order it is used,
+  // as raw buffer loads (vector memory, so the waits stay in issue order;
+  // out-of-range reads return 0): the two policy fields needed right after
+  // pass 1 (temperature, top_k), then for each register slot j the chunk's
+  // allow byte and its 16 bytes of logits.  The rest of the policy and the
+  // uniform are fetched after pass 1, so their registers stay free during it.
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.policy + row), (short)0, (int)sizeof(dsr_policy_t), 0x00020000);
+  const auto pT = __builtin_amdgcn_raw_buffer_load_b64(prs, 0, 0, 0);
+  const uint32_t pK = __builtin_amdgcn_raw_buffer_load_b32(prs, 48, 0, 0);
+  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+      a.allow_bits ? (void*)(a.allow_bits + row * a.allow_ld) : (void*)&kAllowAll, (short)0, (int)C, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)a.logits + row * a.ld), (short)0, (int)(V * 2), 0x00020000);
+  uint32_t mb[kFastChunks];
   uint4 d[kFastChunks];
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
-    const uint32_t off = cw < CW ? (wave * CW + cw) * 16u : 0x7FFFFFF0u;  // chunks of the next wave read as 0
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, 0, 0);
+    const uint32_t c = (uint32_t)wave * CW + cw;
+    const bool mine = cw < CW;  // chunks past this wave's range belong to the next wave: read as 0
+    mb[j] = __builtin_amdgcn_raw_buffer_load_b8(mrs, (int)(mine ? c : 0x7FFFFFF0u), 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)(mine ? c * 16u : 0x7FFFFFF0u), 0, 0);
     d[j] = make_uint4(v[0], v[1], v[2], v[3]);
   }
-  // While the row streams in: stage the allow bitmask (one byte per 8-token
-  // chunk) and the mask lookup table, and clear the histograms.
-  const int64_t mwords = (V + 31) >> 5;
-  if (mrow) {
-    for (int64_t i = tid; i < mwords; i += kThreads) sh.stage.allow[i] = mrow[i];
-  }
+  __builtin_amdgcn_sched_barrier(0);
+  // While the row streams in: the mask lookup table (allow byte -> per-lane
+  // "disallowed" masks) and cleared histograms.
   {
     const uint32_t m = (uint32_t)tid >> 2, q = (uint32_t)tid & 3u;
-    sh.stage.lut[m][q] = (((m >> (2 * q)) & 1u) ? 0x0000FFFFu : 0u) | (((m >> (2 * q + 1)) & 1u) ? 0xFFFF0000u : 0u);
-  }
-  for (int j = tid; j < 2 * kBins; j += kThreads) (&sh.hist[0][0])[j] = 0u;
-  for (int j = tid; j < kBins; j += kThreads) sh.mass[j] = 0ull;
-  if (tid < 16) {
-    sh.sub[tid] = 0u;
-    sh.submass[tid] = 0ull;
+    sh.lut[m][q] = (((m >> (2 * q)) & 1u) ? 0u : 0x0000FFFFu) | (((m >> (2 * q + 1)) & 1u) ? 0u : 0xFFFF0000u);
+    uint4* z = (uint4*)&sh.cnt[0][0];  // 2 x 4096 words of counts
+#pragma unroll
+    for (int i = 0; i < 2; ++i) z[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
+    uint4* zm = (uint4*)&sh.mass[0];   // 4096 x 8 bytes of mass
+#pragma unroll
+    for (int i = 0; i < 2; ++i) zm[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
   }
   lds_barrier();  // LDS only: the row's loads keep streaming
-  const uint8_t* mbytes = (const uint8_t*)sh.stage.allow;
 
-  // ---- keys, mask, NaN/+inf check, chunk maxima (pass 1, as chunks arrive).
-  uint32_t rmax = 0u, rmin = 0xFFFFFFFFu, cmx[kFastChunks / 2];
-  uint32_t tmax = 0u;
+  // ---- pass 1, chunk by chunk as the loads land.  Disallowed tokens become
+  // 0xFFFF (a negative NaN pattern no valid input holds; its key is 0).
+  // Chunk maxima are taken as signed 16-bit integers of the bf16 bits, which
+  // orders positive values exactly; rows whose top-k reaches zero or below
+  // redo the maxima with full keys (below).
+  uint32_t vmax_s = 0x80008000u, vmax_u = 0u, cmx[kFastChunks / 2];
+  int g[4] = {-32768, -32768, -32768, -32768};
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
     // Keep each chunk's mask lookup next to its use: hoisting all sixteen
     // 16-byte lookups would need 64 more VGPRs than the row leaves free.
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
-    const uint32_t c = wave * CW + cw;  // < 16384: always inside the staged bitmask
-    const uint32_t staged = mbytes[c];  // read unconditionally; selected below without a branch
-    const uint32_t mbyte = (cw < CW && c < C) ? (mrow ? staged : 0xFFu) : 0u;
-    const uint4 lm = *(const uint4*)sh.stage.lut[mbyte];
+    const uint4 lm = *(const uint4*)sh.lut[mb[j] & 0xFFu];
     uint32_t w[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
     const uint32_t m4[4] = {lm.x, lm.y, lm.z, lm.w};
-    uint32_t cm = 0u;
+    uint32_t cm = 0x80008000u;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t k = bf16x2_keys(w[q]);
-      rmax = pk_max_u16(rmax, k);
-      rmin = pk_min_u16(rmin, k);
-      w[q] = k & m4[q];
-      cm = pk_max_u16(cm, w[q]);
+      vmax_s = pk_max_i16(vmax_s, w[q]);  // +inf / +NaN: 0x7F80 and up
+      vmax_u = pk_max_u16(vmax_u, w[q]);  // -NaN: 0xFF81 and up
+      w[q] |= m4[q];
+      cm = pk_max_i16(cm, w[q]);
     }
     d[j] = make_uint4(w[0], w[1], w[2], w[3]);
-    const uint32_t cmj = max(cm & 0xFFFFu, cm >> 16);
-    if (j & 1) cmx[j >> 1] |= cmj << 16; else cmx[j >> 1] = cmj;
-    tmax = max(tmax, cmj);
+    const int cmj = max((int)(short)(cm & 0xFFFFu), (int)(short)(cm >> 16));
+    if (j & 1) cmx[j >> 1] |= (uint32_t)cmj << 16; else cmx[j >> 1] = (uint32_t)cmj & 0xFFFFu;
+    g[j >> 2] = max(g[j >> 2], cmj);
   }
-  const long long bad = max(rmax & 0xFFFFu, rmax >> 16) >= kKeyPosInf || min(rmin & 0xFFFFu, rmin >> 16) < kKeyNegInf;
-  // One reduction carries both the row maximum and the NaN/+inf flag, so no
-  // branch separates pass 1 from the uses of its masked keys.
-  const long long red = bs.max((long long)tmax | (bad << 32));
-  if (red >> 32) {
-    if (tid == 0) fast_write_result(a, row, DSR_E_LOGITS, -1, 0, 0);
-    return 0;
-  }
-  const uint32_t Mkey = (uint32_t)red;
-  if (Mkey <= kKeyNegInf) {
-    if (tid == 0) fast_write_result(a, row, DSR_E_MASKED, -1, 0, 0);
-    return 0;
-  }
-  if (zero_key(Mkey)) return kHandZero;  // +0 and -0 tie in value but not in key
-
-  // ---- tau: low edge of the 12-bit bin holding the k-th largest chunk maximum.
-  const uint32_t k = greedy ? 1u : (uint32_t)pol.top_k;
-  uint32_t tau = Mkey;
-  if (!greedy) {
+  // Pin pass 1 here: without these the compiler sinks it below the policy
+  // branches, after every load has landed, and the whole row stays live twice.
 #pragma unroll
-    for (int j = 0; j < kFastChunks; ++j) atomicAdd(&sh.hist[0][((cmx[j >> 1] >> (16 * (j & 1))) & 0xFFFFu) >> 4], 1u);
+  for (int j = 0; j < kFastChunks; ++j) asm volatile("" : "+v"(d[j].x), "+v"(d[j].y), "+v"(d[j].z), "+v"(d[j].w));
+#pragma unroll
+  for (int i = 0; i < kFastChunks / 2; ++i) asm volatile("" : "+v"(cmx[i]));
+  asm volatile("" : "+v"(g[0]), "+v"(g[1]), "+v"(g[2]), "+v"(g[3]), "+v"(vmax_s), "+v"(vmax_u));
+  const int gmax = max(max(g[0], g[1]), max(g[2], g[3]));
+  // The policy is read only now: waiting for it earlier would stall pass 1
+  // behind the whole batch's loads.
+  __builtin_amdgcn_sched_barrier(0);
+  const double T = __builtin_bit_cast(
+      double, ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)pT[1]) << 32) |
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)pT[0]));
+  const int top_k = __builtin_amdgcn_readfirstlane((int)pK);
+  const bool greedy = T == 0.0;
+  if (!(T >= 0.0 && T <= 100.0)) return kHandPolicy;
+  if (!greedy && !(top_k >= 1 && top_k <= kFastMaxK && top_k < V)) return kHandTopK;
+  // Late loads: the remaining policy fields and the row's uniform.
+  const auto pq1 = __builtin_amdgcn_raw_buffer_load_b128(prs, 8, 0, 0);   // top_p, min_p
+  const auto pq2 = __builtin_amdgcn_raw_buffer_load_b128(prs, 24, 0, 0);  // repetition, presence
+  const auto pq3 = __builtin_amdgcn_raw_buffer_load_b64(prs, 40, 0, 0);   // frequency
+  const uint32_t pR = __builtin_amdgcn_raw_buffer_load_b32(prs, 52, 0, 0);  // reserved
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+      a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy, (short)0, a.uniforms ? 8 : 0, 0x00020000);
+  const auto uq = __builtin_amdgcn_raw_buffer_load_b64(urs, 0, 0, 0);
+
+  const uint32_t bad = max((int)(short)(vmax_s & 0xFFFFu), (int)(short)(vmax_s >> 16)) >= 0x7F80 ||
+                       max(vmax_u & 0xFFFFu, vmax_u >> 16) >= 0xFF81u;
+  // One reduction carries the row maximum (as a key) and the NaN/+inf flag.
+  const uint32_t red = bs.max((uint32_t)(gmax + 0x8000) | (bad << 16));
+  // Invalid logits: the general path reports them after the policy checks,
+  // in the reference's order.
+  if (red >> 16) return kHandInvalid;
+  const uint32_t k = greedy ? 1u : (uint32_t)top_k;
+  int Ms = (int)(red & 0xFFFFu) - 0x8000;  // the row maximum's level
+  bool full = Ms <= 0;                     // no positive value: signed maxima do not order this row
+  int tau = Ms;                            // level every top-k token reaches
+  if (!full && !greedy) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t dd = (uint32_t)(Ms - g[q]);
+      if (g[q] > 0 && dd < kWindow) atomicAdd(&sh.cnt[0][dd], 1u);
+    }
     lds_barrier();
-    select_count_bin(sh.hist[0], k, sh, bs);
-    tau = (uint32_t)sh.sel[0] << 4;
+    uint32_t above;
+    const int b = select_bin(sh.cnt[0], k, sh, bs, above);
+    if (b >= 0) tau = Ms - b; else full = true;  // fewer than k positive group maxima in the window
+  }
+  if (full) {
+    // Rare: redo the maxima with full order keys (level = key - 0x8000).
+#pragma unroll
+    for (int q = 0; q < 4; ++q) g[q] = -32768;
+#pragma unroll
+    for (int j = 0; j < kFastChunks; ++j) {
+      uint32_t cm = 0u;
+      cm = pk_max_u16(cm, bf16x2_keys(d[j].x));
+      cm = pk_max_u16(cm, bf16x2_keys(d[j].y));
+      cm = pk_max_u16(cm, bf16x2_keys(d[j].z));
+      cm = pk_max_u16(cm, bf16x2_keys(d[j].w));
+      const int cmj = (int)max(cm & 0xFFFFu, cm >> 16) - 0x8000;
+      if (j & 1) cmx[j >> 1] |= (uint32_t)cmj << 16; else cmx[j >> 1] = (uint32_t)cmj & 0xFFFFu;
+      g[j >> 2] = max(g[j >> 2], cmj);
+    }
+    const uint32_t Mk = bs.max((uint32_t)(max(max(g[0], g[1]), max(g[2], g[3])) + 0x8000));
+    if (Mk <= kKeyNegInf) return kHandInvalid;  // every token masked: reported by the general path
+    if (zero_key(Mk)) return kHandZero;  // +0 and -0 tie in value but not in key
+    Ms = (int)Mk - 0x8000;
+    tau = Ms;
+    if (!greedy) {
+      uint4* z = (uint4*)&sh.cnt[0][0];
+      z[tid] = make_uint4(0u, 0u, 0u, 0u);
+      lds_barrier();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t dd = (uint32_t)(Ms - g[q]);
+        if (g[q] > -32768 && dd < kWindow) atomicAdd(&sh.cnt[0][dd], 1u);
+      }
+      lds_barrier();
+      uint32_t above;
+      const int b = select_bin(sh.cnt[0], k, sh, bs, above);
+      if (b < 0) return kHandCapacity;
+      tau = Ms - b;
+    }
+  }
+  const uint32_t Mkey = (uint32_t)(Ms + 0x8000);
+  dsr_policy_t pol;
+  {
+    uint32_t pw[14] = {(uint32_t)pT[0], (uint32_t)pT[1], pq1[0], pq1[1], pq1[2], pq1[3], pq2[0],
+                       pq2[1], pq2[2], pq2[3], pq3[0], pq3[1], pK, pR};
+#pragma unroll
+    for (int i = 0; i < 14; ++i) pw[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)pw[i]);
+    __builtin_memcpy(&pol, pw, sizeof(pol));
   }
 
   // ---- compact the chunks whose maximum reaches tau, whole, in index order.
   uint32_t wn = 0;
 #pragma unroll
-  for (int j = 0; j < kFastChunks; ++j)
-    wn += (uint32_t)__popcll(__ballot(((cmx[j >> 1] >> (16 * (j & 1))) & 0xFFFFu) >= tau));
+  for (int j = 0; j < kFastChunks; ++j) wn += (uint32_t)__popcll(__ballot(chunk_level(cmx, j) >= tau));
   uint32_t nlist;
-  uint32_t lpos = lane_value(bs.scan(lane == 0 ? wn : 0u, nlist), 0);
+  uint32_t lpos = wave_offset(wn, sh.wn, nlist);
   if (nlist > (uint32_t)kChunkCap) return kHandCapacity;  // uniform
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
-    const bool q = ((cmx[j >> 1] >> (16 * (j & 1))) & 0xFFFFu) >= tau;
+    const bool q = chunk_level(cmx, j) >= tau;
     const unsigned long long b = __ballot(q);
     if (q) {
-      const uint32_t p = lpos + lanes_below(b);
-      sh.list.keys[p] = d[j];
-      sh.list.id[p] = wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
+      uint32_t p = lpos + lanes_below(b), pi = p;
+      // Opaque copy: derived from p * 16, the word index would cost a 64-bit multiply-add.
+      asm volatile("" : "+v"(pi));
+      sh.list.raw[p] = d[j];
+      sh.list.id[pi] = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
     }
     lpos += (uint32_t)__popcll(b);
   }
   lds_barrier();
 
+  if (!policy_ok(pol)) return kHandPolicy;
+  const double u = __builtin_bit_cast(double, ((unsigned long long)uq[1] << 32) | uq[0]);
+
   if (greedy) {  // sampling.py:82-85: the first listed chunk holds the first maximum
     if (tid == 0) {
-      const uint4 v = sh.list.keys[0];
+      const uint4 r4 = sh.list.raw[0];
+      const uint4 v = make_uint4(bf16x2_keys(r4.x), bf16x2_keys(r4.y), bf16x2_keys(r4.z), bf16x2_keys(r4.w));
       int e = 0;
       while (e < 7 && key_at(v, e) != Mkey) ++e;
-      sh.bcast_i[0] = (int)(8u * sh.list.id[0]) + e;
+      sh.bc_i[0] = (int)(8u * sh.list.id[0]) + e;
     }
     lds_barrier();
-    const int64_t tok = sh.bcast_i[0];
+    const int64_t tok = sh.bc_i[0];
     if (a.out_probs_f32 || a.out_probs_f64 || a.out_kept_bits) {
       fast_clear_outputs(a, row);
       if (tid == 0) fast_scatter(a, row, tok, 1.0);
@@ -345,47 +503,37 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
     return 0;
   }
 
-  // ---- exact top-k over the listed tokens: 12-bit then 4-bit radix digit.
-  // Thread t holds list chunks 2t and 2t+1 (index order is thread order).
+  // ---- exact top-k over the listed tokens (exact-key histogram).  Thread t
+  // holds list chunks 2t and 2t+1, so thread order is index order.
+  const uint32_t Dtau = (uint32_t)(Ms - tau);
+  const bool busy = (uint32_t)wave * 128u < nlist;  // uniform: this wave holds listed chunks
   uint4 lv[2];
   uint32_t lid[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const uint32_t li = 2u * (uint32_t)tid + c;
     const bool ok = li < nlist;
-    lv[c] = ok ? sh.list.keys[li] : make_uint4(0u, 0u, 0u, 0u);  // masked keys: below any tau
+    const uint4 r4 = ok ? sh.list.raw[li] : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+    lv[c] = make_uint4(bf16x2_keys(r4.x), bf16x2_keys(r4.y), bf16x2_keys(r4.z), bf16x2_keys(r4.w));
     lid[c] = ok ? sh.list.id[li] : 0u;
   }
+  if (busy) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t key = key_at(lv[c], e);
-      if (key >= tau) atomicAdd(&sh.hist[1][key >> 4], 1u);
-    }
-  lds_barrier();
-  select_count_bin(sh.hist[1], k, sh, bs);
-  const uint32_t b1 = (uint32_t)sh.sel[0], rem1 = k - (uint32_t)sh.sel[1];
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t key = key_at(lv[c], e);
-      if (key >= tau && (key >> 4) == b1) atomicAdd(&sh.sub[key & 15u], 1u);
-    }
-  lds_barrier();
-  uint32_t bkey = 0, need = 0;
-  {
-    uint32_t above = 0;
-    for (int j = 15; j >= 0; --j) {  // every thread reads the 16 counts and selects
-      const uint32_t c = sh.sub[j];
-      if (above < rem1 && rem1 <= above + c) {
-        bkey = (b1 << 4) | (uint32_t)j;
-        need = rem1 - above;  // boundary-key tokens kept, lowest index first
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t dd = Mkey - key_at(lv[c], e);
+        if (dd <= Dtau) atomicAdd(&sh.cnt[1][dd], 1u);
       }
-      above += c;
-    }
   }
+  lds_barrier();
+  uint32_t above_k;
+  const int dk_i = select_bin(sh.cnt[1], k, sh, bs, above_k);
+  if (dk_i < 0) return kHandCapacity;  // unreachable: the list holds at least k tokens at or above tau
+  const uint32_t dk = (uint32_t)dk_i;
+  const uint32_t need = k - above_k;  // boundary-key tokens kept, lowest index first
+  const uint32_t bkey = Mkey - dk;
+
   // One scan of (tokens above the boundary, boundary ties) per thread gives
   // every thread its tie rank and the position of its kept tokens.
   uint32_t n_up = 0, n_eq = 0;
@@ -393,162 +541,136 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
   for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t key = key_at(lv[c], e);
-      n_up += key > bkey;
-      n_eq += key == bkey;
+      const uint32_t dd = Mkey - key_at(lv[c], e);
+      n_up += dd < dk;
+      n_eq += dd == dk;
     }
   uint32_t ptot;
   const uint32_t pex = bs.scan(n_up | (n_eq << 16), ptot);
-  uint32_t tr = pex >> 16;                        // ties before this thread
-  uint32_t kb = (pex & 0xFFFFu) + min(tr, need);  // kept tokens before this thread
+  if (busy) {
+    uint32_t tr = pex >> 16;                        // ties before this thread
+    uint32_t kb = (pex & 0xFFFFu) + min(tr, need);  // kept tokens before this thread
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t key = key_at(lv[c], e);
-      bool keep = key > bkey;
-      if (key == bkey) keep = tr++ < need;
-      if (keep && kb < (uint32_t)kFastMaxK) {
-        sh.kkey[kb] = (uint16_t)key;
-        sh.kidx[kb] = 8u * lid[c] + e;
-        ++kb;
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t key = key_at(lv[c], e);
+        const uint32_t dd = Mkey - key;
+        bool keep = dd < dk;
+        if (dd == dk) keep = tr++ < need;
+        if (keep && kb < (uint32_t)kFastMaxK) {
+          sh.kkey[kb] = (uint16_t)key;
+          sh.kidx[kb] = 8u * lid[c] + e;
+          ++kb;
+        }
       }
-    }
+  }
   const uint32_t ktot = (ptot & 0xFFFFu) + min(ptot >> 16, need);
+  const double M = bf16_key_value(Mkey);
   // Boundary certificate: the bf16 neighbours of the k-th value must stay
   // distinct after (v - max) / T, so key order and the reference's float64
   // order agree on which boundary tokens tie (resolved by index).
-  const double T = pol.temperature;
-  const double M = bf16_key_value(Mkey);
-  if (tid == 0) {
-    int ok = ktot == k;
-    if (bkey > kKeyNegInf) {
-      if (zero_key(bkey)) {
-        ok = 0;
-      } else {
-        const double sb = (bf16_key_value(bkey) - M) / T;
-        const double sp = bkey - 1 > kKeyNegInf ? (bf16_key_value(bkey - 1) - M) / T : -INFINITY;
-        const double sn = bkey + 1 < kKeyPosInf ? (bf16_key_value(bkey + 1) - M) / T : INFINITY;
-        ok = ok && sp < sb && sb < sn;
-      }
-    }
-    sh.bcast_i[0] = ok;
+  if (wave == 0) {
+    const uint32_t nk = bkey - 1u + (uint32_t)lane;
+    double s = lane == 0 ? -(double)INFINITY : (double)INFINITY;
+    if (lane < 3 && nk > kKeyNegInf && nk < kKeyPosInf) s = (bf16_key_value(nk) - M) / T;
+    const double s0 = lane_value(s, 0), s1 = lane_value(s, 1), s2 = lane_value(s, 2);
+    if (lane == 0)
+      sh.bc_i[0] = ktot == k && (bkey <= kKeyNegInf || (!zero_key(bkey) && s0 < s1 && s1 < s2));
   }
   lds_barrier();
-  if (!sh.bcast_i[0]) return kHandOrder;
+  if (!sh.bc_i[0]) return kHandOrder;
 
-  // ---- one kept token per thread: softmax, min-p, top-p, categorical.
+  // ---- one kept token per thread: its unnormalised mass r = exp((v - max) / T)
+  // (sampling.py:86-92; the maximum's mass is exactly 1) and min-p, which
+  // keeps r >= min_p (:94-96: result < min_p * max(result) with
+  // max(result) = 1 / sum).
   const bool have = tid < (int)k;
-  const uint32_t key = have ? sh.kkey[tid] : 0u;
-  const int64_t idx = have ? (int64_t)sh.kidx[tid] : 0;
+  const uint32_t key = have ? (uint32_t)sh.kkey[tid] : 0u;
+  const uint32_t idx = have ? sh.kidx[tid] : 0u;
   const bool fin = have && key > kKeyNegInf;
-  unsigned flags = 0;
-  double r = fin ? exp((bf16_key_value(key) - M) / T) : 0.0;  // sampling.py:86-92
-  const double s1 = bs.sum(r);
-  r = r / s1;                                                  // :93
-  double s2 = 0.0;                                             // min-p renormaliser (0: off)
-  bool minp_close = false;
-  if (pol.min_p != 0.0) {                                      // :94-96
-    const double cut = pol.min_p * (1.0 / s1);                 // the maximum is exp(0) / s1
-    minp_close = r > 0.0 && fabs(r - cut) <= cut * 0x1p-49;
-    if (r < cut) r = 0.0;
-    s2 = bs.sum(r);
-    r = r / s2;
+  double r = 0.0;
+  if (fin) r = exp((bf16_key_value(key) - M) / T);
+  bool close = false;
+  if (pol.min_p != 0.0) {
+    close = r > 0.0 && fabs(r - pol.min_p) <= pol.min_p * 0x1p-48;
+    if (r < pol.min_p) r = 0.0;
   }
-  if (pol.top_p < 1.0) {                                       // :97-102
-    unsigned long long tgt = (unsigned long long)(pol.top_p * 0x1p60);
-    if (tgt == 0) tgt = 1;
-    const unsigned long long fx = (unsigned long long)(r * 0x1p60);
-    if (r > 0.0) atomicAdd(&sh.mass[key >> 4], fx);
-    lds_barrier();
-    select_mass_bin(sh.mass, tgt, sh, bs);
-    const int m1 = sh.sel[0];
-    uint32_t lkey = 0;
-    bool found = false;
-    if (m1 >= 0) {
-      const unsigned long long above1 = (unsigned long long)sh.sel_mass;
-      if (r > 0.0 && (int)(key >> 4) == m1) atomicAdd(&sh.submass[key & 15u], fx);
-      lds_barrier();
-      unsigned long long excl = above1;
-      for (int j = 15; j >= 0; --j) {
-        const unsigned long long c = sh.submass[j];
-        if (!found && excl < tgt && tgt <= excl + c) {
-          lkey = ((uint32_t)m1 << 4) | (uint32_t)j;
-          found = true;
-        }
-        excl += c;
-      }
-    }
-    if (!found) {
+  unsigned flags = 0;
+  if (pol.top_p < 1.0) {  // :97-102
+    if (r > 0.0) atomicAdd((unsigned long long*)&sh.mass[Mkey - key], (unsigned long long)(r * 0x1p50));
+    const double S = bs.sum(r);  // its barrier also publishes the mass histogram
+    const double P = pol.top_p * S;
+    long long tgt = (long long)(P * 0x1p50);
+    if (tgt < 1) tgt = 1;
+    long long above1;
+    const int dl = select_bin(sh.mass, tgt, sh, bs, above1);
+    if (dl < 0) {
       // The whole mass stays below top_p: nothing is removed.
-      const double tot = bs.sum(r);
-      if (fabs(tot - pol.top_p) <= ((double)k + 16.0) * 0x1p-51) flags |= DSR_FLAG_MARGIN;
+      if (fabs(S - P) <= ((double)k + 16.0) * 0x1p-51 * S) flags |= DSR_FLAG_MARGIN;
     } else {
+      const uint32_t lkey = Mkey - (uint32_t)dl;
       if (zero_key(lkey)) return kHandZero;
+      // Tie members share one mass rt; any of them publishes it.  Key order
+      // must equal mass order next to the boundary: the bf16 neighbours of
+      // the boundary value must keep (v - max) / T at least 2^-40 apart, so
+      // their masses differ by far more than rounding (else the row is
+      // handed over).
+      if (have && key == lkey && r > 0.0) sh.bc_d[0] = r;
       if (tid == 0) {
-        // Tie members share one probability rt.  Key order must equal
-        // probability order next to the boundary: its bf16 neighbours, taken
-        // through the same arithmetic, must not collapse onto rt (else the
-        // row is handed over); one within a few ulps is a rounding-band
-        // decision.
-        double rt = exp((bf16_key_value(lkey) - M) / T) / s1;
-        if (s2 != 0.0) rt = rt / s2;
-        int ok = 1, near = 0;
+        const double vt = bf16_key_value(lkey);
+        bool ok = true;
         for (int side = -1; side <= 1; side += 2) {
           const uint32_t nk = lkey + side;
           if (nk <= kKeyNegInf || nk >= kKeyPosInf || zero_key(nk)) continue;
-          double rn = exp((bf16_key_value(nk) - M) / T) / s1;
-          if (s2 != 0.0) rn = rn / s2;
-          ok = ok && rn != rt;
-          near = near || fabs(rn - rt) <= rt * 0x1p-50;
+          ok = ok && fabs(bf16_key_value(nk) - vt) / T >= 0x1p-40;
         }
-        sh.bcast_d = rt;
-        sh.bcast_i[0] = ok;
-        sh.bcast_i[1] = near;
+        sh.bc_i[0] = ok;
       }
       const bool pos = r > 0.0;
-      const double A = bs.sum(pos && key > lkey ? r : 0.0);  // its barrier publishes thread 0's values
-      const double rt = sh.bcast_d;
-      if (!sh.bcast_i[0]) return kHandOrder;
-      if (sh.bcast_i[1]) flags |= DSR_FLAG_MARGIN;
       uint32_t cnt_tot;
-      const uint32_t cex = bs.scan((uint32_t)(pos && key > lkey) | ((uint32_t)(pos && key == lkey) << 16), cnt_tot);
+      double A;
+      const uint32_t cex = bs.scan_sum((uint32_t)(pos && key > lkey) | ((uint32_t)(pos && key == lkey) << 16),
+                                       (pos && key > lkey) ? r : 0.0, cnt_tot, A);  // publishes rt and the check
+      if (!sh.bc_i[0]) return kHandOrder;
+      const double rt = sh.bc_d[0];
       const long long trank = cex >> 16;
       const long long n_above = cnt_tot & 0xFFFFu, n_tie = cnt_tot >> 16;
+      // Tie member i (index order) keeps iff A + i * rt < P.
       long long keep;
       {
-        const double q = ceil((pol.top_p - A) / rt);
+        const double q = ceil((P - A) / rt);
         keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
-        while (keep > 0 && A + (double)(keep - 1) * rt >= pol.top_p) --keep;
-        while (keep < n_tie && A + (double)keep * rt < pol.top_p) ++keep;
+        while (keep > 0 && A + (double)(keep - 1) * rt >= P) --keep;
+        while (keep < n_tie && A + (double)keep * rt < P) ++keep;
       }
-      if (n_above == 0 && keep == 0) keep = 1;
-      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51;
-      bool close = fabs(A + (double)keep * rt - pol.top_p) <= tol;
-      if (keep >= 1 && n_above + keep > 1) close = close || fabs(A + (double)(keep - 1) * rt - pol.top_p) <= tol;
-      if (keep == 0 && n_above > 0) close = true;
-      if (keep == n_tie && A + (double)n_tie * rt < pol.top_p) close = true;
-      if (close) flags |= DSR_FLAG_MARGIN;
+      if (n_above == 0 && keep == 0) keep = 1;  // the first token is never removed
+      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51 * S;
+      bool near = fabs(A + (double)keep * rt - P) <= tol;
+      if (keep >= 1 && n_above + keep > 1) near = near || fabs(A + (double)(keep - 1) * rt - P) <= tol;
+      if (keep == 0 && n_above > 0) near = true;
+      if (keep == n_tie && A + (double)n_tie * rt < P) near = true;
+      if (near) flags |= DSR_FLAG_MARGIN;
       if (key < lkey || (key == lkey && trank >= keep)) r = 0.0;
     }
   }
 
-  // ---- categorical (sampling.py:103-128): the CDF in index order, its
-  // total, the number of positive tokens and any min-p rounding-band flag.
+  // ---- categorical (sampling.py:103-128): the CDF in index order (thread
+  // order), its total, the number of positive tokens and the min-p bands.
   const bool pos = r > 0.0;
-  double ctot;
-  const double ex = bs.scan(r, ctot);
-  const long long pos_info = bs.sum((long long)pos | ((long long)(minp_close ? 1 : 0) << 40));
-  const long long npos = pos_info & 0xFFFFFFFFll;
-  if (pos_info >> 40) flags |= DSR_FLAG_MARGIN;
+  double ex, ctot;
+  uint32_t tally;
+  const double inc = bs.cdf_scan(r, ex, ctot, (uint32_t)pos | ((uint32_t)close << 16), tally);
+  const uint32_t npos = tally & 0xFFFFu;
+  if (tally >> 16) flags |= DSR_FLAG_MARGIN;
+  const bool dense = a.out_probs_f32 || a.out_probs_f64 || a.out_kept_bits;
+  if (dense) {
+    fast_clear_outputs(a, row);
+    if (fin && ctot > 0.0 && isfinite(ctot)) fast_scatter(a, row, idx, r / ctot);
+  }
   if (!(ctot > 0.0) || !isfinite(ctot)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_NO_MASS, -1, 0, flags);
     return 0;
-  }
-  const double p = r / ctot;
-  if (a.out_probs_f32 || a.out_probs_f64 || a.out_kept_bits) {
-    fast_clear_outputs(a, row);
-    if (fin) fast_scatter(a, row, idx, p);
   }
   if (!a.uniforms) {
     if (tid == 0) fast_write_result(a, row, DSR_OK, -1, 0, flags);
@@ -558,22 +680,20 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
     if (pos) fast_write_result(a, row, DSR_OK, idx, 0, flags);
     return 0;
   }
-  const double u = a.uniforms[row];
   if (!(u >= 0.0 && u < 1.0)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
   }
   const double thr = u * ctot;
-  const double inc = ex + r;
-  // First thread whose inclusive prefix exceeds u * total (thread order is index order).
-  const long long owner = bs.min(pos && inc > thr ? (long long)tid : LLONG_MAX);
-  if (owner == LLONG_MAX) {
-    // Rounding left u * total above every prefix: the last positive token.
+  if (thr >= ctot) {
+    // Rounding left u * total at the total: the last positive token.
     const long long last = bs.max(pos ? (long long)tid : -1ll);
     if (tid == last) fast_write_result(a, row, DSR_OK, idx, 1, flags | DSR_FLAG_MARGIN);
     return 0;
   }
-  if (tid == owner) {
+  // The first token whose CDF value exceeds u * total: the intervals
+  // [ex, inc) tile [0, total), so exactly one positive thread owns thr.
+  if (pos && ex <= thr && thr < inc) {
     const double tol = ((double)npos + 16.0) * 0x1p-51 * ctot;
     if (inc - thr <= tol || (ex > 0.0 && thr - ex <= tol)) flags |= DSR_FLAG_MARGIN;
     fast_write_result(a, row, DSR_OK, idx, 1, flags);

@@ -106,6 +106,20 @@ __device__ __forceinline__ T wave_scan_dpp(T v) {
   return v;
 }
 
+// Running maximum over the 64 lanes in lane order.
+__device__ __forceinline__ double wave_maxscan_dpp(double v) {
+  using B = Bits<double>;
+  const double lo = -(double)INFINITY;
+  const uint64_t lob = B::to(lo);
+  v = fmax(v, B::from(B::template dpp<0x111, 0xF, 0xF, false>(lob, B::to(v))));
+  v = fmax(v, B::from(B::template dpp<0x112, 0xF, 0xF, false>(lob, B::to(v))));
+  v = fmax(v, B::from(B::template dpp<0x114, 0xF, 0xF, false>(lob, B::to(v))));
+  v = fmax(v, B::from(B::template dpp<0x118, 0xF, 0xF, false>(lob, B::to(v))));
+  v = fmax(v, B::from(B::template dpp<0x142, 0xA, 0xF, false>(lob, B::to(v))));
+  v = fmax(v, B::from(B::template dpp<0x143, 0xC, 0xF, false>(lob, B::to(v))));
+  return v;
+}
+
 // Inclusive prefix inside each 16-lane row only.
 template <class T>
 __device__ __forceinline__ T row_scan_dpp(T v) {
@@ -124,14 +138,16 @@ struct SyncSlots {
 };
 
 // Workgroup reductions / scans with one barrier each.  Every thread of the
-// workgroup must make the same sequence of calls.
+// workgroup must make the same sequence of calls.  Each call takes the slot
+// set of the next parity, so a wave that runs ahead into the next call never
+// overwrites slots that a slower wave is still reading.
 class BlockSync {
  public:
   __device__ explicit BlockSync(SyncSlots& s) : s_(s), ph_(0) {}
 
   template <class T, class Op>
   __device__ T reduce(T x, T identity, Op op) {
-    T* slot = slots<T>();
+    T* slot = slots<T>(next());
     x = wave_reduce_dpp(x, op);
     if (lane_id() == 0) slot[wave_id()] = x;
     lds_barrier();
@@ -151,7 +167,7 @@ class BlockSync {
   // Exclusive prefix over threads in thread order, and the workgroup total.
   template <class T>
   __device__ T scan(T x, T& total) {
-    T* slot = slots<T>();
+    T* slot = slots<T>(next());
     const T incl = wave_scan_dpp(x);
     if (lane_id() == 63) slot[wave_id()] = incl;
     lds_barrier();
@@ -162,57 +178,74 @@ class BlockSync {
     return (base + incl) - x;
   }
 
-  // Plain barrier that also advances the slot parity.
-  __device__ void barrier() { lds_barrier(); }
+  // Exclusive prefix of x in thread order (with its total) and the sum of y,
+  // behind one barrier.
+  __device__ uint32_t scan_sum(uint32_t x, double y, uint32_t& xtotal, double& ysum) {
+    const int p = next();
+    uint32_t* su = s_.u[p];
+    double* sf = s_.f[p];
+    const uint32_t incl = wave_scan_dpp(x);
+    const double ws = wave_reduce_dpp(y, OpSum());
+    if (lane_id() == 63) su[wave_id()] = incl;
+    if (lane_id() == 0) sf[wave_id()] = ws;
+    lds_barrier();
+    const uint32_t u = lane_id() < kWaves ? su[lane_id()] : 0u;
+    const uint32_t wincl = row_scan_dpp(u);
+    xtotal = lane_value(wincl, kWaves - 1);
+    const uint32_t base = lane_value(wincl - u, wave_id());
+    double f = lane_id() < kWaves ? sf[lane_id()] : 0.0;
+    f = row_reduce(f, OpSum());
+    ysum = lane_value(f, 0);
+    return base + incl - x;
+  }
+
+  // Index-order CDF of non-negative x behind one barrier.  Returns this
+  // thread's inclusive value; `ex` is exactly the previous thread's inclusive
+  // value (0 for thread 0), so the intervals [ex, inc) tile [0, total)
+  // without gaps or overlaps.  inc never decreases in thread order (a running
+  // maximum removes the ulp-level dips of the tree-shaped scan) and threads
+  // with x == 0 get empty intervals.  Wave bases are summed sequentially, in
+  // the same order in every lane.  Also returns the workgroup sum of `tally`.
+  __device__ double cdf_scan(double x, double& ex, double& total, uint32_t tally, uint32_t& tally_sum) {
+    const int p = next();
+    double* sf = s_.f[p];
+    uint32_t* su = s_.u[p];
+    double incl = wave_scan_dpp(x);
+    incl = x > 0.0 ? incl : -(double)INFINITY;
+    incl = fmax(wave_maxscan_dpp(incl), 0.0);
+    const uint32_t tw = wave_reduce_dpp(tally, OpSum());
+    if (lane_id() == 63) sf[wave_id()] = incl;
+    if (lane_id() == 0) su[wave_id()] = tw;
+    lds_barrier();
+    double base = 0.0, mine = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      if (w == wave_id()) mine = base;
+      base = base + sf[w];
+    }
+    total = base;
+    uint32_t u = lane_id() < kWaves ? su[lane_id()] : 0u;
+    u = row_reduce(u, OpSum());
+    tally_sum = lane_value(u, 0);
+    double prev = __shfl_up(incl, 1);
+    ex = lane_id() == 0 ? mine : mine + prev;
+    return mine + incl;
+  }
 
  private:
-  template <class T> __device__ T* slots();
+  __device__ int next() { ph_ ^= 1; return ph_; }
+  template <class T> __device__ T* slots(int p);
   SyncSlots& s_;
   int ph_;
 };
 
-template <> __device__ __forceinline__ double* BlockSync::slots<double>() { ph_ ^= 1; return s_.f[ph_]; }
-template <> __device__ __forceinline__ long long* BlockSync::slots<long long>() { ph_ ^= 1; return s_.i[ph_]; }
-template <> __device__ __forceinline__ uint32_t* BlockSync::slots<uint32_t>() { ph_ ^= 1; return s_.u[ph_]; }
+template <> __device__ __forceinline__ double* BlockSync::slots<double>(int p) { return s_.f[p]; }
+template <> __device__ __forceinline__ long long* BlockSync::slots<long long>(int p) { return s_.i[p]; }
+template <> __device__ __forceinline__ uint32_t* BlockSync::slots<uint32_t>(int p) { return s_.u[p]; }
 
-// k-th largest (1-based, k <= 64) of one 16-bit value per lane, by a bitwise
-// search over ballots; the result is uniform across the wave.
-__device__ __forceinline__ uint32_t wave_kth_largest_u16(uint32_t v, uint32_t k) {
-  uint32_t prefix = 0;
-#pragma unroll
-  for (int b = 15; b >= 0; --b) {
-    const uint32_t cand = prefix | (1u << b);
-    const uint32_t n = (uint32_t)__popcll(__ballot(v >= cand));
-    if (n >= k) prefix = cand;
-  }
-  return prefix;
-}
-
-// Adds `amount` to hist[bin] for every active lane, one LDS atomic per
-// distinct bin in the wave (lanes sharing a bin are combined first).
-__device__ __forceinline__ void hist_add_u32(uint32_t* hist, uint32_t bin, bool active) {
-  unsigned long long todo = __ballot(active);
-  while (todo) {
-    const int leader = __ffsll((long long)todo) - 1;
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
-    const unsigned long long same = __ballot(active && bin == b);
-    if (lane_id() == leader) atomicAdd(&hist[b], (uint32_t)__popcll(same));
-    todo &= ~same;
-  }
-}
-
-__device__ __forceinline__ void hist_add_u64(unsigned long long* hist, uint32_t bin, bool active,
-                                             unsigned long long amount) {
-  unsigned long long todo = __ballot(active);
-  while (todo) {
-    const int leader = __ffsll((long long)todo) - 1;
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
-    const bool mine = active && bin == b;
-    const unsigned long long same = __ballot(mine);
-    const long long part = wave_reduce_dpp((long long)(mine ? amount : 0ull), OpSum());
-    if (lane_id() == leader) atomicAdd(&hist[b], (unsigned long long)part);
-    todo &= ~same;
-  }
+// Position of this lane among the set lanes of a ballot.
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long b) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
 }
 
 }  // namespace dsr
