@@ -32,7 +32,6 @@
 //     group is settled in exact float64 arithmetic;
 //   * one wave finishes with the index-order CDF search of categorical
 //     (sampling.py:103-128).
-// Histogram selects that fit in 1,024 bins run in one wave with DPP scans.
 //
 // The path is exact only where bf16 key order equals the reference's float64
 // order; each row checks that at its decision boundaries (no +-0 boundary,
@@ -54,7 +53,6 @@ constexpr int64_t kFastMaxVocab = (int64_t)kThreads * kFastChunks * 8;  // 13107
 constexpr int kChunkCap = 2048;                                         // compacted chunk list
 constexpr int kFastMaxK = kThreads;                                     // one kept token per thread
 constexpr uint32_t kWindow = 4096;                                      // keys tracked below the maximum
-constexpr int kWaveBins = 1024;                                         // bins one wave selects over
 
 // Why a row is handed to the general path (reported in out_flags bits 4-7).
 constexpr int kHandPolicy = 1;     // controls out of bounds (the general path reports it)
@@ -201,77 +199,33 @@ __device__ __forceinline__ uint32_t wave_offset(uint32_t wn, uint32_t* slot, uin
   return lane_value(incl - y, wave_id());
 }
 
-template <class T> struct Bins16;
-template <> struct Bins16<uint32_t> {
+template <class T> struct Bins4;
+template <> struct Bins4<uint32_t> {
   static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* c) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint4 v = ((const uint4*)p)[q];
-      c[4 * q] = v.x; c[4 * q + 1] = v.y; c[4 * q + 2] = v.z; c[4 * q + 3] = v.w;
-    }
+    const uint4 v = *(const uint4*)p;
+    c[0] = v.x; c[1] = v.y; c[2] = v.z; c[3] = v.w;
   }
 };
-template <> struct Bins16<long long> {
+template <> struct Bins4<long long> {
   static __device__ __forceinline__ void load(const long long* p, long long* c) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const longlong2 v = ((const longlong2*)p)[q];
-      c[2 * q] = v.x; c[2 * q + 1] = v.y;
-    }
+    const longlong2 a = ((const longlong2*)p)[0], b = ((const longlong2*)p)[1];
+    c[0] = a.x; c[1] = a.y; c[2] = b.x; c[3] = b.y;
   }
 };
 
 // bins[0..kWindow) hold counts (or fixed-point mass) by distance below the
 // maximum key, largest key first.  Returns the first bin where the running
 // total reaches `rem` (-1 if the whole window stays below it) and the total
-// before that bin.  Wave 0 scans the first 1,024 bins with a DPP scan; the
-// workgroup scans the rest only when those fall short.  Every thread calls.
+// before that bin.  Thread t takes bins 4t .. 4t+3: one workgroup scan, then
+// the thread holding the crossing publishes it.  Every thread calls.
 template <class T>
 __device__ int select_bin(const T* bins, T rem, FastLists& sh, BlockSync& bs, T& above) {
-  if (wave_id() == 0) {
-    const int l = lane_id();
-    T c[16];
-    Bins16<T>::load(bins + 16 * l, c);
-    T s = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s += c[j];
-    const T incl = wave_scan_dpp(s);
-    const T ex = incl - s;
-    const unsigned long long hit = __ballot(ex < rem && rem <= incl);
-    if (hit == 0) {
-      if (l == 0) {
-        sh.sel = -1;
-        sh.sel_above = (long long)lane_value(incl, 63);
-      }
-    } else if (l == __ffsll((long long)hit) - 1) {
-      T run = ex, ab = 0;
-      int b = -1;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (b < 0 && run + c[j] >= rem) {
-          b = j;
-          ab = run;
-        }
-        run += c[j];
-      }
-      sh.sel = 16 * l + b;
-      sh.sel_above = (long long)ab;
-    }
-  }
-  lds_barrier();
-  int b = sh.sel;
-  above = (T)sh.sel_above;
-  if (b >= 0) return b;
-  // The first 1,024 bins hold less than rem: the workgroup scans the rest.
-  const T below = above;
   const int t = threadIdx.x;
-  T c[4] = {0, 0, 0, 0};
-  if (t >= kWaveBins / 4) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) c[j] = bins[4 * t + j];
-  }
+  T c[4];
+  Bins4<T>::load(bins + 4 * t, c);
+  if (t == 0) sh.sel = -1;  // the scan's barrier orders this before the writes below
   T total;
-  T run = bs.scan(c[0] + c[1] + c[2] + c[3], total) + below;  // its barrier orders the reads of sel above
+  T run = bs.scan((c[0] + c[1]) + (c[2] + c[3]), total);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (run < rem && rem <= run + c[j]) {
@@ -281,9 +235,8 @@ __device__ int select_bin(const T* bins, T rem, FastLists& sh, BlockSync& bs, T&
     run += c[j];
   }
   lds_barrier();
-  b = sh.sel;
   above = (T)sh.sel_above;
-  return b;
+  return sh.sel;
 }
 
 // Returns 0 if the row was decided here, else the reason it is handed to the

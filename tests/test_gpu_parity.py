@@ -2,9 +2,10 @@
 
 Token ids, consumption flags, top-k index sets and statuses must be bit-exact;
 fp32 probabilities within 1e-5 relative (exactly zero where the oracle is
-zero).  The only tolerated token difference is a decision flagged as lying
-inside the float64 rounding band (by the GPU's DSR_FLAG_MARGIN or the
-oracle's own margin), and such rows must be rare.
+zero).  The only tolerated token difference is a decision that the oracle
+itself places inside the float64 rounding band (its margin below 1e-11, where
+a different exp or summation order may legitimately pick the neighbour); such
+rows, and rows the kernel flags with DSR_FLAG_MARGIN, must be rare.
 """
 import json
 import os
@@ -16,7 +17,7 @@ import torch
 from deepseekrpc_amd import _native as N
 from deepseekrpc_amd import batch, workloads
 from oracle import sampling_oracle as O
-from parity_util import compare, oracle_row, run_gpu
+from parity_util import MARGIN, compare, oracle_row, run_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -24,9 +25,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def check(rep, max_margin_frac=0.01):
-    print(f"rows={rep.rows} exact={rep.exact} margin={rep.margin_rows} max_rel={rep.max_rel:.3g}", flush=True)
+    print(f"rows={rep.rows} exact={rep.exact} margin={rep.margin_rows} flagged={rep.flagged} "
+          f"max_rel={rep.max_rel:.3g}", flush=True)
     assert not rep.mismatches, rep.mismatches[:10]
     assert len(rep.margin_rows) <= max(1, int(max_margin_frac * rep.rows))
+    # The rounding-band flag must stay rare: it marks decisions within a few
+    # ulps of a threshold, which random inputs almost never produce.
+    assert rep.flagged <= max(1, int(max_margin_frac * rep.rows))
 
 
 def test_c1_single_row_fp32():
@@ -88,7 +93,10 @@ def test_golden_vectors_on_gpu(case):
         res = batch.sample_rows(x, [case["policy"]], history=hist, bias=bt, allow_bits=allow,
                                 uniforms=torch.tensor([u], dtype=torch.float64, device=dev), probs="f64")
         assert int(res.status.item()) == 0
-        assert int(res.tokens.item()) == want or int(res.flags.item()) & 1
+        if int(res.tokens.item()) != want:
+            # Tolerated only where the reference's own decision sat in the rounding band.
+            ref = O.sample_row(logits, O.Policy(**case["policy"]), float(u), counts, gen, bias, allowed)
+            assert ref.token == want and ref.margin < MARGIN, (n, u, int(res.tokens.item()), want)
         p = res.probs[0].cpu().numpy()
         if f"{n}/probs" in GOLD:
             ref = GOLD[f"{n}/probs"]
