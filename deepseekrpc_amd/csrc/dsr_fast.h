@@ -72,11 +72,9 @@ struct FastLists {
   };
   uint32_t cnt[2][kWindow];                // counts by distance below the maximum key
   long long mass[kWindow];                 // fixed-point mass by distance below the maximum key
-  double kr[kFastMaxK];                    // final masses of the kept tokens, index order
   uint16_t kkey[kFastMaxK];                // kept tokens, index order
   uint32_t kidx[kFastMaxK];
   uint32_t wn[kWaves];
-  uint32_t wflag[kWaves];
   long long sel_above;
   int sel;
   int bc_i[2];
@@ -537,7 +535,10 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
   // ---- one kept token per thread: its unnormalised mass r = exp((v - max) / T)
   // (sampling.py:86-92; the maximum's mass is exactly 1) and min-p, which
   // keeps r >= min_p (:94-96: result < min_p * max(result) with
-  // max(result) = 1 / sum).
+  // max(result) = 1 / sum).  Masses are summed as exact 64-bit fixed point,
+  // fx = floor(r * 2^50) (k <= 1024 masses <= 1 stay below 2^61), so every
+  // sum and prefix is order-independent and exact; the rounding this adds
+  // (under one unit per token) is part of the decision margins below.
   const bool have = tid < (int)k;
   const uint32_t key = have ? (uint32_t)sh.kkey[tid] : 0u;
   const uint32_t idx = have ? sh.kidx[tid] : 0u;
@@ -549,79 +550,110 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
     close = r > 0.0 && fabs(r - pol.min_p) <= pol.min_p * 0x1p-48;
     if (r < pol.min_p) r = 0.0;
   }
+  long long fx = (long long)(r * 0x1p50);
+  if (pol.top_p < 1.0 && fx > 0) atomicAdd((unsigned long long*)&sh.mass[Mkey - key], (unsigned long long)fx);
   unsigned flags = 0;
   if (pol.top_p < 1.0) {  // :97-102
-    if (r > 0.0) atomicAdd((unsigned long long*)&sh.mass[Mkey - key], (unsigned long long)(r * 0x1p50));
-    const double S = bs.sum(r);  // its barrier also publishes the mass histogram
-    const double P = pol.top_p * S;
-    long long tgt = (long long)(P * 0x1p50);
-    if (tgt < 1) tgt = 1;
-    long long above1;
-    const int dl = select_bin(sh.mass, tgt, sh, bs, above1);
-    if (dl < 0) {
-      // The whole mass stays below top_p: nothing is removed.
-      if (fabs(S - P) <= ((double)k + 16.0) * 0x1p-51 * S) flags |= DSR_FLAG_MARGIN;
-    } else {
-      const uint32_t lkey = Mkey - (uint32_t)dl;
-      if (zero_key(lkey)) return kHandZero;
-      // Tie members share one mass rt; any of them publishes it.  Key order
-      // must equal mass order next to the boundary: the bf16 neighbours of
-      // the boundary value must keep (v - max) / T at least 2^-40 apart, so
-      // their masses differ by far more than rounding (else the row is
-      // handed over).
-      if (have && key == lkey && r > 0.0) sh.bc_d[0] = r;
-      if (tid == 0) {
-        const double vt = bf16_key_value(lkey);
-        bool ok = true;
-        for (int side = -1; side <= 1; side += 2) {
-          const uint32_t nk = lkey + side;
-          if (nk <= kKeyNegInf || nk >= kKeyPosInf || zero_key(nk)) continue;
-          ok = ok && fabs(bf16_key_value(nk) - vt) / T >= 0x1p-40;
+    lds_barrier();  // the mass histogram is complete
+    // One scan over the mass bins (largest key first) and the kept-token
+    // counts per key gives the total S, hence the target P = top_p * S, and
+    // each thread can test its own four bins for the first one whose running
+    // mass reaches P: the boundary key.  Its thread settles the tie group.
+    const int t = threadIdx.x;
+    long long cm[4];
+    uint32_t cc[4];
+    Bins4<long long>::load(sh.mass + 4 * t, cm);
+    {
+      const uint4 c4 = *(const uint4*)(sh.cnt[1] + 4 * t);
+      const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t d = 4u * (uint32_t)t + q;
+        cc[q] = d < dk ? cw[q] : (d == dk ? need : 0u);  // kept tokens per key
+      }
+    }
+    if (t == 0) sh.sel = -1;  // ordered before the crossing's write by the scan's barrier
+    long long S;
+    uint32_t cex, ctot;
+    long long run = bs.scan2((cm[0] + cm[1]) + (cm[2] + cm[3]), (cc[0] + cc[1]) + (cc[2] + cc[3]), S, cex, ctot);
+    const double P = pol.top_p * (double)S;
+    long long tgt = (long long)P;
+    tgt = tgt < 1 ? 1 : (tgt > S ? S : tgt);  // S >= 2^50: the maximum's mass is exactly 1
+    if (run < tgt && tgt <= run + ((cm[0] + cm[1]) + (cm[2] + cm[3]))) {  // the crossing is in this thread's bins
+      uint32_t dl = 0, n_tie = 0;
+      long long A = 0, n_above = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (run < tgt && tgt <= run + cm[q]) {
+          dl = 4u * (uint32_t)t + q;
+          A = run;
+          n_above = cex;
+          n_tie = cc[q];
         }
-        sh.bc_i[0] = ok;
+        run += cm[q];
+        cex += cc[q];
       }
-      const bool pos = r > 0.0;
-      uint32_t cnt_tot;
-      double A;
-      const uint32_t cex = bs.scan_sum((uint32_t)(pos && key > lkey) | ((uint32_t)(pos && key == lkey) << 16),
-                                       (pos && key > lkey) ? r : 0.0, cnt_tot, A);  // publishes rt and the check
-      if (!sh.bc_i[0]) return kHandOrder;
-      const double rt = sh.bc_d[0];
-      const long long trank = cex >> 16;
-      const long long n_above = cnt_tot & 0xFFFFu, n_tie = cnt_tot >> 16;
-      // Tie member i (index order) keeps iff A + i * rt < P.
-      long long keep;
-      {
-        const double q = ceil((P - A) / rt);
-        keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
-        while (keep > 0 && A + (double)(keep - 1) * rt >= P) --keep;
-        while (keep < n_tie && A + (double)keep * rt < P) ++keep;
-      }
+      // Tie member i (index order) keeps iff A + i * rt < P (:98-101).  All
+      // members carry the same fixed-point mass, so rt is the bin's mass over
+      // its count.
+      const uint32_t lkey = Mkey - dl;
+      const long long rt = (long long)((unsigned long long)sh.mass[dl] / n_tie);
+      long long keep = (long long)ceil((P - (double)A) / (double)rt);
+      keep = keep < 0 ? 0 : (keep > (long long)n_tie ? (long long)n_tie : keep);
+      while (keep > 0 && (double)(A + (keep - 1) * rt) >= P) --keep;
+      while (keep < (long long)n_tie && (double)(A + keep * rt) < P) ++keep;
       if (n_above == 0 && keep == 0) keep = 1;  // the first token is never removed
-      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51 * S;
-      bool near = fabs(A + (double)keep * rt - P) <= tol;
-      if (keep >= 1 && n_above + keep > 1) near = near || fabs(A + (double)(keep - 1) * rt - P) <= tol;
+      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51 * (double)S + (double)(n_above + n_tie + 2);
+      bool near = fabs((double)(A + keep * rt) - P) <= tol;
+      if (keep >= 1 && n_above + keep > 1) near = near || fabs((double)(A + (keep - 1) * rt) - P) <= tol;
       if (keep == 0 && n_above > 0) near = true;
-      if (keep == n_tie && A + (double)n_tie * rt < P) near = true;
-      if (near) flags |= DSR_FLAG_MARGIN;
-      if (key < lkey || (key == lkey && trank >= keep)) r = 0.0;
+      if (keep == (long long)n_tie && (double)(A + (long long)n_tie * rt) < P) near = true;
+      // Key order must equal mass order next to the boundary: its bf16
+      // neighbours must keep (v - max) / T at least 2^-40 apart, so their
+      // masses differ by far more than rounding; ties with +-0 never pass.
+      int hand = zero_key(lkey) ? kHandZero : 0;
+      for (int side = -1; side <= 1 && !hand; side += 2) {
+        const uint32_t nk = lkey + side;
+        if (nk <= kKeyNegInf || nk >= kKeyPosInf || zero_key(nk)) continue;
+        if (!(fabs(bf16_key_value(nk) - bf16_key_value(lkey)) / T >= 0x1p-40)) hand = kHandOrder;
+      }
+      sh.sel = (int)lkey;
+      sh.bc_i[0] = (int)keep;
+      sh.bc_i[1] = hand | (near ? 0x100 : 0) | ((keep > 0 && keep < (long long)n_tie) ? 0x200 : 0);
+    }
+    lds_barrier();
+    if (sh.sel < 0) return kHandCapacity;  // unreachable: the running mass reaches tgt <= S
+    const uint32_t lkey = (uint32_t)sh.sel;
+    const long long keep = sh.bc_i[0];
+    const int info = sh.bc_i[1];
+    if (info & 0xFF) return info & 0xFF;
+    if (info & 0x100) flags |= DSR_FLAG_MARGIN;
+    long long trank = 0;
+    if (info & 0x200) {  // a partly kept tie group: ranks by index (thread order)
+      uint32_t tt;
+      trank = bs.scan((uint32_t)(fx > 0 && key == lkey), tt);
+    }
+    if (key < lkey || (key == lkey && trank >= keep)) {
+      r = 0.0;
+      fx = 0;
     }
   }
 
   // ---- categorical (sampling.py:103-128): the CDF in index order (thread
-  // order), its total, the number of positive tokens and the min-p bands.
+  // order) as an exact integer scan, the number of positive tokens and the
+  // min-p rounding bands.
   const bool pos = r > 0.0;
-  double ex, ctot;
-  uint32_t tally;
-  const double inc = bs.cdf_scan(r, ex, ctot, (uint32_t)pos | ((uint32_t)close << 16), tally);
+  long long ctot;
+  uint32_t tex, tally;
+  const long long ex = bs.scan2(fx, (uint32_t)pos | ((uint32_t)close << 16), ctot, tex, tally);
   const uint32_t npos = tally & 0xFFFFu;
   if (tally >> 16) flags |= DSR_FLAG_MARGIN;
   const bool dense = a.out_probs_f32 || a.out_probs_f64 || a.out_kept_bits;
   if (dense) {
     fast_clear_outputs(a, row);
-    if (fin && ctot > 0.0 && isfinite(ctot)) fast_scatter(a, row, idx, r / ctot);
+    if (fin && ctot > 0) fast_scatter(a, row, idx, r / ((double)ctot * 0x1p-50));
   }
-  if (!(ctot > 0.0) || !isfinite(ctot)) {
+  if (ctot <= 0) {
     if (tid == 0) fast_write_result(a, row, DSR_E_NO_MASS, -1, 0, flags);
     return 0;
   }
@@ -637,18 +669,19 @@ __device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShar
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
   }
-  const double thr = u * ctot;
+  // First token whose CDF value exceeds u * total (c_i / c_last > u): with
+  // integer CDF values that is the token whose interval [ex, ex + fx) holds
+  // floor(u * total).  If rounding leaves u * total at the total, the last
+  // positive token (its interval ends at the total).
+  const double thr_d = u * (double)ctot;
+  long long thr = (long long)thr_d;
   if (thr >= ctot) {
-    // Rounding left u * total at the total: the last positive token.
-    const long long last = bs.max(pos ? (long long)tid : -1ll);
-    if (tid == last) fast_write_result(a, row, DSR_OK, idx, 1, flags | DSR_FLAG_MARGIN);
-    return 0;
+    thr = ctot - 1;
+    flags |= DSR_FLAG_MARGIN;
   }
-  // The first token whose CDF value exceeds u * total: the intervals
-  // [ex, inc) tile [0, total), so exactly one positive thread owns thr.
-  if (pos && ex <= thr && thr < inc) {
-    const double tol = ((double)npos + 16.0) * 0x1p-51 * ctot;
-    if (inc - thr <= tol || (ex > 0.0 && thr - ex <= tol)) flags |= DSR_FLAG_MARGIN;
+  if (fx > 0 && ex <= thr && thr < ex + fx) {
+    const double tol = ((double)npos + 16.0) * 0x1p-51 * (double)ctot + (double)npos + 2.0;
+    if ((double)(ex + fx) - thr_d <= tol || (ex > 0 && thr_d - (double)ex <= tol)) flags |= DSR_FLAG_MARGIN;
     fast_write_result(a, row, DSR_OK, idx, 1, flags);
   }
   return 0;

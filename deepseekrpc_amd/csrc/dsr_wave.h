@@ -199,6 +199,30 @@ class BlockSync {
     return base + incl - x;
   }
 
+  // Exclusive prefixes (thread order) of a 64-bit and a 32-bit integer, with
+  // their totals, behind one barrier.  Integer sums are exact, so the
+  // intervals [ex, ex + x) tile [0, total) exactly.
+  __device__ long long scan2(long long a, uint32_t b, long long& atotal, uint32_t& bex, uint32_t& btotal) {
+    const int p = next();
+    long long* si = s_.i[p];
+    uint32_t* su = s_.u[p];
+    const long long ai = wave_scan_dpp(a);
+    const uint32_t bi = wave_scan_dpp(b);
+    if (lane_id() == 63) {
+      si[wave_id()] = ai;
+      su[wave_id()] = bi;
+    }
+    lds_barrier();
+    const long long ya = lane_id() < kWaves ? si[lane_id()] : 0ll;
+    const uint32_t yb = lane_id() < kWaves ? su[lane_id()] : 0u;
+    const long long wa = row_scan_dpp(ya);
+    const uint32_t wb = row_scan_dpp(yb);
+    atotal = lane_value(wa, kWaves - 1);
+    btotal = lane_value(wb, kWaves - 1);
+    bex = lane_value(wb - yb, wave_id()) + bi - b;
+    return lane_value(wa - ya, wave_id()) + ai - a;
+  }
+
   // Index-order CDF of non-negative x behind one barrier.  Returns this
   // thread's inclusive value; `ex` is exactly the previous thread's inclusive
   // value (0 for thread 0), so the intervals [ex, inc) tile [0, total)
