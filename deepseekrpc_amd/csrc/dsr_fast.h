@@ -239,7 +239,7 @@ __device__ int select_bin(const T* bins, T rem, FastLists& sh, BlockSync& bs, T&
 
 // Returns 0 if the row was decided here, else the reason it is handed to the
 // general path (kHand*).
-__device__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShared& shu) {
+__device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShared& shu) {
   FastLists& sh = shu.f;
   const int tid = threadIdx.x, lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());

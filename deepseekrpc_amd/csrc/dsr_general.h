@@ -1,16 +1,25 @@
 // The exact per-row sampling pipeline over a float64 workspace row.
 //
 // One workgroup owns one row.  The row's adjusted logits live in a float64
-// workspace row W[0, V); each stage is one strided, coalesced pass over W.
+// workspace row W[0, V); each stage is one strided, coalesced pass over W in
+// which every thread keeps kUnroll independent loads in flight (a pass with
+// one load in flight per thread is latency-bound, not bandwidth-bound).
 // This path accepts every input the reference accepts (any vocabulary size,
 // bf16 / f32 / f64 logits, penalties, bias, masks, any top-k / min-p / top-p),
 // so it is the fallback for rows the register-resident fast path does not
 // take.  The stages follow SamplingPolicy.probabilities (sampling.py:48-106)
-// in order; selection uses radix passes over order-preserving keys instead of
-// the reference's two stable argsorts (:90, :98).
+// in order and keep its float64 arithmetic; selection uses 11-bit radix
+// passes over order-preserving keys instead of the reference's two stable
+// argsorts (:90, :98).  Passes are fused where the reference's values allow
+// it: the row maximum and its first index come out of the pass that writes
+// the adjusted logits, the top-k mask is applied inside the exp pass, min-p
+// inside the first normalisation (max(r) is 1 / sum, since the maximum's
+// exp is exactly 1), and each normalisation carries the sum of what it
+// wrote, so no pass exists only to sum.
 #pragma once
 
 #include "dsr_common.h"
+#include "dsr_wave.h"
 
 namespace dsr {
 
@@ -32,56 +41,134 @@ struct RowSpec {
   double* W;               // workspace row
   uint32_t* kept_bits;     // optional output: finite after top-k
   int64_t kept_words;
+  float* probs_f32;        // optional outputs: the final distribution
+  double* probs_f64;
 };
+
+constexpr int kRadixBits = 11;
+constexpr int kBins = 1 << kRadixBits;  // two per thread
+static_assert(kBins == 2 * kThreads, "radix selection assumes two bins per thread");
+constexpr int kRadixPasses = 6;         // 5 x 11 bits + 9 bits = 64
 
 struct GenShared {
   BlockScratch b;
-  unsigned int hist[256];
-  unsigned long long hmass[256];
+  unsigned int hist[kBins];
+  unsigned long long hmass[kBins];
   int sel_bin;
-  unsigned int sel_above_cnt;
-  unsigned long long sel_above_mass;
+  long long sel_above;
+  long long bc[4];
 };
 
-// Strided loop over [0, V): consecutive threads touch consecutive elements.
-#define DSR_FOR_ROW(i, V) for (int64_t i = threadIdx.x; i < (V); i += kThreads)
+constexpr int kUnroll = 8;
+
+// Strided pass over [0, n): thread t visits t, t + kThreads, ... in increasing
+// order (so per-thread accumulations keep one fixed order), kUnroll elements
+// at a time with all of their loads issued before the first use.
+template <class T, class Load, class Body>
+__device__ __forceinline__ void row_pass(int64_t n, Load load, Body body) {
+  for (int64_t b = threadIdx.x; b < n; b += (int64_t)kUnroll * kThreads) {
+    T x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = b + (int64_t)u * kThreads;
+      x[u] = i < n ? load(i) : T();
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = b + (int64_t)u * kThreads;
+      if (i < n) body(i, x[u]);
+    }
+  }
+}
+
+// The same over one contiguous range [lo, hi), in index order.
+template <class T, class Load, class Body>
+__device__ __forceinline__ void slice_pass(int64_t lo, int64_t hi, Load load, Body body) {
+  for (int64_t b = lo; b < hi; b += kUnroll) {
+    T x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) x[u] = b + u < hi ? load(b + u) : T();
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (b + u < hi) body(b + u, x[u]);
+  }
+}
 
 __device__ __forceinline__ bool allowed_bit(const uint32_t* allow, int64_t i) {
   return allow == nullptr || ((allow[i >> 5] >> (i & 31)) & 1u);
 }
 
 // Contiguous per-thread slice, used where index order matters.
-__device__ __forceinline__ void thread_slice(int64_t V, int64_t& lo, int64_t& hi) {
-  int64_t ch = (V + kThreads - 1) / kThreads;
-  lo = (int64_t)threadIdx.x * ch;
+__device__ __forceinline__ void slice_of(int64_t t, int64_t V, int64_t& lo, int64_t& hi) {
+  const int64_t ch = (V + kThreads - 1) / kThreads;
+  lo = t * ch;
   hi = lo + ch < V ? lo + ch : V;
   if (lo > V) lo = V;
 }
+__device__ __forceinline__ void thread_slice(int64_t V, int64_t& lo, int64_t& hi) { slice_of(threadIdx.x, V, lo, hi); }
 
-// Index of the need-th (1-based, in index order) element with keyfn(W[i]) == key.
-template <class KeyFn>
-__device__ int64_t nth_equal_index(const double* W, int64_t V, uint64_t key, long long need, KeyFn keyfn,
-                                   GenShared& sh) {
-  if (need <= 0) return -1;
-  int64_t lo, hi;
-  thread_slice(V, lo, hi);
-  long long cnt = 0;
-  for (int64_t i = lo; i < hi; ++i) cnt += keyfn(W[i]) == key;
-  long long total;
-  long long base = block_exclusive_scan_i64(cnt, sh.b, total);
-  if (base < need && need <= base + cnt) {
-    long long left = need - base;
-    for (int64_t i = lo; i < hi; ++i) {
-      if (keyfn(W[i]) == key && --left == 0) {
-        sh.b.bcast_i[0] = i;
-        break;
-      }
+__device__ __forceinline__ uint64_t raw_bits(double x) { return (uint64_t)__double_as_longlong(x); }
+
+// Histogram adds merged per thread while consecutive adds hit one bin, and
+// per wave at the end when every pending lane shares a bin: the first radix
+// digits of a row are nearly constant, and unmerged LDS atomics on one
+// address serialise.
+template <class T>
+struct RunAdd {
+  int bin = -1;
+  T n = 0;
+  __device__ __forceinline__ void add(T* h, int b, T c) {
+    if (b != bin) {
+      if (n) atomicAdd(&h[bin], n);
+      bin = b;
+      n = 0;
     }
+    n += c;
+  }
+  // Every lane of the wave calls.
+  __device__ __forceinline__ void flush(T* h) {
+    const unsigned long long act = __ballot(n != 0);
+    if (act == 0) return;
+    const int b0 = __shfl(bin, __ffsll((long long)act) - 1);
+    if (__ballot(n != 0 && bin != b0) == 0) {
+      const T s = wave_sum(n);
+      if (lane_id() == 0) atomicAdd(&h[b0], s);
+    } else if (n) {
+      atomicAdd(&h[bin], n);
+    }
+    n = 0;
+    bin = -1;
+  }
+};
+
+// bins[] ranked from the top (largest digit first): the bin where the running
+// total reaches rem (1-based), or -1, and the total of the bins above it.
+// Thread t holds bins kBins-1-2t and kBins-2-2t.  Every thread calls.
+template <class T>
+__device__ int select_from_top(const T* bins, long long rem, GenShared& sh, long long& above) {
+  const int t = threadIdx.x;
+  const int b0 = kBins - 1 - 2 * t, b1 = b0 - 1;
+  const long long c0 = (long long)bins[b0], c1 = (long long)bins[b1];
+  if (t == 0) sh.sel_bin = -1;  // ordered before the writes below by the scan's barrier
+  long long total;
+  const long long ex = block_exclusive_scan_i64(c0 + c1, sh.b, total);
+  if (ex < rem && rem <= ex + c0) {
+    sh.sel_bin = b0;
+    sh.sel_above = ex;
+  } else if (ex + c0 < rem && rem <= ex + c0 + c1) {
+    sh.sel_bin = b1;
+    sh.sel_above = ex + c0;
   }
   __syncthreads();
-  int64_t r = sh.b.bcast_i[0];
+  const int b = sh.sel_bin;
+  above = sh.sel_above;
   __syncthreads();
-  return r;
+  return b;
+}
+
+__device__ __forceinline__ int radix_shift(int pass) { return pass < kRadixPasses - 1 ? 64 - kRadixBits * (pass + 1) : 0; }
+__device__ __forceinline__ uint64_t radix_mask(int pass) {
+  return pass < kRadixPasses - 1 ? (uint64_t)(kBins - 1) : (1ull << (64 - kRadixBits * (kRadixPasses - 1))) - 1;
 }
 
 // Radix select: key of the k-th largest element (1-based, ties counted) and
@@ -90,38 +177,25 @@ __device__ void radix_kth_largest(const double* W, int64_t V, long long k, GenSh
                                   long long& need) {
   uint64_t prefix = 0, pmask = 0;
   long long rem = k;
-  for (int shift = 56; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += kThreads) sh.hist[b] = 0;
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
+    const int shift = radix_shift(pass);
+    const uint64_t dm = radix_mask(pass);
+    for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
     __syncthreads();
-    DSR_FOR_ROW(i, V) {
-      uint64_t key = order_key(W[i]);
-      if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
-    }
+    RunAdd<unsigned int> ra;
+    row_pass<double>(
+        V, [&](int64_t i) { return W[i]; },
+        [&](int64_t, double x) {
+          const uint64_t key = order_key(x);
+          if ((key & pmask) == prefix) ra.add(sh.hist, (int)((key >> shift) & dm), 1u);
+        });
+    ra.flush(sh.hist);
     __syncthreads();
-    if (threadIdx.x < 64) {
-      const int l = threadIdx.x;
-      unsigned c[4];
-      for (int j = 0; j < 4; ++j) c[j] = sh.hist[4 * l + j];
-      unsigned lsum = c[0] + c[1] + c[2] + c[3];
-      unsigned suf = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        unsigned y = __shfl_down(suf, o);
-        if (l + o < 64) suf += y;
-      }
-      long long above = (long long)(suf - lsum);
-      for (int j = 3; j >= 0; --j) {
-        if (above < rem && rem <= above + (long long)c[j]) {
-          sh.sel_bin = 4 * l + j;
-          sh.sel_above_cnt = (unsigned)above;
-        }
-        above += c[j];
-      }
-    }
-    __syncthreads();
-    rem -= (long long)sh.sel_above_cnt;
-    prefix |= (uint64_t)sh.sel_bin << shift;
-    pmask |= 0xFFull << shift;
-    __syncthreads();
+    long long above;
+    const int b = select_from_top(sh.hist, rem, sh, above);
+    rem -= above;
+    prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
+    pmask |= dm << shift;
   }
   kth = prefix;
   need = rem;
@@ -134,85 +208,210 @@ __device__ void radix_kth_largest(const double* W, int64_t V, long long k, GenSh
 // re-derives the decision exactly in float64.  Returns false if the whole
 // mass stays below top_p.
 __device__ bool radix_mass_crossing(const double* W, int64_t V, double top_p, GenShared& sh, uint64_t& lbits) {
-  unsigned long long tgt = (unsigned long long)(top_p * 0x1p60);
+  long long tgt = (long long)(top_p * 0x1p60);
   if (tgt == 0) tgt = 1;  // top_p == 0: the first ranked element is L
   uint64_t prefix = 0, pmask = 0;
-  unsigned long long above = 0;
-  for (int shift = 56; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += kThreads) sh.hmass[b] = 0;
-    if (threadIdx.x == 0) sh.sel_bin = -1;
+  long long above = 0;
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
+    const int shift = radix_shift(pass);
+    const uint64_t dm = radix_mask(pass);
+    for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hmass[b] = 0;
     __syncthreads();
-    DSR_FOR_ROW(i, V) {
-      double x = W[i];
-      if (x > 0.0) {
-        uint64_t key = (uint64_t)__double_as_longlong(x);
-        if ((key & pmask) == prefix)
-          atomicAdd(&sh.hmass[(key >> shift) & 255u], (unsigned long long)(x * 0x1p60));
-      }
-    }
+    RunAdd<unsigned long long> ra;
+    row_pass<double>(
+        V, [&](int64_t i) { return W[i]; },
+        [&](int64_t, double x) {
+          if (x > 0.0) {
+            const uint64_t key = raw_bits(x);
+            if ((key & pmask) == prefix) ra.add(sh.hmass, (int)((key >> shift) & dm), (unsigned long long)(x * 0x1p60));
+          }
+        });
+    ra.flush(sh.hmass);
     __syncthreads();
-    if (threadIdx.x < 64) {
-      const int l = threadIdx.x;
-      unsigned long long m[4];
-      for (int j = 0; j < 4; ++j) m[j] = sh.hmass[4 * l + j];
-      unsigned long long lsum = m[0] + m[1] + m[2] + m[3];
-      unsigned long long suf = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        unsigned long long y = __shfl_down(suf, o);
-        if (l + o < 64) suf += y;
-      }
-      unsigned long long excl = above + (suf - lsum);
-      for (int j = 3; j >= 0; --j) {
-        if (excl < tgt && tgt <= excl + m[j]) {
-          sh.sel_bin = 4 * l + j;
-          sh.sel_above_mass = excl;
-        }
-        excl += m[j];
-      }
-    }
-    __syncthreads();
-    int b = sh.sel_bin;
-    unsigned long long ab = sh.sel_above_mass;
-    __syncthreads();
+    long long ab;
+    const int b = select_from_top(sh.hmass, tgt - above, sh, ab);
     if (b < 0) return false;
-    above = ab;
+    above += ab;
     prefix |= (uint64_t)b << shift;
-    pmask |= 0xFFull << shift;
+    pmask |= dm << shift;
   }
   lbits = prefix;
   return true;
 }
 
-__device__ __forceinline__ uint64_t raw_bits(double x) { return (uint64_t)__double_as_longlong(x); }
-
-// Writes one bit per token (1 = W[i] finite) into `bits`.  A wave covers 64
-// consecutive tokens per iteration, so each ballot is two whole words.
-__device__ void write_finite_bits(const double* W, int64_t V, uint32_t* bits, int64_t words) {
-  for (int64_t base = 0; base < V; base += kThreads) {
-    int64_t i = base + threadIdx.x;
-    bool f = i < V && isfinite(W[i]);
-    unsigned long long m = __ballot(f);
-    int64_t w0 = (base + 64 * wave_id()) >> 5;
-    if (lane_id() == 0 && w0 < words) bits[w0] = (uint32_t)m;
-    if (lane_id() == 0 && w0 + 1 < words) bits[w0 + 1] = (uint32_t)(m >> 32);
+// Index of the need-th (1-based, in index order) element with keyfn(W[i]) == key.
+// Slices are counted per thread; wave 0 then walks the owning slice together.
+template <class KeyFn>
+__device__ int64_t nth_equal_index(const double* W, int64_t V, uint64_t key, long long need, KeyFn keyfn,
+                                   GenShared& sh) {
+  if (need <= 0) return -1;
+  int64_t lo, hi;
+  thread_slice(V, lo, hi);
+  long long cnt = 0;
+  slice_pass<double>(lo, hi, [&](int64_t i) { return W[i]; }, [&](int64_t, double x) { cnt += keyfn(x) == key; });
+  if (threadIdx.x == 0) {
+    sh.bc[0] = -1;
+    sh.bc[2] = -1;
   }
+  long long total;
+  const long long base = block_exclusive_scan_i64(cnt, sh.b, total);
+  if (base < need && need <= base + cnt) {
+    sh.bc[0] = threadIdx.x;
+    sh.bc[1] = need - base;
+  }
+  __syncthreads();
+  if (wave_id() == 0 && sh.bc[0] >= 0) {
+    const int l = lane_id();
+    long long left = sh.bc[1];
+    int64_t olo, ohi;
+    slice_of(sh.bc[0], V, olo, ohi);
+    for (int64_t s = olo; s < ohi; s += 128) {
+      const int64_t e0 = s + 2 * l, e1 = e0 + 1;
+      const bool m0 = e0 < ohi && keyfn(W[e0]) == key;
+      const bool m1 = e1 < ohi && keyfn(W[e1]) == key;
+      const uint32_t c = (uint32_t)m0 + (uint32_t)m1;
+      const uint32_t incl = wave_scan_dpp(c);
+      const uint32_t excl = incl - c;
+      const bool hit = (long long)excl < left && left <= (long long)incl;
+      const unsigned long long hb = __ballot(hit);
+      if (hb) {
+        if (hit) sh.bc[2] = (m0 && (long long)excl + 1 == left) ? e0 : e1;
+        break;
+      }
+      left -= (long long)lane_value(incl, 63);
+    }
+  }
+  __syncthreads();
+  const int64_t r = sh.bc[2];
+  __syncthreads();
+  return r;
 }
 
+// Wave 0 of the workgroup finishes a CDF search inside one contiguous slice
+// [lo, hi): the first element whose running sum (from `base`) exceeds thr.
+// Two elements per lane, one wave scan per 128 elements.  `margin` is set
+// when the decision sits within tol of a boundary, or when rounding left no
+// crossing inside the slice (the last positive element is taken).
+template <class WF>
+__device__ void wave_slice_cdf(WF wf, int64_t lo, int64_t hi, double base, double thr, double tol, int64_t& tok,
+                               int& margin) {
+  const int l = lane_id();
+  double c = base;
+  int64_t last = -1;
+  for (int64_t s = lo; s < hi; s += 128) {
+    const int64_t e0 = s + 2 * l, e1 = e0 + 1;
+    const double w0 = e0 < hi ? wf(e0) : 0.0, w1 = e1 < hi ? wf(e1) : 0.0;
+    const double pr = w0 + w1;
+    const double incl = wave_scan_dpp(pr);
+    double excl = __shfl_up(incl, 1);
+    if (l == 0) excl = 0.0;
+    const double b0 = c + excl;  // running sum before e0
+    const double c0 = b0 + w0;
+    const double c1 = c0 + w1;
+    const bool x0 = w0 > 0.0 && c0 > thr, x1 = w1 > 0.0 && c1 > thr;
+    const unsigned long long cross = __ballot(x0 || x1);
+    if (cross) {
+      const int f = __ffsll((long long)cross) - 1;
+      const int64_t t = x0 ? e0 : e1;
+      const double cv = x0 ? c0 : c1;
+      const double before = x0 ? b0 : (w0 > 0.0 ? c0 : b0);
+      const int m = (cv - thr <= tol || (before > 0.0 && thr - before <= tol)) ? 1 : 0;
+      tok = (int64_t)__shfl((long long)t, f);
+      margin = __shfl(m, f);
+      return;
+    }
+    const unsigned long long pb = __ballot(w0 > 0.0 || w1 > 0.0);
+    if (pb) {
+      const int g = 63 - __clzll((long long)pb);
+      last = (int64_t)__shfl((long long)(w1 > 0.0 ? e1 : e0), g);
+    }
+    c = c + lane_value(incl, 63);
+  }
+  tok = last;
+  margin = 1;
+}
+
+// categorical's CDF search (sampling.py:126-128) over weights wf(i) >= 0: the
+// first index whose running sum exceeds u times the total, in index order.
+// Per-thread contiguous slices are summed, scanned across the workgroup, and
+// wave 0 walks the slice that holds the crossing.
+template <class WF>
+__device__ int64_t cdf_search_fn(int64_t V, WF wf, double u, long long npos, GenShared& sh, unsigned& flags) {
+  int64_t lo, hi;
+  thread_slice(V, lo, hi);
+  double part = 0.0;
+  slice_pass<double>(lo, hi, wf, [&](int64_t, double w) { part += w; });
+  double total;
+  const double base = block_exclusive_scan_f64(part, sh.b, total);
+  const double thr = u * total;
+  const long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
+  const long long owner = block_max_i64(cand, sh.b);
+  if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(base);
+  __syncthreads();
+  if (wave_id() == 0 && owner >= 0) {
+    int64_t olo, ohi;
+    slice_of(owner, V, olo, ohi);
+    const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
+    int64_t tok;
+    int margin;
+    wave_slice_cdf(wf, olo, ohi, __longlong_as_double(sh.bc[0]), thr, tol, tok, margin);
+    if (lane_id() == 0) {
+      sh.bc[1] = tok;
+      sh.bc[2] = margin;
+    }
+  }
+  __syncthreads();
+  const int64_t tok = owner >= 0 ? (int64_t)sh.bc[1] : -1;
+  if (owner < 0 || sh.bc[2]) flags |= DSR_FLAG_MARGIN;
+  __syncthreads();
+  return tok;
+}
+
+__device__ int64_t cdf_search(const double* W, int64_t V, double u, long long npos, GenShared& sh, unsigned& flags) {
+  return cdf_search_fn(V, [&](int64_t i) { return W[i]; }, u, npos, sh, flags);
+}
+
+// Row maximum and the first index holding it (each thread visits its indices
+// in increasing order, so a strict comparison keeps the first), plus whether
+// any value is finite.
+struct RowMax {
+  double m = -INFINITY;
+  long long first = LLONG_MAX;
+  int fin = 0;
+  __device__ __forceinline__ void add(int64_t i, double x) {
+    if (x > m) {
+      m = x;
+      first = i;
+    }
+    fin |= isfinite(x) ? 1 : 0;
+  }
+};
+
 // Adjusted logits: float64 copy, penalties, bias, mask (sampling.py:49-81).
-// Returns a status code; on DSR_OK W holds the adjusted logits.
-__device__ int adjust_logits(const RowSpec& r, GenShared& sh) {
+// Returns a status code; on DSR_OK W holds the adjusted logits, M their
+// maximum and `first` the first index holding it.
+__device__ int adjust_logits(const RowSpec& r, GenShared& sh, double& M, long long& first) {
   const int64_t V = r.V;
   double* W = r.W;
   int bad = 0;
-  DSR_FOR_ROW(i, V) {
-    double x = load_logit(r.logits, r.dtype, i);
-    if (x != x || x == INFINITY) bad = 1;
-    if (!allowed_bit(r.allow, i)) x = -INFINITY;  // masking first is equivalent: -inf is a fixed point below
-    W[i] = x;
-  }
+  RowMax st;
+  struct LX {
+    double x;
+    uint32_t w;
+  };
+  row_pass<LX>(
+      V, [&](int64_t i) { return LX{load_logit(r.logits, r.dtype, i), r.allow ? r.allow[i >> 5] : ~0u}; },
+      [&](int64_t i, LX v) {
+        double x = v.x;
+        if (x != x || x == INFINITY) bad = 1;
+        if (!((v.w >> (i & 31)) & 1u)) x = -INFINITY;  // masking first is equivalent: -inf is a fixed point below
+        W[i] = x;
+        st.add(i, x);
+      });
   if (block_or(bad, sh.b)) return DSR_E_LOGITS;
 
   const dsr_policy_t& p = r.pol;
+  const bool touched = r.pen_n > 0 || r.prefix_n > 0 || r.bias_n > 0;
   if (r.pen_n > 0 || r.prefix_n > 0) {
     // Validate the table (sampling.py:55-58,62-65) with the prefix tokens added.
     long long csum = 0;
@@ -273,15 +472,15 @@ __device__ int adjust_logits(const RowSpec& r, GenShared& sh) {
     if (threadIdx.x < r.prefix_n) {
       const int q = threadIdx.x;
       int32_t id = r.prefix[q];
-      bool first = true;
-      for (int j = 0; j < q; ++j) first = first && r.prefix[j] != id;
+      bool first_q = true;
+      for (int j = 0; j < q; ++j) first_q = first_q && r.prefix[j] != id;
       int64_t lo = 0, hi = r.pen_n;
       while (lo < hi) {
         int64_t mid = (lo + hi) >> 1;
         if (r.pen_ids[mid] < id) lo = mid + 1; else hi = mid;
       }
       bool in_table = lo < r.pen_n && r.pen_ids[lo] == id;
-      if (first && !in_table) {
+      if (first_q && !in_table) {
         long long c = 0;
         for (int j = 0; j < r.prefix_n; ++j) c += r.prefix[j] == id;
         double x = W[id];
@@ -303,88 +502,145 @@ __device__ int adjust_logits(const RowSpec& r, GenShared& sh) {
     for (int64_t e = threadIdx.x; e < r.bias_n; e += kThreads) W[r.bias_ids[e]] += r.bias_val[e];
     __syncthreads();
   }
-  int fin = 0;
-  DSR_FOR_ROW(i, V) fin |= isfinite(W[i]) ? 1 : 0;
-  if (!block_or(fin, sh.b)) return DSR_E_MASKED;
+  if (touched) {
+    st = RowMax();
+    row_pass<double>(V, [&](int64_t i) { return W[i]; }, [&](int64_t i, double x) { st.add(i, x); });
+  }
+  if (!block_or(st.fin, sh.b)) return DSR_E_MASKED;
+  M = block_max(st.m, sh.b);
+  first = block_min_i64(st.m == M ? st.first : LLONG_MAX, sh.b);
   return DSR_OK;
 }
 
+// Kept-token bits after top-k (1 = finite after step 9 of sampling.py:89-91).
+// A wave covers 64 consecutive tokens per round, so each ballot is two whole words.
+__device__ void write_kept_bits(const double* W, int64_t V, bool topk, uint64_t kth, int64_t cut, uint32_t* bits,
+                                int64_t words) {
+  for (int64_t base = 0; base < V; base += (int64_t)kUnroll * kThreads) {
+    double z[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads + threadIdx.x;
+      z[u] = i < V ? W[i] : -(double)INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + (int64_t)u * kThreads + threadIdx.x;
+      bool f = z[u] > -(double)INFINITY;
+      if (topk) {
+        const uint64_t key = order_key(z[u]);
+        f = f && (key > kth || (key == kth && i <= cut));
+      }
+      const unsigned long long m = __ballot(f);
+      const int64_t w0 = (base + (int64_t)u * kThreads + 64 * wave_id()) >> 5;
+      if (lane_id() == 0 && w0 < words) bits[w0] = (uint32_t)m;
+      if (lane_id() == 0 && w0 + 1 < words) bits[w0 + 1] = (uint32_t)(m >> 32);
+    }
+  }
+}
+
+struct DistOut {
+  int64_t onehot;   // greedy argmax, or -1
+  long long npos;   // positive entries of the final distribution
+  long long first;  // first positive index
+};
+
 // Full distribution (sampling.py:48-106).  On DSR_OK, W holds the final
-// probabilities; `onehot` is the greedy argmax (or -1).
-__device__ int general_distribution(const RowSpec& r, GenShared& sh, unsigned& flags, int64_t& onehot) {
-  onehot = -1;
+// probabilities (also written to the optional outputs).
+__device__ __forceinline__ int general_distribution(const RowSpec& r, GenShared& sh, unsigned& flags, DistOut& out) {
+  out.onehot = -1;
+  out.npos = 0;
+  out.first = -1;
   if (!policy_ok(r.pol)) return DSR_E_POLICY;
-  int st = adjust_logits(r, sh);
+  double M;
+  long long amax;
+  int st = adjust_logits(r, sh, M, amax);
   if (st != DSR_OK) return st;
   const int64_t V = r.V;
   double* W = r.W;
   const dsr_policy_t& p = r.pol;
-
-  double m = -INFINITY;
-  DSR_FOR_ROW(i, V) m = W[i] > m ? W[i] : m;
-  const double M = block_max(m, sh.b);
+  auto ldW = [&](int64_t i) { return W[i]; };
 
   if (p.temperature == 0.0) {  // sampling.py:82-85: first index of the maximum
-    long long first = LLONG_MAX;
-    DSR_FOR_ROW(i, V) if (W[i] == M && i < first) first = i;
-    onehot = block_min_i64(first, sh.b);
-    DSR_FOR_ROW(i, V) W[i] = i == onehot ? 1.0 : 0.0;
+    out.onehot = amax;
+    out.npos = 1;
+    out.first = amax;
+    row_pass<int>(
+        V, [&](int64_t) { return 0; },
+        [&](int64_t i, int) {
+          const double x = i == amax ? 1.0 : 0.0;
+          W[i] = x;
+          if (r.probs_f32) r.probs_f32[i] = (float)x;
+          if (r.probs_f64) r.probs_f64[i] = x;
+        });
     if (r.kept_bits) {
       // A greedy row keeps the argmax alone.
       for (int64_t w = threadIdx.x; w < r.kept_words; w += kThreads) r.kept_bits[w] = 0;
       __syncthreads();
-      if (threadIdx.x == 0) r.kept_bits[onehot >> 5] = 1u << (onehot & 31);
+      if (threadIdx.x == 0) r.kept_bits[amax >> 5] = 1u << (amax & 31);
     }
     __syncthreads();
     return DSR_OK;
   }
   if (M == INFINITY) return DSR_E_NO_MASS;  // inf - inf: the reference's sum turns NaN
 
-  DSR_FOR_ROW(i, V) W[i] = (W[i] - M) / p.temperature;  // sampling.py:86-88, true division
+  const double T = p.temperature;
+  row_pass<double>(V, ldW, [&](int64_t i, double x) { W[i] = (x - M) / T; });  // sampling.py:86-88, true division
   __syncthreads();
 
-  if (p.top_k > 0 && p.top_k < V) {  // sampling.py:89-91
-    uint64_t kth;
+  const bool topk = p.top_k > 0 && p.top_k < V;  // sampling.py:89-91
+  uint64_t kth = 0;
+  int64_t cut = -1;
+  if (topk) {
     long long need;
     radix_kth_largest(W, V, p.top_k, sh, kth, need);
-    int64_t cut = nth_equal_index(W, V, kth, need, [](double x) { return order_key(x); }, sh);
-    DSR_FOR_ROW(i, V) {
-      uint64_t key = order_key(W[i]);
-      if (key < kth || (key == kth && i > cut)) W[i] = -INFINITY;
-    }
-    __syncthreads();
+    cut = nth_equal_index(W, V, kth, need, [](double x) { return order_key(x); }, sh);
   }
-  if (r.kept_bits) write_finite_bits(W, V, r.kept_bits, r.kept_words);
+  if (r.kept_bits) write_kept_bits(W, V, topk, kth, cut, r.kept_bits, r.kept_words);
 
-  double acc = 0.0;  // sampling.py:92-93
-  DSR_FOR_ROW(i, V) {
-    double e = exp(W[i]);
+  double acc = 0.0;  // sampling.py:92-93; removed tokens are exp(-inf) = 0
+  row_pass<double>(V, ldW, [&](int64_t i, double z) {
+    bool keep = z > -(double)INFINITY;
+    if (topk) {
+      const uint64_t key = order_key(z);
+      keep = keep && (key > kth || (key == kth && i <= cut));
+    }
+    double e = 0.0;
+    if (keep) e = exp(z);
     W[i] = e;
     acc += e;
-  }
+  });
   const double s1 = block_sum(acc, sh.b);
-  DSR_FOR_ROW(i, V) W[i] = W[i] / s1;
-  __syncthreads();
 
+  double cur = 0.0;  // sum of what the last pass wrote
   if (p.min_p != 0.0) {  // sampling.py:94-96
-    double rm = -INFINITY;
-    DSR_FOR_ROW(i, V) rm = W[i] > rm ? W[i] : rm;
-    const double cut = p.min_p * block_max(rm, sh.b);
-    const double tol = cut * 0x1p-49;
+    // max(r) = 1 / s1: the maximum's exp is exactly 1 and division is monotone.
+    const double cut_p = p.min_p * (1.0 / s1);
+    const double tol = cut_p * 0x1p-49;
     int close = 0;
     double acc2 = 0.0;
-    DSR_FOR_ROW(i, V) {
-      double x = W[i];
-      if (x > 0.0 && fabs(x - cut) <= tol) close = 1;
-      if (x < cut) x = 0.0;
+    row_pass<double>(V, ldW, [&](int64_t i, double e) {
+      double x = e / s1;
+      if (x > 0.0 && fabs(x - cut_p) <= tol) close = 1;
+      if (x < cut_p) x = 0.0;
       W[i] = x;
       acc2 += x;
-    }
+    });
     if (block_or(close, sh.b)) flags |= DSR_FLAG_MARGIN;
     const double s2 = block_sum(acc2, sh.b);
-    DSR_FOR_ROW(i, V) W[i] = W[i] / s2;
-    __syncthreads();
+    row_pass<double>(V, ldW, [&](int64_t i, double x) {
+      x = x / s2;
+      W[i] = x;
+      cur += x;
+    });
+  } else {
+    row_pass<double>(V, ldW, [&](int64_t i, double e) {
+      const double x = e / s1;
+      W[i] = x;
+      cur += x;
+    });
   }
+  __syncthreads();
 
   if (p.top_p < 1.0) {  // sampling.py:97-102
     uint64_t lbits;
@@ -392,15 +648,11 @@ __device__ int general_distribution(const RowSpec& r, GenShared& sh, unsigned& f
       const double rt = __longlong_as_double((long long)lbits);
       double a = 0.0;
       long long n_above = 0, n_tie = 0;
-      DSR_FOR_ROW(i, V) {
-        double x = W[i];
-        if (x > rt) {
-          a += x;
-          ++n_above;
-        } else if (x == rt) {
-          ++n_tie;
-        }
-      }
+      row_pass<double>(V, ldW, [&](int64_t, double x) {
+        a += x > rt ? x : 0.0;
+        n_above += x > rt ? 1 : 0;
+        n_tie += x == rt ? 1 : 0;
+      });
       const double A = block_sum(a, sh.b);
       n_above = block_sum_i64(n_above, sh.b);
       n_tie = block_sum_i64(n_tie, sh.b);
@@ -422,86 +674,50 @@ __device__ int general_distribution(const RowSpec& r, GenShared& sh, unsigned& f
       if (keep == 0 && n_above > 0) close = true;                          // crossing above this group
       if (keep == n_tie && A + (double)n_tie * rt < p.top_p) close = true;  // crossing below it
       if (close) flags |= DSR_FLAG_MARGIN;
-      const uint64_t tkey = lbits;
-      int64_t cut = nth_equal_index(W, V, tkey, keep, [](double x) { return raw_bits(x); }, sh);
-      DSR_FOR_ROW(i, V) {
-        double x = W[i];
-        if (x < rt || (x == rt && i > cut)) W[i] = 0.0;
-      }
+      const int64_t cutp = nth_equal_index(W, V, lbits, keep, [](double x) { return raw_bits(x); }, sh);
+      cur = 0.0;
+      row_pass<double>(V, ldW, [&](int64_t i, double x) {
+        if (x < rt || (x == rt && i > cutp)) {
+          x = 0.0;
+          W[i] = 0.0;
+        }
+        cur += x;
+      });
       __syncthreads();
     } else {
       // The whole mass stays below top_p: nothing is removed.
-      double tot = 0.0;
-      DSR_FOR_ROW(i, V) tot += W[i];
-      tot = block_sum(tot, sh.b);
+      const double tot = block_sum(cur, sh.b);
       if (fabs(tot - p.top_p) <= ((double)V + 16.0) * 0x1p-51) flags |= DSR_FLAG_MARGIN;
     }
   }
 
-  double acc3 = 0.0;  // sampling.py:103-106
-  DSR_FOR_ROW(i, V) acc3 += W[i];
-  const double total = block_sum(acc3, sh.b);
+  const double total = block_sum(cur, sh.b);  // sampling.py:103-106
   if (!(total > 0.0) || !isfinite(total)) return DSR_E_NO_MASS;
-  DSR_FOR_ROW(i, V) W[i] = W[i] / total;
-  __syncthreads();
+  long long npos = 0, fpos = LLONG_MAX;
+  row_pass<double>(V, ldW, [&](int64_t i, double x) {
+    x = x / total;
+    W[i] = x;
+    if (r.probs_f32) r.probs_f32[i] = (float)x;
+    if (r.probs_f64) r.probs_f64[i] = x;
+    if (x > 0.0) {
+      ++npos;
+      if (i < fpos) fpos = i;
+    }
+  });
+  out.npos = block_sum_i64(npos, sh.b);
+  out.first = block_min_i64(fpos, sh.b);
   return DSR_OK;
-}
-
-// categorical's CDF search (sampling.py:126-128): the first index whose
-// running sum exceeds u times the total, in index order.
-__device__ int64_t cdf_search(const double* W, int64_t V, double u, long long npos, GenShared& sh,
-                              unsigned& flags) {
-  int64_t lo, hi;
-  thread_slice(V, lo, hi);
-  double part = 0.0;
-  for (int64_t i = lo; i < hi; ++i) part += W[i];
-  double total;
-  const double base = block_exclusive_scan_f64(part, sh.b, total);
-  const double thr = u * total;
-  long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
-  const long long owner = block_max_i64(cand, sh.b);
-  if ((long long)threadIdx.x == owner) {
-    double c = base, before = base;
-    int64_t tok = -1, last = -1;
-    for (int64_t i = lo; i < hi; ++i) {
-      double w = W[i];
-      if (w > 0.0) {
-        before = c;
-        c += w;
-        last = i;
-        if (c > thr) {
-          tok = i;
-          break;
-        }
-      }
-    }
-    const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
-    int margin = 0;
-    if (tok < 0) {
-      tok = last;
-      margin = 1;
-    } else if (c - thr <= tol || (before > 0.0 && thr - before <= tol)) {
-      margin = 1;
-    }
-    sh.b.bcast_i[0] = tok;
-    sh.b.bcast_i[1] = margin;
-  }
-  __syncthreads();
-  const int64_t tok = sh.b.bcast_i[0];
-  if (sh.b.bcast_i[1]) flags |= DSR_FLAG_MARGIN;
-  __syncthreads();
-  return tok;
 }
 
 // Number of positive entries and the first positive index.
 __device__ void positive_support(const double* W, int64_t V, GenShared& sh, long long& npos, long long& first) {
   long long n = 0, f = LLONG_MAX;
-  DSR_FOR_ROW(i, V) {
-    if (W[i] > 0.0) {
+  row_pass<double>(V, [&](int64_t i) { return W[i]; }, [&](int64_t i, double x) {
+    if (x > 0.0) {
       ++n;
       if (i < f) f = i;
     }
-  }
+  });
   npos = block_sum_i64(n, sh.b);
   first = block_min_i64(f, sh.b);
 }

@@ -23,33 +23,21 @@ __host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(in
 // ---------------------------------------------------------------------------
 // dsr_sample_rows: general path.
 
-__device__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int st, unsigned flags,
-                           GenShared& sh) {
+__device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int st, const DistOut& d,
+                           unsigned flags, GenShared& sh) {
   const int64_t V = a.vocab;
   int64_t token = -1;
   int consumed = 0;
-  if (st == DSR_OK) {
-    if (a.out_probs_f32) {
-      float* o = a.out_probs_f32 + row * a.probs_ld;
-      DSR_FOR_ROW(i, V) o[i] = (float)W[i];
-    }
-    if (a.out_probs_f64) {
-      double* o = a.out_probs_f64 + row * a.probs_ld;
-      DSR_FOR_ROW(i, V) o[i] = W[i];
-    }
-    if (a.uniforms) {
-      long long npos, first;
-      positive_support(W, V, sh, npos, first);
-      if (npos == 1) {
-        token = first;  // sampling.py:120-122: no uniform is drawn
+  if (st == DSR_OK && a.uniforms) {
+    if (d.npos == 1) {
+      token = d.first;  // sampling.py:120-122: no uniform is drawn
+    } else {
+      const double u = a.uniforms[row];
+      if (!(u >= 0.0 && u < 1.0)) {
+        st = DSR_E_UNIFORM;
       } else {
-        const double u = a.uniforms[row];
-        if (!(u >= 0.0 && u < 1.0)) {
-          st = DSR_E_UNIFORM;
-        } else {
-          token = cdf_search(W, V, u, npos, sh, flags);
-          consumed = 1;
-        }
+        token = cdf_search(W, V, u, d.npos, sh, flags);
+        consumed = 1;
       }
     }
   }
@@ -61,7 +49,7 @@ __device__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double
   }
 }
 
-__device__ RowSpec sample_row_spec(const dsr_sample_args_t& a, int64_t row, double* W) {
+__device__ __forceinline__ RowSpec sample_row_spec(const dsr_sample_args_t& a, int64_t row, double* W) {
   RowSpec r;
   r.V = a.vocab;
   r.dtype = a.dtype;
@@ -92,6 +80,8 @@ __device__ RowSpec sample_row_spec(const dsr_sample_args_t& a, int64_t row, doub
   r.W = W;
   r.kept_bits = a.out_kept_bits ? a.out_kept_bits + row * a.kept_ld : nullptr;
   r.kept_words = (a.vocab + 31) >> 5;
+  r.probs_f32 = a.out_probs_f32 ? a.out_probs_f32 + row * a.probs_ld : nullptr;
+  r.probs_f64 = a.out_probs_f64 ? a.out_probs_f64 + row * a.probs_ld : nullptr;
   return r;
 }
 
@@ -101,9 +91,9 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
   RowSpec r = sample_row_spec(a, row, W);
   unsigned flags = DSR_FLAG_GENERAL;
-  int64_t onehot;
-  int st = general_distribution(r, sh, flags, onehot);
-  finish_row(a, row, W, st, flags, sh);
+  DistOut d;
+  int st = general_distribution(r, sh, flags, d);
+  finish_row(a, row, W, st, d, flags, sh);
 }
 
 // Fast path for bf16 rows; rows it does not take are redone by the general
@@ -118,9 +108,9 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
   RowSpec r = sample_row_spec(a, row, W);
   unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
-  int64_t onehot;
-  int st = general_distribution(r, gs, flags, onehot);
-  finish_row(a, row, W, st, flags, gs);
+  DistOut d;
+  int st = general_distribution(r, gs, flags, d);
+  finish_row(a, row, W, st, d, flags, gs);
 }
 
 // ---------------------------------------------------------------------------
@@ -178,31 +168,39 @@ __global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, 
   r.W = L.W + (row * L.slots + slot) * L.stride;
   r.kept_bits = nullptr;
   r.kept_words = 0;
+  r.probs_f32 = nullptr;
+  r.probs_f64 = nullptr;
   unsigned flags = 0;
-  int64_t onehot;
-  int st = general_distribution(r, sh, flags, onehot);
+  DistOut d;
+  int st = general_distribution(r, sh, flags, d);
   if (threadIdx.x == 0) {
     int32_t* info = L.info + (row * L.slots + slot) * 4;
     info[0] = st;
-    info[1] = (int32_t)onehot;
+    info[1] = (int32_t)d.onehot;
     info[2] = (int32_t)flags;
   }
 }
 
 // Categorical draw over max(p - q, 0) / sum (correction_distribution,
 // sampling.py:131-139, then categorical :118-128); q == nullptr draws from p.
+struct ProbPair {
+  double p, q;
+};
+
 __device__ int draw_from(const double* P, const double* Q, int64_t V, double u, GenShared& sh, int64_t& token,
                          int& used, unsigned& flags) {
   double acc = 0.0;
   long long n = 0, f = LLONG_MAX;
-  DSR_FOR_ROW(i, V) {
-    double x = Q ? fmax(P[i] - Q[i], 0.0) : P[i];
-    acc += x;
-    if (x > 0.0) {
-      ++n;
-      if (i < f) f = i;
-    }
-  }
+  row_pass<ProbPair>(
+      V, [&](int64_t i) { return ProbPair{P[i], Q ? Q[i] : 0.0}; },
+      [&](int64_t i, ProbPair v) {
+        const double x = Q ? fmax(v.p - v.q, 0.0) : v.p;
+        acc += x;
+        if (x > 0.0) {
+          ++n;
+          if (i < f) f = i;
+        }
+      });
   const double total = block_sum(acc, sh.b);
   n = block_sum_i64(n, sh.b);
   f = block_min_i64(f, sh.b);
@@ -215,45 +213,10 @@ __device__ int draw_from(const double* P, const double* Q, int64_t V, double u, 
   if (!(u >= 0.0 && u < 1.0)) return DSR_E_UNIFORM;
   used = 1;
   // CDF of the normalised residual, computed on the fly in index order.
-  int64_t lo, hi;
-  thread_slice(V, lo, hi);
-  double part = 0.0;
-  for (int64_t i = lo; i < hi; ++i) part += Q ? fmax(P[i] - Q[i], 0.0) / total : P[i];
-  double ctot;
-  const double base = block_exclusive_scan_f64(part, sh.b, ctot);
-  const double thr = u * ctot;
-  long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
-  const long long owner = block_max_i64(cand, sh.b);
-  if ((long long)threadIdx.x == owner) {
-    double c = base, before = base;
-    int64_t tok = -1, last = -1;
-    for (int64_t i = lo; i < hi; ++i) {
-      double w = Q ? fmax(P[i] - Q[i], 0.0) / total : P[i];
-      if (w > 0.0) {
-        before = c;
-        c += w;
-        last = i;
-        if (c > thr) {
-          tok = i;
-          break;
-        }
-      }
-    }
-    const double tol = ((double)n + 16.0) * 0x1p-51 * ctot;
-    int margin = 0;
-    if (tok < 0) {
-      tok = last;
-      margin = 1;
-    } else if (c - thr <= tol || (before > 0.0 && thr - before <= tol)) {
-      margin = 1;
-    }
-    sh.b.bcast_i[0] = tok;
-    sh.b.bcast_i[1] = margin;
-  }
-  __syncthreads();
-  token = sh.b.bcast_i[0];
-  if (sh.b.bcast_i[1]) flags |= DSR_FLAG_MARGIN;
-  __syncthreads();
+  if (Q)
+    token = cdf_search_fn(V, [&](int64_t i) { return fmax(P[i] - Q[i], 0.0) / total; }, u, n, sh, flags);
+  else
+    token = cdf_search_fn(V, [&](int64_t i) { return P[i]; }, u, n, sh, flags);
   return DSR_OK;
 }
 
@@ -401,27 +364,25 @@ __global__ __launch_bounds__(kThreads) void k_verify_decide(dsr_verify_args_t a,
 __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_t n, double* out_sum,
                                                          int32_t* out) {
   __shared__ GenShared sh;
-  double acc = 0.0, mx = -INFINITY;
+  double acc = 0.0;
   int bad = 0;
   long long npos = 0, first = LLONG_MAX;
-  DSR_FOR_ROW(i, n) {
-    double x = p[i];
+  RowMax mx;
+  row_pass<double>(n, [&](int64_t i) { return p[i]; }, [&](int64_t i, double x) {
     if (!isfinite(x) || x < 0.0) bad = 1;
     acc += x;
     if (x > 0.0) {
       ++npos;
       if (i < first) first = i;
     }
-    mx = x > mx ? x : mx;
-  }
+    mx.add(i, x);
+  });
   const double s = block_sum(acc, sh.b);
   bad = block_or(bad, sh.b);
   npos = block_sum_i64(npos, sh.b);
   first = block_min_i64(first, sh.b);
-  const double M = block_max(mx, sh.b);
-  long long am = LLONG_MAX;
-  DSR_FOR_ROW(i, n) if (p[i] == M && i < am) am = i;
-  am = block_min_i64(am, sh.b);
+  const double M = block_max(mx.m, sh.b);
+  const long long am = block_min_i64(mx.m == M ? mx.first : LLONG_MAX, sh.b);
   if (threadIdx.x == 0) {
     out_sum[0] = s;
     out[0] = bad ? 0 : 1;
@@ -447,14 +408,14 @@ __global__ __launch_bounds__(kThreads) void k_prob_correction(const double* p, c
                                                               double* out, int32_t* st) {
   __shared__ GenShared sh;
   double acc = 0.0;
-  DSR_FOR_ROW(i, n) {
-    double r = fmax(p[i] - q[i], 0.0);
+  row_pass<ProbPair>(n, [&](int64_t i) { return ProbPair{p[i], q[i]}; }, [&](int64_t i, ProbPair v) {
+    const double r = fmax(v.p - v.q, 0.0);
     out[i] = r;
     acc += r;
-  }
+  });
   const double total = block_sum(acc, sh.b);
   const bool ok = total > 0.0 && isfinite(total);
-  if (ok) DSR_FOR_ROW(i, n) out[i] = out[i] / total;
+  if (ok) row_pass<double>(n, [&](int64_t i) { return out[i]; }, [&](int64_t i, double x) { out[i] = x / total; });
   if (threadIdx.x == 0) st[0] = ok ? DSR_OK : DSR_E_CORRECTION;
 }
 
