@@ -161,6 +161,36 @@ __device__ __forceinline__ double load_logit(const void* base, int dtype, int64_
   return ((const double*)base)[off];
 }
 
+// exp(z) for float64 z <= 0 by Tang's table-driven method (P. T. P. Tang,
+// "Table-driven implementation of the exponential function in IEEE
+// floating-point arithmetic", ACM TOMS 15(2), 1989): z = (64m + j) ln2/64 + r
+// with |r| <= ln2/128 (Cody-Waite reduction, ln2/64 split so that k * hi is
+// exact), exp(z) = 2^m * 2^(j/64) * p(r), p the degree-5 Taylor polynomial of
+// exp (truncation below 2^-54 relative).  `tab` holds 2^(j/64), j = 0..63
+// (exp_table_init).  Relative error a few ulps; z = -inf gives 0.  Used where
+// a decision is certified with a tolerance far above that, never where the
+// reference's own float64 exp must be mirrored.
+__device__ __forceinline__ void exp_table_init(double* tab) {
+  for (int j = threadIdx.x; j < 64; j += blockDim.x) tab[j] = exp2((double)j / 64.0);
+}
+
+__device__ __forceinline__ double exp_nonpos(double z, const double* tab) {
+  const double kInvL = 92.33248261689366;        // 64 / ln 2
+  const double kLhi = 0x1.62e42ff000000p-7;      // ln 2 / 64, leading 29 bits
+  const double kLlo = -0x1.718432a1b0e26p-41;    // ln 2 / 64 - kLhi
+  z = fmax(z, -746.0);                           // below -745.14 the result underflows to 0
+  const double kd = rint(z * kInvL);
+  const int k = (int)kd;
+  double r = fma(-kd, kLhi, z);
+  r = fma(-kd, kLlo, r);
+  double p = fma(1.0 / 120.0, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  return ldexp(tab[k & 63] * p, k >> 6);
+}
+
 __device__ __forceinline__ bool policy_ok(const dsr_policy_t& p) {
   // Bounds of SamplingPolicy.__post_init__ (sampling.py:38-43); NaN fails every test.
   return p.temperature >= 0.0 && p.temperature <= 100.0 && p.top_p >= 0.0 && p.top_p <= 1.0 &&

@@ -15,10 +15,9 @@
 
 #include "dsr_fast.h"
 #include "dsr_general.h"
+#include "dsr_verify.h"
 
 namespace dsr {
-
-__host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(int64_t)31; }
 
 // ---------------------------------------------------------------------------
 // dsr_sample_rows: general path.
@@ -111,251 +110,6 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   DistOut d;
   int st = general_distribution(r, gs, flags, d);
   finish_row(a, row, W, st, d, flags, gs);
-}
-
-// ---------------------------------------------------------------------------
-// dsr_verify_drafts.
-
-struct VerifyLayout {
-  int64_t slots;   // 2K+1 distributions per request: targets 0..K, drafts K+1..2K
-  int64_t stride;  // doubles per workspace row
-  double* W;       // [rows * slots * stride]
-  int32_t* info;   // [rows * slots * 4]: status, onehot, flags, unused
-};
-
-__device__ __forceinline__ bool in_eos(const dsr_verify_args_t& a, int64_t row, int32_t t) {
-  if (!a.eos_off) return false;
-  for (int64_t e = a.eos_off[row]; e < a.eos_off[row + 1]; ++e)
-    if (a.eos_ids[e] == t) return true;
-  return false;
-}
-
-__global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ GenShared sh;
-  const int64_t row = blockIdx.x / L.slots;
-  const int slot = (int)(blockIdx.x % L.slots);
-  const int K = a.K;
-  const bool is_target = slot <= K;
-  const int j = is_target ? slot : slot - (K + 1);
-  const size_t esz = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
-  RowSpec r;
-  r.V = a.vocab;
-  r.dtype = a.dtype;
-  r.logits = is_target ? (const char*)a.target + ((size_t)row * (K + 1) + j) * (size_t)a.ld * esz
-                       : (const char*)a.draft + ((size_t)row * K + j) * (size_t)a.ld * esz;
-  r.pol = a.policy[row];
-  r.pen_n = 0;
-  r.pen_ids = r.pen_count = r.pen_gen = nullptr;
-  if (a.pen_off) {
-    int64_t o = a.pen_off[row];
-    r.pen_n = a.pen_off[row + 1] - o;
-    r.pen_ids = a.pen_ids + o;
-    r.pen_count = a.pen_count + o;
-    r.pen_gen = a.pen_gen + o;
-  }
-  r.prefix = a.draft_ids + row * K;
-  r.prefix_n = j;
-  r.bias_n = 0;
-  r.bias_ids = nullptr;
-  r.bias_val = nullptr;
-  if (a.bias_off) {
-    int64_t o = a.bias_off[row];
-    r.bias_n = a.bias_off[row + 1] - o;
-    r.bias_ids = a.bias_ids + o;
-    r.bias_val = a.bias_val + o;
-  }
-  r.allow = a.allow_bits ? a.allow_bits + (row * (K + 1) + j) * a.allow_ld : nullptr;
-  r.W = L.W + (row * L.slots + slot) * L.stride;
-  r.kept_bits = nullptr;
-  r.kept_words = 0;
-  r.probs_f32 = nullptr;
-  r.probs_f64 = nullptr;
-  unsigned flags = 0;
-  DistOut d;
-  int st = general_distribution(r, sh, flags, d);
-  if (threadIdx.x == 0) {
-    int32_t* info = L.info + (row * L.slots + slot) * 4;
-    info[0] = st;
-    info[1] = (int32_t)d.onehot;
-    info[2] = (int32_t)flags;
-  }
-}
-
-// Categorical draw over max(p - q, 0) / sum (correction_distribution,
-// sampling.py:131-139, then categorical :118-128); q == nullptr draws from p.
-struct ProbPair {
-  double p, q;
-};
-
-__device__ int draw_from(const double* P, const double* Q, int64_t V, double u, GenShared& sh, int64_t& token,
-                         int& used, unsigned& flags) {
-  double acc = 0.0;
-  long long n = 0, f = LLONG_MAX;
-  row_pass<ProbPair>(
-      V, [&](int64_t i) { return ProbPair{P[i], Q ? Q[i] : 0.0}; },
-      [&](int64_t i, ProbPair v) {
-        const double x = Q ? fmax(v.p - v.q, 0.0) : v.p;
-        acc += x;
-        if (x > 0.0) {
-          ++n;
-          if (i < f) f = i;
-        }
-      });
-  const double total = block_sum(acc, sh.b);
-  n = block_sum_i64(n, sh.b);
-  f = block_min_i64(f, sh.b);
-  if (Q && (!(total > 0.0) || !isfinite(total))) return DSR_E_CORRECTION;
-  used = 0;
-  if (n == 1) {
-    token = f;
-    return DSR_OK;
-  }
-  if (!(u >= 0.0 && u < 1.0)) return DSR_E_UNIFORM;
-  used = 1;
-  // CDF of the normalised residual, computed on the fly in index order.
-  if (Q)
-    token = cdf_search_fn(V, [&](int64_t i) { return fmax(P[i] - Q[i], 0.0) / total; }, u, n, sh, flags);
-  else
-    token = cdf_search_fn(V, [&](int64_t i) { return P[i]; }, u, n, sh, flags);
-  return DSR_OK;
-}
-
-__global__ __launch_bounds__(kThreads) void k_verify_decide(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ GenShared sh;
-  __shared__ int s_status, s_accepted, s_count, s_pending, s_stop, s_ua, s_ut, s_next;
-  __shared__ double s_u;
-  const int64_t row = blockIdx.x;
-  const int K = a.K;
-  const int64_t V = a.vocab;
-  const int32_t* info = L.info + row * L.slots * 4;
-  auto Prow = [&](int slot) { return L.W + (row * L.slots + slot) * L.stride; };
-  const bool greedy = a.policy[row].temperature == 0.0;
-  unsigned flags = 0;
-  int32_t* out_ids = a.out_ids + row * (K + 1);
-  if (threadIdx.x == 0) {
-    for (int j = 0; j <= K; ++j) out_ids[j] = -1;
-    s_status = DSR_OK;
-    s_accepted = 0;
-    s_count = 0;
-    s_pending = -1;
-    s_stop = DSR_STOP_NONE;
-    s_ua = 0;
-    s_ut = 0;
-    s_next = 0;
-    for (int j = 0; j < K; ++j) flags |= (unsigned)info[(K + 1 + j) * 4 + 2] & DSR_FLAG_MARGIN;
-    // Order of the reference's checks (sampling.py:255-272): proposals, the
-    // first target, then token ids.
-    const int limit = a.output_limit[row];
-    if (limit < 1 || limit > DSR_MAX_COUNT) s_status = DSR_E_COUNTS;
-    for (int j = 0; j < K && s_status == DSR_OK; ++j) s_status = info[(K + 1 + j) * 4];
-    if (s_status == DSR_OK) s_status = info[0];
-    if (s_status == DSR_OK) {
-      for (int j = 0; j < K; ++j) {
-        int32_t t = a.draft_ids[row * K + j];
-        if (t < 0 || t >= V) s_status = DSR_E_TOKEN;
-      }
-      if (a.eos_off) {
-        for (int64_t e = a.eos_off[row]; e < a.eos_off[row + 1]; ++e)
-          if (a.eos_ids[e] < 0 || a.eos_ids[e] >= V) s_status = DSR_E_TOKEN;
-      }
-    }
-  }
-  __syncthreads();
-  // Sequential accept chain; thread 0 decides, the block joins for residual draws.
-  for (int j = 0; j < K; ++j) {
-    if (threadIdx.x == 0 && s_status == DSR_OK && s_next == 0) {
-      const int32_t x = a.draft_ids[row * K + j];
-      if (j > 0 && info[j * 4] != DSR_OK) {
-        s_status = info[j * 4];  // the lazily built target j fails only when reached
-      } else {
-        flags |= (unsigned)info[j * 4 + 2] & DSR_FLAG_MARGIN;
-        const double* P = Prow(j);
-        const double* Q = Prow(K + 1 + j);
-        if (!(Q[x] > 0.0)) {
-          s_status = DSR_E_PROPOSAL_ZERO;
-        } else {
-          bool ok;
-          if (greedy) {
-            ok = x == info[j * 4 + 1];
-          } else {
-            const double u = a.u_accept[row * K + j];
-            ++s_ua;
-            if (!(u >= 0.0 && u < 1.0)) {
-              s_status = DSR_E_UNIFORM;
-              ok = false;
-            } else {
-              double ratio = P[x] / Q[x];
-              ratio = ratio < 1.0 ? ratio : 1.0;
-              if (fabs(u - ratio) <= 0x1p-48 * ratio) flags |= DSR_FLAG_MARGIN;
-              ok = u < ratio;
-            }
-          }
-          if (s_status == DSR_OK) {
-            if (!ok) {
-              s_accepted = j;
-              s_next = 1;  // reject: replacement below
-            } else {
-              out_ids[s_count++] = x;
-              if (in_eos(a, row, x) || s_count >= a.output_limit[row]) {
-                s_accepted = j + 1;
-                s_stop = in_eos(a, row, x) ? DSR_STOP_EOS : DSR_STOP_LENGTH;
-                s_next = 3;  // finished inside the drafts: no bonus
-              }
-            }
-          }
-        }
-      }
-      if (s_status == DSR_OK && s_next == 0 && j == K - 1) s_next = 2;  // all accepted: bonus
-    }
-    __syncthreads();
-    if (s_status != DSR_OK || s_next != 0) break;
-  }
-  if (K == 0 && threadIdx.x == 0 && s_status == DSR_OK) s_next = 2;
-  __syncthreads();
-  if (s_status == DSR_OK && (s_next == 1 || s_next == 2)) {
-    const int j = s_next == 1 ? s_accepted : K;
-    if (s_next == 2 && j > 0 && info[j * 4] != DSR_OK) {
-      if (threadIdx.x == 0) s_status = info[j * 4];
-    } else {
-      if (s_next == 2) flags |= (unsigned)info[j * 4 + 2] & DSR_FLAG_MARGIN;
-      int64_t rep = -1;
-      int used = 0;
-      int st = DSR_OK;
-      if (greedy) {
-        rep = info[j * 4 + 1];
-      } else {
-        const double u = a.u_target[row];
-        st = draw_from(Prow(j), s_next == 1 ? Prow(K + 1 + j) : nullptr, V, u, sh, rep, used, flags);
-      }
-      if (threadIdx.x == 0) {
-        if (st != DSR_OK) {
-          s_status = st;
-        } else {
-          s_ut += used;
-          if (s_next == 2) s_accepted = K;
-          const int before = s_count;
-          out_ids[s_count++] = (int32_t)rep;
-          s_pending = (int)rep;
-          s_stop = in_eos(a, row, (int32_t)rep) ? DSR_STOP_EOS
-                   : (before + 1 >= a.output_limit[row] ? DSR_STOP_LENGTH : DSR_STOP_NONE);
-        }
-      }
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const bool ok = s_status == DSR_OK;
-    a.out_status[row] = s_status;
-    a.out_accepted[row] = ok ? s_accepted : 0;
-    a.out_count[row] = ok ? s_count : 0;
-    a.out_pending[row] = ok ? s_pending : -1;
-    a.out_stop[row] = ok ? s_stop : DSR_STOP_NONE;
-    a.out_used_accept[row] = ok ? s_ua : 0;
-    a.out_used_target[row] = ok ? s_ut : 0;
-    if (!ok)
-      for (int j = 0; j <= K; ++j) out_ids[j] = -1;
-    if (a.out_flags) a.out_flags[row] = (uint8_t)flags;
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -468,8 +222,7 @@ size_t dsr_sample_workspace_bytes(int64_t rows, int64_t vocab) {
 
 size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab) {
   if (rows < 0 || vocab < 1 || K < 0) return 0;
-  const size_t slots = (size_t)(2 * K + 1);
-  return (size_t)rows * slots * (size_t)ws_stride(vocab) * sizeof(double) + (size_t)rows * slots * 4 * sizeof(int32_t);
+  return verify_ws_bytes(rows, K, vocab);
 }
 
 static bool dtype_ok(int32_t d) { return d == DSR_BF16 || d == DSR_F32 || d == DSR_F64; }
@@ -512,20 +265,30 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   if (a.eos_off && !a.eos_ids) return DSR_ERR_ARG;
   if (a.allow_bits && a.allow_ld < (a.vocab + 31) / 32) return DSR_ERR_ARG;
   const int64_t slots = 2 * (int64_t)a.K + 1;
-  if ((int64_t)a.rows * slots > INT_MAX) return DSR_ERR_ARG;
+  if ((int64_t)a.rows * slots * kVerifySplit > INT_MAX || (int64_t)a.rows * kDrawSplit > INT_MAX) return DSR_ERR_ARG;
   if (!a.workspace || a.workspace_bytes < dsr_verify_workspace_bytes(a.rows, a.K, a.vocab) ||
       ((uintptr_t)a.workspace & 7u))
     return DSR_ERR_WORKSPACE;
   if (a.rows == 0) return 0;
-  VerifyLayout L;
-  L.slots = slots;
-  L.stride = ws_stride(a.vocab);
-  L.W = (double*)a.workspace;
-  L.info = (int32_t*)(L.W + (size_t)a.rows * slots * L.stride);
+  VerifyLayout L = verify_layout(a.workspace, a.rows, a.K, a.vocab);
+  L.fast_inputs = !a.pen_off && !a.bias_off && !a.allow_bits;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_verify_dists, dim3((unsigned)(a.rows * slots)), dim3(kThreads), 0, s, a, L);
   if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
-  hipLaunchKernelGGL(k_verify_decide, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
+  if (L.fast_inputs) {
+    const dim3 grid((unsigned)(a.rows * slots * kVerifySplit));
+    if (a.dtype == DSR_BF16) hipLaunchKernelGGL(k_verify_stats<DSR_BF16>, grid, dim3(kStatThreads), 0, s, a, L);
+    else if (a.dtype == DSR_F32) hipLaunchKernelGGL(k_verify_stats<DSR_F32>, grid, dim3(kStatThreads), 0, s, a, L);
+    else hipLaunchKernelGGL(k_verify_stats<DSR_F64>, grid, dim3(kStatThreads), 0, s, a, L);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(k_verify_chain, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
+  if (L.fast_inputs) {
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_verify_draw, dim3((unsigned)(a.rows * kDrawSplit)), dim3(kThreads), 0, s, a, L);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
+  }
   return launched();
 }
 

@@ -1,0 +1,788 @@
+// Exact sampled speculative verification (SamplingWork.verify -> verify_drafts,
+// terminal_sampling.py:170-183, sampling.py:247-294), two paths.
+//
+// General path: every conditional distribution (targets 0..K, drafts 0..K-1,
+// row j conditioned on the prefix draft_ids[:j], terminal_sampling.py:234-244)
+// is built in full by general_distribution into a float64 workspace row, one
+// workgroup each; one workgroup per request then runs the sequential accept
+// chain and draws the replacement or bonus token from those rows.
+//
+// Fast path, for requests whose policy has no filter (top_k 0 or >= V,
+// top_p 1, min_p 0) and that carry no history, bias or allow mask: such a
+// distribution is exp((v - M) / T) / s1 followed by a renormalisation that
+// only moves it by rounding, so each row is summarised by its maximum M, the
+// first index holding it and s1 = sum exp((v - M) / T).  Those come out of
+// one pass over the logits (an online maximum / rescaled sum per thread),
+// split over kVerifySplit workgroups per row and combined by whichever of
+// them finishes last.  The accept chain needs p and q only at the draft ids;
+// the one replacement or bonus draw per request is spread over kDrawSplit
+// workgroups (slice sums, then the last one walks the slice that holds the
+// crossing).  Dropping the renormalisation by total ~ 1 (sampling.py:103-106)
+// perturbs each probability by at most a few hundred ulps, so accept tests
+// within 2^-40 relative of the uniform are reported with DSR_FLAG_MARGIN.
+#pragma once
+
+#include "dsr_general.h"
+
+namespace dsr {
+
+constexpr int kStatThreads = 256;   // statistics workgroups: 4 waves, several resident per CU
+constexpr int kStatWaves = kStatThreads / 64;
+constexpr int kStatPer = 16;        // logits per thread of one share
+constexpr int kVerifySplit = 32;    // shares (workgroups) per distribution row
+static_assert((int64_t)kVerifySplit * kStatThreads * kStatPer >= DSR_MAX_VOCAB, "a share must fit in registers");
+constexpr int kDrawSplit = 8;    // workgroups per request (replacement / bonus draw)
+constexpr size_t kDecisionBytes = 64;
+
+struct VerifyStat {  // one distribution row, fast path
+  double M;          // maximum logit
+  double s1;         // sum of exp((v - M) / T)
+  int32_t status;
+  int32_t amax;      // first index of the maximum
+  int32_t pad[2];
+};
+
+struct VerifyPart {  // one workgroup's share of a row
+  double m, s;
+  int32_t amax;
+  int32_t flags;     // 1: NaN / +inf seen, 2: a finite value seen
+  int32_t pad[2];
+};
+
+struct DrawPart {    // one workgroup's share of a draw
+  double sum;
+  long long npos;
+  long long first;
+  long long pad;
+};
+
+struct VerifyLayout {
+  int64_t slots;     // 2K+1 distributions per request: targets 0..K, drafts K+1..2K
+  int64_t stride;    // doubles per workspace row
+  double* W;         // [rows * slots * stride]
+  int32_t* info;     // [rows * slots * 4]: status, onehot, flags, unused
+  VerifyStat* stat;  // [rows * slots]
+  VerifyPart* part;  // [rows * slots * kVerifySplit]
+  DrawPart* dpart;   // [rows * kDrawSplit]
+  struct Decision* dec;  // [rows] chain outcome handed to the draw kernels
+  int64_t rows;
+  int fast_inputs;   // no history, bias or allow mask
+};
+
+__host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(int64_t)31; }
+
+__host__ __device__ inline size_t verify_ws_bytes(int64_t rows, int32_t K, int64_t V) {
+  const size_t slots = (size_t)(2 * K + 1);
+  size_t b = (size_t)rows * slots * (size_t)ws_stride(V) * sizeof(double);
+  b += (size_t)rows * slots * 4 * sizeof(int32_t);
+  b += (size_t)rows * slots * sizeof(VerifyStat);
+  b += (size_t)rows * slots * kVerifySplit * sizeof(VerifyPart);
+  b += (size_t)rows * kDrawSplit * sizeof(DrawPart);
+  b += (size_t)rows * kDecisionBytes;
+  return b;
+}
+
+__host__ inline VerifyLayout verify_layout(void* ws, int64_t rows, int32_t K, int64_t V) {
+  VerifyLayout L;
+  L.slots = 2 * (int64_t)K + 1;
+  L.stride = ws_stride(V);
+  char* p = (char*)ws;
+  L.W = (double*)p;
+  p += (size_t)rows * L.slots * L.stride * sizeof(double);
+  L.info = (int32_t*)p;
+  p += (size_t)rows * L.slots * 4 * sizeof(int32_t);
+  L.stat = (VerifyStat*)p;
+  p += (size_t)rows * L.slots * sizeof(VerifyStat);
+  L.part = (VerifyPart*)p;
+  p += (size_t)rows * L.slots * kVerifySplit * sizeof(VerifyPart);
+  L.dpart = (DrawPart*)p;
+  p += (size_t)rows * kDrawSplit * sizeof(DrawPart);
+  L.dec = (struct Decision*)p;
+  L.rows = rows;
+  L.fast_inputs = 0;
+  return L;
+}
+
+__device__ __forceinline__ size_t dtype_size(int dtype) { return dtype == DSR_BF16 ? 2 : (dtype == DSR_F32 ? 4 : 8); }
+
+// Logits of distribution `slot` of request `row`.
+__device__ __forceinline__ const char* verify_logits(const dsr_verify_args_t& a, int64_t row, int slot) {
+  const int K = a.K;
+  const size_t esz = dtype_size(a.dtype);
+  return slot <= K ? (const char*)a.target + ((size_t)row * (K + 1) + slot) * (size_t)a.ld * esz
+                   : (const char*)a.draft + ((size_t)row * K + (slot - K - 1)) * (size_t)a.ld * esz;
+}
+
+// Whether request `row` takes the fast path (uniform over its workgroups).
+__device__ __forceinline__ bool verify_fast_row(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row) {
+  if (!L.fast_inputs) return false;
+  const dsr_policy_t& p = a.policy[row];
+  return policy_ok(p) && (p.top_k == 0 || p.top_k >= a.vocab) && p.top_p >= 1.0 && p.min_p == 0.0;
+}
+
+// One request's scalar inputs: draft ids, accept uniforms, EOS ids and the
+// output limit, read either from the arguments or from LDS copies.
+struct Request {
+  const int32_t* ids;   // [K]
+  const double* ua;     // [K]
+  const int32_t* eos;   // [n_eos]
+  int n_eos;
+  int limit;
+  __device__ __forceinline__ bool is_eos(int32_t t) const {
+    for (int e = 0; e < n_eos; ++e)
+      if (eos[e] == t) return true;
+    return false;
+  }
+};
+
+__device__ __forceinline__ Request request_of(const dsr_verify_args_t& a, int64_t row) {
+  Request q;
+  q.ids = a.draft_ids + row * a.K;
+  q.ua = a.u_accept + row * a.K;
+  q.eos = a.eos_off ? a.eos_ids + a.eos_off[row] : nullptr;
+  q.n_eos = a.eos_off ? (int)(a.eos_off[row + 1] - a.eos_off[row]) : 0;
+  q.limit = a.output_limit[row];
+  return q;
+}
+
+// ---------------------------------------------------------------------------
+// General path.
+
+__global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x / L.slots;
+  const int slot = (int)(blockIdx.x % L.slots);
+  if (verify_fast_row(a, L, row)) return;
+  const int K = a.K;
+  const bool is_target = slot <= K;
+  const int j = is_target ? slot : slot - (K + 1);
+  RowSpec r;
+  r.V = a.vocab;
+  r.dtype = a.dtype;
+  r.logits = verify_logits(a, row, slot);
+  r.pol = a.policy[row];
+  r.pen_n = 0;
+  r.pen_ids = r.pen_count = r.pen_gen = nullptr;
+  if (a.pen_off) {
+    int64_t o = a.pen_off[row];
+    r.pen_n = a.pen_off[row + 1] - o;
+    r.pen_ids = a.pen_ids + o;
+    r.pen_count = a.pen_count + o;
+    r.pen_gen = a.pen_gen + o;
+  }
+  r.prefix = a.draft_ids + row * K;
+  r.prefix_n = j;
+  r.bias_n = 0;
+  r.bias_ids = nullptr;
+  r.bias_val = nullptr;
+  if (a.bias_off) {
+    int64_t o = a.bias_off[row];
+    r.bias_n = a.bias_off[row + 1] - o;
+    r.bias_ids = a.bias_ids + o;
+    r.bias_val = a.bias_val + o;
+  }
+  r.allow = a.allow_bits ? a.allow_bits + (row * (K + 1) + j) * a.allow_ld : nullptr;
+  r.W = L.W + (row * L.slots + slot) * L.stride;
+  r.kept_bits = nullptr;
+  r.kept_words = 0;
+  r.probs_f32 = nullptr;
+  r.probs_f64 = nullptr;
+  unsigned flags = 0;
+  DistOut d;
+  int st = general_distribution(r, sh, flags, d);
+  if (threadIdx.x == 0) {
+    int32_t* info = L.info + (row * L.slots + slot) * 4;
+    info[0] = st;
+    info[1] = (int32_t)d.onehot;
+    info[2] = (int32_t)flags;
+  }
+}
+
+// Categorical draw over max(p - q, 0) / sum (correction_distribution,
+// sampling.py:131-139, then categorical :118-128); q == nullptr draws from p.
+struct ProbPair {
+  double p, q;
+};
+
+__device__ int draw_from(const double* P, const double* Q, int64_t V, double u, GenShared& sh, int64_t& token,
+                         int& used, unsigned& flags) {
+  double acc = 0.0;
+  long long n = 0, f = LLONG_MAX;
+  row_pass<ProbPair>(
+      V, [&](int64_t i) { return ProbPair{P[i], Q ? Q[i] : 0.0}; },
+      [&](int64_t i, ProbPair v) {
+        const double x = Q ? fmax(v.p - v.q, 0.0) : v.p;
+        acc += x;
+        if (x > 0.0) {
+          ++n;
+          if (i < f) f = i;
+        }
+      });
+  const double total = block_sum(acc, sh.b);
+  n = block_sum_i64(n, sh.b);
+  f = block_min_i64(f, sh.b);
+  if (Q && (!(total > 0.0) || !isfinite(total))) return DSR_E_CORRECTION;
+  used = 0;
+  if (n == 1) {
+    token = f;
+    return DSR_OK;
+  }
+  if (!(u >= 0.0 && u < 1.0)) return DSR_E_UNIFORM;
+  used = 1;
+  // CDF of the normalised residual, computed on the fly in index order.
+  if (Q)
+    token = cdf_search_fn(V, [&](int64_t i) { return fmax(P[i] - Q[i], 0.0) / total; }, u, n, sh, flags);
+  else
+    token = cdf_search_fn(V, [&](int64_t i) { return P[i]; }, u, n, sh, flags);
+  return DSR_OK;
+}
+
+// The request's decision, shared by the workgroups that produce it.
+struct Decision {
+  int status, accepted, count, pending, stop, ua, ut, next;
+  int draw_j;         // position of the replacement / bonus draw
+  unsigned flags;
+  int ids[DSR_MAX_DRAFTS + 1];
+};
+static_assert(sizeof(Decision) == kDecisionBytes, "workspace slot of a decision");
+
+__device__ void write_decision(const dsr_verify_args_t& a, int64_t row, const Decision& d) {
+  const int K = a.K;
+  int32_t* out_ids = a.out_ids + row * (K + 1);
+  const bool ok = d.status == DSR_OK;
+  for (int j = 0; j <= K; ++j) out_ids[j] = ok && j < d.count ? d.ids[j] : -1;
+  a.out_status[row] = d.status;
+  a.out_accepted[row] = ok ? d.accepted : 0;
+  a.out_count[row] = ok ? d.count : 0;
+  a.out_pending[row] = ok ? d.pending : -1;
+  a.out_stop[row] = ok ? d.stop : DSR_STOP_NONE;
+  a.out_used_accept[row] = ok ? d.ua : 0;
+  a.out_used_target[row] = ok ? d.ut : 0;
+  if (a.out_flags) a.out_flags[row] = (uint8_t)d.flags;
+}
+
+// Checks made before the chain, in the reference's order (sampling.py:255-272):
+// the output limit, every proposal, the first target, then token ids.
+// status_of(slot) gives a distribution's status.
+template <class StatusOf>
+__device__ void verify_precheck(const dsr_verify_args_t& a, const Request& rq, StatusOf status_of, Decision& d) {
+  const int K = a.K;
+  const int64_t V = a.vocab;
+  d.status = DSR_OK;
+  d.accepted = 0;
+  d.count = 0;
+  d.pending = -1;
+  d.stop = DSR_STOP_NONE;
+  d.ua = 0;
+  d.ut = 0;
+  d.next = 0;
+  d.draw_j = -1;
+  d.flags = 0;
+  if (rq.limit < 1 || rq.limit > DSR_MAX_COUNT) d.status = DSR_E_COUNTS;
+  for (int j = 0; j < K && d.status == DSR_OK; ++j) d.status = status_of(K + 1 + j);
+  if (d.status == DSR_OK) d.status = status_of(0);
+  if (d.status == DSR_OK) {
+    for (int j = 0; j < K; ++j) {
+      const int32_t t = rq.ids[j];
+      if (t < 0 || t >= V) d.status = DSR_E_TOKEN;
+    }
+    for (int e = 0; e < rq.n_eos; ++e)
+      if (rq.eos[e] < 0 || rq.eos[e] >= V) d.status = DSR_E_TOKEN;
+  }
+}
+
+// The sequential accept chain (sampling.py:273-294), run by one thread.
+// prob(slot, j) gives distribution `slot`'s probability at draft id j,
+// onehot(slot) its greedy argmax, and reach(j) is called as target j is
+// reached.  On return d.next is 0 (decided), 1 (replacement draw at
+// d.draw_j) or 2 (bonus draw at d.draw_j = K).
+template <class StatusOf, class Prob, class Onehot, class Reach>
+__device__ void verify_chain(const dsr_verify_args_t& a, const Request& rq, bool greedy, double margin_rel,
+                             StatusOf status_of, Prob prob, Onehot onehot, Reach reach, Decision& d) {
+  const int K = a.K;
+  for (int j = 0; j < K && d.status == DSR_OK; ++j) {
+    if (j > 0 && status_of(j) != DSR_OK) {
+      d.status = status_of(j);  // the lazily built target j fails only when reached
+      break;
+    }
+    reach(j);
+    const int32_t x = rq.ids[j];
+    const double q = prob(K + 1 + j, j);
+    if (!(q > 0.0)) {
+      d.status = DSR_E_PROPOSAL_ZERO;
+      break;
+    }
+    bool ok;
+    if (greedy) {
+      ok = x == onehot(j);
+    } else {
+      const double u = rq.ua[j];
+      ++d.ua;
+      if (!(u >= 0.0 && u < 1.0)) {
+        d.status = DSR_E_UNIFORM;
+        break;
+      }
+      double ratio = prob(j, j) / q;
+      ratio = ratio < 1.0 ? ratio : 1.0;
+      if (fabs(u - ratio) <= margin_rel * ratio) d.flags |= DSR_FLAG_MARGIN;
+      ok = u < ratio;
+    }
+    if (!ok) {
+      d.accepted = j;
+      d.next = 1;
+      d.draw_j = j;
+      return;
+    }
+    d.ids[d.count++] = x;
+    if (rq.is_eos(x) || d.count >= rq.limit) {
+      d.accepted = j + 1;
+      d.stop = rq.is_eos(x) ? DSR_STOP_EOS : DSR_STOP_LENGTH;
+      return;  // finished inside the drafts: no bonus
+    }
+  }
+  if (d.status != DSR_OK) return;
+  if (K > 0 && status_of(K) != DSR_OK) {
+    d.status = status_of(K);
+    return;
+  }
+  reach(K);
+  d.next = 2;
+  d.draw_j = K;
+}
+
+// Appends the replacement / bonus token `rep` and its stop reason.
+__device__ __forceinline__ void verify_append(const dsr_verify_args_t& a, const Request& rq, Decision& d, int64_t rep,
+                                              int used) {
+  d.ut += used;
+  if (d.next == 2) d.accepted = a.K;
+  const int before = d.count;
+  d.ids[d.count++] = (int)rep;
+  d.pending = (int)rep;
+  d.stop = rq.is_eos((int32_t)rep) ? DSR_STOP_EOS : (before + 1 >= rq.limit ? DSR_STOP_LENGTH : DSR_STOP_NONE);
+}
+
+__device__ void general_decide(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row, GenShared& sh,
+                               Decision& d) {
+  const int K = a.K;
+  const int32_t* info = L.info + row * L.slots * 4;
+  auto Prow = [&](int slot) { return L.W + (row * L.slots + slot) * L.stride; };
+  auto status_of = [&](int slot) { return (int)info[slot * 4]; };
+  const bool greedy = a.policy[row].temperature == 0.0;
+  const Request rq = request_of(a, row);
+  if (threadIdx.x == 0) {
+    verify_precheck(a, rq, status_of, d);
+    for (int j = 0; j < K; ++j) d.flags |= (unsigned)info[(K + 1 + j) * 4 + 2] & DSR_FLAG_MARGIN;
+    if (d.status == DSR_OK)
+      verify_chain(
+          a, rq, greedy, 0x1p-48, status_of, [&](int slot, int j) { return Prow(slot)[rq.ids[j]]; },
+          [&](int j) { return (int64_t)info[j * 4 + 1]; },
+          [&](int j) { d.flags |= (unsigned)info[j * 4 + 2] & DSR_FLAG_MARGIN; }, d);
+  }
+  __syncthreads();
+  if (d.status == DSR_OK && d.next != 0) {
+    const int j = d.draw_j;
+    int64_t rep = -1;
+    int used = 0;
+    int st = DSR_OK;
+    unsigned flags = 0;
+    if (greedy) {
+      rep = info[j * 4 + 1];
+    } else {
+      st = draw_from(Prow(j), d.next == 1 ? Prow(K + 1 + j) : nullptr, a.vocab, a.u_target[row], sh, rep, used, flags);
+    }
+    if (threadIdx.x == 0) {
+      d.flags |= flags;
+      if (st != DSR_OK) d.status = st; else verify_append(a, rq, d, rep, used);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) write_decision(a, row, d);
+}
+
+// ---------------------------------------------------------------------------
+// Fast path.  Kernel boundaries order its steps; no workgroup waits for another.
+
+// bf16 and f32 logits are held as float (exactly), f64 ones as double.
+template <int DT> struct LogitT { using T = float; };
+template <> struct LogitT<DSR_F64> { using T = double; };
+
+template <int DT>
+__device__ __forceinline__ typename LogitT<DT>::T logit_as(const char* base, int64_t i) {
+  if constexpr (DT == DSR_BF16) return __uint_as_float((uint32_t)((const uint16_t*)base)[i] << 16);
+  else if constexpr (DT == DSR_F32) return ((const float*)base)[i];
+  else return ((const double*)base)[i];
+}
+
+// Reduction over the kStatWaves waves of a statistics workgroup: DPP inside
+// each wave, then every lane combines the per-wave partials in wave order.
+// Every call needs its own slot array.
+template <class T, class Op>
+__device__ __forceinline__ T stat_reduce(T x, T* slot, T id, Op op) {
+  x = wave_reduce_dpp(x, op);
+  if (lane_id() == 0) slot[wave_id()] = x;
+  __syncthreads();
+  T y = id;
+#pragma unroll
+  for (int w = 0; w < kStatWaves; ++w) y = op(y, slot[w]);
+  return y;
+}
+
+// Step 1: one share of one row, held in registers: its maximum, the first
+// index holding it, sum exp((v - max) / T) and the NaN/+inf / finite flags.
+template <int DT>
+__global__ __launch_bounds__(kStatThreads) void k_verify_stats(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ double etab[64];
+  __shared__ double sf[2][kStatWaves];
+  __shared__ long long si[2][kStatWaves];
+  __shared__ uint32_t su[kStatWaves];
+  const int64_t rs = blockIdx.x / kVerifySplit;
+  const int g = (int)(blockIdx.x % kVerifySplit);
+  const int64_t row = rs / L.slots;
+  const int slot = (int)(rs % L.slots);
+  if (!verify_fast_row(a, L, row)) return;
+  const double T = a.policy[row].temperature;
+  const bool greedy = T == 0.0;
+  const char* base = verify_logits(a, row, slot);
+  const int64_t V = a.vocab;
+  const int64_t seg = (V + kVerifySplit - 1) / kVerifySplit;
+  const int64_t lo = (int64_t)g * seg < V ? (int64_t)g * seg : V;
+  const int64_t hi = lo + seg < V ? lo + seg : V;
+  using X = typename LogitT<DT>::T;
+  X x[kStatPer];
+#pragma unroll
+  for (int u = 0; u < kStatPer; ++u) {
+    const int64_t i = lo + threadIdx.x + (int64_t)u * kStatThreads;
+    x[u] = i < hi ? logit_as<DT>(base, i) : -(X)INFINITY;
+  }
+  exp_table_init(etab);
+  double m = -INFINITY;
+  long long am = LLONG_MAX;
+  uint32_t fl = 0;  // 1: NaN / +inf, 2: a finite value
+#pragma unroll
+  for (int u = 0; u < kStatPer; ++u) {
+    const double v = (double)x[u];
+    fl |= (v != v || v == INFINITY) ? 1u : 0u;
+    fl |= (v > -(double)INFINITY && v < (double)INFINITY) ? 2u : 0u;
+    if (v > m && v < (double)INFINITY) {  // increasing index order: the first maximum stays
+      m = v;
+      am = lo + threadIdx.x + (int64_t)u * kStatThreads;
+    }
+  }
+  const double Mg = stat_reduce(m, sf[0], -(double)INFINITY, OpMax());
+  const uint32_t flags = stat_reduce(fl, su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
+  const long long amg = stat_reduce(m == Mg && m > -INFINITY ? am : LLONG_MAX, si[0], LLONG_MAX, OpMin());
+  double s = 0.0;
+  if (!greedy && Mg > -INFINITY) {
+    const double iT = 1.0 / T;
+#pragma unroll
+    for (int u = 0; u < kStatPer; ++u) {
+      const double v = (double)x[u];
+      if (v > -(double)INFINITY && v < (double)INFINITY) s += exp_nonpos((v - Mg) * iT, etab);
+    }
+  }
+  const double Sg = stat_reduce(s, sf[1], 0.0, OpSum());
+  if (threadIdx.x == 0) {
+    VerifyPart p;
+    p.m = Mg;
+    p.s = Sg;
+    p.amax = amg == LLONG_MAX ? -1 : (int32_t)amg;
+    p.flags = (int32_t)flags;
+    L.part[rs * kVerifySplit + g] = p;
+  }
+}
+
+// Combines the kVerifySplit shares of one row, in index order; called by
+// every lane of one wave (lane q reads share q), result in every lane.
+__device__ VerifyStat combine_shares(const VerifyPart* parts, double T, const double* etab) {
+  static_assert(kVerifySplit <= 64, "one share per lane");
+  const int q = lane_id();
+  VerifyPart p;
+  p.m = -INFINITY;
+  p.s = 0.0;
+  p.amax = -1;
+  p.flags = 0;
+  if (q < kVerifySplit) p = parts[q];
+  const uint32_t any = wave_reduce_dpp((uint32_t)p.flags, [](uint32_t u, uint32_t v) { return u | v; });
+  const bool f = (p.flags & 2) != 0;
+  const double M = wave_reduce_dpp(f ? p.m : -(double)INFINITY, OpMax());
+  const double sq = (T != 0.0 && f) ? p.s * exp_nonpos((p.m - M) / T, etab) : 0.0;
+  const long long fq = (f && p.m == M) ? (long long)q : LLONG_MAX;
+  const long long fw = wave_reduce_dpp(fq, OpMin());
+  VerifyStat st;
+  st.M = M;
+  st.s1 = wave_reduce_dpp(sq, OpSum());
+  st.status = (any & 1) ? DSR_E_LOGITS : ((any & 2) ? DSR_OK : DSR_E_MASKED);
+  st.amax = fw == LLONG_MAX ? -1 : __shfl(p.amax, (int)fw);
+  return st;
+}
+
+constexpr int kEosCached = 256;  // EOS ids copied to LDS (longer lists are read in place)
+
+// Step 2, one workgroup per request: general requests run their whole
+// decision here; fast ones combine each distribution's shares (one wave per
+// distribution), fetch every input of the chain in parallel into LDS, run it
+// and hand a pending draw to steps 3-4.
+__global__ __launch_bounds__(kThreads) void k_verify_chain(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  __shared__ Decision d;
+  __shared__ double etab[64];
+  __shared__ VerifyStat sst[2 * DSR_MAX_DRAFTS + 1];
+  __shared__ double sprob[2 * DSR_MAX_DRAFTS + 1];
+  __shared__ int32_t sids[DSR_MAX_DRAFTS];
+  __shared__ double sua[DSR_MAX_DRAFTS];
+  __shared__ int32_t seos[kEosCached];
+  const int64_t row = blockIdx.x;
+  if (!verify_fast_row(a, L, row)) {
+    general_decide(a, L, row, sh, d);
+    return;
+  }
+  const int K = a.K;
+  const double T = a.policy[row].temperature;
+  const bool greedy = T == 0.0;
+  const int slots = (int)L.slots;
+  const int t = threadIdx.x;
+  exp_table_init(etab);
+  __syncthreads();
+  if (wave_id() < slots) {
+    const int sl = wave_id();
+    const VerifyStat v = combine_shares(L.part + (row * L.slots + sl) * kVerifySplit, T, etab);
+    if (lane_id() == 0) {
+      sst[sl] = v;
+      L.stat[row * L.slots + sl] = v;
+    }
+  }
+  __syncthreads();
+  if (t < slots) {
+    const VerifyStat v = sst[t];
+    const int j = t <= K ? t : t - K - 1;
+    double pr = 0.0;
+    if (j < K) {
+      const int32_t x = a.draft_ids[row * K + j];
+      if (x >= 0 && x < a.vocab && v.status == DSR_OK) {
+        if (greedy) pr = x == v.amax ? 1.0 : 0.0;
+        else pr = exp((load_logit(verify_logits(a, row, t), a.dtype, x) - v.M) / T) / v.s1;  // s1: this path's sum
+      }
+      if (t < K) {
+        sids[t] = x;
+        sua[t] = a.u_accept[row * K + t];
+      }
+    }
+    sprob[t] = pr;
+  }
+  const int n_eos = a.eos_off ? (int)(a.eos_off[row + 1] - a.eos_off[row]) : 0;
+  if (n_eos <= kEosCached && t >= 64 && t < 64 + n_eos) seos[t - 64] = a.eos_ids[a.eos_off[row] + (t - 64)];
+  __syncthreads();
+  if (t == 0) {
+    Request rq = request_of(a, row);
+    rq.ids = sids;
+    rq.ua = sua;
+    if (n_eos <= kEosCached) rq.eos = seos;
+    auto status_of = [&](int sl) { return (int)sst[sl].status; };
+    verify_precheck(a, rq, status_of, d);
+    if (d.status == DSR_OK)
+      verify_chain(
+          a, rq, greedy, 0x1p-40, status_of, [&](int sl, int) { return sprob[sl]; },
+          [&](int j) { return (int64_t)sst[j].amax; }, [](int) {}, d);
+    if (d.status == DSR_OK && d.next != 0 && greedy) {
+      verify_append(a, rq, d, sst[d.draw_j].amax, 0);
+      d.next = 0;
+    }
+    L.dec[row] = d;
+    if (d.status != DSR_OK || d.next == 0) write_decision(a, row, d);
+  }
+}
+
+// The draw's weights at token i: p_j (bonus) or max(p_j - q_j, 0)
+// (replacement, correction_distribution, sampling.py:131-139).
+struct DrawWeights {
+  const char* P;
+  const char* Q;
+  int dt;
+  bool resid;
+  double Mp, iTp, isp, Mq, isq;
+  const double* etab;
+  __device__ __forceinline__ double operator()(int64_t i) const {
+    const double p = exp_nonpos((load_logit(P, dt, i) - Mp) * iTp, etab) * isp;
+    if (!resid) return p;
+    const double q = exp_nonpos((load_logit(Q, dt, i) - Mq) * iTp, etab) * isq;
+    return fmax(p - q, 0.0);
+  }
+};
+
+__device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row,
+                                                    const Decision& d, const double* etab) {
+  const int K = a.K;
+  const VerifyStat* st = L.stat + row * L.slots;
+  DrawWeights w;
+  w.resid = d.next == 1;
+  w.P = verify_logits(a, row, d.draw_j);
+  w.Q = w.resid ? verify_logits(a, row, K + 1 + d.draw_j) : nullptr;
+  w.dt = a.dtype;
+  w.iTp = 1.0 / a.policy[row].temperature;
+  w.Mp = st[d.draw_j].M;
+  w.isp = 1.0 / st[d.draw_j].s1;
+  w.Mq = w.resid ? st[K + 1 + d.draw_j].M : 0.0;
+  w.isq = w.resid ? 1.0 / st[K + 1 + d.draw_j].s1 : 0.0;
+  w.etab = etab;
+  return w;
+}
+
+__device__ __forceinline__ void draw_segment(int64_t V, int q, int64_t& lo, int64_t& hi) {
+  const int64_t seg = (V + kDrawSplit - 1) / kDrawSplit;
+  lo = (int64_t)q * seg < V ? (int64_t)q * seg : V;
+  hi = lo + seg < V ? lo + seg : V;
+}
+
+// Step 3: share g of a pending draw -> its weight sum, positive count and
+// first positive index.
+__global__ __launch_bounds__(kThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  __shared__ double etab[64];
+  const int64_t row = blockIdx.x / kDrawSplit;
+  const int g = (int)(blockIdx.x % kDrawSplit);
+  if (!verify_fast_row(a, L, row)) return;
+  const Decision d = L.dec[row];
+  if (d.status != DSR_OK || d.next == 0) return;
+  exp_table_init(etab);
+  __syncthreads();
+  const DrawWeights wf = draw_weights(a, L, row, d, etab);
+  int64_t lo, hi;
+  draw_segment(a.vocab, g, lo, hi);
+  double acc = 0.0;
+  long long npos = 0, first = LLONG_MAX;
+  row_pass<double>(hi - lo, [&](int64_t i) { return wf(lo + i); }, [&](int64_t i, double w) {
+    acc += w;
+    if (w > 0.0) {
+      ++npos;
+      if (lo + i < first) first = lo + i;
+    }
+  });
+  acc = block_sum(acc, sh.b);
+  npos = block_sum_i64(npos, sh.b);
+  first = block_min_i64(first, sh.b);
+  if (threadIdx.x == 0) {
+    DrawPart p;
+    p.sum = acc;
+    p.npos = npos;
+    p.first = first;
+    p.pad = 0;
+    L.dpart[row * kDrawSplit + g] = p;
+  }
+}
+
+// Slice sums in [lo, hi) by contiguous per-thread slices, a scan from `base`,
+// and wave 0 walking the slice of the thread that holds the crossing of thr.
+template <class WF>
+__device__ int64_t range_cdf_search(int64_t lo, int64_t hi, WF wf, double base, double thr, double tol,
+                                    GenShared& sh, int& margin) {
+  const int64_t n = hi - lo;
+  int64_t slo, shi;
+  thread_slice(n, slo, shi);
+  double part = 0.0;
+  slice_pass<double>(lo + slo, lo + shi, wf, [&](int64_t, double w) { part += w; });
+  double total;
+  const double ex = base + block_exclusive_scan_f64(part, sh.b, total);
+  const long long cand = (part > 0.0 && ex <= thr) ? (long long)threadIdx.x : -1;
+  const long long owner = block_max_i64(cand, sh.b);
+  if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(ex);
+  __syncthreads();
+  if (wave_id() == 0 && owner >= 0) {
+    int64_t olo, ohi;
+    slice_of(owner, n, olo, ohi);
+    int64_t tok;
+    int m;
+    wave_slice_cdf(wf, lo + olo, lo + ohi, __longlong_as_double(sh.bc[0]), thr, tol, tok, m);
+    if (lane_id() == 0) {
+      sh.bc[1] = tok;
+      sh.bc[2] = m;
+    }
+  }
+  __syncthreads();
+  const int64_t tok = owner >= 0 ? (int64_t)sh.bc[1] : -1;
+  margin = owner < 0 || sh.bc[2] ? 1 : 0;
+  __syncthreads();
+  return tok;
+}
+
+// Step 4, one workgroup per request with a pending draw: combine the shares
+// in index order, then walk the share that holds the crossing of u * total.
+__global__ __launch_bounds__(kThreads) void k_verify_finish(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  __shared__ double etab[64];
+  __shared__ Decision d;
+  const int64_t row = blockIdx.x;
+  if (!verify_fast_row(a, L, row)) return;
+  if (threadIdx.x == 0) d = L.dec[row];
+  exp_table_init(etab);
+  __syncthreads();
+  if (d.status != DSR_OK || d.next == 0) return;
+  const DrawWeights wf = draw_weights(a, L, row, d, etab);
+  const DrawPart* parts = L.dpart + row * kDrawSplit;
+  double sums[kDrawSplit];
+  double total = 0.0;
+  long long n = 0, f = LLONG_MAX;
+#pragma unroll
+  for (int q = 0; q < kDrawSplit; ++q) {
+    const DrawPart p = parts[q];
+    sums[q] = p.sum;
+    total += p.sum;
+    n += p.npos;
+    if (p.npos > 0 && p.first < f) f = p.first;
+  }
+  int64_t rep = -1;
+  int used = 0, status = DSR_OK, margin = 0;
+  if (wf.resid && (!(total > 0.0) || !isfinite(total))) {
+    status = DSR_E_CORRECTION;
+  } else if (n == 1) {
+    rep = f;  // a single positive token: no uniform is drawn (sampling.py:120-122)
+  } else {
+    const double u = a.u_target[row];
+    if (!(u >= 0.0 && u < 1.0)) {
+      status = DSR_E_UNIFORM;
+    } else {
+      used = 1;
+      const double thr = u * total;
+      // The share holding the crossing: the last one with mass starting at or below thr.
+      double base = 0.0, obase = 0.0;
+      int owner = -1;
+#pragma unroll
+      for (int q = 0; q < kDrawSplit; ++q) {
+        if (sums[q] > 0.0 && base <= thr) {
+          owner = q;
+          obase = base;
+        }
+        base += sums[q];
+      }
+      if (owner < 0) {  // rounding left no share at or below thr: the last one with mass
+        base = 0.0;
+#pragma unroll
+        for (int q = 0; q < kDrawSplit; ++q) {
+          if (sums[q] > 0.0) {
+            owner = q;
+            obase = base;
+          }
+          base += sums[q];
+        }
+        margin = 1;
+      }
+      const double tol = ((double)n + 16.0) * 0x1p-51 * total;
+      int64_t lo, hi;
+      draw_segment(a.vocab, owner, lo, hi);
+      int m2 = 0;
+      rep = range_cdf_search(lo, hi, wf, obase, thr, tol, sh, m2);
+      margin |= m2;
+    }
+  }
+  if (threadIdx.x == 0) {
+    if (margin) d.flags |= DSR_FLAG_MARGIN;
+    if (status != DSR_OK) {
+      d.status = status;
+    } else {
+      Request rq = request_of(a, row);
+      verify_append(a, rq, d, rep, used);
+    }
+    write_decision(a, row, d);
+  }
+}
+
+}  // namespace dsr

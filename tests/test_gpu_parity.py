@@ -250,6 +250,51 @@ def test_verify_c4_against_oracle():
     assert hits >= R - 1
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_fast_path_matches_general_path(dtype):
+    """Filter-free requests take the statistics-only verifier; an all-ones
+    allow mask sends the same requests through the full-distribution path.
+    Decisions must agree except where either side flags the rounding band."""
+    rng = np.random.default_rng(11)
+    R, K, V = 24, 3, 5003
+    tgt_np = rng.normal(0, 2, (R, K + 1, V)).astype(np.float32)
+    drf_np = tgt_np[:, :K] + rng.normal(0, 0.5, (R, K, V)).astype(np.float32)
+    dev = "cuda"
+    tgt = torch.from_numpy(tgt_np).to(dev).to(dtype)
+    drf = torch.from_numpy(drf_np).to(dev).to(dtype)
+    pols = [dict(temperature=[1.0, 0.7, 1.3, 0.0][r % 4]) for r in range(R)]
+    # Draft ids from the draft rows themselves, so most are plausible.
+    draw = batch.sample_rows(drf.reshape(R * K, V).contiguous(), [dict()] * (R * K),
+                             uniforms=torch.from_numpy(rng.random(R * K)).to(dev))
+    ids = draw.tokens.reshape(R, K).contiguous()
+    # Greedy requests (every fourth) propose each draft row's argmax, so their
+    # proposals have probability one.
+    greedy = torch.arange(R, device=dev) % 4 == 3
+    ids[greedy] = drf.float().argmax(dim=-1).to(torch.int32)[greedy]
+    ua = torch.from_numpy(rng.random((R, K))).to(dev)
+    ut = torch.from_numpy(rng.random(R)).to(dev)
+    lim = torch.from_numpy(np.array([10, 2, 3, 10] * (R // 4), dtype=np.int32)).to(dev)
+    eos_ids = ids[:, 1].contiguous()  # the second draft of each request is an EOS token
+    eos_off = torch.arange(0, R + 1, dtype=torch.int64, device=dev)
+    words = (V + 31) // 32
+    ones = torch.full((R, K + 1, words), -1, dtype=torch.int32, device=dev)  # every bit set
+    kw = dict(eos_offsets=eos_off, eos_ids=eos_ids)
+    fast = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim, **kw)
+    gen = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim, allow_bits=ones, **kw)
+    torch.cuda.synchronize()
+    fields = ("status", "accepted", "count", "pending", "stop", "used_accept", "used_target")
+    same = 0
+    for r in range(R):
+        a = tuple(int(getattr(fast, f)[r]) for f in fields) + (tuple(fast.ids[r].tolist()),)
+        b = tuple(int(getattr(gen, f)[r]) for f in fields) + (tuple(gen.ids[r].tolist()),)
+        if a == b:
+            same += 1
+        else:
+            assert (int(fast.flags[r]) | int(gen.flags[r])) & 1, (r, a, b)
+    assert same >= R - 1
+    assert int(fast.status.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("case", META["verify"], ids=lambda c: c["name"])
 def test_verify_golden_on_gpu(case):
     dev = "cuda"

@@ -43,7 +43,12 @@ def test_workspace_queries():
     lib = N.load()
     assert lib.dsr_sample_workspace_bytes(256, 129280) == 256 * 129280 * 8
     assert lib.dsr_sample_workspace_bytes(1, 3) == 32 * 8
-    assert lib.dsr_verify_workspace_bytes(32, 4, 129280) == 32 * 9 * 129280 * 8 + 32 * 9 * 16
+    # float64 rows + per-distribution info, statistics and 32 share partials,
+    # eight draw partials and one 64-byte decision per request.
+    rows, slots = 32, 9
+    expect = (rows * slots * 129280 * 8 + rows * slots * 16 + rows * slots * 32 + rows * slots * 32 * 32
+              + rows * 8 * 32 + rows * 64)
+    assert lib.dsr_verify_workspace_bytes(rows, 4, 129280) == expect
 
 
 def test_argument_errors_return_before_any_launch():
