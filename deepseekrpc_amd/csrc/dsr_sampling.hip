@@ -14,6 +14,7 @@
 #include <stdint.h>
 
 #include "dsr_fast.h"
+#include "dsr_full.h"
 #include "dsr_general.h"
 #include "dsr_verify.h"
 
@@ -110,6 +111,29 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   DistOut d;
   int st = general_distribution(r, gs, flags, d);
   finish_row(a, row, W, st, d, flags, gs);
+}
+
+// Full-vocabulary path for bf16 rows that carry a token history (no bias);
+// rows it does not take are redone by the general path in the same workgroup.
+struct FullKernelShared {
+  union {
+    FullShared f;
+    GenShared g;
+  };
+};
+
+__global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t a) {
+  __shared__ FullKernelShared sh;
+  const int64_t row = blockIdx.x;
+  const int why = full_sample_row(a, row, sh.f);
+  if (why == 0) return;
+  __syncthreads();
+  double* W = (double*)a.workspace + row * ws_stride(a.vocab);
+  RowSpec r = sample_row_spec(a, row, W);
+  unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
+  DistOut d;
+  int st = general_distribution(r, sh.g, flags, d);
+  finish_row(a, row, W, st, d, flags, sh.g);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,6 +270,8 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (fast_path_eligible(a)) {
     hipLaunchKernelGGL(k_sample_bf16_fast, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+  } else if (full_path_eligible(a)) {
+    hipLaunchKernelGGL(k_sample_bf16_full, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   } else {
     hipLaunchKernelGGL(k_sample_general, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   }
