@@ -42,7 +42,7 @@ constexpr int kFxBits = 45;                       // fixed-point mass scale 2^45
 constexpr int kLutBinades = 32;                   // per sign
 constexpr int kLutSize = 2 * kLutBinades * 128;   // 8192 keys
 constexpr int kPenItems = 64;                     // penalised values resolved exactly at the boundary
-constexpr int kPenPre = 16;                       // history ids per thread fetched ahead of the row
+constexpr int kPenPre = 8;                        // history ids per thread fetched ahead of the row
 
 struct PenItem {
   double v;
@@ -57,28 +57,36 @@ static inline bool full_path_eligible(const dsr_sample_args_t& a) {
          ((uintptr_t)a.logits & 15u) == 0 && a.bias_off == nullptr;
 }
 
+constexpr int kLutSlots = 64;  // binade slots of the mass table; slot 0 stays zero
+
 struct FullShared {
   union {
-    uint32_t cnt[32768];  // key counts, key k in bits 16*(k&1) of word k>>1
-    struct {
-      double lut[kLutSize];          // kept mass by (sign, binade, mantissa); 0 when not kept
-      long long pm[kLutSize];        // penalised fixed-point masses of the walking wave's tokens
-    } cdf;
+    uint32_t cnt[32768];               // key counts, key k in bits 16*(k&1) of word k>>1
+    long long lut[kLutSlots * 128];    // kept fixed-point mass by (binade slot, mantissa)
   } big;
   union {
     struct {
-      uint32_t pbits[kFastMaxVocab / 32];  // penalised tokens
+      uint32_t pbits[kFastMaxVocab / 32];  // tokens kept in registers: allowed, untouched by the history
       uint32_t lut[256][4];                // allow byte -> disallowed masks
     } p1;
     struct {
       long long bm[1024];  // mass per 64-key block
       uint32_t bp[1024];   // positive tokens per block
+      uint32_t bc[1024];   // register-resident tokens per block
     } blk;
+    struct {
+      long long pen[1024];  // kept penalised mass per chunk of the walking wave
+      long long reg[1024];  // kept register-resident mass per chunk of that wave
+    } cm;
   } mid;
+  uint16_t boff[512];         // binade -> mass-table slot (0: none)
+  uint16_t bslot[kLutSlots];  // slot -> binade
   PenItem items[kPenItems];
   long long kmass[64];
   uint32_t kpos[64];
   long long wtot[kWaves];
+  uint32_t wtie[kWaves];
+  long long pe[8];            // kept penalised masses of the crossing chunk, by element
   double etab[64];
   SyncSlots sync;
   long long bc_l[4];
@@ -132,6 +140,25 @@ __device__ __forceinline__ long long uni(long long x) {
 }
 __device__ __forceinline__ double uni(double x) { return __longlong_as_double(uni((long long)__double_as_longlong(x))); }
 
+// Element e of a chunk for a runtime e.  It selects between two computed
+// 64-bit halves, never between the chunk's words themselves: a select between
+// the words of an array element is folded into a dynamically indexed load,
+// which moves the whole register array to scratch memory.
+__device__ __forceinline__ uint32_t key_at_rt(const uint4& v, int e) {
+  const uint64_t lo = ((uint64_t)v.y << 32) | v.x, hi = ((uint64_t)v.w << 32) | v.z;
+  return (uint32_t)((e < 4 ? lo : hi) >> (16 * (e & 3))) & 0xFFFFu;
+}
+
+// Bit e set when element e of the chunk holds key L.
+__device__ __forceinline__ uint32_t key_bits(const uint4& v, uint32_t L) {
+  const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  uint32_t m = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    m |= ((w4[q] & 0xFFFFu) == L ? 1u : 0u) << (2 * q) | ((w4[q] >> 16) == L ? 1u : 0u) << (2 * q + 1);
+  return m;
+}
+
 // Whether history entry e of a row changes its token (count or generated count positive).
 __device__ __forceinline__ bool pen_touches(long long c, long long g) { return c > 0 || g > 0; }
 
@@ -145,12 +172,19 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   BlockSync bs(sh.sync);
 
   // ---- loads, smallest first so that waiting for them never waits for the
-  // row: the exp table constants, the policy and history bounds (scalar),
-  // the first kPenPre history ids per thread, then the row and its allow
-  // bytes as raw buffer loads, as the fast path issues them.
+  // row: the allow words (4 per thread), the policy and history bounds
+  // (scalar), the first kPenPre history ids per thread, then the row as raw
+  // buffer loads, as the fast path issues them.
   const dsr_policy_t pol = a.policy[row];
   const int64_t o0 = a.pen_off ? a.pen_off[row] : 0;
   const int64_t pn = a.pen_off ? a.pen_off[row + 1] - o0 : 0;
+  const uint32_t nwords = (uint32_t)((V + 31) >> 5);
+  uint32_t aw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = (uint32_t)tid + (uint32_t)i * kThreads;
+    aw[i] = (a.allow_bits && w < nwords) ? a.allow_bits[row * a.allow_ld + w] : 0xFFFFFFFFu;
+  }
   const double etv = kExp2Frac[lane];
   int32_t pid[kPenPre];
 #pragma unroll
@@ -158,18 +192,14 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     const int64_t e = tid + (int64_t)i * kThreads;
     pid[i] = e < pn ? a.pen_ids[o0 + e] : -1;
   }
-  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
-      a.allow_bits ? (void*)(a.allow_bits + row * a.allow_ld) : (void*)&kAllowAll, (short)0, (int)C, 0x00020000);
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const uint16_t*)a.logits + row * a.ld), (short)0, (int)(V * 2), 0x00020000);
-  uint32_t mb[kFastChunks];
   uint4 d[kFastChunks];
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
     const uint32_t c = (uint32_t)wave * CW + cw;
     const bool mine = cw < CW;
-    mb[j] = __builtin_amdgcn_raw_buffer_load_b8(mrs, (int)(mine ? c : 0x7FFFFFF0u), 0, 0);
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)(mine ? c * 16u : 0x7FFFFFF0u), 0, 0);
     d[j] = make_uint4(v[0], v[1], v[2], v[3]);
   }
@@ -181,14 +211,15 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   double* Wv = (double*)a.workspace + row * ((V + 31) & ~(int64_t)31);    // adjusted values
   long long* Wp = (long long*)(Wv + pn);                                     // mass | floor key << 48
 
-  // ---- LDS set-up while the row streams in: mask table, bitmap, key counts,
-  // exp table; then the penalised-token bitmap from the prefetched ids (ids
-  // out of range are left to the validity check after pass 1).
+  // ---- LDS set-up while the row streams in: the mask table, the key
+  // counts, the exp table and one bitmap of the tokens that stay in
+  // registers (allowed and untouched by the history).  Ids out of range are
+  // left to the validity check after pass 1.
   {
     const uint32_t m = (uint32_t)tid >> 2, q = (uint32_t)tid & 3u;
     sh.mid.p1.lut[m][q] = (((m >> (2 * q)) & 1u) ? 0u : 0x0000FFFFu) | (((m >> (2 * q + 1)) & 1u) ? 0u : 0xFFFF0000u);
-    uint4* zb = (uint4*)sh.mid.p1.pbits;
-    zb[tid] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sh.mid.p1.pbits[tid + i * kThreads] = aw[i];
     uint4* zc = (uint4*)sh.big.cnt;
 #pragma unroll
     for (int i = 0; i < 8; ++i) zc[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
@@ -197,23 +228,29 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < kPenPre; ++i)
-    if (pid[i] >= 0 && pid[i] < V) atomicOr(&sh.mid.p1.pbits[pid[i] >> 5], 1u << (pid[i] & 31));
+    if (pid[i] >= 0 && pid[i] < V) atomicAnd(&sh.mid.p1.pbits[pid[i] >> 5], ~(1u << (pid[i] & 31)));
   for (int64_t e = tid + (int64_t)kPenPre * kThreads; e < pn; e += kThreads) {  // long histories
     const int32_t id = a.pen_ids[o0 + e];
-    if (id >= 0 && id < V) atomicOr(&sh.mid.p1.pbits[id >> 5], 1u << (id & 31));
+    if (id >= 0 && id < V) atomicAnd(&sh.mid.p1.pbits[id >> 5], ~(1u << (id & 31)));
   }
   lds_barrier();
 
   // ---- pass 1, chunk by chunk as the loads land: keys, with masked and
-  // penalised tokens set to key 0; raw NaN/+inf check; key max and min.
+  // penalised tokens set to keys below every value's (2 + lane: no LDS
+  // atomic contention on them later); raw NaN/+inf check; key max and min.
   uint32_t vmax_s = 0x80008000u, vmax_u = 0u, kmax = 0u, kmin = 0xFFFFFFFFu;
+  const uint32_t dummy2 = (2u + (uint32_t)lane) * 0x00010001u;  // keys 2..65 hold no value
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
-    const uint32_t cc = c < C ? c : C - 1u;  // chunks past the row are masked by their zero allow byte
-    const uint32_t pb = (sh.mid.p1.pbits[cc >> 2] >> ((cc & 3u) * 8u)) & 0xFFu;
-    const uint4 lm = *(const uint4*)sh.mid.p1.lut[(mb[j] & ~pb) & 0xFFu];
+    const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
+    const uint32_t c = (uint32_t)wave * CW + cw;
+    // Slots past this wave's chunks or past the row were not loaded (they
+    // read as +0.0) and stay masked; the read itself is not branched around.
+    const bool live = cw < CW && c < C;
+    const uint32_t cc = live ? c : 0u;
+    const uint32_t stay = (sh.mid.p1.pbits[cc >> 2] >> ((cc & 3u) * 8u)) & (live ? 0xFFu : 0u);
+    const uint4 lm = *(const uint4*)sh.mid.p1.lut[stay];
     uint32_t w[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
     const uint32_t m4[4] = {lm.x, lm.y, lm.z, lm.w};
 #pragma unroll
@@ -223,7 +260,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       const uint32_t k = bf16x2_keys(w[q] | m4[q]);  // excluded -> key 0
       kmax = pk_max_u16(kmax, k);
       kmin = pk_min_u16(kmin, k | m4[q]);            // excluded -> 0xFFFF, neutral for the minimum
-      w[q] = k;
+      w[q] = k | (m4[q] & dummy2);                   // excluded -> a per-lane key below the real ones
     }
     d[j] = make_uint4(w[0], w[1], w[2], w[3]);
   }
@@ -308,59 +345,83 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   unsigned flags = 0;
 
-  // ---- key-count histogram of the register-resident tokens.
-  uint32_t nlive = 0;
+  // ---- key-count histogram of the register-resident tokens (excluded and
+  // dummy keys land below 128 and are ignored from here on).
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) {
+    const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t k = key_at(d[j], e);
-      if (k > kKeyNegInf) {
-        atomicAdd(&sh.big.cnt[k >> 1], 1u << ((k & 1u) << 4));
-        ++nlive;
-      }
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t k0 = w4[q] & 0xFFFFu, k1 = w4[q] >> 16;
+      atomicAdd(&sh.big.cnt[k0 >> 1], 1u << ((k0 & 1u) << 4));
+      atomicAdd(&sh.big.cnt[k1 >> 1], 1u << ((k1 & 1u) << 4));
     }
   }
   lds_barrier();
 
-  // ---- masses of the present keys, per 64-key block (thread t owns block t),
-  // with min-p (sampling.py:94-96: r < min_p * max(r), and max(r) is 1 / sum).
+  // ---- masses of the present keys (sampling.py:86-96: exp((v - max) / T),
+  // min-p keeping r >= min_p since max(r) = 1 / sum).  Thread t takes the
+  // 8-key groups t + 1024 i, so dense key ranges spread over many threads;
+  // the 8 groups of a 64-key block sit in 8 neighbouring lanes and are
+  // summed by DPP.
   const double min_p = pol.min_p;
   auto mass_of = [&](double v) {
-    double e = exp_nonpos((v - M) / T, etab);  // (v - max) / T as the reference divides
+    double e = exp_nonpos((v - M) / T, etab);  // (v - max) / T divided as the reference divides
     if (e < min_p) e = 0.0;
     return e;
   };
   int close = 0;
   {
-    long long bmass = 0;
-    uint32_t bpos = 0, bcount = 0;
-    const uint4* cw4 = (const uint4*)&sh.big.cnt[32 * tid];
+    uint32_t nlive = 0;
 #pragma unroll 1
     for (int i = 0; i < 8; ++i) {
-      const uint4 q = cw4[i];
-      const uint32_t ws[4] = {q.x, q.y, q.z, q.w};
+      const uint32_t g = (uint32_t)tid + 1024u * (uint32_t)i;
+      const uint4 q4 = *(const uint4*)&sh.big.cnt[4u * g];
+      long long gm = 0;
+      uint32_t gp = 0, gc = 0;
+      if ((q4.x | q4.y | q4.z | q4.w) != 0u && g >= 16u) {  // keys below 128 hold no value
 #pragma unroll 1
-      for (int h = 0; h < 8; ++h) {
-        const uint32_t wq = h < 4 ? (h < 2 ? ws[0] : ws[1]) : (h < 6 ? ws[2] : ws[3]);
-        const uint32_t c = (wq >> (16 * (h & 1))) & 0xFFFFu;
-        if (c) {
-          const uint32_t k = 64u * (uint32_t)tid + 8u * (uint32_t)i + (uint32_t)h;
-          const double e0 = exp_nonpos((bf16_key_value(k) - M) / T, etab);
-          if (min_p != 0.0 && e0 > 0.0 && fabs(e0 - min_p) <= min_p * 0x1p-48) close = 1;
-          const double e = e0 < min_p ? 0.0 : e0;
-          bmass += (long long)c * to_fx(e);
-          bpos += e > 0.0 ? c : 0u;
-          bcount += c;
+        for (int h = 0; h < 8; ++h) {
+          const uint32_t wq = h < 4 ? (h < 2 ? q4.x : q4.y) : (h < 6 ? q4.z : q4.w);
+          const uint32_t c = (wq >> (16 * (h & 1))) & 0xFFFFu;
+          if (c) {
+            const double e0 = exp_nonpos((bf16_key_value(8u * g + (uint32_t)h) - M) / T, etab);
+            if (min_p != 0.0 && e0 > 0.0 && fabs(e0 - min_p) <= min_p * 0x1p-48) close = 1;
+            const double e = e0 < min_p ? 0.0 : e0;
+            gm += (long long)c * to_fx(e);
+            gp += e > 0.0 ? c : 0u;
+            gc += c;
+          }
         }
       }
+      nlive += gc;
+      // Sum the 8 groups of block g >> 3 (lanes with equal tid >> 3).
+      gm = gm + dpp_move<long long, 0xB1>(gm);
+      gm = gm + dpp_move<long long, 0x4E>(gm);
+      gm = gm + dpp_move<long long, 0x141>(gm);
+      gp = gp + dpp_move<uint32_t, 0xB1>(gp);
+      gp = gp + dpp_move<uint32_t, 0x4E>(gp);
+      gp = gp + dpp_move<uint32_t, 0x141>(gp);
+      gc = gc + dpp_move<uint32_t, 0xB1>(gc);
+      gc = gc + dpp_move<uint32_t, 0x4E>(gc);
+      gc = gc + dpp_move<uint32_t, 0x141>(gc);
+      if ((tid & 7) == 0) {
+        sh.mid.blk.bm[g >> 3] = gm;
+        sh.mid.blk.bp[g >> 3] = gp;
+        sh.mid.blk.bc[g >> 3] = gc;
+      }
     }
-    sh.mid.blk.bm[tid] = bmass;
-    sh.mid.blk.bp[tid] = bpos;
-    const uint32_t chk = bs.sum(bcount) ^ bs.sum(nlive);  // a 16-bit count that wrapped shows here
-    if (chk) return kHandCapacity;
+    // Every counted token is a real key: a 16-bit count that wrapped shows here.
+    uint32_t real = 0;
+#pragma unroll
+    for (int j = 0; j < kFastChunks; ++j) {
+      const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) real += ((w4[q] & 0xFFFFu) >= 128u ? 1u : 0u) + ((w4[q] >> 16) >= 128u ? 1u : 0u);
+    }
+    if (bs.sum(nlive) != bs.sum(real)) return kHandCapacity;
   }
-  // Penalised tokens: mass, floor key, added to their block.
+  // Penalised tokens: mass, floor key, added to the block of their floor key.
   for (int64_t e = tid; e < pn; e += kThreads) {
     const double v = Wv[e];
     long long packed = 0;
@@ -387,12 +448,15 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   long long S;
   uint32_t pex, ptot;
   const long long run = bs.scan2(bmt, bpt, S, pex, ptot);
-  uint32_t L = 0;           // boundary key; 0: nothing removed by top-p
-  long long keep = 0;       // boundary tie members kept, lowest index first
-  long long cut_idx = -1;   // index of the last kept tie member when the group is split
-  long long Sk = S;         // kept mass
-  uint32_t npos_k = ptot;   // kept tokens with positive mass
-  int nkept_items = 0;      // penalised values kept inside the boundary bucket (sorted first)
+  S = uni(S);
+  uint32_t L = 0;          // boundary key; 0: nothing removed by top-p
+  long long keep = 0;      // boundary tie members kept, lowest index first
+  long long n_tie = 0;
+  long long mtie = 0;      // fixed-point mass of one tie member
+  long long cut_idx = -1;  // index of the last kept tie member when the group is split
+  long long Sk = S;        // kept mass
+  uint32_t npos_k = uni(ptot);
+  int nkept_items = 0;     // penalised values kept inside the boundary bucket (first in sorted order)
   if (pol.top_p < 1.0) {
     const double P = pol.top_p * (double)S;
     long long tgt = (long long)P;
@@ -408,7 +472,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
     if (tid == 0) sh.nitems = 0;
     lds_barrier();
-    const int B = sh.bc_i[0];
+    const int B = uni(sh.bc_i[0]);
     if (B < 0) return kHandCapacity;  // unreachable: the running mass reaches tgt <= S
     const long long AB = sh.bc_l[0];
     const uint32_t posAB = (uint32_t)sh.bc_i[1];
@@ -423,8 +487,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     lds_barrier();
     if (wave == 0) {  // keys of block B, descending, one per lane
       const uint32_t k = 64u * (uint32_t)B + 63u - (uint32_t)lane;
-      const uint32_t c = (sh.big.cnt[k >> 1] >> ((k & 1u) << 4)) & 0xFFFFu;
-      const double e = (c && k > kKeyNegInf) ? mass_of(bf16_key_value(k)) : 0.0;
+      const uint32_t c = k >= 128u ? (sh.big.cnt[k >> 1] >> ((k & 1u) << 4)) & 0xFFFFu : 0u;
+      const double e = c ? mass_of(bf16_key_value(k)) : 0.0;
       const long long fk = to_fx(e);
       const long long mk = (long long)c * fk + sh.kmass[k & 63u];
       const uint32_t pk = (e > 0.0 ? c : 0u) + sh.kpos[k & 63u];
@@ -444,8 +508,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     L = uni((uint32_t)sh.bc_i[2]);
     const long long AL = sh.bc_l[1];
     const uint32_t posAL = (uint32_t)sh.bc_i[3];
-    const long long n_tie = sh.bc_i[4];
-    const long long mt = sh.bc_l[2];
+    n_tie = uni((long long)sh.bc_i[4]);
+    mtie = uni(sh.bc_l[2]);
     const int tie_pos = sh.bc_i[5];
     // Penalised values in the boundary bucket and its two neighbours.
     for (int64_t e = tid; e < pn; e += kThreads) {
@@ -482,11 +546,10 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
         }
       }
       __builtin_amdgcn_wave_barrier();
-      if (lane < nit) sh.items[rank] = mine;  // every lane read before any writes (one wave, in order)
+      if (lane < nit) sh.items[rank] = mine;  // every lane has read its item before any write (one wave)
     }
     lds_barrier();
     if (tid == 0) {
-      const double vL = bf16_key_value(L);
       int hand = (zero_key(L) && n_tie > 0) ? kHandZero : 0;
       // Distinct values around the boundary must keep (v - max) / T at least
       // 2^-40 apart, so the reference's float64 masses order them as the
@@ -496,7 +559,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       int ii = 0;
       for (int dk = 1; dk >= -1 && !hand; --dk) {
         const uint32_t kk = L + (uint32_t)dk;
-        if (kk == 0u || kk > 0xFFFFu) continue;
+        if (kk < 128u || kk > 0xFFFFu) continue;
         const uint32_t ck = (sh.big.cnt[kk >> 1] >> ((kk & 1u) << 4)) & 0xFFFFu;
         const double vk = bf16_key_value(kk);
         while (ii < nit && (uint16_t)sh.items[ii].key > kk) ++ii;  // items sort by value, hence by bucket
@@ -512,14 +575,13 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
           prev = vk;
         }
       }
-      // The walk: items of bucket L, in order.
+      // The walk: items of bucket L, in order, then its tie group.
       long long cum = AL;
       bool removed = false;
-      int nk = 0, nk_pos = 0, first_item = -1;
+      int nk = 0, nk_pos = 0;
       long long ex_last = -1, ex_first_removed = -1;
       for (int q = 0; q < nit && !hand; ++q) {
         if ((uint16_t)sh.items[q].key != L) continue;
-        if (first_item < 0) first_item = q;
         const long long ex = cum;
         if (!removed && ((double)ex < P || ex == 0)) {
           cum += sh.items[q].fx;
@@ -532,15 +594,15 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
         }
       }
       long long kp = 0;
-      if (!removed) {
-        if (n_tie > 0 && mt > 0) {
-          double q = ceil((P - (double)cum) / (double)mt);
+      if (!removed && n_tie > 0) {
+        if (mtie > 0) {
+          const double q = ceil((P - (double)cum) / (double)mtie);
           kp = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
-          while (kp > 0 && (double)(cum + (kp - 1) * mt) >= P) --kp;
-          while (kp < n_tie && (double)(cum + kp * mt) < P) ++kp;
+          while (kp > 0 && (double)(cum + (kp - 1) * mtie) >= P) --kp;
+          while (kp < n_tie && (double)(cum + kp * mtie) < P) ++kp;
           if (cum == 0 && kp == 0) kp = 1;  // the first token is never removed
-        } else if (n_tie > 0) {
-          kp = n_tie;  // zero-mass members: kept or not, they carry nothing
+        } else {
+          kp = n_tie;  // zero-mass members carry nothing either way
         }
       }
       const long long nab = (long long)posAL + nk;  // tokens ranked above the tie group
@@ -549,18 +611,17 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       if (removed) {
         near = fabs((double)ex_first_removed - P) <= tol || (ex_last >= 0 && fabs((double)ex_last - P) <= tol);
       } else if (n_tie > 0) {
-        near = fabs((double)(cum + kp * mt) - P) <= tol;
-        if (kp >= 1 && nab + kp > 1) near = near || fabs((double)(cum + (kp - 1) * mt) - P) <= tol;
-        if (kp == n_tie && (double)(cum + n_tie * mt) < P) near = true;
+        near = fabs((double)(cum + kp * mtie) - P) <= tol;
+        if (kp >= 1 && nab + kp > 1) near = near || fabs((double)(cum + (kp - 1) * mtie) - P) <= tol;
+        if (kp == n_tie && (double)(cum + n_tie * mtie) < P) near = true;
+        if (kp == 0 && nab > 0) near = true;
       } else {
         near = (ex_last >= 0 && fabs((double)ex_last - P) <= tol) || fabs((double)cum - P) <= tol;
       }
-      if (kp == 0 && !removed && nab > 0 && n_tie > 0) near = true;
-      (void)first_item;
       sh.bc_i[6] = hand;
       sh.bc_i[7] = nk | (near ? 0x10000 : 0);
       sh.bc_l[3] = kp;
-      sh.bc_l[0] = cum + kp * mt;  // kept mass up to the boundary
+      sh.bc_l[0] = cum + kp * mtie;  // kept mass
       sh.bc_l[2] = (long long)posAL + nk_pos + (tie_pos ? kp : 0);
     }
     lds_barrier();
@@ -570,52 +631,129 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     keep = uni(sh.bc_l[3]);
     Sk = uni(sh.bc_l[0]);
     npos_k = uni((uint32_t)sh.bc_l[2]);
-    // A split tie group: the index of its keep-th member, in index order
-    // (wave, register slot, lane, element).
-    if (keep > 0 && keep < n_tie) {
-      uint32_t before = 0;  // ties in this wave before the current slot
-      long long found = -1;
-      uint32_t tw[kFastChunks];
-      uint32_t wsum = 0;
-#pragma unroll
-      for (int j = 0; j < kFastChunks; ++j) {
-        uint32_t t = 0;
-#pragma unroll 1
-        for (int e = 0; e < 8; ++e) t += key_at(d[j], e) == L ? 1u : 0u;
-        tw[j] = t;
-        wsum += lane_value(wave_scan_dpp(t), 63);
-      }
-      if (lane == 0) sh.wtot[wave] = wsum;
-      lds_barrier();
-      uint32_t base = 0;
-      for (int w = 0; w < wave; ++w) base += (uint32_t)sh.wtot[w];
-#pragma unroll
-      for (int j = 0; j < kFastChunks; ++j) {
-        const uint32_t incl = wave_scan_dpp(tw[j]);
-        uint32_t r = base + before + incl - tw[j];
-        const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
-#pragma unroll 1
-        for (int e = 0; e < 8; ++e) {
-          if (key_at(d[j], e) == L) {
-            if ((long long)r == keep - 1) found = 8ll * c + e;
-            ++r;
-          }
-        }
-        before += lane_value(incl, 63);
-      }
-      if (found >= 0) sh.bc_l[1] = found;
-      lds_barrier();
-      cut_idx = uni(sh.bc_l[1]);
-    }
   }
-
-  // ---- categorical (sampling.py:103-128) on the kept masses.
   if (Sk <= 0) {
     if (tid == 0) fast_write_result(a, row, DSR_E_NO_MASS, -1, 0, flags);
     return 0;
   }
-  // Kept penalised values of the boundary bucket: the first nkept_items of
-  // its items in sorted order.
+  // Tie members of a split boundary group are kept up to the keep-th in
+  // index order (wave, register slot, lane, element): ties per wave, then
+  // per slot, give each member its rank.  wtie[w] ends as the kept members
+  // of wave w.
+  const bool split = keep > 0 && keep < n_tie;
+  if (split) {
+    auto ties_in = [&](const uint4& v) { return (uint32_t)__popc(key_bits(v, L)); };
+    uint32_t wsum = 0;
+#pragma unroll
+    for (int j = 0; j < kFastChunks; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      wsum += lane_value(wave_scan_dpp(ties_in(d[j])), 63);
+    }
+    if (lane == 0) sh.wtie[wave] = wsum;
+    lds_barrier();
+    uint32_t base = 0;
+    for (int w = 0; w < wave; ++w) base += sh.wtie[w];
+    long long found = -1;
+    uint32_t before = 0, fj = 0, fm = 0, fn = 0;
+#pragma unroll
+    for (int j = 0; j < kFastChunks; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      uint4 v = d[j];  // opaque copy: the first loop's counts are recomputed, not kept live
+      asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+      const uint32_t m = key_bits(v, L);
+      const uint32_t t = (uint32_t)__popc(m);
+      const uint32_t incl = wave_scan_dpp(t);
+      const uint32_t r0 = base + before + incl - t;  // ties before this lane's chunk
+      // The keep-th member lies in this chunk when n = keep-1-r0 is in [0, t).
+      const long long n = keep - 1 - (long long)r0;
+      const bool here = n >= 0 && n < (long long)t;
+      fj = here ? (uint32_t)j : fj;
+      fm = here ? m : fm;
+      fn = here ? (uint32_t)n : fn;
+      before += lane_value(incl, 63);
+    }
+    if (fm) {
+      // Set bit fn of fm: its position counts the prefixes of fm holding at most fn bits.
+      uint32_t e = 0;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) e += (uint32_t)__popc(fm & ((2u << b) - 1u)) <= fn ? 1u : 0u;
+      const uint32_t c = (uint32_t)wave * CW + fj * 64u + (uint32_t)lane;
+      found = 8ll * c + e;
+    }
+    lds_barrier();  // every wave has read wtie
+    if (found >= 0) sh.bc_l[1] = found;
+    if (lane == 0) {
+      const long long kw = keep - (long long)base;  // kept members of this wave
+      sh.wtie[wave] = (uint32_t)(kw <= 0 ? 0 : (kw >= (long long)wsum ? wsum : kw));
+    }
+    lds_barrier();
+    cut_idx = uni(sh.bc_l[1]);
+  }
+
+  // ---- mass table of the kept register-resident keys: every binade (128
+  // keys) holding a kept key gets a slot of 128 fixed-point masses; absent
+  // binades map to slot 0, all zero.  A split tie group's key stays 0 in the
+  // table (its kept members are added by index).
+  {
+    const uint32_t b = (uint32_t)tid;  // binade, threads 0..511
+    uint32_t present = 0;
+    if (b < 512u && b >= 1u) {
+      const uint32_t lo = 128u * b, hi = lo + 127u;
+      const bool inr = lo <= Mk && (L == 0u || hi >= L);
+      present = inr && (sh.mid.blk.bc[2u * b] + sh.mid.blk.bc[2u * b + 1u]) > 0u ? 1u : 0u;
+    }
+    uint32_t nbin;
+    const uint32_t rank = bs.scan(present, nbin);
+    if (nbin > (uint32_t)(kLutSlots - 1)) return kHandCapacity;  // more binades than the table holds
+    if (b < 512u) sh.boff[b] = present ? (uint16_t)(1u + rank) : (uint16_t)0;
+    if (present) sh.bslot[1u + rank] = (uint16_t)b;
+  }
+  lds_barrier();
+  {
+    const int slot = tid >> 4, m0 = (tid & 15) * 8;  // 8 table entries per thread
+    const uint32_t nbin = bs.sum((uint32_t)(tid < 512 && sh.boff[tid] != 0 ? 1 : 0));
+    const bool mine = slot >= 1 && (uint32_t)slot <= nbin;
+    const uint32_t b = mine ? (uint32_t)sh.bslot[slot] : 0u;
+    auto entry = [&](int i) -> long long {
+      const uint32_t k = 128u * b + (uint32_t)(m0 + i);
+      const uint32_t c = (sh.big.cnt[k >> 1] >> ((k & 1u) << 4)) & 0xFFFFu;
+      const bool kept = k <= Mk && (L == 0u || k > L || (k == L && !split && keep > 0));
+      return (mine && c && kept) ? to_fx(mass_of(bf16_key_value(k))) : 0ll;
+    };
+    // Two rounds of four: every count is read before the table overwrites it.
+    long long f0 = entry(0), f1 = entry(1), f2 = entry(2), f3 = entry(3);
+    const long long g0 = entry(4), g1 = entry(5), g2 = entry(6), g3 = entry(7);
+    lds_barrier();
+    long long* dst = &sh.big.lut[8 * tid];
+    dst[0] = f0;
+    dst[1] = f1;
+    dst[2] = f2;
+    dst[3] = f3;
+    dst[4] = g0;
+    dst[5] = g1;
+    dst[6] = g2;
+    dst[7] = g3;
+    if (tid < kWaves) sh.wtot[tid] = 0;
+  }
+  lds_barrier();
+  // Fixed-point kept mass of a register-resident key (split tie members excluded).
+  auto key_fx = [&](uint32_t k) -> long long {
+    return sh.big.lut[((uint32_t)sh.boff[k >> 7] << 7) | (k & 127u)];
+  };
+  // Index-order CDF: kept mass per wave, then the wave holding u * total
+  // walks its chunks.
+  {
+    long long acc = 0;
+#pragma unroll
+    for (int j = 0; j < kFastChunks; ++j) {
+      const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
+    }
+    acc = wave_reduce_dpp(acc, OpSum());
+    if (split) acc += (long long)sh.wtie[wave] * mtie;
+    if (lane == 0) atomicAdd((unsigned long long*)&sh.wtot[wave], (unsigned long long)acc);
+  }
   auto pen_kept = [&](uint32_t kb, int32_t id) {
     if (L == 0u || kb > L) return true;
     if (kb < L) return false;
@@ -626,65 +764,14 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
     return false;
   };
-  auto unpen_kept = [&](uint32_t k, long long idx) {
-    return k > kKeyNegInf && (L == 0u || k > L || (k == L && (keep >= 1) && (cut_idx < 0 || idx <= cut_idx)));
-  };
-  // Mass table over the kept keys' top 32 binades per sign.  Values too
-  // small to move v - max (|v| < ulp(max) / 2) all have the mass of 0; a kept
-  // key in neither hands the row over.
-  const int epos = uni((Mk & 0x8000u) ? (int)((Mk ^ 0x8000u) >> 7) : -1);
-  const uint32_t kneg = L ? L : Kmin;  // most negative kept value's key
-  const int eneg = uni((kneg < 0x8000u && kneg > kKeyNegInf) ? (int)((kneg ^ 0x7FFFu) >> 7) : -1);
-  const double tiny = uni(M != 0.0 ? ldexp(1.0, ilogb(M) - 53) : 0.0);
-  const double e_zero = uni(mass_of(0.0));
-  lds_barrier();  // every read of the key counts is done
-  for (int i = tid; i < kLutSize; i += kThreads) {
-    const int half = i / (kLutBinades * 128), s = (i / 128) % kLutBinades, mant = i & 127;
-    const int ex = (half ? eneg : epos) - s;
-    double m = 0.0;
-    if (ex >= 0) {
-      const uint32_t bits = ((uint32_t)ex << 7) | (uint32_t)mant;
-      const uint32_t k = half ? (bits ^ 0x7FFFu) : (bits | 0x8000u);
-      if (k > kKeyNegInf && k < kKeyPosInf && k <= Mk && (L == 0u || k >= L)) m = mass_of(bf16_key_value(k));
+  for (int64_t e = tid; e < pn; e += kThreads) {
+    const long long pk = Wp[e];
+    if (pk == 0) continue;
+    const int32_t id = a.pen_ids[o0 + e];
+    if (pen_kept((uint32_t)((unsigned long long)pk >> 48), id)) {
+      const int w = (int)((uint32_t)(id >> 3) / CW);
+      atomicAdd((unsigned long long*)&sh.wtot[w], (unsigned long long)(pk & ((1ll << 47) - 1)));
     }
-    sh.big.cdf.lut[i] = m;
-  }
-  if (tid < kWaves) sh.wtot[tid] = 0;
-  lds_barrier();
-  // Mass of a register-resident token (0 when not kept); `miss` when its key
-  // is outside the table.
-  auto unpen_e = [&](uint32_t k, long long idx, int& miss) -> double {
-    if (!unpen_kept(k, idx)) return 0.0;
-    const int sl = lut_slot(k, epos, eneg);
-    if (sl >= 0) return sh.big.cdf.lut[sl];
-    if (fabs(bf16_key_value(k)) < tiny) return e_zero;
-    miss = 1;
-    return 0.0;
-  };
-  // Kept mass per wave (index order is wave-major).
-  {
-    long long acc = 0;
-    int miss = 0;
-#pragma unroll
-    for (int j = 0; j < kFastChunks; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
-#pragma unroll 1
-      for (int e = 0; e < 8; ++e) acc += to_fx(unpen_e(key_at(d[j], e), 8ll * c + e, miss));
-    }
-    acc = wave_reduce_dpp(acc, OpSum());
-    if (lane == 0) atomicAdd((unsigned long long*)&sh.wtot[wave], (unsigned long long)acc);
-    for (int64_t e = tid; e < pn; e += kThreads) {
-      const long long pk = Wp[e];
-      if (pk == 0) continue;
-      const uint32_t kb = (uint32_t)((unsigned long long)pk >> 48);
-      const int32_t id = a.pen_ids[o0 + e];
-      if (pen_kept(kb, id)) {
-        const int w = (int)((uint32_t)(id >> 3) / CW);
-        atomicAdd((unsigned long long*)&sh.wtot[w], (unsigned long long)(pk & ((1ll << 47) - 1)));
-      }
-    }
-    if (bs.max((uint32_t)miss)) return kHandCapacity;
   }
   lds_barrier();
   if (tid == 0) {
@@ -694,22 +781,23 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   lds_barrier();
   if (sh.bc_l[1] != Sk) return kHandCapacity;  // the per-wave masses must add up to the kept total
+
   if (dense) {
-    // Kept probabilities mass / kept total in float64 (from the masses, not
-    // the fixed-point sums), zero elsewhere; kept bits mark every finite
-    // token (no top-k on this path).
+    // Kept probabilities mass / kept total in float64 (recomputed, not the
+    // fixed-point masses), zero elsewhere; kept bits mark every finite token
+    // (no top-k on this path).
     fast_clear_outputs(a, row);
     const double Sd = (double)Sk * 0x1p-45;
 #pragma unroll
     for (int j = 0; j < kFastChunks; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
       const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
 #pragma unroll 1
       for (int e = 0; e < 8; ++e) {
-        const uint32_t k = key_at(d[j], e);
+        const uint32_t k = key_at_rt(d[j], e);
         if (k > kKeyNegInf) {
-          int miss = 0;
-          fast_scatter(a, row, 8ll * c + e, unpen_e(k, 8ll * c + e, miss) / Sd);
+          const long long idx = 8ll * c + e;
+          const bool kept = L == 0u || k > L || (k == L && keep > 0 && (!split || idx <= cut_idx));
+          fast_scatter(a, row, idx, kept ? mass_of(bf16_key_value(k)) / Sd : 0.0);
         }
       }
     }
@@ -737,12 +825,13 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
   }
-  const double thr_d = u * (double)Sk;
-  long long thr = (long long)thr_d;
+  const double thr_d = uni(u * (double)Sk);
+  long long thr = uni((long long)thr_d);
   if (thr >= Sk) {
     thr = Sk - 1;
     flags |= DSR_FLAG_MARGIN;
   }
+  flags = uni(flags);
   // The wave holding thr, and the mass before it.
   if (tid == 0) {
     long long base = 0, obase = 0;
@@ -758,72 +847,113 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     sh.bc_l[0] = obase;
   }
   lds_barrier();
-  const int ow = sh.bc_i[0];
+  const int ow = uni(sh.bc_i[0]);
   if (ow < 0) return kHandCapacity;  // unreachable: thr < Sk
-  const long long obase = sh.bc_l[0];
-  // Penalised masses of that wave's tokens, by token offset.
-  const int64_t wlo = (int64_t)ow * CW * 8;
-  for (int i = tid; i < kLutSize; i += kThreads) sh.big.cdf.pm[i] = 0;
+  const long long obase = uni(sh.bc_l[0]);
+  // Kept penalised mass per chunk of that wave.
+  for (int i = tid; i < 1024; i += kThreads) sh.mid.cm.pen[i] = 0;
   lds_barrier();
   for (int64_t e = tid; e < pn; e += kThreads) {
     const long long pk = Wp[e];
     if (pk == 0) continue;
     const int32_t id = a.pen_ids[o0 + e];
-    const int64_t off = (int64_t)id - wlo;
-    if (off >= 0 && off < (int64_t)CW * 8 && pen_kept((uint32_t)((unsigned long long)pk >> 48), id))
-      sh.big.cdf.pm[off] = pk & ((1ll << 47) - 1);
+    const int64_t cw = (int64_t)(id >> 3) - (int64_t)ow * CW;
+    if (cw >= 0 && cw < (int64_t)CW && pen_kept((uint32_t)((unsigned long long)pk >> 48), id))
+      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cw], (unsigned long long)(pk & ((1ll << 47) - 1)));
+  }
+  if (tid < 8) sh.pe[tid] = 0;
+  if (tid == 0) {
+    sh.bc_i[1] = -1;
+    sh.bc_i[2] = 1;
   }
   lds_barrier();
-  // That wave walks its chunks in index order (slot, lane, element).
+  // That wave adds the kept mass of its register-resident tokens to each of
+  // its chunks (one slot per chunk), then finds the chunk holding thr by an
+  // ordered scan of the chunk masses in LDS.
   if (wave == ow) {
-    long long runw = obase;
-    long long tok = -1;
 #pragma unroll
     for (int j = 0; j < kFastChunks; ++j) {
       __builtin_amdgcn_sched_barrier(0);
-      if (tok < 0) {  // uniform over the wave
-        const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
-        const uint32_t c = (uint32_t)wave * CW + cw;
-        int miss = 0;
-        long long cm = 0;
-#pragma unroll 1
-        for (int e = 0; e < 8; ++e) {
-          cm += to_fx(unpen_e(key_at(d[j], e), 8ll * c + e, miss));
-          if (cw < CW) cm += sh.big.cdf.pm[8 * cw + e];
-        }
-        const long long incl = wave_scan_dpp(cm);
-        const long long ex = runw + incl - cm;
-        const bool hit = cm > 0 && ex <= thr && thr < ex + cm;
-        const unsigned long long hb = __ballot(hit);
-        if (hb) {
-          long long t = -1;
-          if (hit) {
-            long long x = ex, tex = 0, tfx = 0;
-#pragma unroll 1
-            for (int e = 0; e < 8; ++e) {
-              long long f = to_fx(unpen_e(key_at(d[j], e), 8ll * c + e, miss));
-              if (cw < CW) f += sh.big.cdf.pm[8 * cw + e];
-              if (t < 0 && f > 0 && x <= thr && thr < x + f) {
-                t = 8ll * c + e;
-                tex = x;
-                tfx = f;
-              }
-              x += f;
-            }
-            const double tol = ((double)npos_k + 16.0) * 0x1p-50 * (double)Sk + (double)npos_k + 2.0;
-            unsigned fl = flags;
-            if ((double)(tex + tfx) - thr_d <= tol || (tex > 0 && thr_d - (double)tex <= tol)) fl |= DSR_FLAG_MARGIN;
-            fast_write_result(a, row, DSR_OK, t, 1, fl);
-          }
-          tok = __shfl(t, __ffsll((long long)hb) - 1);
-        }
-        runw += lane_value(incl, 63);
+      const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
+      const uint32_t c = (uint32_t)wave * CW + cw;
+      uint4 v = d[j];  // opaque copy: the per-wave pass's table reads are redone, not kept live
+      asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+      long long cm = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cm += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
+      if (split) {  // tie members at or before cut_idx
+        const long long lim = cut_idx - 8ll * c;
+        const uint32_t m = key_bits(v, L);
+        const uint32_t km = lim < 0 ? 0u : (lim >= 7 ? m : m & ((2u << lim) - 1u));
+        cm += (long long)__popc(km) * mtie;
       }
+      if (cw < CW) sh.mid.cm.reg[cw] = cm;
     }
-    if (lane == 0) sh.bc_i[1] = tok < 0 ? 1 : 0;
   }
   lds_barrier();
-  return sh.bc_i[1] ? kHandCapacity : 0;  // unreachable: the crossing lies in the wave found above
+  if (wave == ow) {
+    long long runw = obase;
+    for (uint32_t b0 = 0; b0 < CW; b0 += 64u) {
+      const uint32_t cw = b0 + (uint32_t)lane;
+      const long long cm = cw < CW ? sh.mid.cm.pen[cw] + sh.mid.cm.reg[cw] : 0ll;
+      const long long incl = wave_scan_dpp(cm);
+      const long long ex = runw + incl - cm;
+      const bool hit = cm > 0 && ex <= thr && thr < ex + cm;
+      if (__ballot(hit)) {
+        if (hit) {
+          sh.bc_i[1] = (int)((uint32_t)wave * CW + cw);
+          sh.bc_l[0] = ex;
+        }
+        break;
+      }
+      runw += lane_value(incl, 63);
+    }
+  }
+  lds_barrier();
+  const int cstar = uni(sh.bc_i[1]);
+  if (cstar < 0) return kHandCapacity;  // unreachable: the crossing lies in the wave found above
+  // Kept penalised masses of that chunk, by element; then its lane walks it.
+  for (int64_t e = tid; e < pn; e += kThreads) {
+    const long long pk = Wp[e];
+    if (pk == 0) continue;
+    const int32_t id = a.pen_ids[o0 + e];
+    if ((id >> 3) == cstar && pen_kept((uint32_t)((unsigned long long)pk >> 48), id))
+      sh.pe[id & 7] = pk & ((1ll << 47) - 1);
+  }
+  lds_barrier();
+  if (wave == ow) {
+    const uint32_t cw = (uint32_t)cstar - (uint32_t)ow * CW;  // slot and lane of the crossing chunk
+    const int js = uni((int)(cw >> 6));
+    uint4 v = d[0];
+#pragma unroll
+    for (int j = 1; j < kFastChunks; ++j)
+      if (js == j) v = d[j];
+    if ((uint32_t)lane == (cw & 63u)) {
+      const uint32_t c = (uint32_t)cstar;
+      long long x = sh.bc_l[0], tok = -1, tex = 0, tfx = 0;
+#pragma unroll 1
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t k = key_at_rt(v, e);
+        const long long idx = 8ll * c + e;
+        long long f = key_fx(k) + sh.pe[e];
+        if (split && k == L && idx <= cut_idx) f += mtie;
+        if (tok < 0 && f > 0 && x <= thr && thr < x + f) {
+          tok = idx;
+          tex = x;
+          tfx = f;
+        }
+        x += f;
+      }
+      const double tol = ((double)npos_k + 16.0) * 0x1p-50 * (double)Sk + (double)npos_k + 2.0;
+      unsigned fl = flags;
+      if ((double)(tex + tfx) - thr_d <= tol || (tex > 0 && thr_d - (double)tex <= tol)) fl |= DSR_FLAG_MARGIN;
+      if (tok >= 0) fast_write_result(a, row, DSR_OK, tok, 1, fl);
+      sh.bc_i[2] = tok < 0 ? 1 : 0;
+    }
+  }
+  lds_barrier();
+  return sh.bc_i[2] ? kHandCapacity : 0;  // unreachable: thr lies inside the chunk found above
 }
 
 }  // namespace dsr
