@@ -1,15 +1,23 @@
-"""Sampled rows/s of the fused sampling kernel on one MI355X.
+"""Throughput of the fused sampling kernels on one MI355X.
 
-Workload: 256 rows x 129,280-token bf16 logits with a heavy tail (N(0,1) plus
-32 spikes of +U[8,15] per row), per-row temperature U[0.2,1.5], top-k
-U{1..1024}, top-p U[0.5,1], a packed allow bitmask disallowing 10% of
-tokens, one pre-drawn uniform per row.  Inputs are resident in HBM before
-the timed region; one step is one ``dsr_sample_rows`` launch over the batch.
+Default workload (c3, the headline): 256 rows x 129,280-token bf16 logits
+with a heavy tail (N(0,1) plus 32 spikes of +U[8,15] per row), per-row
+temperature U[0.2,1.5], top-k U{1..1024}, top-p U[0.5,1], a packed allow
+bitmask disallowing 10% of tokens, one pre-drawn uniform per row.  Inputs are
+resident in HBM before the timed region; one step is one ``dsr_sample_rows``
+launch over the batch.
 
-Prints one JSON line with rows/s, the roofline of the kernel (algorithmic
-HBM bytes / measured kernel time against 8 TB/s) and the CPU baseline: the
-float64 oracle (a restatement of the reference's NumPy sampler) timed on the
-host cores over all 256 rows of the same workload.
+``--workload`` selects one of the other seeded row families instead (see
+deepseekrpc_amd/workloads.py): c1 (1 fp32 row with probabilities out), c2 (64
+bf16 rows with 4,096-token histories), c4 (32 verifier requests x 4 fp32
+drafts; one step is one ``dsr_verify_drafts`` call) and c5 (1,024 bf16 rows,
+mixed greedy, 16,384-token histories).
+
+Prints one JSON line: the throughput, the roofline of the step (algorithmic
+HBM bytes / HIP-event time of the launches on their stream, against 8 TB/s)
+and the CPU baseline: the float64 oracle (a restatement of the reference's
+NumPy sampler) timed on the host cores over a bounded sample of the same
+workload, on every core and per core.
 """
 from __future__ import annotations
 
@@ -25,30 +33,85 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PEAK_HBM_GBS = 8000.0
 
+# name -> (metric, unit, CPU sample passes over the workload's rows, kernels of one step)
+WORKLOADS = {
+    "c3": ("sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline", "rows/s", 5,
+           "k_sample_bf16_fast"),
+    "c1": ("sampled rows/sec at B=1×V=129,280 fp32 with fp32 probabilities out", "rows/s", 1000,
+           "k_sample_general"),
+    "c2": ("sampled rows/sec at B=64×V=129,280 bf16 with 4,096-token histories", "rows/s", 20,
+           "k_sample_bf16_full"),
+    "c4": ("verify-rows/sec at B=32 requests × K=4 drafts × V=129,280 fp32", "verify-rows/s", 60,
+           "k_verify_dists + k_verify_stats + k_verify_chain + k_verify_draw + k_verify_finish"),
+    "c5": ("sampled rows/sec at B=1024×V=129,280 bf16, mixed greedy, 16,384-token histories", "rows/s", 2,
+           "k_sample_bf16_full"),
+}
 
-_CPU_WORKLOAD = None
+DESCRIPTIONS = {
+    "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
+    "c2": "c2: 64 rows x 129280 bf16 N(0,3^2), 4096-token generated histories, rep 1.1 / pres 0.5 / freq 0.3, "
+          "T 1, top-p 0.95",
+    "c3": "c3: 256 rows x 129280 bf16 heavy-tail logits, per-row T/top-k/top-p, 10% allow mask",
+    "c4": "c4: 32 requests x 4 drafts, fp32 target [32,5,129280] and draft [32,4,129280], default policy, limit 10",
+    "c5": "c5: 1024 rows x 129280 bf16 (N(0,1) / near-flat with 8-way max ties), even rows greedy, odd rows T 1 "
+          "top-p 0.9, rep 1.1 / pres 0.5 / freq 0.3 over 16384-token histories",
+}
+
+_CPU = {}
+
+
+def _units(name, w):
+    """Rows of a sampling workload; requests of the verifier workload."""
+    return w.extra["target"].shape[0] if name == "c4" else w.rows
+
+
+def _draft_ids_cpu(e, r):
+    """Draft ids of request r drawn from its draft rows by the oracle (the
+    proposal step the GPU run performs with the sampling kernel)."""
+    from oracle import sampling_oracle as O
+    ids = []
+    for j in range(e["K"]):
+        ids.append(O.sample_row(e["draft"][r][j], O.Policy(), float(e["u_draft"][r][j]), keep_probs=False).token)
+    return ids
 
 
 def _cpu_rows(span):
     from oracle import sampling_oracle as O
-    w = _CPU_WORKLOAD
+    w, name = _CPU["w"], _CPU["name"]
     lo, hi = span
-    t0 = time.perf_counter()
+    V = w.logits.shape[1]
+    jobs = []
     for r in range(lo, hi):
-        O.sample_row(w.logits[r], O.Policy(**w.policies[r]), float(w.uniforms[r]), allowed=w.allowed[r],
-                     keep_probs=False)
+        r = r % _units(name, w)
+        if name == "c4":
+            jobs.append((r, _draft_ids_cpu(w.extra, r)))
+        else:
+            counts = None
+            if w.histories is not None:
+                counts = np.bincount(np.asarray(w.histories[r]), minlength=V).astype(np.int32)
+            jobs.append((r, counts))
+    t0 = time.perf_counter()  # input preparation above is not timed
+    for r, x in jobs:
+        if name == "c4":
+            e = w.extra
+            O.verify(e["target"][r], e["draft"][r], x, O.Policy(), e["u_accept"][r], float(e["u_target"][r]),
+                     output_limit=int(e["limit"][r]))
+        else:
+            allowed = None if w.allowed is None else w.allowed[r]
+            O.sample_row(w.logits[r], O.Policy(**w.policies[r]), float(w.uniforms[r]), x, x, None, allowed,
+                         keep_probs=name == "c1")
     return hi - lo, time.perf_counter() - t0
 
 
-def cpu_baseline(w, passes=2):
-    """Oracle rows/s on the host cores: one forked worker per core, rows split
-    evenly; run before the GPU is initialised.  Only the mapped work is timed."""
-    global _CPU_WORKLOAD
-    _CPU_WORKLOAD = w
+def cpu_baseline(name, w, passes):
+    """Oracle throughput on the host cores: one forked worker per core (at
+    most 16), the sample split evenly; run before the GPU is initialised."""
+    _CPU.update(w=w, name=name)
     os.environ["OMP_NUM_THREADS"] = "1"
     cores = min(16, os.cpu_count() or 1)
-    edges = np.linspace(0, w.rows, cores + 1).astype(int)
-    spans = [(int(a), int(b)) for a, b in zip(edges[:-1], edges[1:])] * passes
+    total = _units(name, w) * passes
+    edges = np.linspace(0, total, cores + 1).astype(int)
+    spans = [(int(a), int(b)) for a, b in zip(edges[:-1], edges[1:]) if b > a]
     with mp.get_context("fork").Pool(cores) as pool:
         pool.map(_cpu_rows, [(0, 1)] * cores)            # warm the workers
         t0 = time.perf_counter()
@@ -56,10 +119,34 @@ def cpu_baseline(w, passes=2):
         wall = time.perf_counter() - t0
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
-    return {"value": n / wall, "unit": "rows/s", "cores": cores, "kind": "port",
-            "sample": f"{passes} passes over all {w.rows} rows of the same workload ({n} rows, {busy:.1f} s of CPU "
-                      f"work) with the float64 NumPy oracle on {cores} worker processes; "
-                      f"{n / busy:.1f} rows/s per core"}
+    unit = WORKLOADS[name][1]
+    return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port", "value_per_core": n / busy,
+            "sample": f"{n} {'requests' if name == 'c4' else 'rows'} ({passes} pass(es) over the {_units(name, w)} of the "
+                      f"same workload, {busy:.1f} s of CPU work) with the float64 NumPy oracle on {cores} worker "
+                      f"processes; {n / busy:.2f} {unit} per core"}
+
+
+def _prepare(name, w):
+    """Device inputs and a launch closure for one step of the workload."""
+    import torch
+
+    from deepseekrpc_amd import batch, workloads
+    if name == "c4":
+        e = w.extra
+        R, K, V = e["target"].shape[0], e["K"], e["target"].shape[2]
+        tgt = torch.from_numpy(e["target"]).cuda()
+        drf = torch.from_numpy(e["draft"]).cuda()
+        draw = batch.sample_rows(drf.reshape(R * K, V), [dict()] * (R * K),
+                                 uniforms=torch.from_numpy(e["u_draft"].reshape(-1)).cuda())
+        ids = draw.tokens.reshape(R, K).contiguous()
+        prep = batch.PreparedVerify(tgt, drf, ids, [dict()] * R, torch.from_numpy(e["u_accept"]).cuda(),
+                                    torch.from_numpy(e["u_target"]).cuda(), torch.from_numpy(e["limit"]).cuda())
+        return prep, workloads.algorithmic_bytes_verify(w), R
+    d = workloads.to_device(w)
+    prep = batch.PreparedSample(d.logits, d.policies, history=d.history, allow_bits=d.allow_bits,
+                                uniforms=d.uniforms, probs="f32" if name == "c1" else None)
+    probs_bytes = 4 * w.logits.shape[1] if name == "c1" else 0
+    return prep, workloads.algorithmic_bytes(w, probs_bytes), w.rows
 
 
 def main():
@@ -67,6 +154,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain copy kernel over the batch's logit bytes (for HBM counter scaling)")
@@ -77,16 +165,16 @@ def main():
         sys.exit(2)
 
     from deepseekrpc_amd import workloads
-    w = workloads.c3()
-    cpu = None if args.no_cpu_baseline else cpu_baseline(w)
+    name = args.workload
+    metric, unit, passes, kernels = WORKLOADS[name]
+    w = getattr(workloads, name)()
+    cpu = None if args.no_cpu_baseline else cpu_baseline(name, w, passes)
 
     import torch
     from deepseekrpc_amd import _native as N
-    from deepseekrpc_amd import batch
 
     N.load()
-    d = workloads.to_device(w)
-    prep = batch.PreparedSample(d.logits, d.policies, allow_bits=d.allow_bits, uniforms=d.uniforms)
+    prep, alg_bytes, units = _prepare(name, w)
     torch.cuda.synchronize()
     res = prep.result
     status = res.status.cpu().numpy()
@@ -98,7 +186,7 @@ def main():
     torch.cuda.synchronize()
     # The timed region: K back-to-back steps on the launch stream, bracketed by
     # synchronisation (host wall clock) and by HIP events on that stream
-    # (average launch duration of the kernel).
+    # (average duration of one step's launches).
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -112,31 +200,29 @@ def main():
     status = res.status.cpu().numpy()
     if (status != 0).any():
         raise SystemExit("kernel reported row errors in the timed region")
-    fast_rows = int(((res.flags.cpu().numpy() & N.FLAG_GENERAL) == 0).sum())
+    general = int(((res.flags.cpu().numpy() & N.FLAG_GENERAL) != 0).sum())
     if args.copy_calibration:
         # A plain read-N/write-N kernel over the batch's logit bytes, for
         # scaling the FETCH_SIZE / WRITE_SIZE counters.
-        src = d.logits.view(torch.int32).reshape(-1)
+        src = prep.inputs[0].view(torch.int32).reshape(-1) if name != "c4" else prep.inputs[0][0].reshape(-1)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
             torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
 
-    rows = w.rows
     ms_per_step = wall * 1e3 / args.steps
-    alg_bytes = workloads.algorithmic_bytes(w)
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     traffic = None
-    tf = os.path.join(ROOT, "profiles", "k_sample_bf16_fast_c3_traffic.json")
+    tf = os.path.join(ROOT, "profiles", f"{kernels.split(' ')[0]}_{name}_traffic.json")
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("bytes_per_launch")
+    cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]),
+           "general_path_rows": general, "kernels": kernels}
     line = {
-        "metric": "sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline",
-        "value": rows / (ms_per_step * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "c3: 256 rows x 129280 bf16 heavy-tail logits, per-row T/top-k/top-p, 10% allow mask",
-                   "rows": rows, "vocab": int(w.logits.shape[1]), "fast_path_rows": fast_rows},
+        "vs_baseline": None, "dtype": "bf16" if w.dtype == "bf16" else "f32", "data": "synthetic",
+        "config": cfg,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel_ms": kern_ms,
                      "algorithmic_bytes": alg_bytes},

@@ -298,6 +298,7 @@ class VerifyResult:
     used_target: torch.Tensor
     status: torch.Tensor
     flags: torch.Tensor
+    args: object = None  # the marshalled dsr_verify_args_t
 
 
 def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, policies, u_accept: torch.Tensor,
@@ -358,8 +359,27 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     a.out_used_accept, a.out_used_target = res.used_accept.data_ptr(), res.used_target.data_ptr()
     a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    res.args = a
     N.check(lib.dsr_verify_drafts(ctypes.byref(a), _stream()), "dsr_verify_drafts")
     return res
+
+
+class PreparedVerify:
+    """A ``dsr_verify_drafts`` call whose arguments are marshalled once;
+    ``launch()`` re-issues it on the current stream, overwriting the outputs."""
+
+    def __init__(self, *args, **kw):
+        self.workspace = kw.pop("workspace", None) or Workspace()
+        self.inputs = (args, kw)
+        self.result = verify_drafts(*args, workspace=self.workspace, **kw)
+        self.args = self.result.args
+        self._lib = N.load()
+
+    def launch(self):
+        rc = self._lib.dsr_verify_drafts(ctypes.byref(self.args), _stream())
+        if rc != 0:
+            N.check(rc, "dsr_verify_drafts")
+        return self.result
 
 
 # ---------------------------------------------------------------------------
