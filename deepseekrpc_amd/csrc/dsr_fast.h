@@ -75,6 +75,7 @@ struct FastLists {
   uint16_t kkey[kFastMaxK];                // kept tokens, index order
   uint32_t kidx[kFastMaxK];
   uint32_t wn[kWaves];
+  uint32_t polw[16];                       // the row's policy words, then its uniform
   long long sel_above;
   int sel;
   int bc_i[2];
@@ -250,14 +251,18 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
 
   // ---- one HBM pass, every load issued up front in the order it is used,
   // as raw buffer loads (vector memory, so the waits stay in issue order;
-  // out-of-range reads return 0): the two policy fields needed right after
-  // pass 1 (temperature, top_k), then for each register slot j the chunk's
-  // allow byte and its 16 bytes of logits.  The rest of the policy and the
-  // uniform are fetched after pass 1, so their registers stay free during it.
+  // out-of-range reads return 0): first one word per thread of the policy
+  // (threads 0-13) and of the uniform (threads 14-15), parked in LDS by the
+  // set-up below (waiting for them never waits for the row), then for each
+  // register slot j the chunk's allow byte and its 16 bytes of logits.
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.policy + row), (short)0, (int)sizeof(dsr_policy_t), 0x00020000);
-  const auto pT = __builtin_amdgcn_raw_buffer_load_b64(prs, 0, 0, 0);
-  const uint32_t pK = __builtin_amdgcn_raw_buffer_load_b32(prs, 48, 0, 0);
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+      a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy, (short)0, a.uniforms ? 8 : 0, 0x00020000);
+  constexpr int kPolWords = (int)(sizeof(dsr_policy_t) / 4);
+  const uint32_t pw = __builtin_amdgcn_raw_buffer_load_b32(prs, tid < kPolWords ? 4 * tid : 0x7FFFFFF0, 0, 0) |
+                      __builtin_amdgcn_raw_buffer_load_b32(
+                          urs, (tid >= kPolWords && tid < kPolWords + 2) ? 4 * (tid - kPolWords) : 0x7FFFFFF0, 0, 0);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
       a.allow_bits ? (void*)(a.allow_bits + row * a.allow_ld) : (void*)&kAllowAll, (short)0, (int)C, 0x00020000);
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -285,6 +290,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     uint4* zm = (uint4*)&sh.mass[0];   // 4096 x 8 bytes of mass
 #pragma unroll
     for (int i = 0; i < 2; ++i) zm[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < kPolWords + 2) sh.polw[tid] = pw;
   }
   lds_barrier();  // LDS only: the row's loads keep streaming
 
@@ -324,24 +330,21 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   for (int i = 0; i < kFastChunks / 2; ++i) asm volatile("" : "+v"(cmx[i]));
   asm volatile("" : "+v"(g[0]), "+v"(g[1]), "+v"(g[2]), "+v"(g[3]), "+v"(vmax_s), "+v"(vmax_u));
   const int gmax = max(max(g[0], g[1]), max(g[2], g[3]));
-  // The policy is read only now: waiting for it earlier would stall pass 1
-  // behind the whole batch's loads.
   __builtin_amdgcn_sched_barrier(0);
-  const double T = __builtin_bit_cast(
-      double, ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)pT[1]) << 32) |
-                  (uint32_t)__builtin_amdgcn_readfirstlane((int)pT[0]));
-  const int top_k = __builtin_amdgcn_readfirstlane((int)pK);
+  dsr_policy_t pol;
+  double u;
+  {
+    uint32_t w[kPolWords + 2];
+#pragma unroll
+    for (int i = 0; i < kPolWords + 2; ++i) w[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)sh.polw[i]);
+    __builtin_memcpy(&pol, w, sizeof(pol));
+    u = __builtin_bit_cast(double, ((unsigned long long)w[kPolWords + 1] << 32) | w[kPolWords]);
+  }
+  const double T = pol.temperature;
+  const int top_k = pol.top_k;
   const bool greedy = T == 0.0;
   if (!(T >= 0.0 && T <= 100.0)) return kHandPolicy;
   if (!greedy && !(top_k >= 1 && top_k <= kFastMaxK && top_k < V)) return kHandTopK;
-  // Late loads: the remaining policy fields and the row's uniform.
-  const auto pq1 = __builtin_amdgcn_raw_buffer_load_b128(prs, 8, 0, 0);   // top_p, min_p
-  const auto pq2 = __builtin_amdgcn_raw_buffer_load_b128(prs, 24, 0, 0);  // repetition, presence
-  const auto pq3 = __builtin_amdgcn_raw_buffer_load_b64(prs, 40, 0, 0);   // frequency
-  const uint32_t pR = __builtin_amdgcn_raw_buffer_load_b32(prs, 52, 0, 0);  // reserved
-  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
-      a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy, (short)0, a.uniforms ? 8 : 0, 0x00020000);
-  const auto uq = __builtin_amdgcn_raw_buffer_load_b64(urs, 0, 0, 0);
 
   const uint32_t bad = max((int)(short)(vmax_s & 0xFFFFu), (int)(short)(vmax_s >> 16)) >= 0x7F80 ||
                        max(vmax_u & 0xFFFFu, vmax_u >> 16) >= 0xFF81u;
@@ -402,14 +405,6 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     }
   }
   const uint32_t Mkey = (uint32_t)(Ms + 0x8000);
-  dsr_policy_t pol;
-  {
-    uint32_t pw[14] = {(uint32_t)pT[0], (uint32_t)pT[1], pq1[0], pq1[1], pq1[2], pq1[3], pq2[0],
-                       pq2[1], pq2[2], pq2[3], pq3[0], pq3[1], pK, pR};
-#pragma unroll
-    for (int i = 0; i < 14; ++i) pw[i] = (uint32_t)__builtin_amdgcn_readfirstlane((int)pw[i]);
-    __builtin_memcpy(&pol, pw, sizeof(pol));
-  }
 
   // ---- compact the chunks whose maximum reaches tau, whole, in index order.
   uint32_t wn = 0;
@@ -434,7 +429,6 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   lds_barrier();
 
   if (!policy_ok(pol)) return kHandPolicy;
-  const double u = __builtin_bit_cast(double, ((unsigned long long)uq[1] << 32) | uq[0]);
 
   if (greedy) {  // sampling.py:82-85: the first listed chunk holds the first maximum
     if (tid == 0) {
