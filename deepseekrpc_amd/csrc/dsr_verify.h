@@ -13,11 +13,12 @@
 // only moves it by rounding, so each row is summarised by its maximum M, the
 // first index holding it and s1 = sum exp((v - M) / T).  Those come out of
 // one pass over the logits (an online maximum / rescaled sum per thread),
-// split over kVerifySplit workgroups per row and combined by whichever of
-// them finishes last.  The accept chain needs p and q only at the draft ids;
-// the one replacement or bonus draw per request is spread over kDrawSplit
-// workgroups (slice sums, then the last one walks the slice that holds the
-// crossing).  Dropping the renormalisation by total ~ 1 (sampling.py:103-106)
+// split over kVerifySplit workgroups per row (k_verify_stats) and combined
+// at the start of the next kernel (k_verify_chain): kernel boundaries order
+// the shares, so no device-scope fence is needed.  The accept chain needs p
+// and q only at the draft ids; the one replacement or bonus draw per request
+// is spread over kDrawSplit workgroups (slice sums in k_verify_draw, then
+// k_verify_finish walks the slice that holds the crossing).  Dropping the renormalisation by total ~ 1 (sampling.py:103-106)
 // perturbs each probability by at most a few hundred ulps, so accept tests
 // within 2^-40 relative of the uniform are reported with DSR_FLAG_MARGIN.
 #pragma once
