@@ -86,6 +86,7 @@ struct FullShared {
   uint32_t kpos[64];
   long long wtot[kWaves];
   uint32_t wtie[kWaves];
+  int32_t elo[kWaves + 1];    // first history entry whose token lies at or after wave w's chunks; elo[16] = pn
   long long pe[8];            // kept penalised masses of the crossing chunk, by element
   double etab[64];
   SyncSlots sync;
@@ -159,6 +160,35 @@ __device__ __forceinline__ uint32_t key_bits(const uint4& v, uint32_t L) {
   return m;
 }
 
+constexpr int kPenBatch = 4;  // history entries per thread whose loads are in flight together
+
+// Visits this thread's history entries e = first + kThreads * i in batches of
+// kPenBatch: fetch(e) for the whole batch first (fetch(-1) for entries past
+// the end must not load), so the batch's global loads are in flight together
+// and the loop waits once per batch instead of once per entry; then
+// body(e, fetched) in entry order.
+template <class F, class B>
+__device__ __forceinline__ void pen_batches(int64_t pn, int64_t first, F fetch, B body) {
+  for (int64_t base = first; base < pn; base += (int64_t)kPenBatch * kThreads) {
+    decltype(fetch((int64_t)0)) x[kPenBatch];
+#pragma unroll
+    for (int i = 0; i < kPenBatch; ++i) {
+      const int64_t e = base + (int64_t)i * kThreads;
+      x[i] = fetch(e < pn ? e : (int64_t)-1);
+    }
+#pragma unroll
+    for (int i = 0; i < kPenBatch; ++i) {
+      const int64_t e = base + (int64_t)i * kThreads;
+      if (e < pn) body(e, x[i]);
+    }
+  }
+}
+
+struct PenPk {  // a history entry's packed mass word and token id
+  long long pk;
+  int32_t id;
+};
+
 // Whether history entry e of a row changes its token (count or generated count positive).
 __device__ __forceinline__ bool pen_touches(long long c, long long g) { return c > 0 || g > 0; }
 
@@ -224,15 +254,17 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
 #pragma unroll
     for (int i = 0; i < 8; ++i) zc[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < 64) sh.etab[tid] = etv;
+    if (tid <= kWaves) sh.elo[tid] = (int32_t)pn;
   }
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < kPenPre; ++i)
     if (pid[i] >= 0 && pid[i] < V) atomicAnd(&sh.mid.p1.pbits[pid[i] >> 5], ~(1u << (pid[i] & 31)));
-  for (int64_t e = tid + (int64_t)kPenPre * kThreads; e < pn; e += kThreads) {  // long histories
-    const int32_t id = a.pen_ids[o0 + e];
-    if (id >= 0 && id < V) atomicAnd(&sh.mid.p1.pbits[id >> 5], ~(1u << (id & 31)));
-  }
+  pen_batches(  // long histories
+      pn, tid + (int64_t)kPenPre * kThreads, [&](int64_t e) { return e >= 0 ? a.pen_ids[o0 + e] : -1; },
+      [&](int64_t, int32_t id) {
+        if (id >= 0 && id < V) atomicAnd(&sh.mid.p1.pbits[id >> 5], ~(1u << (id & 31)));
+      });
   lds_barrier();
 
   // ---- pass 1, chunk by chunk as the loads land: keys, with masked and
@@ -277,28 +309,54 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   double pmax = -INFINITY;
   long long pfirst = LLONG_MAX;
   const uint32_t* allow = a.allow_bits ? a.allow_bits + row * a.allow_ld : nullptr;
-  for (int64_t e = tid; e < pn; e += kThreads) {
-    const int32_t id = a.pen_ids[o0 + e];
-    const long long c = a.pen_count[o0 + e], g = a.pen_gen[o0 + e];
-    const bool ok = id >= 0 && id < V && (e == 0 || a.pen_ids[o0 + e - 1] < id) && c >= 0 && c <= DSR_MAX_COUNT &&
-                    g >= 0 && g <= c;
-    bad |= ok ? 0 : 1;
-    csum += c;
-    double v = -INFINITY;
-    if (ok) {
-      const uint32_t raw = ((const uint16_t*)a.logits)[row * a.ld + id];
-      double x = (double)__uint_as_float(raw << 16);
-      if (c > 0) x = x >= 0.0 ? x / pol.repetition_penalty : x * pol.repetition_penalty;
-      const double pen = pol.presence_penalty * (g > 0 ? 1.0 : 0.0) + pol.frequency_penalty * (double)g;
-      v = x - pen;
-      if (!allowed_bit(allow, id)) v = -INFINITY;
-      if (v != v) v = -INFINITY;  // NaN logits are caught by the raw check below
-      if (v > pmax) {  // ids increase with e: the first holder of the maximum stays
-        pmax = v;
-        pfirst = id;
-      }
+  // kPenBatch entries per thread at a time: their ids, counts and the previous
+  // ids are fetched together, then their logits are gathered together.
+  for (int64_t base = tid; base < pn; base += (int64_t)kPenBatch * kThreads) {
+    int32_t id[kPenBatch], prv[kPenBatch], c[kPenBatch], g[kPenBatch];
+#pragma unroll
+    for (int i = 0; i < kPenBatch; ++i) {
+      const int64_t e = base + (int64_t)i * kThreads;
+      const bool in = e < pn;
+      id[i] = in ? a.pen_ids[o0 + e] : 0;
+      prv[i] = (in && e > 0) ? a.pen_ids[o0 + e - 1] : INT_MIN;
+      c[i] = in ? a.pen_count[o0 + e] : 0;
+      g[i] = in ? a.pen_gen[o0 + e] : 0;
     }
-    Wv[e] = v;
+    uint32_t raw[kPenBatch];
+    bool ok[kPenBatch];
+#pragma unroll
+    for (int i = 0; i < kPenBatch; ++i) {
+      const int64_t e = base + (int64_t)i * kThreads;
+      ok[i] = e < pn && id[i] >= 0 && id[i] < V && prv[i] < id[i] && c[i] >= 0 && c[i] <= DSR_MAX_COUNT &&
+              g[i] >= 0 && g[i] <= c[i];
+      raw[i] = ok[i] ? ((const uint16_t*)a.logits)[row * a.ld + id[i]] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kPenBatch; ++i) {
+      const int64_t e = base + (int64_t)i * kThreads;
+      if (e >= pn) continue;
+      bad |= ok[i] ? 0 : 1;
+      csum += c[i];
+      {  // ids increase with e: this entry starts the run of every wave after its predecessor's, up to its own
+        const int wv = id[i] < 0 ? -1 : (int)min((uint32_t)id[i] / 8u / CW, (uint32_t)kWaves - 1u);
+        const int wp = prv[i] < 0 ? -1 : (int)min((uint32_t)prv[i] / 8u / CW, (uint32_t)kWaves - 1u);
+        for (int w = wp + 1; w <= wv; ++w) sh.elo[w] = (int32_t)e;
+      }
+      double v = -INFINITY;
+      if (ok[i]) {
+        double x = (double)__uint_as_float(raw[i] << 16);
+        if (c[i] > 0) x = x >= 0.0 ? x / pol.repetition_penalty : x * pol.repetition_penalty;
+        const double pen = pol.presence_penalty * (g[i] > 0 ? 1.0 : 0.0) + pol.frequency_penalty * (double)g[i];
+        v = x - pen;
+        if (!allowed_bit(allow, id[i])) v = -INFINITY;
+        if (v != v) v = -INFINITY;  // NaN logits are caught by the raw check below
+        if (v > pmax) {  // ids increase with e: the first holder of the maximum stays
+          pmax = v;
+          pfirst = id[i];
+        }
+      }
+      Wv[e] = v;
+    }
   }
 
   // ---- row maximum over keys and penalised values; invalid rows hand over.
@@ -422,21 +480,21 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     if (bs.sum(nlive) != bs.sum(real)) return kHandCapacity;
   }
   // Penalised tokens: mass, floor key, added to the block of their floor key.
-  for (int64_t e = tid; e < pn; e += kThreads) {
-    const double v = Wv[e];
-    long long packed = 0;
-    if (v > -(double)INFINITY) {
-      const double m0 = exp_nonpos((v - M) / T, etab);
-      if (min_p != 0.0 && m0 > 0.0 && fabs(m0 - min_p) <= min_p * 0x1p-48) close = 1;
-      const double m = m0 < min_p ? 0.0 : m0;
-      const long long fx = to_fx(m);
-      const uint32_t kb = floor_key(v);
-      atomicAdd((unsigned long long*)&sh.mid.blk.bm[kb >> 6], (unsigned long long)fx);
-      if (m > 0.0) atomicAdd(&sh.mid.blk.bp[kb >> 6], 1u);
-      packed = fx | (m > 0.0 ? (1ll << 47) : 0ll) | ((long long)kb << 48);
-    }
-    Wp[e] = packed;
-  }
+  pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? Wv[e] : -(double)INFINITY; },
+              [&](int64_t e, double v) {
+                long long packed = 0;
+                if (v > -(double)INFINITY) {
+                  const double m0 = exp_nonpos((v - M) / T, etab);
+                  if (min_p != 0.0 && m0 > 0.0 && fabs(m0 - min_p) <= min_p * 0x1p-48) close = 1;
+                  const double m = m0 < min_p ? 0.0 : m0;
+                  const long long fx = to_fx(m);
+                  const uint32_t kb = floor_key(v);
+                  atomicAdd((unsigned long long*)&sh.mid.blk.bm[kb >> 6], (unsigned long long)fx);
+                  if (m > 0.0) atomicAdd(&sh.mid.blk.bp[kb >> 6], 1u);
+                  packed = fx | (m > 0.0 ? (1ll << 47) : 0ll) | ((long long)kb << 48);
+                }
+                Wp[e] = packed;
+              });
   lds_barrier();
   if (bs.max((uint32_t)close)) flags |= DSR_FLAG_MARGIN;
 
@@ -476,14 +534,14 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     if (B < 0) return kHandCapacity;  // unreachable: the running mass reaches tgt <= S
     const long long AB = sh.bc_l[0];
     const uint32_t posAB = (uint32_t)sh.bc_i[1];
-    for (int64_t e = tid; e < pn; e += kThreads) {
-      const long long pk = Wp[e];
-      const uint32_t kb = (uint32_t)((unsigned long long)pk >> 48);
-      if (pk != 0 && (int)(kb >> 6) == B) {
-        atomicAdd((unsigned long long*)&sh.kmass[kb & 63u], (unsigned long long)(pk & ((1ll << 47) - 1)));
-        if ((pk >> 47) & 1) atomicAdd(&sh.kpos[kb & 63u], 1u);
-      }
-    }
+    pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? Wp[e] : 0ll; },
+                [&](int64_t, long long pk) {
+                  const uint32_t kb = (uint32_t)((unsigned long long)pk >> 48);
+                  if (pk != 0 && (int)(kb >> 6) == B) {
+                    atomicAdd((unsigned long long*)&sh.kmass[kb & 63u], (unsigned long long)(pk & ((1ll << 47) - 1)));
+                    if ((pk >> 47) & 1) atomicAdd(&sh.kpos[kb & 63u], 1u);
+                  }
+                });
     lds_barrier();
     if (wave == 0) {  // keys of block B, descending, one per lane
       const uint32_t k = 64u * (uint32_t)B + 63u - (uint32_t)lane;
@@ -512,8 +570,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     mtie = uni(sh.bc_l[2]);
     const int tie_pos = sh.bc_i[5];
     // Penalised values in the boundary bucket and its two neighbours.
-    for (int64_t e = tid; e < pn; e += kThreads) {
-      const long long pk = Wp[e];
+    pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? Wp[e] : 0ll; }, [&](int64_t e, long long pk) {
       const uint32_t kb = (uint32_t)((unsigned long long)pk >> 48);
       if (pk != 0 && kb + 1u >= L && kb <= L + 1u) {
         const int slot = atomicAdd(&sh.nitems, 1);
@@ -527,7 +584,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
           sh.items[slot] = it;
         }
       }
-    }
+    });
     lds_barrier();
     const int nit = sh.nitems;
     if (nit > kPenItems) return kHandCapacity;
@@ -764,15 +821,13 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
     return false;
   };
-  for (int64_t e = tid; e < pn; e += kThreads) {
-    const long long pk = Wp[e];
-    if (pk == 0) continue;
-    const int32_t id = a.pen_ids[o0 + e];
-    if (pen_kept((uint32_t)((unsigned long long)pk >> 48), id)) {
-      const int w = (int)((uint32_t)(id >> 3) / CW);
-      atomicAdd((unsigned long long*)&sh.wtot[w], (unsigned long long)(pk & ((1ll << 47) - 1)));
+  auto fetch_pk = [&](int64_t e) { return e >= 0 ? PenPk{Wp[e], a.pen_ids[o0 + e]} : PenPk{0ll, 0}; };
+  pen_batches(pn, tid, fetch_pk, [&](int64_t, PenPk x) {
+    if (x.pk != 0 && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
+      const int w = (int)((uint32_t)(x.id >> 3) / CW);
+      atomicAdd((unsigned long long*)&sh.wtot[w], (unsigned long long)(x.pk & ((1ll << 47) - 1)));
     }
-  }
+  });
   lds_barrier();
   if (tid == 0) {
     long long base = 0;
@@ -853,14 +908,13 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // Kept penalised mass per chunk of that wave.
   for (int i = tid; i < 1024; i += kThreads) sh.mid.cm.pen[i] = 0;
   lds_barrier();
-  for (int64_t e = tid; e < pn; e += kThreads) {
-    const long long pk = Wp[e];
-    if (pk == 0) continue;
-    const int32_t id = a.pen_ids[o0 + e];
-    const int64_t cw = (int64_t)(id >> 3) - (int64_t)ow * CW;
-    if (cw >= 0 && cw < (int64_t)CW && pen_kept((uint32_t)((unsigned long long)pk >> 48), id))
-      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cw], (unsigned long long)(pk & ((1ll << 47) - 1)));
-  }
+  // Only the run of entries whose tokens lie in that wave's chunks.
+  const int64_t elo = sh.elo[ow], ehi = sh.elo[ow + 1];
+  pen_batches(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
+    const int64_t cw = (int64_t)(x.id >> 3) - (int64_t)ow * CW;
+    if (x.pk != 0 && cw >= 0 && cw < (int64_t)CW && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id))
+      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cw], (unsigned long long)(x.pk & ((1ll << 47) - 1)));
+  });
   if (tid < 8) sh.pe[tid] = 0;
   if (tid == 0) {
     sh.bc_i[1] = -1;
@@ -914,13 +968,10 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   const int cstar = uni(sh.bc_i[1]);
   if (cstar < 0) return kHandCapacity;  // unreachable: the crossing lies in the wave found above
   // Kept penalised masses of that chunk, by element; then its lane walks it.
-  for (int64_t e = tid; e < pn; e += kThreads) {
-    const long long pk = Wp[e];
-    if (pk == 0) continue;
-    const int32_t id = a.pen_ids[o0 + e];
-    if ((id >> 3) == cstar && pen_kept((uint32_t)((unsigned long long)pk >> 48), id))
-      sh.pe[id & 7] = pk & ((1ll << 47) - 1);
-  }
+  pen_batches(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
+    if (x.pk != 0 && (x.id >> 3) == cstar && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id))
+      sh.pe[x.id & 7] = x.pk & ((1ll << 47) - 1);
+  });
   lds_barrier();
   if (wave == ow) {
     const uint32_t cw = (uint32_t)cstar - (uint32_t)ow * CW;  // slot and lane of the crossing chunk
