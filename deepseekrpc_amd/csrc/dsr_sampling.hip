@@ -303,17 +303,28 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
   if (L.fast_inputs) {
     const dim3 grid((unsigned)(a.rows * slots * kVerifySplit));
-    if (a.dtype == DSR_BF16) hipLaunchKernelGGL(k_verify_stats<DSR_BF16>, grid, dim3(kStatThreads), 0, s, a, L);
-    else if (a.dtype == DSR_F32) hipLaunchKernelGGL(k_verify_stats<DSR_F32>, grid, dim3(kStatThreads), 0, s, a, L);
-    else hipLaunchKernelGGL(k_verify_stats<DSR_F64>, grid, dim3(kStatThreads), 0, s, a, L);
+    // 16-byte loads when every row starts on a 16-byte boundary.
+    const size_t elt = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
+    const bool vec = ((uintptr_t)a.target & 15u) == 0 && (a.K == 0 || ((uintptr_t)a.draft & 15u) == 0) &&
+                     ((size_t)a.ld * elt) % 16 == 0;
+    if (a.dtype == DSR_BF16) {
+      if (vec) hipLaunchKernelGGL((k_verify_stats<DSR_BF16, true>), grid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_stats<DSR_BF16, false>), grid, dim3(kStatThreads), 0, s, a, L);
+    } else if (a.dtype == DSR_F32) {
+      if (vec) hipLaunchKernelGGL((k_verify_stats<DSR_F32, true>), grid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_stats<DSR_F32, false>), grid, dim3(kStatThreads), 0, s, a, L);
+    } else {
+      if (vec) hipLaunchKernelGGL((k_verify_stats<DSR_F64, true>), grid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_stats<DSR_F64, false>), grid, dim3(kStatThreads), 0, s, a, L);
+    }
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
   }
   hipLaunchKernelGGL(k_verify_chain, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
   if (L.fast_inputs) {
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_verify_draw, dim3((unsigned)(a.rows * kDrawSplit)), dim3(kThreads), 0, s, a, L);
+    hipLaunchKernelGGL(k_verify_draw, dim3((unsigned)(a.rows * kDrawSplit)), dim3(kStatThreads), 0, s, a, L);
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
+    hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
   }
   return launched();
 }

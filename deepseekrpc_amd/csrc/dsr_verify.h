@@ -23,6 +23,8 @@
 // within 2^-40 relative of the uniform are reported with DSR_FLAG_MARGIN.
 #pragma once
 
+#include <type_traits>
+
 #include "dsr_general.h"
 
 namespace dsr {
@@ -30,9 +32,11 @@ namespace dsr {
 constexpr int kStatThreads = 256;   // statistics workgroups: 4 waves, several resident per CU
 constexpr int kStatWaves = kStatThreads / 64;
 constexpr int kStatPer = 16;        // logits per thread of one share
-constexpr int kVerifySplit = 32;    // shares (workgroups) per distribution row
-static_assert((int64_t)kVerifySplit * kStatThreads * kStatPer >= DSR_MAX_VOCAB, "a share must fit in registers");
-constexpr int kDrawSplit = 8;    // workgroups per request (replacement / bonus draw)
+constexpr int kVerifySplit = 32;    // shares per distribution row
+constexpr int kDrawSplit = 32;   // workgroups per request (replacement / bonus draw)
+constexpr int kDrawBlocks = kStatWaves * kStatPer;  // 64-token blocks per draw workgroup (one per wave step)
+constexpr int kDrawParts = kDrawSplit * kDrawBlocks;  // block partial sums per request
+static_assert((int64_t)kDrawParts * 64 >= DSR_MAX_VOCAB, "the draw blocks cover a row");
 constexpr size_t kDecisionBytes = 64;
 
 struct VerifyStat {  // one distribution row, fast path
@@ -65,6 +69,7 @@ struct VerifyLayout {
   VerifyStat* stat;  // [rows * slots]
   VerifyPart* part;  // [rows * slots * kVerifySplit]
   DrawPart* dpart;   // [rows * kDrawSplit]
+  double* bsum;      // [rows * kDrawParts]: weight sum of each 64-token block of a pending draw
   struct Decision* dec;  // [rows] chain outcome handed to the draw kernels
   int64_t rows;
   int fast_inputs;   // no history, bias or allow mask
@@ -79,6 +84,7 @@ __host__ __device__ inline size_t verify_ws_bytes(int64_t rows, int32_t K, int64
   b += (size_t)rows * slots * sizeof(VerifyStat);
   b += (size_t)rows * slots * kVerifySplit * sizeof(VerifyPart);
   b += (size_t)rows * kDrawSplit * sizeof(DrawPart);
+  b += (size_t)rows * kDrawParts * sizeof(double);
   b += (size_t)rows * kDecisionBytes;
   return b;
 }
@@ -98,6 +104,8 @@ __host__ inline VerifyLayout verify_layout(void* ws, int64_t rows, int32_t K, in
   p += (size_t)rows * L.slots * kVerifySplit * sizeof(VerifyPart);
   L.dpart = (DrawPart*)p;
   p += (size_t)rows * kDrawSplit * sizeof(DrawPart);
+  L.bsum = (double*)p;
+  p += (size_t)rows * kDrawParts * sizeof(double);
   L.dec = (struct Decision*)p;
   L.rows = rows;
   L.fast_inputs = 0;
@@ -114,10 +122,28 @@ __device__ __forceinline__ const char* verify_logits(const dsr_verify_args_t& a,
                    : (const char*)a.draft + ((size_t)row * K + (slot - K - 1)) * (size_t)a.ld * esz;
 }
 
+// The policy of request `row` read through the constant address space: the
+// index is uniform, so the loads are scalar and waiting for them never waits
+// for vector loads in flight.  The policy array is not written by any kernel.
+__device__ __forceinline__ dsr_policy_t policy_of(const dsr_verify_args_t& a, int64_t row) {
+  typedef const __attribute__((address_space(4))) dsr_policy_t* CP;
+  const CP p = (CP)(uintptr_t)a.policy + row;
+  dsr_policy_t r;
+  r.temperature = p->temperature;
+  r.top_p = p->top_p;
+  r.min_p = p->min_p;
+  r.repetition_penalty = p->repetition_penalty;
+  r.presence_penalty = p->presence_penalty;
+  r.frequency_penalty = p->frequency_penalty;
+  r.top_k = p->top_k;
+  r.reserved = p->reserved;
+  return r;
+}
+
 // Whether request `row` takes the fast path (uniform over its workgroups).
 __device__ __forceinline__ bool verify_fast_row(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row) {
   if (!L.fast_inputs) return false;
-  const dsr_policy_t& p = a.policy[row];
+  const dsr_policy_t p = policy_of(a, row);
   return policy_ok(p) && (p.top_k == 0 || p.top_k >= a.vocab) && p.top_p >= 1.0 && p.min_p == 0.0;
 }
 
@@ -421,75 +447,165 @@ template <class T, class Op>
 __device__ __forceinline__ T stat_reduce(T x, T* slot, T id, Op op) {
   x = wave_reduce_dpp(x, op);
   if (lane_id() == 0) slot[wave_id()] = x;
-  __syncthreads();
+  lds_barrier();  // LDS only: loads in flight for the next share keep streaming
   T y = id;
 #pragma unroll
   for (int w = 0; w < kStatWaves; ++w) y = op(y, slot[w]);
   return y;
 }
 
+// Share g of a row is [g * seg, (g + 1) * seg) with seg a multiple of 8, so
+// every share starts on a 16-byte boundary of an aligned row.
+__host__ __device__ inline int64_t stat_segment(int64_t V) {
+  return ((V + kVerifySplit - 1) / kVerifySplit + 7) & ~(int64_t)7;
+}
+static_assert((int64_t)kVerifySplit * kStatThreads * kStatPer >= (((DSR_MAX_VOCAB + kVerifySplit - 1) / kVerifySplit + 7) & ~7) * kVerifySplit,
+              "a rounded share must fit in registers");
+
 // Step 1: one share of one row, held in registers: its maximum, the first
 // index holding it, sum exp((v - max) / T) and the NaN/+inf / finite flags.
-template <int DT>
-__global__ __launch_bounds__(kStatThreads) void k_verify_stats(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ double etab[64];
-  __shared__ double sf[2][kStatWaves];
-  __shared__ long long si[2][kStatWaves];
-  __shared__ uint32_t su[kStatWaves];
-  const int64_t rs = blockIdx.x / kVerifySplit;
-  const int g = (int)(blockIdx.x % kVerifySplit);
-  const int64_t row = rs / L.slots;
-  const int slot = (int)(rs % L.slots);
-  if (!verify_fast_row(a, L, row)) return;
-  const double T = a.policy[row].temperature;
-  const bool greedy = T == 0.0;
-  const char* base = verify_logits(a, row, slot);
-  const int64_t V = a.vocab;
-  const int64_t seg = (V + kVerifySplit - 1) / kVerifySplit;
-  const int64_t lo = (int64_t)g * seg < V ? (int64_t)g * seg : V;
-  const int64_t hi = lo + seg < V ? lo + seg : V;
+// VEC (rows 16-byte aligned): 16-byte loads, load q of thread t holding
+// elements lo + (q * kStatThreads + t) * W .. + W - 1 (W per 16 bytes), so
+// each load instruction reads 4 KB in one piece; otherwise element
+// lo + t + u * kStatThreads.  Either way a thread's elements increase with
+// u, so a strict comparison keeps the first maximum.  Each thread sums its
+// exps against its own maximum as soon as its loads land (no workgroup step
+// in between) and rescales once by exp((m_t - M) / T).
+struct StatShared {
+  double etab[64];
+  double sf[2][kStatWaves];
+  long long si[kStatWaves];
+  uint32_t su[kStatWaves];
+};
+
+// Share g of distribution rs: [lo, hi) and the index of the u-th element a
+// thread holds.  VEC (rows 16-byte aligned): 16-byte loads, load q of thread
+// t holding elements lo + (q * kStatThreads + t) * W .. + W - 1 (W per 16
+// bytes), so each load instruction reads 4 KB in one piece; otherwise element
+// lo + t + u * kStatThreads.  Either way a thread's elements increase with u.
+template <int DT, bool VEC>
+struct StatItem {
   using X = typename LogitT<DT>::T;
-  X x[kStatPer];
-#pragma unroll
-  for (int u = 0; u < kStatPer; ++u) {
-    const int64_t i = lo + threadIdx.x + (int64_t)u * kStatThreads;
-    x[u] = i < hi ? logit_as<DT>(base, i) : -(X)INFINITY;
+  static constexpr int kElt = DT == DSR_BF16 ? 2 : (int)sizeof(X);
+  static constexpr int W = 16 / kElt;
+  int64_t rs, lo, hi;
+  int g;
+  __device__ StatItem(const dsr_verify_args_t& a, int64_t item) {
+    rs = item / kVerifySplit;
+    g = (int)(item % kVerifySplit);
+    const int64_t V = a.vocab, seg = stat_segment(V);
+    lo = (int64_t)g * seg < V ? (int64_t)g * seg : V;
+    hi = lo + seg < V ? lo + seg : V;
   }
-  exp_table_init(etab);
+  __device__ __forceinline__ int64_t index_of(int u) const {
+    const int t = threadIdx.x;
+    if constexpr (VEC) return lo + ((int64_t)(u / W) * kStatThreads + t) * W + (u % W);
+    else return lo + t + (int64_t)u * kStatThreads;
+  }
+  // The raw words of this thread's elements: 16-byte vectors (VEC) or one
+  // element per slot at a clamped index; decoded and masked by value().
+  static constexpr int kRaw = VEC ? kStatPer / W : kStatPer;
+  using Raw = typename std::conditional<VEC, uint4, X>::type;
+  // Issues this thread's loads; nothing here waits for them.
+  __device__ __forceinline__ void load(const dsr_verify_args_t& a, const VerifyLayout& L, Raw* r) const {
+    const char* base = verify_logits(a, rs / L.slots, (int)(rs % L.slots));
+    if constexpr (VEC) {
+      // The row as a buffer: out-of-range vectors read as 0 and are masked by value().
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(a.vocab * kElt), 0x00020000);
+#pragma unroll
+      for (int q = 0; q < kRaw; ++q) {
+        const int64_t e0 = index_of(q * W);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(e0 < hi ? e0 * kElt : 0x7FFFFFF0), 0, 0);
+        r[q] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kStatPer; ++u) {
+        const int64_t i = index_of(u);
+        r[u] = logit_as<DT>(base, i < hi ? i : (hi > 0 ? hi - 1 : 0));
+      }
+    }
+  }
+  // Element u (-inf outside [lo, hi)).
+  __device__ __forceinline__ double value(const Raw* r, int u) const {
+    X y;
+    if constexpr (VEC) {
+      const uint4 v = r[u / W];
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+      const int e = u % W;
+      if constexpr (DT == DSR_BF16) y = __uint_as_float(((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
+      else if constexpr (DT == DSR_F32) y = __uint_as_float(w4[e]);
+      else y = __longlong_as_double((long long)(((unsigned long long)w4[2 * e + 1] << 32) | w4[2 * e]));
+    } else {
+      y = r[u];
+    }
+    return index_of(u) < hi ? (double)y : -(double)INFINITY;
+  }
+};
+
+// One share held in registers -> its maximum, the first index holding it,
+// sum exp((v - max) / T) and the NaN/+inf / finite flags.  A strict
+// comparison in increasing index order keeps the first maximum.  Each thread
+// sums its exps against its own maximum and rescales once by
+// exp((m_t - M) / T), so the exps need no workgroup step before them.
+template <int DT, bool VEC>
+__device__ __forceinline__ void stat_share(const dsr_verify_args_t& a, const VerifyLayout& L,
+                                           const StatItem<DT, VEC>& it, const typename StatItem<DT, VEC>::Raw* x,
+                                           StatShared& sm) {
+  const double* etab = sm.etab;
+  const int64_t row = it.rs / L.slots;
+  if (!verify_fast_row(a, L, row)) return;  // uniform over the workgroup
+  const double T = policy_of(a, row).temperature;
+  const bool greedy = T == 0.0;
   double m = -INFINITY;
   long long am = LLONG_MAX;
   uint32_t fl = 0;  // 1: NaN / +inf, 2: a finite value
 #pragma unroll
   for (int u = 0; u < kStatPer; ++u) {
-    const double v = (double)x[u];
+    const double v = it.value(x, u);
     fl |= (v != v || v == INFINITY) ? 1u : 0u;
     fl |= (v > -(double)INFINITY && v < (double)INFINITY) ? 2u : 0u;
-    if (v > m && v < (double)INFINITY) {  // increasing index order: the first maximum stays
+    if (v > m && v < (double)INFINITY) {
       m = v;
-      am = lo + threadIdx.x + (int64_t)u * kStatThreads;
+      am = it.index_of(u);
     }
   }
-  const double Mg = stat_reduce(m, sf[0], -(double)INFINITY, OpMax());
-  const uint32_t flags = stat_reduce(fl, su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
-  const long long amg = stat_reduce(m == Mg && m > -INFINITY ? am : LLONG_MAX, si[0], LLONG_MAX, OpMin());
+  const double iT = greedy ? 0.0 : 1.0 / T;
   double s = 0.0;
-  if (!greedy && Mg > -INFINITY) {
-    const double iT = 1.0 / T;
+  if (!greedy && m > -(double)INFINITY) {
 #pragma unroll
     for (int u = 0; u < kStatPer; ++u) {
-      const double v = (double)x[u];
-      if (v > -(double)INFINITY && v < (double)INFINITY) s += exp_nonpos((v - Mg) * iT, etab);
+      const double v = it.value(x, u);
+      if (v > -(double)INFINITY && v < (double)INFINITY) s += exp_nonpos((v - m) * iT, etab);
     }
   }
-  const double Sg = stat_reduce(s, sf[1], 0.0, OpSum());
+  const double Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
+  const uint32_t flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
+  const long long amg = stat_reduce(m == Mg && m > -INFINITY ? am : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
+  const double sc = s > 0.0 ? s * exp_nonpos((m - Mg) * iT, etab) : 0.0;
+  const double Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
   if (threadIdx.x == 0) {
     VerifyPart p;
     p.m = Mg;
     p.s = Sg;
     p.amax = amg == LLONG_MAX ? -1 : (int32_t)amg;
     p.flags = (int32_t)flags;
-    L.part[rs * kVerifySplit + g] = p;
+    L.part[it.rs * kVerifySplit + it.g] = p;
   }
+}
+
+// Step 1, one workgroup per share of every distribution row.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kStatThreads) void k_verify_stats(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ StatShared sm;
+  using It = StatItem<DT, VEC>;
+  const It it(a, blockIdx.x);
+  typename It::Raw x[It::kRaw];
+  it.load(a, L, x);
+  exp_table_init(sm.etab);
+  lds_barrier();
+  stat_share<DT, VEC>(a, L, it, x, sm);
 }
 
 // Combines the kVerifySplit shares of one row, in index order; called by
@@ -628,17 +744,14 @@ __device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, 
   return w;
 }
 
-__device__ __forceinline__ void draw_segment(int64_t V, int q, int64_t& lo, int64_t& hi) {
-  const int64_t seg = (V + kDrawSplit - 1) / kDrawSplit;
-  lo = (int64_t)q * seg < V ? (int64_t)q * seg : V;
-  hi = lo + seg < V ? lo + seg : V;
-}
-
-// Step 3: share g of a pending draw -> its weight sum, positive count and
-// first positive index.
-__global__ __launch_bounds__(kThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ GenShared sh;
+// Step 3: share g of a pending draw, 64-token blocks in index order, one
+// per wave step (lane l takes token l of the block, so each load is
+// coalesced): each block's weight sum is kept for step 4's search; the
+// share's sum, positive count and first positive index go to its DrawPart.
+__global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
   __shared__ double etab[64];
+  __shared__ double sf[kStatWaves];
+  __shared__ long long si[2][kStatWaves];
   const int64_t row = blockIdx.x / kDrawSplit;
   const int g = (int)(blockIdx.x % kDrawSplit);
   if (!verify_fast_row(a, L, row)) return;
@@ -647,89 +760,100 @@ __global__ __launch_bounds__(kThreads) void k_verify_draw(dsr_verify_args_t a, V
   exp_table_init(etab);
   __syncthreads();
   const DrawWeights wf = draw_weights(a, L, row, d, etab);
-  int64_t lo, hi;
-  draw_segment(a.vocab, g, lo, hi);
+  const int64_t V = a.vocab;
+  const int l = lane_id(), w = wave_id();
   double acc = 0.0;
   long long npos = 0, first = LLONG_MAX;
-  row_pass<double>(hi - lo, [&](int64_t i) { return wf(lo + i); }, [&](int64_t i, double w) {
-    acc += w;
-    if (w > 0.0) {
-      ++npos;
-      if (lo + i < first) first = lo + i;
-    }
-  });
-  acc = block_sum(acc, sh.b);
-  npos = block_sum_i64(npos, sh.b);
-  first = block_min_i64(first, sh.b);
+  double* bs = L.bsum + row * kDrawParts + (int64_t)g * kDrawBlocks;
+#pragma unroll
+  for (int u = 0; u < kStatPer; ++u) {
+    const int blk = w * kStatPer + u;                     // block within the share
+    const int64_t i = ((int64_t)g * kDrawBlocks + blk) * 64 + l;  // token of this lane
+    const double x = i < V ? wf(i) : 0.0;
+    const double sum = wave_reduce_dpp(x, OpSum());
+    const unsigned long long pb = __ballot(x > 0.0);
+    if (l == 0) bs[blk] = sum;
+    acc += sum;
+    npos += __popcll(pb);
+    if (pb && first == LLONG_MAX) first = i - l + (__ffsll((long long)pb) - 1);
+  }
+  // Blocks in index order: wave w holds blocks 16w .. 16w+15.
+  if (l == 0) {
+    sf[w] = acc;
+    si[0][w] = npos;
+    si[1][w] = first;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
     DrawPart p;
-    p.sum = acc;
-    p.npos = npos;
-    p.first = first;
+    p.sum = 0.0;
+    p.npos = 0;
+    p.first = LLONG_MAX;
+    for (int q = 0; q < kStatWaves; ++q) {
+      p.sum += sf[q];
+      p.npos += si[0][q];
+      if (si[1][q] < p.first) p.first = si[1][q];
+    }
     p.pad = 0;
     L.dpart[row * kDrawSplit + g] = p;
   }
 }
 
-// Slice sums in [lo, hi) by contiguous per-thread slices, a scan from `base`,
-// and wave 0 walking the slice of the thread that holds the crossing of thr.
+// The 64-token block of share `owner` that holds the crossing of thr: one
+// wave scans the share's block sums (one per lane, index order, from base),
+// takes the last block with mass starting at or below thr, and walks it.
+// margin is set when the decision sits within tol of a boundary or when
+// rounding left no crossing (the last positive token is taken).
+static_assert(kDrawBlocks == 64, "one block per lane");
 template <class WF>
-__device__ int64_t range_cdf_search(int64_t lo, int64_t hi, WF wf, double base, double thr, double tol,
-                                    GenShared& sh, int& margin) {
-  const int64_t n = hi - lo;
-  int64_t slo, shi;
-  thread_slice(n, slo, shi);
-  double part = 0.0;
-  slice_pass<double>(lo + slo, lo + shi, wf, [&](int64_t, double w) { part += w; });
-  double total;
-  const double ex = base + block_exclusive_scan_f64(part, sh.b, total);
-  const long long cand = (part > 0.0 && ex <= thr) ? (long long)threadIdx.x : -1;
-  const long long owner = block_max_i64(cand, sh.b);
-  if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(ex);
-  __syncthreads();
-  if (wave_id() == 0 && owner >= 0) {
-    int64_t olo, ohi;
-    slice_of(owner, n, olo, ohi);
-    int64_t tok;
-    int m;
-    wave_slice_cdf(wf, lo + olo, lo + ohi, __longlong_as_double(sh.bc[0]), thr, tol, tok, m);
-    if (lane_id() == 0) {
-      sh.bc[1] = tok;
-      sh.bc[2] = m;
-    }
+__device__ void block_cdf_search(int64_t V, const double* bsum, int owner, WF wf, double base, double thr,
+                                 double tol, int64_t& tok, int& margin) {
+  const int l = lane_id();
+  const double b = bsum[l];
+  const double incl = wave_scan_dpp(b);
+  double excl = __shfl_up(incl, 1);
+  if (l == 0) excl = 0.0;
+  const double start = base + excl;
+  const unsigned long long cb = __ballot(b > 0.0 && start <= thr);
+  const unsigned long long pb = __ballot(b > 0.0);
+  int m = 0, blk;
+  if (cb) {
+    blk = 63 - __clzll((long long)cb);
+  } else {
+    blk = pb ? 63 - __clzll((long long)pb) : 0;
+    m = 1;
   }
-  __syncthreads();
-  const int64_t tok = owner >= 0 ? (int64_t)sh.bc[1] : -1;
-  margin = owner < 0 || sh.bc[2] ? 1 : 0;
-  __syncthreads();
-  return tok;
+  const double bbase = __shfl(start, blk);
+  const int64_t lo = ((int64_t)owner * kDrawBlocks + blk) * 64;
+  const int64_t hi = lo + 64 < V ? lo + 64 : V;
+  int m2 = 0;
+  wave_slice_cdf(wf, lo, hi, bbase, thr, tol, tok, m2);
+  margin = m | m2;
 }
 
-// Step 4, one workgroup per request with a pending draw: combine the shares
-// in index order, then walk the share that holds the crossing of u * total.
-__global__ __launch_bounds__(kThreads) void k_verify_finish(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ GenShared sh;
+// Step 4, one wave per request with a pending draw: combine the shares in
+// index order, then search the share that holds the crossing of u * total.
+__global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, VerifyLayout L) {
   __shared__ double etab[64];
-  __shared__ Decision d;
   const int64_t row = blockIdx.x;
   if (!verify_fast_row(a, L, row)) return;
-  if (threadIdx.x == 0) d = L.dec[row];
+  Decision d = L.dec[row];
+  if (d.status != DSR_OK || d.next == 0) return;
   exp_table_init(etab);
   __syncthreads();
-  if (d.status != DSR_OK || d.next == 0) return;
   const DrawWeights wf = draw_weights(a, L, row, d, etab);
-  const DrawPart* parts = L.dpart + row * kDrawSplit;
-  double sums[kDrawSplit];
-  double total = 0.0;
-  long long n = 0, f = LLONG_MAX;
-#pragma unroll
-  for (int q = 0; q < kDrawSplit; ++q) {
-    const DrawPart p = parts[q];
-    sums[q] = p.sum;
-    total += p.sum;
-    n += p.npos;
-    if (p.npos > 0 && p.first < f) f = p.first;
-  }
+  // Lane q holds share q; sums and the share prefix come from fixed-order
+  // wave reductions and scans.
+  static_assert(kDrawSplit <= 64, "one share per lane");
+  const int l = lane_id();
+  DrawPart pq;
+  pq.sum = 0.0;
+  pq.npos = 0;
+  pq.first = LLONG_MAX;
+  if (l < kDrawSplit) pq = L.dpart[row * kDrawSplit + l];
+  const double total = wave_reduce_dpp(pq.sum, OpSum());
+  const long long n = wave_reduce_dpp(pq.npos, OpSum());
+  const long long f = wave_reduce_dpp(pq.npos > 0 ? pq.first : LLONG_MAX, OpMin());
   int64_t rep = -1;
   int used = 0, status = DSR_OK, margin = 0;
   if (wf.resid && (!(total > 0.0) || !isfinite(total))) {
@@ -743,34 +867,24 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(dsr_verify_args_t a,
     } else {
       used = 1;
       const double thr = u * total;
-      // The share holding the crossing: the last one with mass starting at or below thr.
-      double base = 0.0, obase = 0.0;
-      int owner = -1;
-#pragma unroll
-      for (int q = 0; q < kDrawSplit; ++q) {
-        if (sums[q] > 0.0 && base <= thr) {
-          owner = q;
-          obase = base;
-        }
-        base += sums[q];
-      }
-      if (owner < 0) {  // rounding left no share at or below thr: the last one with mass
-        base = 0.0;
-#pragma unroll
-        for (int q = 0; q < kDrawSplit; ++q) {
-          if (sums[q] > 0.0) {
-            owner = q;
-            obase = base;
-          }
-          base += sums[q];
-        }
+      // The share holding the crossing: the last one with mass starting at or
+      // below thr (else, rounding having left none, the last one with mass).
+      const double incl = wave_scan_dpp(pq.sum);
+      const double start = incl - pq.sum;
+      const unsigned long long cb = __ballot(pq.sum > 0.0 && start <= thr);
+      const unsigned long long pb = __ballot(pq.sum > 0.0);
+      int owner;
+      if (cb) {
+        owner = 63 - __clzll((long long)cb);
+      } else {
+        owner = pb ? 63 - __clzll((long long)pb) : 0;
         margin = 1;
       }
+      const double obase = __shfl(start, owner);
       const double tol = ((double)n + 16.0) * 0x1p-51 * total;
-      int64_t lo, hi;
-      draw_segment(a.vocab, owner, lo, hi);
       int m2 = 0;
-      rep = range_cdf_search(lo, hi, wf, obase, thr, tol, sh, m2);
+      block_cdf_search(a.vocab, L.bsum + row * kDrawParts + (int64_t)owner * kDrawBlocks, owner, wf, obase, thr, tol,
+                       rep, m2);
       margin |= m2;
     }
   }
