@@ -75,8 +75,8 @@ struct FullShared {
       uint32_t bc[1024];   // register-resident tokens per block
     } blk;
     struct {
-      long long pen[1024];  // kept penalised mass per chunk of the walking wave
-      long long reg[1024];  // kept register-resident mass per chunk of that wave
+      long long pe[512];    // kept penalised mass by element of the crossing slot's 64 chunks
+      long long pen[64];    // kept penalised mass per chunk of that slot
     } cm;
   } mid;
   uint16_t boff[512];         // binade -> mass-table slot (0: none)
@@ -85,9 +85,10 @@ struct FullShared {
   long long kmass[64];
   uint32_t kpos[64];
   long long wtot[kWaves];
-  uint32_t wtie[kWaves];
+  uint32_t wtie[kWaves];      // tie members of a split boundary group per wave
   int32_t elo[kWaves + 1];    // first history entry whose token lies at or after wave w's chunks; elo[16] = pn
-  long long pe[8];            // kept penalised masses of the crossing chunk, by element
+  long long smass[kWaves][kFastChunks];  // kept register-resident mass per (wave, register slot)
+  long long spen[kWaves][kFastChunks];   // kept penalised mass per (wave, register slot)
   double etab[64];
   SyncSlots sync;
   long long bc_l[4];
@@ -167,17 +168,17 @@ constexpr int kPenBatch = 4;  // history entries per thread whose loads are in f
 // the end must not load), so the batch's global loads are in flight together
 // and the loop waits once per batch instead of once per entry; then
 // body(e, fetched) in entry order.
-template <class F, class B>
+template <int NB = kPenBatch, class F, class B>
 __device__ __forceinline__ void pen_batches(int64_t pn, int64_t first, F fetch, B body) {
-  for (int64_t base = first; base < pn; base += (int64_t)kPenBatch * kThreads) {
-    decltype(fetch((int64_t)0)) x[kPenBatch];
+  for (int64_t base = first; base < pn; base += (int64_t)NB * kThreads) {
+    decltype(fetch((int64_t)0)) x[NB];
 #pragma unroll
-    for (int i = 0; i < kPenBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int64_t e = base + (int64_t)i * kThreads;
       x[i] = fetch(e < pn ? e : (int64_t)-1);
     }
 #pragma unroll
-    for (int i = 0; i < kPenBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int64_t e = base + (int64_t)i * kThreads;
       if (e < pn) body(e, x[i]);
     }
@@ -255,6 +256,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     for (int i = 0; i < 8; ++i) zc[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
     if (tid < 64) sh.etab[tid] = etv;
     if (tid <= kWaves) sh.elo[tid] = (int32_t)pn;
+    if (tid < kWaves * kFastChunks) sh.spen[tid / kFastChunks][tid % kFastChunks] = 0;
   }
   lds_barrier();
 #pragma unroll
@@ -695,8 +697,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   // Tie members of a split boundary group are kept up to the keep-th in
   // index order (wave, register slot, lane, element): ties per wave, then
-  // per slot, give each member its rank.  wtie[w] ends as the kept members
-  // of wave w.
+  // per slot, give each member its rank; cut_idx is the index of the last
+  // kept member.
   const bool split = keep > 0 && keep < n_tie;
   if (split) {
     auto ties_in = [&](const uint4& v) { return (uint32_t)__popc(key_bits(v, L)); };
@@ -737,12 +739,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       const uint32_t c = (uint32_t)wave * CW + fj * 64u + (uint32_t)lane;
       found = 8ll * c + e;
     }
-    lds_barrier();  // every wave has read wtie
     if (found >= 0) sh.bc_l[1] = found;
-    if (lane == 0) {
-      const long long kw = keep - (long long)base;  // kept members of this wave
-      sh.wtie[wave] = (uint32_t)(kw <= 0 ? 0 : (kw >= (long long)wsum ? wsum : kw));
-    }
     lds_barrier();
     cut_idx = uni(sh.bc_l[1]);
   }
@@ -797,18 +794,33 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   auto key_fx = [&](uint32_t k) -> long long {
     return sh.big.lut[((uint32_t)sh.boff[k >> 7] << 7) | (k & 127u)];
   };
-  // Index-order CDF: kept mass per wave, then the wave holding u * total
-  // walks its chunks.
+  // Index-order CDF: kept mass per (wave, register slot) -- slot j of wave w
+  // is the 64 consecutive chunks w*CW + 64j .. 64j + 63 -- and per wave; then
+  // the wave and slot holding u * total, and one lane of that slot walks its
+  // chunk.  Tie members of a split group count up to cut_idx.
+  auto chunk_mass = [&](const uint4& v, uint32_t c) -> long long {
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    long long cm = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cm += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
+    if (split) {
+      const long long lim = cut_idx - 8ll * c;
+      const uint32_t m = key_bits(v, L);
+      const uint32_t km = lim < 0 ? 0u : (lim >= 7 ? m : m & ((2u << lim) - 1u));
+      cm += (long long)__popc(km) * mtie;
+    }
+    return cm;
+  };
   {
     long long acc = 0;
 #pragma unroll
     for (int j = 0; j < kFastChunks; ++j) {
-      const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
+      const long long sj = wave_reduce_dpp(chunk_mass(d[j], c), OpSum());
+      if (lane == 0) sh.smass[wave][j] = sj;
+      acc += sj;
     }
-    acc = wave_reduce_dpp(acc, OpSum());
-    if (split) acc += (long long)sh.wtie[wave] * mtie;
     if (lane == 0) atomicAdd((unsigned long long*)&sh.wtot[wave], (unsigned long long)acc);
   }
   auto pen_kept = [&](uint32_t kb, int32_t id) {
@@ -824,8 +836,11 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   auto fetch_pk = [&](int64_t e) { return e >= 0 ? PenPk{Wp[e], a.pen_ids[o0 + e]} : PenPk{0ll, 0}; };
   pen_batches(pn, tid, fetch_pk, [&](int64_t, PenPk x) {
     if (x.pk != 0 && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
-      const int w = (int)((uint32_t)(x.id >> 3) / CW);
-      atomicAdd((unsigned long long*)&sh.wtot[w], (unsigned long long)(x.pk & ((1ll << 47) - 1)));
+      const uint32_t cid = (uint32_t)(x.id >> 3);
+      const int w = (int)(cid / CW), js = (int)((cid - (uint32_t)w * CW) >> 6);
+      const unsigned long long fx = (unsigned long long)(x.pk & ((1ll << 47) - 1));
+      atomicAdd((unsigned long long*)&sh.wtot[w], fx);
+      atomicAdd((unsigned long long*)&sh.spen[w][js], fx);
     }
   });
   lds_barrier();
@@ -888,6 +903,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   flags = uni(flags);
   // The wave holding thr, and the mass before it.
+  if (tid < 512) sh.mid.cm.pe[tid] = 0;
+  if (tid < 64) sh.mid.cm.pen[tid] = 0;
   if (tid == 0) {
     long long base = 0, obase = 0;
     int ow = -1;
@@ -900,94 +917,58 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
     sh.bc_i[0] = ow;
     sh.bc_l[0] = obase;
+    sh.bc_i[2] = 1;
   }
   lds_barrier();
   const int ow = uni(sh.bc_i[0]);
   if (ow < 0) return kHandCapacity;  // unreachable: thr < Sk
   const long long obase = uni(sh.bc_l[0]);
-  // Kept penalised mass per chunk of that wave.
-  for (int i = tid; i < 1024; i += kThreads) sh.mid.cm.pen[i] = 0;
-  lds_barrier();
-  // Only the run of entries whose tokens lie in that wave's chunks.
+  // The register slot of that wave holding thr, from its 16 slot masses in
+  // order (every wave finds the same one).
+  int js;
+  long long jbase;
+  {
+    const long long m = lane < kFastChunks ? sh.smass[ow][lane] + sh.spen[ow][lane] : 0ll;
+    const long long incl = wave_scan_dpp(m);
+    const long long ex = obase + incl - m;
+    const unsigned long long hb = __ballot(m > 0 && ex <= thr && thr < ex + m);
+    if (!hb) return kHandCapacity;  // unreachable: the crossing lies in the wave found above
+    js = uni(__ffsll((long long)hb) - 1);
+    jbase = uni(__shfl(ex, js));
+  }
+  const uint32_t cw0 = (uint32_t)ow * CW + (uint32_t)js * 64u;  // first chunk of that slot
+  // Kept penalised masses of that slot's chunks, per chunk and per element
+  // (only the run of entries whose tokens lie in the wave's chunks).
   const int64_t elo = sh.elo[ow], ehi = sh.elo[ow + 1];
-  pen_batches(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
-    const int64_t cw = (int64_t)(x.id >> 3) - (int64_t)ow * CW;
-    if (x.pk != 0 && cw >= 0 && cw < (int64_t)CW && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id))
-      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cw], (unsigned long long)(x.pk & ((1ll << 47) - 1)));
-  });
-  if (tid < 8) sh.pe[tid] = 0;
-  if (tid == 0) {
-    sh.bc_i[1] = -1;
-    sh.bc_i[2] = 1;
-  }
-  lds_barrier();
-  // That wave adds the kept mass of its register-resident tokens to each of
-  // its chunks (one slot per chunk), then finds the chunk holding thr by an
-  // ordered scan of the chunk masses in LDS.
-  if (wave == ow) {
-#pragma unroll
-    for (int j = 0; j < kFastChunks; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
-      const uint32_t c = (uint32_t)wave * CW + cw;
-      uint4 v = d[j];  // opaque copy: the per-wave pass's table reads are redone, not kept live
-      asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-      long long cm = 0;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) cm += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
-      if (split) {  // tie members at or before cut_idx
-        const long long lim = cut_idx - 8ll * c;
-        const uint32_t m = key_bits(v, L);
-        const uint32_t km = lim < 0 ? 0u : (lim >= 7 ? m : m & ((2u << lim) - 1u));
-        cm += (long long)__popc(km) * mtie;
-      }
-      if (cw < CW) sh.mid.cm.reg[cw] = cm;
+  pen_batches<1>(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
+    const uint32_t cid = (uint32_t)(x.id >> 3);
+    if (x.pk != 0 && cid >= cw0 && cid < cw0 + 64u && cid < (uint32_t)(ow + 1) * CW &&
+        pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
+      const long long fx = x.pk & ((1ll << 47) - 1);
+      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cid - cw0], (unsigned long long)fx);
+      sh.mid.cm.pe[(cid - cw0) * 8u + (uint32_t)(x.id & 7)] = fx;  // one entry per token
     }
-  }
-  lds_barrier();
-  if (wave == ow) {
-    long long runw = obase;
-    for (uint32_t b0 = 0; b0 < CW; b0 += 64u) {
-      const uint32_t cw = b0 + (uint32_t)lane;
-      const long long cm = cw < CW ? sh.mid.cm.pen[cw] + sh.mid.cm.reg[cw] : 0ll;
-      const long long incl = wave_scan_dpp(cm);
-      const long long ex = runw + incl - cm;
-      const bool hit = cm > 0 && ex <= thr && thr < ex + cm;
-      if (__ballot(hit)) {
-        if (hit) {
-          sh.bc_i[1] = (int)((uint32_t)wave * CW + cw);
-          sh.bc_l[0] = ex;
-        }
-        break;
-      }
-      runw += lane_value(incl, 63);
-    }
-  }
-  lds_barrier();
-  const int cstar = uni(sh.bc_i[1]);
-  if (cstar < 0) return kHandCapacity;  // unreachable: the crossing lies in the wave found above
-  // Kept penalised masses of that chunk, by element; then its lane walks it.
-  pen_batches(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
-    if (x.pk != 0 && (x.id >> 3) == cstar && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id))
-      sh.pe[x.id & 7] = x.pk & ((1ll << 47) - 1);
   });
   lds_barrier();
+  // The chunk of that slot holding thr (a scan over its 64 lanes), then that
+  // lane walks its 8 tokens.
   if (wave == ow) {
-    const uint32_t cw = (uint32_t)cstar - (uint32_t)ow * CW;  // slot and lane of the crossing chunk
-    const int js = uni((int)(cw >> 6));
     uint4 v = d[0];
 #pragma unroll
     for (int j = 1; j < kFastChunks; ++j)
       if (js == j) v = d[j];
-    if ((uint32_t)lane == (cw & 63u)) {
-      const uint32_t c = (uint32_t)cstar;
-      long long x = sh.bc_l[0], tok = -1, tex = 0, tfx = 0;
+    const uint32_t cw = (uint32_t)js * 64u + (uint32_t)lane;
+    const uint32_t c = (uint32_t)ow * CW + cw;
+    const long long cm = cw < CW ? chunk_mass(v, c) + sh.mid.cm.pen[lane] : 0ll;
+    const long long incl = wave_scan_dpp(cm);
+    const long long ex = jbase + incl - cm;
+    if (cm > 0 && ex <= thr && thr < ex + cm) {
+      long long x = ex, tok = -1, tex = 0, tfx = 0;
 #pragma unroll 1
       for (int e = 0; e < 8; ++e) {
         const uint32_t k = key_at_rt(v, e);
         const long long idx = 8ll * c + e;
-        long long f = key_fx(k) + sh.pe[e];
+        long long f = key_fx(k) + sh.mid.cm.pe[(uint32_t)lane * 8u + (uint32_t)e];
         if (split && k == L && idx <= cut_idx) f += mtie;
         if (tok < 0 && f > 0 && x <= thr && thr < x + f) {
           tok = idx;
