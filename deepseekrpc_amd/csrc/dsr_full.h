@@ -86,6 +86,8 @@ struct FullShared {
   uint32_t kpos[64];
   long long wtot[kWaves];
   uint32_t wtie[kWaves];      // tie members of a split boundary group per wave
+  uint32_t tslot[kWaves][kFastChunks];  // ... and per (wave, register slot)
+  int cut_w, cut_j, cut_r;    // wave, slot and rank within the slot of the last kept member
   int32_t elo[kWaves + 1];    // first history entry whose token lies at or after wave w's chunks; elo[16] = pn
   long long smass[kWaves][kFastChunks];  // kept register-resident mass per (wave, register slot)
   long long spen[kWaves][kFastChunks];   // kept penalised mass per (wave, register slot)
@@ -701,48 +703,72 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // kept member.
   const bool split = keep > 0 && keep < n_tie;
   if (split) {
-    auto ties_in = [&](const uint4& v) { return (uint32_t)__popc(key_bits(v, L)); };
+    // A compare per element gives the wave-wide mask of the tie members at
+    // that element of a register slot; member counts are scalar bit counts.
+    uint32_t tslot[kFastChunks];  // members per register slot of this wave (uniform)
     uint32_t wsum = 0;
 #pragma unroll
     for (int j = 0; j < kFastChunks; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      wsum += lane_value(wave_scan_dpp(ties_in(d[j])), 63);
+      uint32_t t = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t += (uint32_t)__popcll(__ballot(key_at(d[j], e) == L));
+      tslot[j] = t;
+      wsum += t;
     }
-    if (lane == 0) sh.wtie[wave] = wsum;
+    if (lane == 0) {
+      sh.wtie[wave] = wsum;
+#pragma unroll
+      for (int j = 0; j < kFastChunks; ++j) sh.tslot[wave][j] = tslot[j];
+    }
     lds_barrier();
     uint32_t base = 0;
     for (int w = 0; w < wave; ++w) base += sh.wtie[w];
-    long long found = -1;
-    uint32_t before = 0, fj = 0, fm = 0, fn = 0;
+    base = uni(base);
+    // Only the wave holding the member of rank keep - 1 looks for it: the
+    // slot from the slot counts, the lane from the members in lanes below
+    // (chunk order within a slot is lane order), the element from its mask.
+    const long long r0 = keep - 1 - (long long)base;
+    if (r0 >= 0 && r0 < (long long)wsum) {
+      uint32_t r = (uint32_t)r0;
+      int js = 0;
 #pragma unroll
-    for (int j = 0; j < kFastChunks; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      uint4 v = d[j];  // opaque copy: the first loop's counts are recomputed, not kept live
-      asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
-      const uint32_t m = key_bits(v, L);
+      for (int j = 0; j < kFastChunks; ++j) {
+        const bool here = js == j && r >= tslot[j];
+        r -= here ? tslot[j] : 0u;
+        js += here ? 1 : 0;
+      }
+      if (lane == 0) {
+        sh.cut_w = wave;
+        sh.cut_j = js;
+        sh.cut_r = (int)r;
+      }
+      uint4 v = d[0];
+#pragma unroll
+      for (int j = 1; j < kFastChunks; ++j)
+        if (js == j) v = d[j];
+      uint32_t below = 0, m = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool hit = key_at(v, e) == L;
+        const unsigned long long mk = __ballot(hit);
+        below += __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        m |= (hit ? 1u : 0u) << e;
+      }
       const uint32_t t = (uint32_t)__popc(m);
-      const uint32_t incl = wave_scan_dpp(t);
-      const uint32_t r0 = base + before + incl - t;  // ties before this lane's chunk
-      // The keep-th member lies in this chunk when n = keep-1-r0 is in [0, t).
-      const long long n = keep - 1 - (long long)r0;
-      const bool here = n >= 0 && n < (long long)t;
-      fj = here ? (uint32_t)j : fj;
-      fm = here ? m : fm;
-      fn = here ? (uint32_t)n : fn;
-      before += lane_value(incl, 63);
-    }
-    if (fm) {
-      // Set bit fn of fm: its position counts the prefixes of fm holding at most fn bits.
-      uint32_t e = 0;
+      if (below <= r && r < below + t) {
+        const uint32_t fn = r - below;  // set bit fn of m
+        uint32_t e = 0;
 #pragma unroll
-      for (int b = 0; b < 8; ++b) e += (uint32_t)__popc(fm & ((2u << b) - 1u)) <= fn ? 1u : 0u;
-      const uint32_t c = (uint32_t)wave * CW + fj * 64u + (uint32_t)lane;
-      found = 8ll * c + e;
+        for (int b = 0; b < 8; ++b) e += (uint32_t)__popc(m & ((2u << b) - 1u)) <= fn ? 1u : 0u;
+        const uint32_t c = (uint32_t)wave * CW + (uint32_t)js * 64u + (uint32_t)lane;
+        sh.bc_l[1] = 8ll * c + e;
+      }
     }
-    if (found >= 0) sh.bc_l[1] = found;
     lds_barrier();
     cut_idx = uni(sh.bc_l[1]);
   }
+  const int cut_w = split ? uni(sh.cut_w) : -1, cut_j = split ? uni(sh.cut_j) : 0;
+  const int cut_r = split ? uni(sh.cut_r) : 0;
 
   // ---- mass table of the kept register-resident keys: every binade (128
   // keys) holding a kept key gets a slot of 128 fixed-point masses; absent
@@ -798,12 +824,12 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // is the 64 consecutive chunks w*CW + 64j .. 64j + 63 -- and per wave; then
   // the wave and slot holding u * total, and one lane of that slot walks its
   // chunk.  Tie members of a split group count up to cut_idx.
-  auto chunk_mass = [&](const uint4& v, uint32_t c) -> long long {
+  auto chunk_mass = [&](const uint4& v, uint32_t c, bool ties) -> long long {
     const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
     long long cm = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) cm += key_fx(w4[q] & 0xFFFFu) + key_fx(w4[q] >> 16);
-    if (split) {
+    if (ties) {
       const long long lim = cut_idx - 8ll * c;
       const uint32_t m = key_bits(v, L);
       const uint32_t km = lim < 0 ? 0u : (lim >= 7 ? m : m & ((2u << lim) - 1u));
@@ -817,7 +843,12 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     for (int j = 0; j < kFastChunks; ++j) {
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t c = (uint32_t)wave * CW + (uint32_t)j * 64u + (uint32_t)lane;
-      const long long sj = wave_reduce_dpp(chunk_mass(d[j], c), OpSum());
+      long long sj = wave_reduce_dpp(chunk_mass(d[j], c, false), OpSum());
+      if (split) {  // kept tie members of this slot: all before the cut, r + 1 in its slot, none after
+        const long long t = (long long)sh.tslot[wave][j];
+        const long long kt = wave < cut_w ? t : (wave > cut_w ? 0 : (j < cut_j ? t : (j == cut_j ? cut_r + 1 : 0)));
+        sj += kt * mtie;
+      }
       if (lane == 0) sh.smass[wave][j] = sj;
       acc += sj;
     }
@@ -959,7 +990,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       if (js == j) v = d[j];
     const uint32_t cw = (uint32_t)js * 64u + (uint32_t)lane;
     const uint32_t c = (uint32_t)ow * CW + cw;
-    const long long cm = cw < CW ? chunk_mass(v, c) + sh.mid.cm.pen[lane] : 0ll;
+    const long long cm = cw < CW ? chunk_mass(v, c, split) + sh.mid.cm.pen[lane] : 0ll;
     const long long incl = wave_scan_dpp(cm);
     const long long ex = jbase + incl - cm;
     if (cm > 0 && ex <= thr && thr < ex + cm) {
