@@ -482,14 +482,16 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   // One scan of (tokens above the boundary, boundary ties) per thread gives
   // every thread its tie rank and the position of its kept tokens.
   uint32_t n_up = 0, n_eq = 0;
+  if (busy) {  // waves past the list hold no tokens
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t dd = Mkey - key_at(lv[c], e);
-      n_up += dd < dk;
-      n_eq += dd == dk;
-    }
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t dd = Mkey - key_at(lv[c], e);
+        n_up += dd < dk;
+        n_eq += dd == dk;
+      }
+  }
   uint32_t ptot;
   const uint32_t pex = bs.scan(n_up | (n_eq << 16), ptot);
   if (busy) {
