@@ -192,6 +192,11 @@ struct PenPk {  // a history entry's packed mass word and token id
   int32_t id;
 };
 
+struct PenVal {  // a history entry's adjusted value and token id
+  double v;
+  int32_t id;
+};
+
 // Whether history entry e of a row changes its token (count or generated count positive).
 __device__ __forceinline__ bool pen_touches(long long c, long long g) { return c > 0 || g > 0; }
 
@@ -483,9 +488,19 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
     if (bs.sum(nlive) != bs.sum(real)) return kHandCapacity;
   }
+  // Kept penalised mass by the wave and register slot whose chunks hold the
+  // token (the index-order CDF below works by wave, then slot).
+  auto add_kept = [&](int32_t id, long long fx) {
+    const uint32_t cid = (uint32_t)(id >> 3);
+    const int w = (int)(cid / CW), js = (int)((cid - (uint32_t)w * CW) >> 6);
+    atomicAdd((unsigned long long*)&sh.spen[w][js], (unsigned long long)fx);
+  };
+  const bool all_kept = !(pol.top_p < 1.0);  // no top-p: every positive mass stays
   // Penalised tokens: mass, floor key, added to the block of their floor key.
-  pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? Wv[e] : -(double)INFINITY; },
-              [&](int64_t e, double v) {
+  pen_batches(pn, tid,
+              [&](int64_t e) { return e >= 0 ? PenVal{Wv[e], a.pen_ids[o0 + e]} : PenVal{-(double)INFINITY, 0}; },
+              [&](int64_t e, PenVal x) {
+                const double v = x.v;
                 long long packed = 0;
                 if (v > -(double)INFINITY) {
                   const double m0 = exp_nonpos((v - M) / T, etab);
@@ -495,6 +510,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
                   const uint32_t kb = floor_key(v);
                   atomicAdd((unsigned long long*)&sh.mid.blk.bm[kb >> 6], (unsigned long long)fx);
                   if (m > 0.0) atomicAdd(&sh.mid.blk.bp[kb >> 6], 1u);
+                  if (all_kept && fx > 0) add_kept(x.id, fx);
                   packed = fx | (m > 0.0 ? (1ll << 47) : 0ll) | ((long long)kb << 48);
                 }
                 Wp[e] = packed;
@@ -574,15 +590,22 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     mtie = uni(sh.bc_l[2]);
     const int tie_pos = sh.bc_i[5];
     // Penalised values in the boundary bucket and its two neighbours.
-    pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? Wp[e] : 0ll; }, [&](int64_t e, long long pk) {
+    // Entries above the boundary bucket are kept: their masses go to their
+    // wave and slot here; the bucket's own entries once the walk below has
+    // decided them.
+    pen_batches(pn, tid, [&](int64_t e) { return e >= 0 ? PenPk{Wp[e], a.pen_ids[o0 + e]} : PenPk{0ll, 0}; },
+                [&](int64_t e, PenPk x) {
+      const long long pk = x.pk;
       const uint32_t kb = (uint32_t)((unsigned long long)pk >> 48);
+      const long long fx = pk & ((1ll << 47) - 1);
+      if (pk != 0 && kb > L && fx > 0) add_kept(x.id, fx);
       if (pk != 0 && kb + 1u >= L && kb <= L + 1u) {
         const int slot = atomicAdd(&sh.nitems, 1);
         if (slot < kPenItems) {
           PenItem it;
           it.v = Wv[e];
-          it.fx = pk & ((1ll << 47) - 1);
-          it.id = a.pen_ids[o0 + e];
+          it.fx = fx;
+          it.id = x.id;
           it.key = (int16_t)kb;
           it.pos = (int16_t)((pk >> 47) & 1);
           sh.items[slot] = it;
@@ -689,6 +712,12 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     if (sh.bc_i[6]) return sh.bc_i[6];
     nkept_items = uni(sh.bc_i[7] & 0xFFFF);
     if (sh.bc_i[7] & 0x10000) flags |= DSR_FLAG_MARGIN;
+    if (wave == 0) {  // the kept entries of the boundary bucket: the first nkept_items in sorted order
+      const bool inb = lane < nit && (uint16_t)sh.items[lane].key == L;
+      const unsigned long long mb = __ballot(inb);
+      const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mb, 0u));
+      if (inb && (int)rank < nkept_items && sh.items[lane].fx > 0) add_kept(sh.items[lane].id, sh.items[lane].fx);
+    }
     keep = uni(sh.bc_l[3]);
     Sk = uni(sh.bc_l[0]);
     npos_k = uni((uint32_t)sh.bc_l[2]);
@@ -813,7 +842,6 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     dst[5] = g1;
     dst[6] = g2;
     dst[7] = g3;
-    if (tid < kWaves) sh.wtot[tid] = 0;
   }
   lds_barrier();
   // Fixed-point kept mass of a register-resident key (split tie members excluded).
@@ -852,7 +880,9 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       if (lane == 0) sh.smass[wave][j] = sj;
       acc += sj;
     }
-    if (lane == 0) atomicAdd((unsigned long long*)&sh.wtot[wave], (unsigned long long)acc);
+    // The wave's total: its register-resident mass and its slots' penalised masses.
+    const long long pw = wave_reduce_dpp(lane < kFastChunks ? sh.spen[wave][lane] : 0ll, OpSum());
+    if (lane == 0) sh.wtot[wave] = acc + pw;
   }
   auto pen_kept = [&](uint32_t kb, int32_t id) {
     if (L == 0u || kb > L) return true;
@@ -865,15 +895,6 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     return false;
   };
   auto fetch_pk = [&](int64_t e) { return e >= 0 ? PenPk{Wp[e], a.pen_ids[o0 + e]} : PenPk{0ll, 0}; };
-  pen_batches(pn, tid, fetch_pk, [&](int64_t, PenPk x) {
-    if (x.pk != 0 && pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
-      const uint32_t cid = (uint32_t)(x.id >> 3);
-      const int w = (int)(cid / CW), js = (int)((cid - (uint32_t)w * CW) >> 6);
-      const unsigned long long fx = (unsigned long long)(x.pk & ((1ll << 47) - 1));
-      atomicAdd((unsigned long long*)&sh.wtot[w], fx);
-      atomicAdd((unsigned long long*)&sh.spen[w][js], fx);
-    }
-  });
   lds_barrier();
   if (tid == 0) {
     long long base = 0;
