@@ -439,11 +439,13 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   };
   int close = 0;
   {
-    uint32_t nlive = 0;
+    uint32_t counted = 0;  // every register slot, dummy keys included
 #pragma unroll 1
     for (int i = 0; i < 8; ++i) {
       const uint32_t g = (uint32_t)tid + 1024u * (uint32_t)i;
       const uint4 q4 = *(const uint4*)&sh.big.cnt[4u * g];
+      counted += ((q4.x & 0xFFFFu) + (q4.x >> 16)) + ((q4.y & 0xFFFFu) + (q4.y >> 16)) +
+                 ((q4.z & 0xFFFFu) + (q4.z >> 16)) + ((q4.w & 0xFFFFu) + (q4.w >> 16));
       long long gm = 0;
       uint32_t gp = 0, gc = 0;
       if ((q4.x | q4.y | q4.z | q4.w) != 0u && g >= 16u) {  // keys below 128 hold no value
@@ -461,7 +463,6 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
           }
         }
       }
-      nlive += gc;
       // Sum the 8 groups of block g >> 3 (lanes with equal tid >> 3).
       gm = gm + dpp_move<long long, 0xB1>(gm);
       gm = gm + dpp_move<long long, 0x4E>(gm);
@@ -478,15 +479,9 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
         sh.mid.blk.bc[g >> 3] = gc;
       }
     }
-    // Every counted token is a real key: a 16-bit count that wrapped shows here.
-    uint32_t real = 0;
-#pragma unroll
-    for (int j = 0; j < kFastChunks; ++j) {
-      const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) real += ((w4[q] & 0xFFFFu) >= 128u ? 1u : 0u) + ((w4[q] >> 16) >= 128u ? 1u : 0u);
-    }
-    if (bs.sum(nlive) != bs.sum(real)) return kHandCapacity;
+    // The histogram holds one count per register slot (16 x 8 per thread), so a
+    // 16-bit count that wrapped (more than 65,535 equal keys) shows in the total.
+    if (bs.sum(counted) != (uint32_t)(kThreads * kFastChunks * 8)) return kHandCapacity;
   }
   // Kept penalised mass by the wave and register slot whose chunks hold the
   // token (the index-order CDF below works by wave, then slot).

@@ -78,6 +78,27 @@ GOLD = np.load(os.path.join(HERE, "golden", "sampling_golden.npz"))
 META = json.load(open(os.path.join(HERE, "golden", "sampling_golden.json")))
 
 
+def test_full_path_rows_with_many_equal_values():
+    """bf16 rows with a history where more than 65,535 tokens share one value
+    (a 16-bit key count would wrap): the register-resident path must hand them
+    to the general path, and the result must still match the oracle."""
+    rng = np.random.default_rng(5150)
+    V, R = workloads.VOCAB, 4
+    x = rng.normal(0, 1, (R, V))
+    x[:, : 100_000] = 0.25                 # one bf16 value, 100k times
+    x[1, 5] = 3.0                           # a clear maximum in one row
+    logits = workloads.bf16_round(x)
+    hist = [rng.choice(V, 300, replace=False) for _ in range(R)]
+    pols = [dict(temperature=1.0, top_p=0.9, repetition_penalty=1.2, presence_penalty=0.4),
+            dict(temperature=0.7, repetition_penalty=1.1, frequency_penalty=0.2),
+            dict(temperature=0.0, presence_penalty=0.5),
+            dict(temperature=1.3, top_p=0.5, min_p=0.01, frequency_penalty=0.3)]
+    w = workloads.Workload("equal", "bf16", logits, pols, rng.random(R), histories=hist)
+    gpu = run_gpu(w)
+    check(compare(w, gpu))
+    assert (gpu["flags"][[0, 1, 3]] & N.FLAG_GENERAL).all()  # sampled rows: the count check hands them over
+
+
 @pytest.mark.parametrize("case", META["probabilities"], ids=lambda c: c["name"])
 def test_golden_vectors_on_gpu(case):
     from test_oracle_golden import golden_case
