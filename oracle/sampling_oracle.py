@@ -1,6 +1,6 @@
 """CPU float64 oracle for the token-sampling hot path.
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker that the HIP path is
+TEST INFRASTRUCTURE ONLY.  This module is the oracle that the HIP path is
 compared against.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it; the product package never
 does, and it is never the thing that is measured or shipped.

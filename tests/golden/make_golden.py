@@ -1,6 +1,7 @@
 """Write the golden vectors that only the reference itself can pin.
 
-Run in the build container only (the reference tree is not on the GPU box):
+Run only where the reference sources are present (the GPU tests read the
+committed vectors, never the reference):
 
     PYTHONPATH=/root/reference/src python tests/golden/make_golden.py
 
