@@ -78,6 +78,25 @@ GOLD = np.load(os.path.join(HERE, "golden", "sampling_golden.npz"))
 META = json.load(open(os.path.join(HERE, "golden", "sampling_golden.json")))
 
 
+@pytest.mark.skip(reason="routing of history-less top-k rows to the top-k register path inside the "
+                         "full-vocabulary kernel is not built: its one GPU run ended in a memory fault "
+                         "whose cause was not found, so the routing was taken out")
+def test_mixed_batch_of_history_and_top_k_rows():
+    """One launch with bf16 rows that carry histories (no top-k) and rows with
+    an empty history and a top-k: the latter take the top-k register path
+    inside the full-vocabulary kernel, not the general path."""
+    c2, c3 = workloads.c2(rows=8), workloads.c3(rows=8)
+    logits = np.concatenate([c2.logits, c3.logits])
+    pols = c2.policies + c3.policies
+    hist = list(c2.histories) + [np.zeros(0, np.int64)] * 8
+    w = workloads.Workload("mixed", "bf16", logits, pols, np.concatenate([c2.uniforms, c3.uniforms]),
+                           histories=hist)
+    gpu = run_gpu(w)
+    check(compare(w, gpu))
+    assert not (gpu["flags"][8:] & N.FLAG_GENERAL).any()
+    assert not (gpu["flags"][:8] & N.FLAG_GENERAL).any()
+
+
 def test_full_path_rows_with_many_equal_values():
     """bf16 rows with a history where more than 65,535 tokens share one value
     (a 16-bit key count would wrap): the register-resident path must hand them
