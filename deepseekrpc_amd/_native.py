@@ -29,6 +29,9 @@ E_TOKEN = 9
 E_DISTRIBUTION = 10
 E_POLICY = 11
 E_GENERATED = 12
+E_HISTORY = 13
+E_APPEND = 14
+MAX_APPEND = 16384
 
 FLAG_MARGIN = 1
 FLAG_GENERAL = 2
@@ -37,7 +40,7 @@ STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 EXPORTS = (
     "dsr_abi_version", "dsr_status_message", "dsr_sample_workspace_bytes", "dsr_verify_workspace_bytes",
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
-    "dsr_prob_accept",
+    "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append",
 )
 
 _p = ctypes.c_void_p
@@ -115,6 +118,10 @@ def load(path: str = LIB_PATH):
     lib.dsr_prob_correction.argtypes = [_p, _p, _i64, _p, _p, _p]
     lib.dsr_prob_accept.restype = _i32
     lib.dsr_prob_accept.argtypes = [_p, _p, _i64, _i32, _f64, _p, _p]
+    lib.dsr_history_from_dense.restype = _i32
+    lib.dsr_history_from_dense.argtypes = [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p]
+    lib.dsr_history_append.restype = _i32
+    lib.dsr_history_append.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p]
     _lib = lib
     return lib
 

@@ -120,6 +120,109 @@ class HistoryTable:
             offs.append(offs[-1] + len(nz))
         return cls._upload(offs, ids, cnt, gen, device)
 
+    @property
+    def rows(self) -> int:
+        return self.offsets.numel() - 1
+
+    # -- built on the device (dsr_history_from_dense / dsr_history_append) --
+
+    @classmethod
+    def from_dense_device(cls, counts: torch.Tensor, generated: torch.Tensor | None = None):
+        """Dense ``[rows, V]`` int32 device counts (and generated counts) -> a
+        table built on the device.  Returns ``(table, status)``: ``status[r]``
+        is 0, E_COUNTS or E_GENERATED (sampling.py:54-58, 62-65); a rejected
+        row has no entries."""
+        _require_cuda(counts, "counts", rows_strided=True)
+        if counts.dtype != torch.int32:
+            raise ValueError("counts must be int32")
+        if generated is not None:
+            _require_cuda(generated, "generated", rows_strided=True)
+            if generated.dtype != torch.int32 or generated.shape != counts.shape or \
+                    generated.stride(0) != counts.stride(0):
+                raise ValueError("generated must be int32 with the shape and row stride of counts")
+        rows, vocab = counts.shape
+        dev = counts.device
+        off = torch.empty(rows + 1, dtype=torch.int64, device=dev)
+        status = torch.empty(rows, dtype=torch.int32, device=dev)
+        lib = N.load()
+
+        def call(cap):
+            out = [torch.empty(max(cap, 1), dtype=torch.int32, device=dev) for _ in range(3)]
+            rc = lib.dsr_history_from_dense(_ptr(counts), _ptr(generated), rows, vocab, counts.stride(0), _ptr(off),
+                                            *(_ptr(o) for o in out), cap, _ptr(status), _stream())
+            N.check(rc, "dsr_history_from_dense")
+            return out
+
+        cap = rows * vocab if rows * vocab <= (1 << 22) else 0  # large batches: count first, then exact outputs
+        out = call(cap)
+        total = int(off[-1].item())
+        if total > cap:
+            out = call(total)
+        return cls(off, *(o[:total] for o in out)), status
+
+    def append(self, tokens: torch.Tensor, tok_off: torch.Tensor, gen_from: torch.Tensor | None = None,
+               vocab: int = VOCAB):
+        """Adds ``tokens[tok_off[r]:tok_off[r+1]]`` to row ``r`` on the device
+        (np.add.at on both counts, history.py:136-137; only positions at or
+        after ``gen_from[r]`` count as generated).  At most MAX_APPEND tokens
+        per row.  Returns ``(table, status)``."""
+        return HistoryTable._append(self, tokens, tok_off, gen_from, vocab)
+
+    @classmethod
+    def _append(cls, table, tokens, tok_off, gen_from, vocab):
+        _require(tokens, "tokens", torch.int32)
+        _require(tok_off, "tok_off", torch.int64)
+        rows = tok_off.numel() - 1
+        if table is not None and table.rows != rows:
+            raise ValueError("tok_off must have one entry per table row plus one")
+        if gen_from is not None:
+            _require(gen_from, "gen_from", torch.int64, rows)
+        dev = tok_off.device
+        # The kernels read tokens[tok_off[r] .. tok_off[r+1]): the offsets must
+        # start at 0, never decrease and stay inside the token buffer.
+        if rows > 0 and not bool(((tok_off[1:] >= tok_off[:-1]).all() & (tok_off[0] == 0)
+                                  & (tok_off[-1] <= tokens.numel())).item()):
+            raise ValueError("tok_off must be non-decreasing from 0 and within tokens")
+        old = 0 if table is None else table.ids.numel()
+        cap = old + tokens.numel()
+        off = torch.empty(rows + 1, dtype=torch.int64, device=dev)
+        status = torch.empty(rows, dtype=torch.int32, device=dev)
+        out = [torch.empty(max(cap, 1), dtype=torch.int32, device=dev) for _ in range(3)]
+        has = table is not None and old > 0
+        rc = N.load().dsr_history_append(
+            _ptr(table.offsets) if has else None, _ptr(table.ids) if has else None,
+            _ptr(table.counts) if has else None, _ptr(table.generated) if has else None,
+            _ptr(tokens) if tokens.numel() else ctypes.c_void_p(_ptr(tok_off).value),  # never read: no tokens
+            _ptr(tok_off), _ptr(gen_from), rows, vocab, _ptr(off), *(_ptr(o) for o in out), cap, _ptr(status),
+            _stream())
+        N.check(rc, "dsr_history_append")
+        total = int(off[-1].item())
+        return cls(off, *(o[:total] for o in out)), status
+
+    @classmethod
+    def from_token_lists_device(cls, histories, generated_start=None, vocab: int = VOCAB, device="cuda"):
+        """Token-id histories -> a table built on the device; ids before
+        ``generated_start[r]`` are prompt tokens (history.py:92-94), the rest
+        output tokens (:136-137).  Rows longer than MAX_APPEND are appended in
+        rounds.  Returns ``(table, status)``."""
+        lens = [len(h) for h in histories]
+        rounds = max(1, -(-max(lens, default=0) // N.MAX_APPEND))
+        table, status = None, None
+        for k in range(rounds):
+            lo = k * N.MAX_APPEND
+            parts = [np.asarray(h[lo:lo + N.MAX_APPEND], np.int64) for h in histories]
+            off = np.zeros(len(parts) + 1, np.int64)
+            off[1:] = np.cumsum([len(p) for p in parts])
+            flat = np.concatenate(parts) if off[-1] else np.zeros(0, np.int64)
+            flat = np.clip(flat, -1, vocab)  # ids out of range stay out of range through the int32 cast
+            gf = None
+            if generated_start is not None:
+                gf = torch.tensor([int(s) - lo for s in generated_start], dtype=torch.int64, device=device)
+            tok = torch.from_numpy(flat.astype(np.int32)).to(device)
+            table, st = cls._append(table, tok, torch.from_numpy(off).to(device), gf, vocab)
+            status = st if status is None else torch.where(status != 0, status, st)
+        return table, status
+
     @classmethod
     def _upload(cls, offs, ids, cnt, gen, device):
         cat = lambda xs: np.concatenate(xs) if xs and sum(len(x) for x in xs) else np.zeros(0)

@@ -1,0 +1,289 @@
+// Device history tables (gfx950): the reference's dense `counts` /
+// `generated_counts` pair (history.py:46-47,92,136-137; sampling.py:54-66)
+// kept on the device as the sparse CSR table dsr_sample_rows reads: per row,
+// strictly increasing token ids with their count and generated count.
+//
+// Two builders, each three launches on the caller's stream (no allocation,
+// no synchronisation):
+//   1. a count pass, one 1024-thread workgroup per row: validates the row and
+//      writes its entry count to out_off[row + 1] and its status;
+//   2. k_history_offsets turns those counts into offsets in place (one
+//      workgroup; out_off[rows] is the total);
+//   3. the write pass repeats the count pass's work and writes the entries,
+//      or nothing at all when the total exceeds the caller's capacity.
+//
+// dsr_history_from_dense compacts dense count vectors (np.flatnonzero of
+// counts > 0) with the reference's validation.  dsr_history_append adds
+// tokens to a table as np.add.at does (history.py:136-137; the tentative
+// prefix of terminal_sampling.py:129-133): the row's new tokens mark a
+// presence bitmap of the vocabulary in LDS next to a bitmap of the row's old
+// ids; per-word rank bases of both bitmaps and of their difference (new ids
+// the table lacks) give every output position in closed form:
+//   old id y, old rank i:  i + #(new ids absent from the table below y)
+//   absent new id x:       #(old ids below x) + #(absent new ids below x)
+// and a count table indexed by rank among the new ids carries each new id's
+// multiplicity and generated multiplicity (16 bits each).
+#pragma once
+
+#include "dsr_wave.h"
+
+namespace dsr {
+
+constexpr int kHistWords = (DSR_MAX_VOCAB + 31) / 32;  // 4040 bitmap words
+constexpr int kMaxAppend = DSR_MAX_APPEND;            // new tokens per row and call
+static_assert(4 * kThreads >= kHistWords, "four bitmap words per thread");
+static_assert(kMaxAppend < 65536, "multiplicities are packed in 16 bits");
+
+struct HistAppendArgs {
+  const int64_t* off;   // [rows + 1] or null: empty input table
+  const int32_t* ids;
+  const int32_t* count;
+  const int32_t* gen;
+  const int32_t* tokens;
+  const int64_t* tok_off;   // [rows + 1]
+  const int64_t* gen_from;  // [rows] or null: every new token is generated
+  int64_t rows, vocab, cap;
+  int64_t* out_off;
+  int32_t* out_ids;
+  int32_t* out_count;
+  int32_t* out_gen;
+  int32_t* out_status;
+};
+
+struct HistDenseArgs {
+  const int32_t* counts;     // [rows, ld]
+  const int32_t* generated;  // [rows, ld] or null: generated counts = counts
+  int64_t rows, vocab, ld, cap;
+  int64_t* out_off;
+  int32_t* out_ids;
+  int32_t* out_count;
+  int32_t* out_gen;
+  int32_t* out_status;
+};
+
+struct HistAppendShared {
+  uint32_t nb[kHistWords];     // new ids present
+  uint32_t ob[kHistWords];     // old ids present
+  uint32_t nbase[kHistWords];  // new ids below the word
+  uint32_t obase[kHistWords];  // old ids below the word
+  uint32_t ubase[kHistWords];  // new ids absent from the table, below the word
+  uint32_t cnt[kMaxAppend];    // by rank among the new ids: multiplicity | generated << 16
+  int bad;
+  SyncSlots sync;
+};
+
+__device__ __forceinline__ uint32_t bits_below(uint32_t w, uint32_t b) { return __popc(w & ((1u << b) - 1u)); }
+
+// One row of dsr_history_append.  WRITE = false: validate and count the
+// merged row; WRITE = true: write it at out_off[row] (rows the count pass
+// rejected, and every row when the total exceeds cap, write nothing).
+template <bool WRITE>
+__global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
+  __shared__ HistAppendShared sh;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  const int words = (int)((V + 31) >> 5);
+  BlockSync bs(sh.sync);
+  const int64_t o0 = a.off ? a.off[row] : 0, o1 = a.off ? a.off[row + 1] : 0;
+  const int64_t t0 = a.tok_off[row], t1 = a.tok_off[row + 1];
+  const int64_t m = t1 - t0;
+  const int64_t gf = a.gen_from ? a.gen_from[row] : 0;  // new tokens at positions >= gf are generated
+  if (WRITE) {
+    if (a.out_status[row] != DSR_OK || a.out_off[a.rows] > a.cap) return;  // uniform
+  } else {
+    int st = DSR_OK;
+    if (m < 0 || m > kMaxAppend) st = DSR_E_APPEND;
+    else if (o1 < o0 || o1 - o0 > V) st = DSR_E_HISTORY;
+    if (st != DSR_OK) {
+      if (tid == 0) {
+        a.out_status[row] = st;
+        a.out_off[row + 1] = 0;
+      }
+      return;
+    }
+  }
+  for (int w = tid; w < words; w += kThreads) {
+    sh.nb[w] = 0u;
+    sh.ob[w] = 0u;
+  }
+  for (int64_t i = tid; i < m; i += kThreads) sh.cnt[i] = 0u;
+  if (tid == 0) sh.bad = 0;
+  lds_barrier();
+  // Old ids: strictly increasing, in range, 1 <= count <= DSR_MAX_COUNT, 0 <= gen <= count.
+  for (int64_t e = o0 + tid; e < o1; e += kThreads) {
+    const int32_t id = a.ids[e], c = a.count[e], g = a.gen[e];
+    const bool ok = id >= 0 && id < V && (e == o0 || a.ids[e - 1] < id) && c >= 1 && c <= DSR_MAX_COUNT && g >= 0 &&
+                    g <= c;
+    if (ok) atomicOr(&sh.ob[id >> 5], 1u << (id & 31));
+    else sh.bad = 1;
+  }
+  for (int64_t i = t0 + tid; i < t1; i += kThreads) {
+    const int32_t t = a.tokens[i];
+    if (t >= 0 && t < V) atomicOr(&sh.nb[t >> 5], 1u << (t & 31));
+    else sh.bad = 1;
+  }
+  lds_barrier();
+  if (sh.bad) {  // uniform: read after the barrier
+    if (!WRITE && tid == 0) {
+      a.out_status[row] = DSR_E_HISTORY;
+      a.out_off[row + 1] = 0;
+    }
+    return;
+  }
+  // Rank bases per word; thread t holds words 4t .. 4t + 3, so thread order
+  // is word order.  New and absent-new counts share one packed scan (each
+  // total is at most kMaxAppend < 2^16).
+  uint32_t nw[4], ow[4], pn = 0, pu = 0;
+  long long po = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int w = 4 * tid + q;
+    nw[q] = w < words ? sh.nb[w] : 0u;
+    ow[q] = w < words ? sh.ob[w] : 0u;
+    pn += __popc(nw[q]);
+    pu += __popc(nw[q] & ~ow[q]);
+    po += __popc(ow[q]);
+  }
+  long long n_old;
+  uint32_t bex, btot;
+  const long long oex = bs.scan2(po, pn | (pu << 16), n_old, bex, btot);
+  if (!WRITE) {
+    if (tid == 0) {
+      a.out_status[row] = DSR_OK;
+      a.out_off[row + 1] = n_old + (long long)(btot >> 16);
+    }
+    return;
+  }
+  {
+    uint32_t nb0 = bex & 0xFFFFu, ub0 = bex >> 16, ob0 = (uint32_t)oex;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int w = 4 * tid + q;
+      if (w < words) {
+        sh.nbase[w] = nb0;
+        sh.obase[w] = ob0;
+        sh.ubase[w] = ub0;
+      }
+      nb0 += __popc(nw[q]);
+      ob0 += __popc(ow[q]);
+      ub0 += __popc(nw[q] & ~ow[q]);
+    }
+  }
+  lds_barrier();
+  // Multiplicities of the new ids (and of their generated occurrences).
+  for (int64_t i = t0 + tid; i < t1; i += kThreads) {
+    const uint32_t t = (uint32_t)a.tokens[i], w = t >> 5, b = t & 31u;
+    atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], (i - t0 >= gf) ? 0x10001u : 1u);
+  }
+  lds_barrier();
+  const int64_t base = a.out_off[row];
+  // The table's entries, shifted past the absent new ids below them.
+  for (int64_t e = o0 + tid; e < o1; e += kThreads) {
+    const int32_t id = a.ids[e];
+    const uint32_t w = (uint32_t)id >> 5, b = (uint32_t)id & 31u;
+    const uint32_t nwv = sh.nb[w], owv = sh.ob[w];
+    const uint32_t add = ((nwv >> b) & 1u) ? sh.cnt[sh.nbase[w] + bits_below(nwv, b)] : 0u;
+    const int64_t pos = base + (e - o0) + sh.ubase[w] + bits_below(nwv & ~owv, b);
+    a.out_ids[pos] = id;
+    a.out_count[pos] = a.count[e] + (int32_t)(add & 0xFFFFu);
+    a.out_gen[pos] = a.gen[e] + (int32_t)(add >> 16);
+  }
+  // New ids the table lacks.
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int w = 4 * tid + q;
+    if (w >= words) continue;
+    const uint32_t uw = nw[q] & ~ow[q];
+    uint32_t left = uw;
+    while (left) {
+      const uint32_t b = (uint32_t)(__ffs(left) - 1);
+      left &= left - 1u;
+      const uint32_t add = sh.cnt[sh.nbase[w] + bits_below(nw[q], b)];
+      const int64_t pos = base + sh.obase[w] + bits_below(ow[q], b) + sh.ubase[w] + bits_below(uw, b);
+      a.out_ids[pos] = 32 * w + (int32_t)b;
+      a.out_count[pos] = (int32_t)(add & 0xFFFFu);
+      a.out_gen[pos] = (int32_t)(add >> 16);
+    }
+  }
+}
+
+// One row of dsr_history_from_dense.  The count pass validates as
+// sampling.py:54-58 then :62-65 do (DSR_E_COUNTS before DSR_E_GENERATED) and
+// counts the nonzero entries; the write pass compacts them in index order:
+// wave w owns ids [w * seg, (w + 1) * seg), counts its nonzero entries, and
+// after one barrier writes them from its base (ballot ranks per 64 ids).
+template <bool WRITE>
+__global__ __launch_bounds__(kThreads) void k_history_dense(HistDenseArgs a) {
+  __shared__ SyncSlots sync;
+  __shared__ uint32_t wn[kWaves];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t V = a.vocab;
+  const int32_t* C = a.counts + row * a.ld;
+  const int32_t* G = a.generated ? a.generated + row * a.ld : C;
+  BlockSync bs(sync);
+  if (!WRITE) {
+    uint32_t bad = 0, nnz = 0;
+    long long sum = 0;
+    for (int64_t i = tid; i < V; i += kThreads) {
+      const int32_t c = C[i], g = G[i];
+      if (c < 0 || c > DSR_MAX_COUNT) bad |= 1u;
+      if (g < 0 || g > c) bad |= 2u;
+      sum += c < 0 ? 0 : (c > DSR_MAX_COUNT ? DSR_MAX_COUNT + 1 : c);
+      nnz += c > 0;
+    }
+    const uint32_t bad_any = bs.reduce(bad, 0u, [](uint32_t p, uint32_t q) { return p | q; });
+    const long long total = bs.sum(sum);
+    const uint32_t n = bs.sum(nnz);
+    if (tid == 0) {
+      const int st = ((bad_any & 1u) || total > DSR_MAX_COUNT) ? DSR_E_COUNTS : ((bad_any & 2u) ? DSR_E_GENERATED : DSR_OK);
+      a.out_status[row] = st;
+      a.out_off[row + 1] = st == DSR_OK ? (int64_t)n : 0;
+    }
+    return;
+  }
+  if (a.out_status[row] != DSR_OK || a.out_off[a.rows] > a.cap) return;  // uniform
+  const int lane = lane_id(), wave = wave_id();
+  const int64_t seg = ((V + kWaves - 1) / kWaves + 63) & ~(int64_t)63;
+  const int64_t lo = (int64_t)wave * seg, hi = lo + seg < V ? lo + seg : V;
+  uint32_t mine = 0;
+  for (int64_t i = lo + lane; i - lane < hi; i += 64) mine += (uint32_t)__popcll(__ballot(i < hi && C[i] > 0));
+  if (lane == 0) wn[wave] = mine;
+  lds_barrier();
+  int64_t pos = a.out_off[row];
+  for (int w = 0; w < wave; ++w) pos += wn[w];
+  for (int64_t i = lo + lane; i - lane < hi; i += 64) {
+    int32_t c = 0;
+    if (i < hi) c = C[i];
+    const unsigned long long b = __ballot(c > 0);
+    if (c > 0) {
+      const int64_t p = pos + lanes_below(b);
+      a.out_ids[p] = (int32_t)i;
+      a.out_count[p] = c;
+      a.out_gen[p] = G[i];
+    }
+    pos += __popcll(b);
+  }
+}
+
+// Entry counts at off[1 .. rows] -> offsets in place; off[0] = 0.  One
+// workgroup; thread t sums a contiguous run of rows.
+__global__ __launch_bounds__(kThreads) void k_history_offsets(int64_t* off, int64_t rows) {
+  __shared__ SyncSlots sync;
+  BlockSync bs(sync);
+  const int tid = threadIdx.x;
+  const int64_t per = (rows + kThreads - 1) / kThreads;
+  const int64_t lo = 1 + (int64_t)tid * per, hi = lo + per < rows + 1 ? lo + per : rows + 1;
+  long long s = 0;
+  for (int64_t i = lo; i < hi; ++i) s += off[i];
+  long long total;
+  long long run = bs.scan(s, total);
+  for (int64_t i = lo; i < hi; ++i) {
+    run += off[i];
+    off[i] = run;
+  }
+  if (tid == 0) off[0] = 0;
+}
+
+}  // namespace dsr

@@ -16,6 +16,7 @@
 #include "dsr_fast.h"
 #include "dsr_full.h"
 #include "dsr_general.h"
+#include "dsr_history.h"
 #include "dsr_verify.h"
 
 namespace dsr {
@@ -235,6 +236,8 @@ const char* dsr_status_message(int32_t code) {
     case DSR_E_DISTRIBUTION: return "verifier requires a normalized complete FP64 probability vector";
     case DSR_E_POLICY: return "invalid sampling policy";
     case DSR_E_GENERATED: return "generated token counts must be a subset of complete sampling history";
+    case DSR_E_HISTORY: return "history needs bounded exact integer token IDs";
+    case DSR_E_APPEND: return "a history append holds at most 16384 tokens per row";
     default: return "unknown sampling status";
   }
 }
@@ -352,6 +355,50 @@ int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, 
                         void* stream) {
   if (!p || !q || !out_i32 || n < 1 || n > DSR_MAX_VOCAB || x < 0 || x >= n) return DSR_ERR_ARG;
   hipLaunchKernelGGL(k_prob_accept, dim3(1), dim3(64), 0, (hipStream_t)stream, p, q, x, u, out_i32);
+  return launched();
+}
+
+int32_t dsr_history_from_dense(const int32_t* counts, const int32_t* generated, int64_t rows, int64_t vocab,
+                               int64_t ld, int64_t* out_off, int32_t* out_ids, int32_t* out_count,
+                               int32_t* out_gen, int64_t cap, int32_t* out_status, void* stream) {
+  if ((!counts && rows > 0) || !out_off || (!out_status && rows > 0) || rows < 0 || rows > INT_MAX || vocab < 1 ||
+      vocab > DSR_MAX_VOCAB ||
+      ld < vocab || cap < 0 || (cap > 0 && (!out_ids || !out_count || !out_gen)))
+    return DSR_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  HistDenseArgs h{counts, generated, rows, vocab, ld, cap, out_off, out_ids, out_count, out_gen, out_status};
+  if (rows > 0) {
+    hipLaunchKernelGGL(k_history_dense<false>, dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(k_history_offsets, dim3(1), dim3(kThreads), 0, s, out_off, rows);
+  if (rows > 0) {
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_history_dense<true>, dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+  }
+  return launched();
+}
+
+int32_t dsr_history_append(const int64_t* off, const int32_t* ids, const int32_t* count, const int32_t* gen,
+                           const int32_t* tokens, const int64_t* tok_off, const int64_t* gen_from, int64_t rows,
+                           int64_t vocab, int64_t* out_off, int32_t* out_ids, int32_t* out_count, int32_t* out_gen,
+                           int64_t cap, int32_t* out_status, void* stream) {
+  if ((off && (!ids || !count || !gen)) || ((!tokens || !tok_off || !out_status) && rows > 0) || !out_off || rows < 0 ||
+      rows > INT_MAX || vocab < 1 || vocab > DSR_MAX_VOCAB || cap < 0 ||
+      (cap > 0 && (!out_ids || !out_count || !out_gen)))
+    return DSR_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  HistAppendArgs h{off, ids, count, gen, tokens, tok_off, gen_from, rows, vocab, cap,
+                   out_off, out_ids, out_count, out_gen, out_status};
+  if (rows > 0) {
+    hipLaunchKernelGGL(k_history_append<false>, dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(k_history_offsets, dim3(1), dim3(kThreads), 0, s, out_off, rows);
+  if (rows > 0) {
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_history_append<true>, dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+  }
   return launched();
 }
 

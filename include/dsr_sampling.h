@@ -38,6 +38,7 @@ extern "C" {
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
+#define DSR_MAX_APPEND 16384        /* new tokens per row in one dsr_history_append call */
 
 /* Logit element types. */
 #define DSR_BF16 1
@@ -58,6 +59,9 @@ extern "C" {
 #define DSR_E_DISTRIBUTION 10   /* sampling.py:109-115: not a distribution */
 #define DSR_E_POLICY 11         /* sampling.py:38-43: control outside its bounds */
 #define DSR_E_GENERATED 12      /* sampling.py:62-65: generated counts not within counts */
+#define DSR_E_HISTORY 13        /* history.py:30-36: token id outside the vocabulary, or a
+                                   malformed history table */
+#define DSR_E_APPEND 14         /* more than DSR_MAX_APPEND new tokens for one row */
 
 /* Launch / argument errors (return values). */
 #define DSR_ERR_ARG (-1)
@@ -215,6 +219,49 @@ int32_t dsr_prob_correction(const double* p, const double* q, int64_t n, double*
  * out_i32[1] = 1 if u < min(1, p[x] / q[x]). */
 int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, double u, int32_t* out_i32,
                         void* stream);
+
+/* Device history tables: the reference's dense per-request counts and
+ * generated counts (history.py:46-47,92,136-137; terminal_sampling.py
+ * :127-136) kept on the device as the sparse CSR table of
+ * dsr_sample_args_t (pen_off / pen_ids / pen_count / pen_gen).
+ *
+ * Both calls write out_off[rows + 1] (row r owns entries [out_off[r],
+ * out_off[r+1]) of out_ids / out_count / out_gen) and a status per row; a
+ * row with a nonzero status gets no entries.  out_off[rows] is the total the
+ * call needs: if it exceeds cap, no entries are written at all (the offsets
+ * and statuses still are), and the caller may repeat the call with larger
+ * outputs.  Three launches each; nothing allocates or synchronises.  With
+ * rows == 0 only out_off[0] = 0 is written and the input pointers may be
+ * NULL.
+ *
+ * dsr_history_from_dense: dense counts [rows, ld] and generated counts
+ * [rows, ld] (NULL: generated = counts) -> their entries with counts > 0, in
+ * id order.  Validation and statuses as SamplingPolicy.probabilities does
+ * it (sampling.py:54-58 then :62-65): DSR_E_COUNTS for a count outside
+ * [0, 1048576] or a row total above 1048576, else DSR_E_GENERATED for a
+ * generated count outside [0, count].  Replaces the dense `counts` /
+ * `generated_counts` hand-over of stage_service.py:252-263. */
+int32_t dsr_history_from_dense(const int32_t* counts, const int32_t* generated, int64_t rows, int64_t vocab,
+                               int64_t ld, int64_t* out_off, int32_t* out_ids, int32_t* out_count,
+                               int32_t* out_gen, int64_t cap, int32_t* out_status, void* stream);
+
+/* dsr_history_append: table (off / ids / count / gen as in
+ * dsr_sample_args_t; off NULL = every row empty) plus the tokens
+ * tokens[tok_off[r] .. tok_off[r+1]) of each row -> the merged table.  Each
+ * token adds one to its id's count (np.add.at, history.py:136-137), and one
+ * to its generated count when its position within the row's tokens is at
+ * least gen_from[r] (gen_from NULL: every token is generated, as for an
+ * appended output token or the tentative prefix of
+ * terminal_sampling.py:129-133; gen_from[r] = the row's token count: prompt
+ * tokens only, as TokenHistory.set_prompt counts them, history.py:92).
+ * Statuses: DSR_E_APPEND for more than DSR_MAX_APPEND tokens in a row,
+ * DSR_E_HISTORY for a token outside [0, vocab) or an input row that is not
+ * a valid table row (ids strictly increasing in [0, vocab), 1 <= count <=
+ * 1048576, 0 <= gen <= count). */
+int32_t dsr_history_append(const int64_t* off, const int32_t* ids, const int32_t* count, const int32_t* gen,
+                           const int32_t* tokens, const int64_t* tok_off, const int64_t* gen_from, int64_t rows,
+                           int64_t vocab, int64_t* out_off, int32_t* out_ids, int32_t* out_count, int32_t* out_gen,
+                           int64_t cap, int32_t* out_status, void* stream);
 
 #ifdef __cplusplus
 }

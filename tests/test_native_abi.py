@@ -60,6 +60,20 @@ def test_argument_errors_return_before_any_launch():
     assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1
     assert lib.dsr_prob_stats(None, 3, None, None, None) == -1
     assert lib.dsr_prob_categorical(None, 3, 0.5, None, None) == -1
+    # History builders: null inputs, vocabularies out of range, ld below the
+    # vocabulary, a capacity without output arrays, a table without its ids.
+    fake = ctypes.c_void_p(16)
+    assert lib.dsr_history_from_dense(None, None, 1, 8, 8, fake, None, None, None, 0, fake, None) == -1
+    assert lib.dsr_history_from_dense(fake, None, 1, 0, 8, fake, None, None, None, 0, fake, None) == -1
+    assert lib.dsr_history_from_dense(fake, None, 1, 129281, 129281, fake, None, None, None, 0, fake, None) == -1
+    assert lib.dsr_history_from_dense(fake, None, 1, 8, 7, fake, None, None, None, 0, fake, None) == -1
+    assert lib.dsr_history_from_dense(fake, None, 1, 8, 8, fake, None, None, None, 5, fake, None) == -1
+    assert lib.dsr_history_append(None, None, None, None, fake, None, None, 1, 8, fake, None, None, None, 0, fake,
+                                  None) == -1
+    assert lib.dsr_history_append(fake, None, fake, fake, fake, fake, None, 1, 8, fake, None, None, None, 0, fake,
+                                  None) == -1
+    assert lib.dsr_history_append(None, None, None, None, fake, fake, None, -1, 8, fake, None, None, None, 0, fake,
+                                  None) == -1
 
 
 LAYOUT_C = r"""
