@@ -40,6 +40,7 @@ _MESSAGES = {
     N.E_NO_MASS: "sampling controls produced no positive probability",
     N.E_COUNTS: "sampling frequency counts do not match the vocabulary",
     N.E_GENERATED: "generated token counts must be a subset of complete sampling history",
+    N.E_HISTORY: "history needs bounded exact integer token IDs",
     N.E_BIAS: "invalid logit bias mapping",
     N.E_UNIFORM: "sampling uniform must lie in [0,1)",
     N.E_CORRECTION: "a rejected proposal has no positive correction distribution",
@@ -95,32 +96,16 @@ class SamplingPolicy:
 
     def probabilities(self, logits, *, counts=None, generated_counts=None, logit_bias=None, allowed=None):
         """Adjusted, filtered and normalised float64 probabilities (sampling.py:48-106)."""
-        device_input = isinstance(logits, torch.Tensor)
-        if device_input:
-            if logits.dim() != 1 or not 1 <= logits.numel() <= VOCAB or \
-                    logits.dtype not in (torch.float32, torch.float64, torch.bfloat16):
-                raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
-            n = logits.numel()
-        else:
-            values = np.asarray(logits)
-            if (values.ndim != 1 or not 1 <= len(values) <= VOCAB or values.dtype not in (np.float32, np.float64)
-                    or np.isnan(values).any() or np.isposinf(values).any()):
-                raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
-            n = len(values)
+        n, device_input = _logit_vector(logits)
         table = None
         if counts is not None:
-            counts = np.asarray(counts.cpu() if isinstance(counts, torch.Tensor) else counts)
-            if (counts.shape != (n,) or counts.dtype not in (np.int32, np.int64) or (counts < 0).any()
-                    or (counts > MAX_COUNT).any() or int(counts.sum(dtype=np.int64)) > MAX_COUNT):
-                raise ValidationError("sampling frequency counts do not match the vocabulary")
-            gen = counts if generated_counts is None else np.asarray(
-                generated_counts.cpu() if isinstance(generated_counts, torch.Tensor) else generated_counts)
-            if (gen.shape != counts.shape or gen.dtype not in (np.int32, np.int64) or (gen < 0).any()
-                    or (gen > counts).any()):
-                raise ValidationError("generated token counts must be a subset of complete sampling history")
-            table = batch.HistoryTable.from_dense(counts[None], gen[None], device=_device())
+            table = _history_table(counts, generated_counts, n)
         elif generated_counts is not None:
             raise ValidationError("generated counts require complete repetition-penalty history")
+        return self._probabilities_with(logits, n, device_input, table, logit_bias, allowed)
+
+    def _probabilities_with(self, logits, n, device_input, table, logit_bias, allowed):
+        """The rest of probabilities, with the history already a device table."""
         bias = None
         if logit_bias is not None:
             if not isinstance(logit_bias, dict) or len(logit_bias) > n:
@@ -143,6 +128,65 @@ class SamplingPolicy:
             _raise_status(status)
         out = res.probs[0]
         return out if device_input else out.cpu().numpy()
+
+
+def _logit_vector(logits):
+    """(length, is a device tensor) of a logit vector the reference accepts
+    (sampling.py:50-52); NaN / +inf in device tensors are reported by the
+    kernel, in the same order."""
+    if isinstance(logits, torch.Tensor):
+        if logits.dim() != 1 or not 1 <= logits.numel() <= VOCAB or \
+                logits.dtype not in (torch.float32, torch.float64, torch.bfloat16):
+            raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
+        return logits.numel(), True
+    values = np.asarray(logits)
+    if (values.ndim != 1 or not 1 <= len(values) <= VOCAB or values.dtype not in (np.float32, np.float64)
+            or np.isnan(values).any() or np.isposinf(values).any()):
+        raise ValidationError("sampling needs one bounded finite-or-masked floating logit vector")
+    return len(values), False
+
+
+_COUNTS_MSG = "sampling frequency counts do not match the vocabulary"
+_GENERATED_MSG = "generated token counts must be a subset of complete sampling history"
+
+
+def _count_vector(x, n):
+    """A count vector as a device int32 [1, n] tensor, or None if its shape or
+    dtype is wrong.  Values are clamped to [-1, MAX_COUNT + 1] first, so an
+    out-of-range int64 count stays out of range after the int32 cast."""
+    if isinstance(x, torch.Tensor):
+        t = x.detach()
+        ok = t.shape == (n,) and t.dtype in (torch.int32, torch.int64)
+        t = t if t.is_cuda else t.to(_device())
+    else:
+        arr = np.asarray(x)
+        ok = arr.shape == (n,) and arr.dtype in (np.int32, np.int64)
+        t = torch.from_numpy(np.ascontiguousarray(arr)).to(_device()) if ok else None
+    if not ok:
+        return None
+    return t.clamp(-1, MAX_COUNT + 1).to(torch.int32).reshape(1, n).contiguous()
+
+
+def _history_table(counts, generated_counts, n):
+    """Dense counts / generated counts -> a device history table, validated in
+    the reference's order (sampling.py:54-58, then :62-65) by the device
+    builder."""
+    c = _count_vector(counts, n)
+    if c is None:
+        raise ValidationError(_COUNTS_MSG)
+    g = None
+    if generated_counts is not None:
+        g = _count_vector(generated_counts, n)
+        if g is None:
+            # The counts are fully validated before the generated counts are looked at.
+            _, st = batch.HistoryTable.from_dense_device(c)
+            if int(st.item()) != N.OK:
+                _raise_status(int(st.item()))
+            raise ValidationError(_GENERATED_MSG)
+    table, st = batch.HistoryTable.from_dense_device(c, g)
+    if int(st.item()) != N.OK:
+        _raise_status(int(st.item()))
+    return table
 
 
 def _distribution(values):

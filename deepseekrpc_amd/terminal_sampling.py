@@ -18,7 +18,8 @@ import numpy as np
 import torch
 
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
-from .sampling import RandomStreams, SamplingPolicy, _on_device, categorical, verify_drafts
+from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _history_table, _logit_vector, _on_device,
+                       _raise_status, categorical, verify_drafts)
 
 
 def _logits_device(logits, rows, vocabulary):
@@ -129,22 +130,38 @@ class SamplingWork:
         self.proposal_ids, self.proposal_rows = [], []
         self.decision, self.closed = None, False
         self._proposal_ready = False
+        self._table = None  # device history table of counts / generated_counts, built on first use
 
     def _open(self):
         if self.closed or self.owner.active is not self:
             raise ValidationError("terminal sampling transaction is closed or stale")
 
     def distribution(self, logits, prefix):
-        """Device distribution of one row conditioned on a tentative prefix."""
+        """Device distribution of one row conditioned on a tentative prefix
+        (terminal_sampling.py:127-136): the transaction's counts live in one
+        device history table, and each prefix token is appended to it on the
+        device (one more count and generated count each) instead of copying
+        and updating the dense vectors on the host."""
         self._open()
-        counts = self.counts.copy()
-        generated = self.generated_counts.copy()
-        for token in prefix:
-            counts[token] += 1
-            generated[token] += 1
+        n, device_input = _logit_vector(logits)
+        if n != len(self.counts):
+            raise ValidationError(_COUNTS_MSG)
+        table = self._history(prefix)
         mask = None if self.allowed is None else self.allowed(tuple(prefix))
-        return self.policy.probabilities(logits, counts=counts, generated_counts=generated,
-                                         logit_bias=self.logit_bias, allowed=mask)
+        return self.policy._probabilities_with(logits, n, device_input, table, self.logit_bias, mask)
+
+    def _history(self, prefix):
+        if self._table is None:
+            self._table = _history_table(self.counts, self.generated_counts, len(self.counts))
+        if not prefix:
+            return self._table
+        dev = self._table.offsets.device
+        tokens = torch.tensor([int(t) for t in prefix], dtype=torch.int32, device=dev)
+        off = torch.tensor([0, len(prefix)], dtype=torch.int64, device=dev)
+        table, status = self._table.append(tokens, off, vocab=len(self.counts))
+        if int(status.item()) != 0:
+            _raise_status(int(status.item()))
+        return table
 
     def propose(self, graph, result):
         """Sequential Markov-conditioned proposals over the five-row draft graph."""

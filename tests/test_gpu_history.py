@@ -164,13 +164,71 @@ def test_append_capacity_too_small_writes_nothing():
 
 
 def test_device_tables_feed_the_sampler_like_host_tables():
-    # The stress rows sampled with a device-built table and with the host-built
-    # one give identical decisions.
+    # The stress rows sampled with a device-built table (as workloads.to_device
+    # builds it) and with the host-built one give identical decisions.
     w = workloads.select_rows(workloads.c5(), list(range(0, 32)) + list(range(512, 544)))
     d = workloads.to_device(w)
-    t, st = batch.HistoryTable.from_token_lists_device(w.histories)
-    assert (st.cpu() == 0).all()
-    a = batch.sample_rows(d.logits, w.policies, history=d.history, uniforms=d.uniforms)
-    b = batch.sample_rows(d.logits, w.policies, history=t, uniforms=d.uniforms)
+    host_table = batch.HistoryTable.from_token_lists(w.histories, device=DEV)
+    a = batch.sample_rows(d.logits, w.policies, history=host_table, uniforms=d.uniforms)
+    b = batch.sample_rows(d.logits, w.policies, history=d.history, uniforms=d.uniforms)
     for f in ("tokens", "consumed", "status", "flags"):
         assert torch.equal(getattr(a, f), getattr(b, f)), f
+
+
+def test_drop_in_count_validation_order_and_messages():
+    from deepseekrpc_amd.jsonutil import ValidationError
+    from deepseekrpc_amd.sampling import SamplingPolicy
+    pol = SamplingPolicy(repetition_penalty=1.5, presence_penalty=0.5, frequency_penalty=0.25)
+    x = np.linspace(-2, 2, 64).astype(np.float32)
+    counts = np.zeros(64, np.int32)
+    counts[[3, 9]] = [2, 1]
+    bad = counts.copy()
+    bad[4] = -1
+    big = counts.astype(np.int64)
+    big[5] = 1 << 40                       # out of range as int64; must stay out of range on the device
+    over = counts.copy()
+    over[[1, 2]] = H.MAX_COUNT // 2 + 1    # sampling.py:57 total above the bound
+    cmsg, gmsg = "sampling frequency counts do not match", "generated token counts must be a subset"
+    for c, g, msg in ((bad, None, cmsg), (big, None, cmsg), (over, None, cmsg),
+                      (counts, counts + (np.arange(64) == 9), gmsg),
+                      (bad, np.zeros(3, np.int32), cmsg),          # counts are validated first
+                      (counts, np.zeros(3, np.int32), gmsg),
+                      (counts[:10], None, cmsg)):
+        with pytest.raises(ValidationError, match=msg):
+            pol.probabilities(x, counts=c, generated_counts=g)
+    # Device count tensors give the numbers the NumPy ones give.
+    a = pol.probabilities(x, counts=counts, generated_counts=np.minimum(counts, 1))
+    b = pol.probabilities(x, counts=torch.from_numpy(counts).to(DEV),
+                          generated_counts=torch.from_numpy(np.minimum(counts, 1)).to(DEV))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_prefix_distribution_equals_dense_prefix_counts():
+    # terminal_sampling.py:127-136: the conditioned distribution uses counts
+    # and generated counts with one added per prefix token.  The device path
+    # appends the prefix to the transaction's table; the result must be
+    # bit-identical to probabilities() on the dense vectors with the prefix
+    # added on the host.
+    from deepseekrpc_amd.sampling import SamplingPolicy
+    from deepseekrpc_amd.terminal_sampling import TerminalSampler
+    V = 129280
+    rng = np.random.default_rng(12)
+    counts = np.zeros(V, np.int32)
+    ids = rng.choice(V, 3000, replace=False)
+    counts[ids] = rng.integers(1, 4, 3000)
+    gen = np.minimum(counts, rng.integers(0, 3, V)).astype(np.int32)
+    pol = SamplingPolicy(temperature=0.9, top_p=0.95, repetition_penalty=1.2, presence_penalty=0.4,
+                         frequency_penalty=0.2)
+    logits = torch.from_numpy(rng.normal(0, 2, V).astype(np.float32)).to(DEV)
+    sampler = TerminalSampler(seed=7, vocabulary=V)
+    work = sampler._begin(pol, counts, 8, frozenset(), generated_counts=gen, logit_bias=None, allowed=None,
+                          grammar_identity=None, stop_identity=None)
+    for prefix in ([], [int(ids[0])], [5, 5, int(ids[1]), V - 1]):
+        got = work.distribution(logits, prefix)
+        c, g = counts.copy(), gen.copy()
+        for t in prefix:
+            c[t] += 1
+            g[t] += 1
+        want = pol.probabilities(logits, counts=c, generated_counts=g)
+        assert torch.equal(got, want), prefix
+    work.abort()
