@@ -10,8 +10,10 @@ launch over the batch.
 ``--workload`` selects one of the other seeded row families instead (see
 deepseekrpc_amd/workloads.py): c1 (1 fp32 row with probabilities out), c2 (64
 bf16 rows with 4,096-token histories), c4 (32 verifier requests x 4 fp32
-drafts; one step is one ``dsr_verify_drafts`` call) and c5 (1,024 bf16 rows,
-mixed greedy, 16,384-token histories).
+drafts; one step is one ``dsr_verify_drafts`` call), c5 (1,024 bf16 rows,
+mixed greedy, 16,384-token histories) and hist (1,024 rows x 16,384 token
+ids built into device history tables; one step is one
+``dsr_history_append`` call).
 
 Prints one JSON line: the throughput, the roofline of the step (algorithmic
 HBM bytes / HIP-event time of the launches on their stream, against 8 TB/s)
@@ -45,6 +47,8 @@ WORKLOADS = {
            "k_verify_dists + k_verify_stats + k_verify_chain + k_verify_draw + k_verify_finish"),
     "c5": ("sampled rows/sec at B=1024×V=129,280 bf16, mixed greedy, 16,384-token histories", "rows/s", 2,
            "k_sample_bf16_full"),
+    "hist": ("history rows/sec: 1,024 rows x 16,384 token ids -> sparse count tables over V=129,280", "rows/s", 10,
+             "k_history_append (count) + k_history_offsets + k_history_append (write)"),
 }
 
 DESCRIPTIONS = {
@@ -55,14 +59,18 @@ DESCRIPTIONS = {
     "c4": "c4: 32 requests x 4 drafts, fp32 target [32,5,129280] and draft [32,4,129280], default policy, limit 10",
     "c5": "c5: 1024 rows x 129280 bf16 (N(0,1) / near-flat with 8-way max ties), even rows greedy, odd rows T 1 "
           "top-p 0.9, rep 1.1 / pres 0.5 / freq 0.3 over 16384-token histories",
+    "hist": "hist: 1024 rows x 16384 token ids U{0..129279}, all generated, appended into an empty history table "
+            "(one dsr_history_append call)",
 }
 
 _CPU = {}
 
 
 def _units(name, w):
-    """Rows of a sampling workload; requests of the verifier workload."""
-    return w.extra["target"].shape[0] if name == "c4" else w.rows
+    """Rows of a sampling or history workload; requests of the verifier workload."""
+    if name == "c4":
+        return w.extra["target"].shape[0]
+    return w.extra["tokens"].shape[0] if name == "hist" else w.rows
 
 
 def _draft_ids_cpu(e, r):
@@ -76,10 +84,18 @@ def _draft_ids_cpu(e, r):
 
 
 def _cpu_rows(span):
+    from oracle import history_oracle as H
     from oracle import sampling_oracle as O
     w, name = _CPU["w"], _CPU["name"]
     lo, hi = span
     V = w.logits.shape[1]
+    if name == "hist":
+        toks = w.extra["tokens"]
+        rows = [toks[r % toks.shape[0]] for r in range(lo, hi)]
+        t0 = time.perf_counter()
+        for row in rows:
+            H.append(None, None, None, None, [row], V)
+        return hi - lo, time.perf_counter() - t0
     jobs = []
     for r in range(lo, hi):
         r = r % _units(name, w)
@@ -122,8 +138,18 @@ def cpu_baseline(name, w, passes):
     unit = WORKLOADS[name][1]
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port", "value_per_core": n / busy,
             "sample": f"{n} {'requests' if name == 'c4' else 'rows'} ({passes} pass(es) over the {_units(name, w)} of the "
-                      f"same workload, {busy:.1f} s of CPU work) with the float64 NumPy oracle on {cores} worker "
-                      f"processes; {n / busy:.2f} {unit} per core"}
+                      f"same workload, {busy:.1f} s of CPU work) with the "
+                      f"{'NumPy history oracle (np.add.at on dense counts)' if name == 'hist' else 'float64 NumPy oracle'}"
+                      f" on {cores} worker processes; {n / busy:.2f} {unit} per core"}
+
+
+class _HistResult:
+    """Status and (empty) flags of a history build, shaped like a sampling result."""
+
+    def __init__(self, status):
+        import torch
+        self.status = status
+        self.flags = torch.zeros_like(status)
 
 
 def _prepare(name, w):
@@ -131,6 +157,14 @@ def _prepare(name, w):
     import torch
 
     from deepseekrpc_amd import batch, workloads
+    if name == "hist":
+        toks = w.extra["tokens"]
+        off = np.arange(toks.shape[0] + 1, dtype=np.int64) * toks.shape[1]
+        prep = batch.PreparedHistoryAppend(torch.from_numpy(toks.reshape(-1)).cuda(), torch.from_numpy(off).cuda(),
+                                           vocab=w.logits.shape[1])
+        prep.launch()
+        prep.result = _HistResult(prep.status)
+        return prep, workloads.algorithmic_bytes_history(w), toks.shape[0]
     if name == "c4":
         e = w.extra
         R, K, V = e["target"].shape[0], e["K"], e["target"].shape[2]
@@ -205,6 +239,8 @@ def main():
         # A plain read-N/write-N kernel over the batch's logit bytes, for
         # scaling the FETCH_SIZE / WRITE_SIZE counters.
         src = prep.inputs[0].view(torch.int32).reshape(-1) if name != "c4" else prep.inputs[0][0].reshape(-1)
+        if name == "hist":
+            src = prep.inputs[0]
         dst = torch.empty_like(src)
         for _ in range(args.steps):
             torch.bitwise_not(src, out=dst)
@@ -221,7 +257,7 @@ def main():
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16" if w.dtype == "bf16" else "f32", "data": "synthetic",
+        "vs_baseline": None, "dtype": {"bf16": "bf16", "i32": "int32"}.get(w.dtype, "f32"), "data": "synthetic",
         "config": cfg,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel_ms": kern_ms,

@@ -390,6 +390,41 @@ class PreparedSample:
         return self.result
 
 
+class PreparedHistoryAppend:
+    """A ``dsr_history_append`` call with its outputs allocated once, at the
+    exact upper bound (old entries plus new tokens).  ``launch()`` re-issues
+    it on the current stream; ``table()`` returns the result (reading the
+    total is the only synchronisation)."""
+
+    def __init__(self, tokens: torch.Tensor, tok_off: torch.Tensor, table: HistoryTable | None = None,
+                 gen_from: torch.Tensor | None = None, vocab: int = VOCAB):
+        _require(tokens, "tokens", torch.int32)
+        _require(tok_off, "tok_off", torch.int64)
+        rows = tok_off.numel() - 1
+        dev = tok_off.device
+        has = table is not None and table.ids.numel() > 0
+        self.cap = (table.ids.numel() if has else 0) + tokens.numel()
+        self.off = torch.empty(rows + 1, dtype=torch.int64, device=dev)
+        self.status = torch.empty(rows, dtype=torch.int32, device=dev)
+        self.out = [torch.empty(max(self.cap, 1), dtype=torch.int32, device=dev) for _ in range(3)]
+        self.inputs = (tokens, tok_off, table, gen_from)
+        self._args = ((_ptr(table.offsets), _ptr(table.ids), _ptr(table.counts), _ptr(table.generated)) if has
+                      else (None,) * 4) + (
+            _ptr(tokens) if tokens.numel() else ctypes.c_void_p(tok_off.data_ptr()), _ptr(tok_off), _ptr(gen_from),
+            rows, vocab, _ptr(self.off), *(_ptr(o) for o in self.out), self.cap, _ptr(self.status))
+        self._lib = N.load()
+
+    def launch(self):
+        rc = self._lib.dsr_history_append(*self._args, _stream())
+        if rc != 0:
+            N.check(rc, "dsr_history_append")
+        return self
+
+    def table(self) -> HistoryTable:
+        total = int(self.off[-1].item())
+        return HistoryTable(self.off, *(o[:total] for o in self.out))
+
+
 @dataclass
 class VerifyResult:
     accepted: torch.Tensor

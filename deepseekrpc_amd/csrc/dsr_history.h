@@ -17,12 +17,13 @@
 // tokens to a table as np.add.at does (history.py:136-137; the tentative
 // prefix of terminal_sampling.py:129-133): the row's new tokens mark a
 // presence bitmap of the vocabulary in LDS next to a bitmap of the row's old
-// ids; per-word rank bases of both bitmaps and of their difference (new ids
-// the table lacks) give every output position in closed form:
-//   old id y, old rank i:  i + #(new ids absent from the table below y)
-//   absent new id x:       #(old ids below x) + #(absent new ids below x)
-// and a count table indexed by rank among the new ids carries each new id's
-// multiplicity and generated multiplicity (16 bits each).
+// ids.  Per-word rank bases of the old ids, of the new ids and of the new ids
+// the table lacks give, for any id, its rank in the merged row (old ids
+// below it plus absent new ids below it), its old entry and its slot in a
+// count table indexed by rank among the new ids, which carries each new id's
+// multiplicity and generated multiplicity (16 bits each).  In the write pass
+// each lane expands one word of the union of the two bitmaps, a wave 64
+// consecutive words, so a wave's stores stay within one stretch of the row.
 #pragma once
 
 #include "dsr_wave.h"
@@ -33,6 +34,8 @@ constexpr int kHistWords = (DSR_MAX_VOCAB + 31) / 32;  // 4040 bitmap words
 constexpr int kMaxAppend = DSR_MAX_APPEND;            // new tokens per row and call
 static_assert(4 * kThreads >= kHistWords, "four bitmap words per thread");
 static_assert(kMaxAppend < 65536, "multiplicities are packed in 16 bits");
+constexpr int kTokPer = kMaxAppend / kThreads;  // a row's new tokens held per thread
+static_assert(kTokPer * kThreads == kMaxAppend, "new tokens split evenly over the threads");
 
 struct HistAppendArgs {
   const int64_t* off;   // [rows + 1] or null: empty input table
@@ -118,10 +121,20 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
     if (ok) atomicOr(&sh.ob[id >> 5], 1u << (id & 31));
     else sh.bad = 1;
   }
-  for (int64_t i = t0 + tid; i < t1; i += kThreads) {
-    const int32_t t = a.tokens[i];
-    if (t >= 0 && t < V) atomicOr(&sh.nb[t >> 5], 1u << (t & 31));
-    else sh.bad = 1;
+  // The row's new tokens, all loaded before any is used: token q of this
+  // thread is at position tid + q * kThreads of the row's tokens.
+  int32_t tk[kTokPer];
+#pragma unroll
+  for (int q = 0; q < kTokPer; ++q) {
+    const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
+    tk[q] = i < m ? a.tokens[t0 + i] : 0;
+  }
+#pragma unroll
+  for (int q = 0; q < kTokPer; ++q) {
+    if ((int64_t)tid + (int64_t)q * kThreads < m) {
+      if (tk[q] >= 0 && tk[q] < V) atomicOr(&sh.nb[tk[q] >> 5], 1u << (tk[q] & 31));
+      else sh.bad = 1;
+    }
   }
   lds_barrier();
   if (sh.bad) {  // uniform: read after the barrier
@@ -172,38 +185,52 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
   }
   lds_barrier();
   // Multiplicities of the new ids (and of their generated occurrences).
-  for (int64_t i = t0 + tid; i < t1; i += kThreads) {
-    const uint32_t t = (uint32_t)a.tokens[i], w = t >> 5, b = t & 31u;
-    atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], (i - t0 >= gf) ? 0x10001u : 1u);
+#pragma unroll
+  for (int q = 0; q < kTokPer; ++q) {
+    const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
+    if (i < m) {
+      const uint32_t t = (uint32_t)tk[q], w = t >> 5, b = t & 31u;
+      atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], i >= gf ? 0x10001u : 1u);
+    }
   }
   lds_barrier();
+  // The merged row is the union of both bitmaps in id order.  Lane = word:
+  // wave w takes the groups of 64 consecutive words g = w, w + 16, ..., and
+  // each lane writes its word's ids in bit order from the word's rank in the
+  // merged row (old ids below it plus absent new ids below it), so a wave's
+  // stores cover one contiguous stretch of the output.  An old id's entry is
+  // its rank in the old bitmap; a new id's multiplicities are at its rank in
+  // the new bitmap.
+  const int lane = lane_id(), wave = wave_id();
   const int64_t base = a.out_off[row];
-  // The table's entries, shifted past the absent new ids below them.
-  for (int64_t e = o0 + tid; e < o1; e += kThreads) {
-    const int32_t id = a.ids[e];
-    const uint32_t w = (uint32_t)id >> 5, b = (uint32_t)id & 31u;
-    const uint32_t nwv = sh.nb[w], owv = sh.ob[w];
-    const uint32_t add = ((nwv >> b) & 1u) ? sh.cnt[sh.nbase[w] + bits_below(nwv, b)] : 0u;
-    const int64_t pos = base + (e - o0) + sh.ubase[w] + bits_below(nwv & ~owv, b);
-    a.out_ids[pos] = id;
-    a.out_count[pos] = a.count[e] + (int32_t)(add & 0xFFFFu);
-    a.out_gen[pos] = a.gen[e] + (int32_t)(add >> 16);
-  }
-  // New ids the table lacks.
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int w = 4 * tid + q;
-    if (w >= words) continue;
-    const uint32_t uw = nw[q] & ~ow[q];
-    uint32_t left = uw;
-    while (left) {
+  for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {
+    const int w = g0 + lane;
+    uint32_t nwv = 0u, owv = 0u, nbw = 0u, obw = 0u, ubw = 0u;
+    if (w < words) {
+      nwv = sh.nb[w];
+      owv = sh.ob[w];
+      nbw = sh.nbase[w];
+      obw = sh.obase[w];
+      ubw = sh.ubase[w];
+    }
+    int64_t p = base + obw + ubw;
+    for (uint32_t left = nwv | owv; left; left &= left - 1u) {
       const uint32_t b = (uint32_t)(__ffs(left) - 1);
-      left &= left - 1u;
-      const uint32_t add = sh.cnt[sh.nbase[w] + bits_below(nw[q], b)];
-      const int64_t pos = base + sh.obase[w] + bits_below(ow[q], b) + sh.ubase[w] + bits_below(uw, b);
-      a.out_ids[pos] = 32 * w + (int32_t)b;
-      a.out_count[pos] = (int32_t)(add & 0xFFFFu);
-      a.out_gen[pos] = (int32_t)(add >> 16);
+      int32_t c = 0, g = 0;
+      if ((owv >> b) & 1u) {
+        const int64_t e = o0 + obw + bits_below(owv, b);
+        c = a.count[e];
+        g = a.gen[e];
+      }
+      if ((nwv >> b) & 1u) {
+        const uint32_t add = sh.cnt[nbw + bits_below(nwv, b)];
+        c += (int32_t)(add & 0xFFFFu);
+        g += (int32_t)(add >> 16);
+      }
+      a.out_ids[p] = 32 * w + (int32_t)b;
+      a.out_count[p] = c;
+      a.out_gen[p] = g;
+      ++p;
     }
   }
 }
