@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_NAME = "libdsr_sampling.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -65,7 +65,7 @@ class SampleArgs(ctypes.Structure):
         ("bias_off", _p), ("bias_ids", _p), ("bias_val", _p), ("allow_bits", _p), ("allow_ld", _i64),
         ("uniforms", _p), ("out_token", _p), ("out_consumed", _p), ("out_status", _p), ("out_flags", _p),
         ("out_probs_f32", _p), ("out_probs_f64", _p), ("probs_ld", _i64), ("out_kept_bits", _p), ("kept_ld", _i64),
-        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_state", _p),
     ]
 
 

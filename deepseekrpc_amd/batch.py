@@ -302,13 +302,17 @@ _default_ws = Workspace()
 
 def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None = None, bias: BiasTable | None = None,
                 allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
-                probs: str | None = None, kept: bool = False, workspace: Workspace | None = None) -> SampleResult:
+                rng_state: torch.Tensor | None = None, probs: str | None = None, kept: bool = False,
+                workspace: Workspace | None = None) -> SampleResult:
     """Sample every row of ``logits [rows, V]`` on the current stream.
 
     ``policies`` is a device tensor made by ``policy_tensor`` or a list of
     policy objects/dicts.  ``uniforms`` (float64 ``[rows]``) are the pre-drawn
-    target-domain draws; without them only the distribution is computed.
-    ``probs`` may be ``"f32"`` or ``"f64"`` to return the final probabilities.
+    target-domain draws.  ``rng_state`` (int64 ``[rows, 4]``, see
+    ``pcg64_states``) instead lets each row that needs a draw take it on the
+    device from its PCG64 state, which is advanced in place.  With neither,
+    only the distribution is computed.  ``probs`` may be ``"f32"`` or
+    ``"f64"`` to return the final probabilities.
     """
     lib = N.load()
     _require_cuda(logits, "logits", rows_strided=True)
@@ -334,6 +338,8 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         _require_cuda(uniforms, "uniforms")
         if uniforms.dtype != torch.float64 or uniforms.numel() != rows:
             raise ValueError("uniforms must be float64 [rows]")
+    if rng_state is not None:
+        _require(rng_state, "rng_state", torch.int64, rows * 4)
     if allow_bits is not None:
         _require_cuda(allow_bits, "allow_bits")
         if allow_bits.dim() != 2 or allow_bits.shape[0] != rows or allow_bits.element_size() != 4:
@@ -353,6 +359,8 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.stride(0)
     if uniforms is not None:
         a.uniforms = uniforms.data_ptr()
+    if rng_state is not None and rows > 0:
+        a.rng_state = rng_state.data_ptr()
     a.out_token, a.out_consumed = res.tokens.data_ptr(), res.consumed.data_ptr()
     a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
     if res.probs is not None:
@@ -367,6 +375,35 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     N.check(lib.dsr_sample_rows(ctypes.byref(a), _stream()), "dsr_sample_rows")
     res.args = a
     return res
+
+
+_M64 = (1 << 64) - 1
+
+
+def pcg64_states(generators, device="cuda") -> torch.Tensor:
+    """The PCG64 states of NumPy Generators (or PCG64 bit generators), one
+    row per generator, as the int64 ``[rows, 4]`` device tensor
+    ``sample_rows(rng_state=...)`` takes: state lo, state hi, increment lo,
+    increment hi (the 128-bit integers of the bit generator's state dict)."""
+    out = np.zeros((len(generators), 4), np.uint64)
+    for i, g in enumerate(generators):
+        st = getattr(g, "bit_generator", g).state
+        if st["bit_generator"] != "PCG64":
+            raise ValueError("device draws reproduce NumPy's PCG64 only")
+        s, inc = st["state"]["state"], st["state"]["inc"]
+        out[i] = (s & _M64, s >> 64, inc & _M64, inc >> 64)
+    return torch.from_numpy(out.view(np.int64)).to(device)
+
+
+def pcg64_restore(generators, states: torch.Tensor) -> None:
+    """Write device-advanced states back into the NumPy generators, so that
+    their next host draws continue the same streams."""
+    words = states.cpu().numpy().view(np.uint64)
+    for g, w in zip(generators, words):
+        bg = getattr(g, "bit_generator", g)
+        st = bg.state
+        st["state"]["state"] = int(w[0]) | (int(w[1]) << 64)
+        bg.state = st
 
 
 class PreparedSample:

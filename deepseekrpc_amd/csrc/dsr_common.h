@@ -210,6 +210,38 @@ __device__ __forceinline__ double exp_nonpos(double z, const double* tab) {
   return ldexp(tab[k & 63] * p, k >> 6);
 }
 
+// One Generator.random() of NumPy's PCG64 bit generator (O'Neill's PCG
+// family: a 128-bit linear congruential state with the XSL-RR output, as
+// numpy/random/src/pcg64 implements it): s <- s * M + inc (mod 2^128),
+// x = hi(s) ^ lo(s), out = rotr64(x, hi(s) >> 58), u = (out >> 11) * 2^-53.
+// st holds s and inc as little-endian 128-bit integers (lo, hi, inc lo,
+// inc hi); next receives the advanced state in the same layout.
+__device__ __forceinline__ double pcg64_random(const uint64_t* st, uint64_t next[4]) {
+  const unsigned __int128 M = ((unsigned __int128)0x2360ED051FC65DA4ull << 64) | 0x4385DF649FCCF645ull;
+  const unsigned __int128 inc = ((unsigned __int128)st[3] << 64) | st[2];
+  unsigned __int128 s = ((unsigned __int128)st[1] << 64) | st[0];
+  s = s * M + inc;
+  const uint64_t hi = (uint64_t)(s >> 64), lo = (uint64_t)s;
+  const uint32_t rot = (uint32_t)(hi >> 58);
+  const uint64_t x = hi ^ lo;
+  const uint64_t out = (x >> rot) | (x << ((64u - rot) & 63u));
+  next[0] = lo;
+  next[1] = hi;
+  next[2] = st[2];
+  next[3] = st[3];
+  return (double)(out >> 11) * 0x1.0p-53;
+}
+
+// A row's draw source: its PCG64 state (rng_state) when the caller gave
+// states, else its pre-drawn uniform.
+__device__ __forceinline__ bool has_draws(const dsr_sample_args_t& a) { return a.uniforms || a.rng_state; }
+
+__device__ __forceinline__ void store_rng(const dsr_sample_args_t& a, int64_t row, const uint64_t next[4]) {
+  uint64_t* o = a.rng_state + 4 * row;
+  o[0] = next[0];
+  o[1] = next[1];
+}
+
 __device__ __forceinline__ bool policy_ok(const dsr_policy_t& p) {
   // Bounds of SamplingPolicy.__post_init__ (sampling.py:38-43); NaN fails every test.
   return p.temperature >= 0.0 && p.temperature <= 100.0 && p.top_p >= 0.0 && p.top_p <= 1.0 &&

@@ -75,7 +75,7 @@ struct FastLists {
   uint16_t kkey[kFastMaxK];                // kept tokens, index order
   uint32_t kidx[kFastMaxK];
   uint32_t wn[kWaves];
-  uint32_t polw[16];                       // the row's policy words, then its uniform
+  uint32_t polw[24];                       // the row's policy words, then its uniform or PCG64 state
   long long sel_above;
   int sel;
   int bc_i[2];
@@ -258,11 +258,12 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.policy + row), (short)0, (int)sizeof(dsr_policy_t), 0x00020000);
   const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
-      a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy, (short)0, a.uniforms ? 8 : 0, 0x00020000);
+      a.rng_state ? (void*)(a.rng_state + 4 * row) : (a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy),
+      (short)0, a.rng_state ? 32 : (a.uniforms ? 8 : 0), 0x00020000);
   constexpr int kPolWords = (int)(sizeof(dsr_policy_t) / 4);
   const uint32_t pw = __builtin_amdgcn_raw_buffer_load_b32(prs, tid < kPolWords ? 4 * tid : 0x7FFFFFF0, 0, 0) |
                       __builtin_amdgcn_raw_buffer_load_b32(
-                          urs, (tid >= kPolWords && tid < kPolWords + 2) ? 4 * (tid - kPolWords) : 0x7FFFFFF0, 0, 0);
+                          urs, (tid >= kPolWords && tid < kPolWords + 8) ? 4 * (tid - kPolWords) : 0x7FFFFFF0, 0, 0);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
       a.allow_bits ? (void*)(a.allow_bits + row * a.allow_ld) : (void*)&kAllowAll, (short)0, (int)C, 0x00020000);
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -290,7 +291,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     uint4* zm = (uint4*)&sh.mass[0];   // 4096 x 8 bytes of mass
 #pragma unroll
     for (int i = 0; i < 2; ++i) zm[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < kPolWords + 2) sh.polw[tid] = pw;
+    if (tid < kPolWords + 8) sh.polw[tid] = pw;
   }
   lds_barrier();  // LDS only: the row's loads keep streaming
 
@@ -444,7 +445,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
       fast_clear_outputs(a, row);
       if (tid == 0) fast_scatter(a, row, tok, 1.0);
     }
-    if (tid == 0) fast_write_result(a, row, DSR_OK, a.uniforms ? tok : -1, 0, 0);
+    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws(a) ? tok : -1, 0, 0);
     return 0;
   }
 
@@ -653,13 +654,22 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     if (tid == 0) fast_write_result(a, row, DSR_E_NO_MASS, -1, 0, flags);
     return 0;
   }
-  if (!a.uniforms) {
+  if (!has_draws(a)) {
     if (tid == 0) fast_write_result(a, row, DSR_OK, -1, 0, flags);
     return 0;
   }
   if (npos == 1) {  // no uniform is drawn (sampling.py:120-122)
     if (pos) fast_write_result(a, row, DSR_OK, idx, 0, flags);
     return 0;
+  }
+  uint64_t rng_next[4];
+  if (a.rng_state) {  // the row's PCG64 state, staged in LDS with the policy words
+    uint64_t st4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      st4[i] = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)sh.polw[kPolWords + 2 * i]) |
+               ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)sh.polw[kPolWords + 2 * i + 1]) << 32);
+    u = pcg64_random(st4, rng_next);
   }
   if (!(u >= 0.0 && u < 1.0)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
@@ -675,6 +685,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     thr = ctot - 1;
     flags |= DSR_FLAG_MARGIN;
   }
+  if (a.rng_state && tid == 0) store_rng(a, row, rng_next);  // the row is decided here
   if (fx > 0 && ex <= thr && thr < ex + fx) {
     const double tol = ((double)npos + 16.0) * 0x1p-51 * (double)ctot + (double)npos + 2.0;
     if ((double)(ex + fx) - thr_d <= tol || (ex > 0 && thr_d - (double)ex <= tol)) flags |= DSR_FLAG_MARGIN;

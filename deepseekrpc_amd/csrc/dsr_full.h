@@ -407,7 +407,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       fast_clear_outputs(a, row);
       if (tid == 0) fast_scatter(a, row, tok, 1.0);
     }
-    if (tid == 0) fast_write_result(a, row, DSR_OK, a.uniforms ? tok : -1, 0, 0);
+    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws(a) ? tok : -1, 0, 0);
     return 0;
   }
   unsigned flags = 0;
@@ -927,7 +927,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       fast_scatter(a, row, id, p);
     }
   }
-  if (!a.uniforms) {
+  if (!has_draws(a)) {
     if (tid == 0) fast_write_result(a, row, DSR_OK, -1, 0, flags);
     return 0;
   }
@@ -937,7 +937,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     if (tid == 0) fast_write_result(a, row, DSR_OK, tok, 0, flags);
     return 0;
   }
-  const double u = a.uniforms[row];
+  uint64_t rng_next[4];
+  const double u = a.rng_state ? pcg64_random(a.rng_state + 4 * row, rng_next) : a.uniforms[row];
   if (!(u >= 0.0 && u < 1.0)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
@@ -1032,6 +1033,9 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     }
   }
   lds_barrier();
+  // The row is decided: its advanced PCG64 state goes back (every thread read
+  // the old one before the barriers above).
+  if (a.rng_state && tid == 0 && !sh.bc_i[2]) store_rng(a, row, rng_next);
   return sh.bc_i[2] ? kHandCapacity : 0;  // unreachable: thr lies inside the chunk found above
 }
 

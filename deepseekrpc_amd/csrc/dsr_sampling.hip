@@ -29,16 +29,21 @@ __device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t r
   const int64_t V = a.vocab;
   int64_t token = -1;
   int consumed = 0;
-  if (st == DSR_OK && a.uniforms) {
+  if (st == DSR_OK && has_draws(a)) {
     if (d.npos == 1) {
       token = d.first;  // sampling.py:120-122: no uniform is drawn
     } else {
-      const double u = a.uniforms[row];
+      uint64_t next[4];
+      const double u = a.rng_state ? pcg64_random(a.rng_state + 4 * row, next) : a.uniforms[row];
       if (!(u >= 0.0 && u < 1.0)) {
         st = DSR_E_UNIFORM;
       } else {
         token = cdf_search(W, V, u, d.npos, sh, flags);
         consumed = 1;
+      }
+      if (a.rng_state) {
+        __syncthreads();  // every thread has read the state
+        if (threadIdx.x == 0) store_rng(a, row, next);
       }
     }
   }

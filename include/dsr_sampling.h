@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSR_ABI_VERSION 1
+#define DSR_ABI_VERSION 2
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
@@ -100,7 +100,17 @@ typedef struct dsr_policy {
  * `generated_counts` pair restricted to counts > 0 (sampling.py:54-66).
  * Logit bias is a second per-row CSR table with strictly increasing ids and
  * values in [-100, 100] (sampling.py:69-74).  allow_bits holds one bit per
- * token, bit (i & 31) of word i >> 5, 1 = allowed (sampling.py:75-79). */
+ * token, bit (i & 31) of word i >> 5, 1 = allowed (sampling.py:75-79).
+ *
+ * Draws: a row that needs its uniform (more than one positive probability,
+ * sampling.py:120-125) takes uniforms[row], or, when rng_state is set, draws
+ * it on the device as Generator.random() of NumPy's PCG64 does from the
+ * row's state and writes the advanced state back (rng_state[4r .. 4r+3] =
+ * state lo, state hi, increment lo, increment hi: the 128-bit integers of
+ * the bit generator's state dict).  A row that needs no draw leaves its state
+ * as it was, as the reference's `target` domain stays untouched
+ * (sampling.py:120-122; terminal_sampling.py:83-95).  out_consumed reports
+ * the draw either way. */
 typedef struct dsr_sample_args {
   const void* logits;          /* [rows, ld] of dtype */
   int32_t dtype;               /* DSR_BF16 | DSR_F32 | DSR_F64 */
@@ -130,6 +140,7 @@ typedef struct dsr_sample_args {
   int64_t kept_ld;
   void* workspace;             /* >= dsr_sample_workspace_bytes(rows, vocab) */
   size_t workspace_bytes;
+  uint64_t* rng_state;         /* [rows, 4] or NULL; see below */
 } dsr_sample_args_t;
 
 /* Arguments of dsr_verify_drafts: the exact sampled speculative verifier for
