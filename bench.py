@@ -152,7 +152,7 @@ class _HistResult:
         self.flags = torch.zeros_like(status)
 
 
-def _prepare(name, w):
+def _prepare(name, w, device_rng=False):
     """Device inputs and a launch closure for one step of the workload."""
     import torch
 
@@ -177,8 +177,11 @@ def _prepare(name, w):
                                     torch.from_numpy(e["u_target"]).cuda(), torch.from_numpy(e["limit"]).cuda())
         return prep, workloads.algorithmic_bytes_verify(w), R
     d = workloads.to_device(w)
+    draws = dict(uniforms=d.uniforms)
+    if device_rng:  # one PCG64 stream per row, drawn and advanced on the device
+        draws = dict(rng_state=batch.pcg64_states([np.random.default_rng(41117 + r) for r in range(w.rows)]))
     prep = batch.PreparedSample(d.logits, d.policies, history=d.history, allow_bits=d.allow_bits,
-                                uniforms=d.uniforms, probs="f32" if name == "c1" else None)
+                                probs="f32" if name == "c1" else None, **draws)
     probs_bytes = 4 * w.logits.shape[1] if name == "c1" else 0
     return prep, workloads.algorithmic_bytes(w, probs_bytes), w.rows
 
@@ -190,6 +193,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--device-rng", action="store_true",
+                    help="sampling workloads: draw each row's uniform on the device from a PCG64 state")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain copy kernel over the batch's logit bytes (for HBM counter scaling)")
     args = ap.parse_args()
@@ -208,7 +213,9 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    prep, alg_bytes, units = _prepare(name, w)
+    if args.device_rng and name in ("c4", "hist"):
+        raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
+    prep, alg_bytes, units = _prepare(name, w, args.device_rng)
     torch.cuda.synchronize()
     res = prep.result
     status = res.status.cpu().numpy()
@@ -254,6 +261,8 @@ def main():
         traffic = json.load(open(tf)).get("bytes_per_launch")
     cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]),
            "general_path_rows": general, "kernels": kernels}
+    if name not in ("c4", "hist"):
+        cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",

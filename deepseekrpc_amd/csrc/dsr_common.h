@@ -232,9 +232,11 @@ __device__ __forceinline__ double pcg64_random(const uint64_t* st, uint64_t next
   return (double)(out >> 11) * 0x1.0p-53;
 }
 
-// A row's draw source: its PCG64 state (rng_state) when the caller gave
-// states, else its pre-drawn uniform.
-__device__ __forceinline__ bool has_draws(const dsr_sample_args_t& a) { return a.uniforms || a.rng_state; }
+// A row's draw source: its PCG64 state (rng_state) in the kernels
+// instantiated with RNG = true (launched when the caller gives states), else
+// its pre-drawn uniform.
+template <bool RNG>
+__device__ __forceinline__ bool has_draws(const dsr_sample_args_t& a) { return RNG || a.uniforms; }
 
 __device__ __forceinline__ void store_rng(const dsr_sample_args_t& a, int64_t row, const uint64_t next[4]) {
   uint64_t* o = a.rng_state + 4 * row;

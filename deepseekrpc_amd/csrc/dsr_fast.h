@@ -240,6 +240,7 @@ __device__ int select_bin(const T* bins, T rem, FastLists& sh, BlockSync& bs, T&
 
 // Returns 0 if the row was decided here, else the reason it is handed to the
 // general path (kHand*).
+template <bool RNG>
 __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64_t row, FastShared& shu) {
   FastLists& sh = shu.f;
   const int tid = threadIdx.x, lane = lane_id();
@@ -258,12 +259,13 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.policy + row), (short)0, (int)sizeof(dsr_policy_t), 0x00020000);
   const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
-      a.rng_state ? (void*)(a.rng_state + 4 * row) : (a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy),
-      (short)0, a.rng_state ? 32 : (a.uniforms ? 8 : 0), 0x00020000);
+      RNG ? (void*)(a.rng_state + 4 * row) : (a.uniforms ? (void*)(a.uniforms + row) : (void*)a.policy),
+      (short)0, RNG ? 32 : (a.uniforms ? 8 : 0), 0x00020000);
   constexpr int kPolWords = (int)(sizeof(dsr_policy_t) / 4);
   const uint32_t pw = __builtin_amdgcn_raw_buffer_load_b32(prs, tid < kPolWords ? 4 * tid : 0x7FFFFFF0, 0, 0) |
                       __builtin_amdgcn_raw_buffer_load_b32(
-                          urs, (tid >= kPolWords && tid < kPolWords + 8) ? 4 * (tid - kPolWords) : 0x7FFFFFF0, 0, 0);
+                          urs, (tid >= kPolWords && tid < kPolWords + (RNG ? 8 : 2)) ? 4 * (tid - kPolWords) : 0x7FFFFFF0,
+                          0, 0);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
       a.allow_bits ? (void*)(a.allow_bits + row * a.allow_ld) : (void*)&kAllowAll, (short)0, (int)C, 0x00020000);
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -291,7 +293,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     uint4* zm = (uint4*)&sh.mass[0];   // 4096 x 8 bytes of mass
 #pragma unroll
     for (int i = 0; i < 2; ++i) zm[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < kPolWords + 8) sh.polw[tid] = pw;
+    if (tid < kPolWords + (RNG ? 8 : 2)) sh.polw[tid] = pw;
   }
   lds_barrier();  // LDS only: the row's loads keep streaming
 
@@ -445,7 +447,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
       fast_clear_outputs(a, row);
       if (tid == 0) fast_scatter(a, row, tok, 1.0);
     }
-    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws(a) ? tok : -1, 0, 0);
+    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws<RNG>(a) ? tok : -1, 0, 0);
     return 0;
   }
 
@@ -654,7 +656,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     if (tid == 0) fast_write_result(a, row, DSR_E_NO_MASS, -1, 0, flags);
     return 0;
   }
-  if (!has_draws(a)) {
+  if (!has_draws<RNG>(a)) {
     if (tid == 0) fast_write_result(a, row, DSR_OK, -1, 0, flags);
     return 0;
   }
@@ -663,7 +665,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     return 0;
   }
   uint64_t rng_next[4];
-  if (a.rng_state) {  // the row's PCG64 state, staged in LDS with the policy words
+  if (RNG) {  // the row's PCG64 state, staged in LDS with the policy words
     uint64_t st4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -685,7 +687,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     thr = ctot - 1;
     flags |= DSR_FLAG_MARGIN;
   }
-  if (a.rng_state && tid == 0) store_rng(a, row, rng_next);  // the row is decided here
+  if (RNG && tid == 0) store_rng(a, row, rng_next);  // the row is decided here
   if (fx > 0 && ex <= thr && thr < ex + fx) {
     const double tol = ((double)npos + 16.0) * 0x1p-51 * (double)ctot + (double)npos + 2.0;
     if ((double)(ex + fx) - thr_d <= tol || (ex > 0 && thr_d - (double)ex <= tol)) flags |= DSR_FLAG_MARGIN;

@@ -201,6 +201,7 @@ struct PenVal {  // a history entry's adjusted value and token id
 __device__ __forceinline__ bool pen_touches(long long c, long long g) { return c > 0 || g > 0; }
 
 // Returns 0 if the row was decided here, else the reason it is handed to the general path.
+template <bool RNG>
 __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64_t row, FullShared& sh) {
   const int tid = threadIdx.x, lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
@@ -407,7 +408,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       fast_clear_outputs(a, row);
       if (tid == 0) fast_scatter(a, row, tok, 1.0);
     }
-    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws(a) ? tok : -1, 0, 0);
+    if (tid == 0) fast_write_result(a, row, DSR_OK, has_draws<RNG>(a) ? tok : -1, 0, 0);
     return 0;
   }
   unsigned flags = 0;
@@ -927,7 +928,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       fast_scatter(a, row, id, p);
     }
   }
-  if (!has_draws(a)) {
+  if (!has_draws<RNG>(a)) {
     if (tid == 0) fast_write_result(a, row, DSR_OK, -1, 0, flags);
     return 0;
   }
@@ -938,7 +939,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     return 0;
   }
   uint64_t rng_next[4];
-  const double u = a.rng_state ? pcg64_random(a.rng_state + 4 * row, rng_next) : a.uniforms[row];
+  const double u = RNG ? pcg64_random(a.rng_state + 4 * row, rng_next) : a.uniforms[row];
   if (!(u >= 0.0 && u < 1.0)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
@@ -1035,7 +1036,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   lds_barrier();
   // The row is decided: its advanced PCG64 state goes back (every thread read
   // the old one before the barriers above).
-  if (a.rng_state && tid == 0 && !sh.bc_i[2]) store_rng(a, row, rng_next);
+  if (RNG && tid == 0 && !sh.bc_i[2]) store_rng(a, row, rng_next);
   return sh.bc_i[2] ? kHandCapacity : 0;  // unreachable: thr lies inside the chunk found above
 }
 

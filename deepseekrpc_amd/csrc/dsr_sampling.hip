@@ -24,24 +24,25 @@ namespace dsr {
 // ---------------------------------------------------------------------------
 // dsr_sample_rows: general path.
 
+template <bool RNG>
 __device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int st, const DistOut& d,
                            unsigned flags, GenShared& sh) {
   const int64_t V = a.vocab;
   int64_t token = -1;
   int consumed = 0;
-  if (st == DSR_OK && has_draws(a)) {
+  if (st == DSR_OK && has_draws<RNG>(a)) {
     if (d.npos == 1) {
       token = d.first;  // sampling.py:120-122: no uniform is drawn
     } else {
       uint64_t next[4];
-      const double u = a.rng_state ? pcg64_random(a.rng_state + 4 * row, next) : a.uniforms[row];
+      const double u = RNG ? pcg64_random(a.rng_state + 4 * row, next) : a.uniforms[row];
       if (!(u >= 0.0 && u < 1.0)) {
         st = DSR_E_UNIFORM;
       } else {
         token = cdf_search(W, V, u, d.npos, sh, flags);
         consumed = 1;
       }
-      if (a.rng_state) {
+      if (RNG) {
         __syncthreads();  // every thread has read the state
         if (threadIdx.x == 0) store_rng(a, row, next);
       }
@@ -91,6 +92,7 @@ __device__ __forceinline__ RowSpec sample_row_spec(const dsr_sample_args_t& a, i
   return r;
 }
 
+template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a) {
   __shared__ GenShared sh;
   const int64_t row = blockIdx.x;
@@ -99,15 +101,16 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
   unsigned flags = DSR_FLAG_GENERAL;
   DistOut d;
   int st = general_distribution(r, sh, flags, d);
-  finish_row(a, row, W, st, d, flags, sh);
+  finish_row<RNG>(a, row, W, st, d, flags, sh);
 }
 
 // Fast path for bf16 rows; rows it does not take are redone by the general
 // path inside the same workgroup.
+template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t a) {
   __shared__ FastShared sh;
   const int64_t row = blockIdx.x;
-  const int why = fast_sample_row(a, row, sh);
+  const int why = fast_sample_row<RNG>(a, row, sh);
   if (why == 0) return;
   __syncthreads();
   GenShared& gs = *reinterpret_cast<GenShared*>(&sh);
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
   DistOut d;
   int st = general_distribution(r, gs, flags, d);
-  finish_row(a, row, W, st, d, flags, gs);
+  finish_row<RNG>(a, row, W, st, d, flags, gs);
 }
 
 // Full-vocabulary path for bf16 rows that carry a token history (no bias);
@@ -128,10 +131,11 @@ struct FullKernelShared {
   };
 };
 
+template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t a) {
   __shared__ FullKernelShared sh;
   const int64_t row = blockIdx.x;
-  const int why = full_sample_row(a, row, sh.f);
+  const int why = full_sample_row<RNG>(a, row, sh.f);
   if (why == 0) return;
   __syncthreads();
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t
   unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
   DistOut d;
   int st = general_distribution(r, sh.g, flags, d);
-  finish_row(a, row, W, st, d, flags, sh.g);
+  finish_row<RNG>(a, row, W, st, d, flags, sh.g);
 }
 
 // ---------------------------------------------------------------------------
@@ -277,11 +281,14 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
   if (a.rows == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   if (fast_path_eligible(a)) {
-    hipLaunchKernelGGL(k_sample_bf16_fast, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    if (a.rng_state) hipLaunchKernelGGL(k_sample_bf16_fast<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_sample_bf16_fast<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   } else if (full_path_eligible(a)) {
-    hipLaunchKernelGGL(k_sample_bf16_full, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    if (a.rng_state) hipLaunchKernelGGL(k_sample_bf16_full<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_sample_bf16_full<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   } else {
-    hipLaunchKernelGGL(k_sample_general, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    if (a.rng_state) hipLaunchKernelGGL(k_sample_general<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_sample_general<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   }
   return launched();
 }
