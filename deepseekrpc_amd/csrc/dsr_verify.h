@@ -527,7 +527,32 @@ struct StatItem {
       }
     }
   }
-  // Element u (-inf outside [lo, hi)).
+  // VEC: elements at or past hi become -inf in the raw words, once, after
+  // the loads have landed (a vector is wholly in range except at the end of
+  // a share), so value() needs no index test.
+  __device__ __forceinline__ void mask(Raw* r) const {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int q = 0; q < kRaw; ++q) {
+        const int64_t e0 = index_of(q * W);
+        if (e0 + W <= hi) continue;
+        const int n = e0 < hi ? (int)(hi - e0) : 0;  // elements of this vector still in range
+        uint32_t w4[4] = {r[q].x, r[q].y, r[q].z, r[q].w};
+#pragma unroll
+        for (int e = 0; e < W; ++e) {
+          if (e < n) continue;
+          if constexpr (DT == DSR_BF16) w4[e >> 1] = (w4[e >> 1] & (0xFFFF0000u >> (16 * (e & 1)))) | (0xFF80u << (16 * (e & 1)));
+          else if constexpr (DT == DSR_F32) w4[e] = 0xFF800000u;
+          else {
+            w4[2 * e] = 0u;
+            w4[2 * e + 1] = 0xFFF00000u;
+          }
+        }
+        r[q] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+      }
+    }
+  }
+  // Element u (-inf outside [lo, hi); VEC: after mask()).
   __device__ __forceinline__ double value(const Raw* r, int u) const {
     X y;
     if constexpr (VEC) {
@@ -537,52 +562,57 @@ struct StatItem {
       if constexpr (DT == DSR_BF16) y = __uint_as_float(((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
       else if constexpr (DT == DSR_F32) y = __uint_as_float(w4[e]);
       else y = __longlong_as_double((long long)(((unsigned long long)w4[2 * e + 1] << 32) | w4[2 * e]));
+      return (double)y;
     } else {
       y = r[u];
+      return index_of(u) < hi ? (double)y : -(double)INFINITY;
     }
-    return index_of(u) < hi ? (double)y : -(double)INFINITY;
   }
 };
 
 // One share held in registers -> its maximum, the first index holding it,
-// sum exp((v - max) / T) and the NaN/+inf / finite flags.  A strict
-// comparison in increasing index order keeps the first maximum.  Each thread
-// sums its exps against its own maximum and rescales once by
-// exp((m_t - M) / T), so the exps need no workgroup step before them.
+// sum exp((v - max) / T) and the NaN/+inf / finite flags.  Each thread sums
+// its exps against its own maximum and rescales once by exp((m_t - M) / T),
+// so the exps need no workgroup step before them.  The exp pass is
+// branch-free: a -inf element adds exactly 0 (exp_nonpos clamps its argument
+// at -746, which underflows), and a NaN or +inf marks the row invalid, whose
+// statistics are then never used.  The first maximum is kept as the slot of
+// the first strict increase, its index formed once.
 template <int DT, bool VEC>
 __device__ __forceinline__ void stat_share(const dsr_verify_args_t& a, const VerifyLayout& L,
-                                           const StatItem<DT, VEC>& it, const typename StatItem<DT, VEC>::Raw* x,
+                                           const StatItem<DT, VEC>& it, typename StatItem<DT, VEC>::Raw* x,
                                            StatShared& sm) {
   const double* etab = sm.etab;
   const int64_t row = it.rs / L.slots;
   if (!verify_fast_row(a, L, row)) return;  // uniform over the workgroup
   const double T = policy_of(a, row).temperature;
   const bool greedy = T == 0.0;
+  it.mask(x);
   double m = -INFINITY;
-  long long am = LLONG_MAX;
-  uint32_t fl = 0;  // 1: NaN / +inf, 2: a finite value
+  bool nan = false;
+  int mu = -1;  // slot of the first maximum (a strict comparison in increasing index order)
 #pragma unroll
   for (int u = 0; u < kStatPer; ++u) {
     const double v = it.value(x, u);
-    fl |= (v != v || v == INFINITY) ? 1u : 0u;
-    fl |= (v > -(double)INFINITY && v < (double)INFINITY) ? 2u : 0u;
-    if (v > m && v < (double)INFINITY) {
+    nan |= v != v;
+    if (v > m) {
       m = v;
-      am = it.index_of(u);
+      mu = u;
     }
   }
+  // 1: a NaN or +inf logit; 2: a finite one.
+  const uint32_t fl = ((nan || m == (double)INFINITY) ? 1u : 0u) | (m > -(double)INFINITY ? 2u : 0u);
   const double iT = greedy ? 0.0 : 1.0 / T;
   double s = 0.0;
-  if (!greedy && m > -(double)INFINITY) {
+  if (!greedy) {
+    const double mm = m > -(double)INFINITY ? m : 0.0;  // a thread with no finite value sums exact zeros
 #pragma unroll
-    for (int u = 0; u < kStatPer; ++u) {
-      const double v = it.value(x, u);
-      if (v > -(double)INFINITY && v < (double)INFINITY) s += exp_nonpos((v - m) * iT, etab);
-    }
+    for (int u = 0; u < kStatPer; ++u) s += exp_nonpos((it.value(x, u) - mm) * iT, etab);
   }
   const double Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
   const uint32_t flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
-  const long long amg = stat_reduce(m == Mg && m > -INFINITY ? am : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
+  const long long amg =
+      stat_reduce(m == Mg && mu >= 0 ? it.index_of(mu) : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
   const double sc = s > 0.0 ? s * exp_nonpos((m - Mg) * iT, etab) : 0.0;
   const double Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
   if (threadIdx.x == 0) {
