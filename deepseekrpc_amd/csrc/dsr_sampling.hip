@@ -337,7 +337,10 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   hipLaunchKernelGGL(k_verify_chain, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, L);
   if (L.fast_inputs) {
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_verify_draw, dim3((unsigned)(a.rows * kDrawSplit)), dim3(kStatThreads), 0, s, a, L);
+    const dim3 dgrid((unsigned)(a.rows * kDrawSplit));
+    if (a.dtype == DSR_BF16) hipLaunchKernelGGL(k_verify_draw<DSR_BF16>, dgrid, dim3(kStatThreads), 0, s, a, L);
+    else if (a.dtype == DSR_F32) hipLaunchKernelGGL(k_verify_draw<DSR_F32>, dgrid, dim3(kStatThreads), 0, s, a, L);
+    else hipLaunchKernelGGL(k_verify_draw<DSR_F64>, dgrid, dim3(kStatThreads), 0, s, a, L);
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
     hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
   }

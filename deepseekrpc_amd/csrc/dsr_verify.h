@@ -778,6 +778,9 @@ __device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, 
 // per wave step (lane l takes token l of the block, so each load is
 // coalesced): each block's weight sum is kept for step 4's search; the
 // share's sum, positive count and first positive index go to its DrawPart.
+// Instantiated per logit type, so every load of the share is issued before
+// the first weight needs one.
+template <int DT>
 __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
   __shared__ double etab[64];
   __shared__ double sf[kStatWaves];
@@ -792,6 +795,15 @@ __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t 
   const DrawWeights wf = draw_weights(a, L, row, d, etab);
   const int64_t V = a.vocab;
   const int l = lane_id(), w = wave_id();
+  using X = typename LogitT<DT>::T;
+  X pv[kStatPer], qv[kStatPer];
+#pragma unroll
+  for (int u = 0; u < kStatPer; ++u) {
+    const int64_t i = ((int64_t)g * kDrawBlocks + w * kStatPer + u) * 64 + l;
+    const int64_t ic = i < V ? i : V - 1;  // past the row: any in-range element, weight forced to 0 below
+    pv[u] = logit_as<DT>(wf.P, ic);
+    qv[u] = wf.resid ? logit_as<DT>(wf.Q, ic) : X(0);
+  }
   double acc = 0.0;
   long long npos = 0, first = LLONG_MAX;
   double* bs = L.bsum + row * kDrawParts + (int64_t)g * kDrawBlocks;
@@ -799,7 +811,9 @@ __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t 
   for (int u = 0; u < kStatPer; ++u) {
     const int blk = w * kStatPer + u;                     // block within the share
     const int64_t i = ((int64_t)g * kDrawBlocks + blk) * 64 + l;  // token of this lane
-    const double x = i < V ? wf(i) : 0.0;
+    double x = exp_nonpos(((double)pv[u] - wf.Mp) * wf.iTp, etab) * wf.isp;
+    if (wf.resid) x = fmax(x - exp_nonpos(((double)qv[u] - wf.Mq) * wf.iTp, etab) * wf.isq, 0.0);
+    x = i < V ? x : 0.0;
     const double sum = wave_reduce_dpp(x, OpSum());
     const unsigned long long pb = __ballot(x > 0.0);
     if (l == 0) bs[blk] = sum;
