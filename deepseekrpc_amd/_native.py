@@ -77,7 +77,7 @@ class VerifyArgs(ctypes.Structure):
         ("u_accept", _p), ("u_target", _p), ("eos_off", _p), ("eos_ids", _p), ("output_limit", _p),
         ("out_accepted", _p), ("out_ids", _p), ("out_count", _p), ("out_pending", _p), ("out_stop", _p),
         ("out_used_accept", _p), ("out_used_target", _p), ("out_status", _p), ("out_flags", _p),
-        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_accept", _p), ("rng_target", _p),
     ]
 
 

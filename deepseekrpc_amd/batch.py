@@ -480,11 +480,16 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
                   u_target: torch.Tensor, output_limit: torch.Tensor, *, history: HistoryTable | None = None,
                   bias: BiasTable | None = None, allow_bits: torch.Tensor | None = None,
                   eos_offsets: torch.Tensor | None = None, eos_ids: torch.Tensor | None = None,
+                  rng_accept: torch.Tensor | None = None, rng_target: torch.Tensor | None = None,
                   workspace: Workspace | None = None) -> VerifyResult:
     """Exact sampled verification of ``rows`` requests with ``K`` drafts each.
 
     ``target [rows, K+1, V]`` and ``draft [rows, K, V]`` are logits; row ``j``
-    of both is conditioned on the prefix ``draft_ids[:, :j]``.
+    of both is conditioned on the prefix ``draft_ids[:, :j]``.  ``u_accept`` /
+    ``u_target`` are pre-drawn uniforms; ``rng_accept`` / ``rng_target``
+    (int64 ``[rows, 4]``, see ``pcg64_states``) instead draw them on the
+    device from each request's accept / target PCG64 state, which is advanced
+    by exactly the draws the decision uses.
     """
     lib = N.load()
     _require_cuda(target, "target")
@@ -496,8 +501,14 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
         if tuple(draft.shape) != (rows, K, V) or draft.dtype != target.dtype:
             raise ValueError("draft must be [rows, K, V] of the target dtype")
         _require(draft_ids, "draft_ids", torch.int32, rows * K)
-        _require(u_accept, "u_accept", torch.float64, rows * K)
-    _require(u_target, "u_target", torch.float64, rows)
+        if rng_accept is None:
+            _require(u_accept, "u_accept", torch.float64, rows * K)
+    if rng_accept is not None:
+        _require(rng_accept, "rng_accept", torch.int64, rows * 4)
+    if rng_target is None:
+        _require(u_target, "u_target", torch.float64, rows)
+    else:
+        _require(rng_target, "rng_target", torch.int64, rows * 4)
     _require(output_limit, "output_limit", torch.int32, rows)
     if target.dtype not in _DTYPES:
         raise ValueError("target must be bf16/f32/f64")
@@ -522,8 +533,12 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     if allow_bits is not None:
         _require_cuda(allow_bits, "allow_bits")
         a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.shape[-1]
-    a.u_accept = u_accept.data_ptr() if K > 0 else None
-    a.u_target = u_target.data_ptr()
+    a.u_accept = u_accept.data_ptr() if K > 0 and u_accept is not None else None
+    a.u_target = u_target.data_ptr() if u_target is not None else None
+    if rng_accept is not None and rows > 0:
+        a.rng_accept = rng_accept.data_ptr()
+    if rng_target is not None and rows > 0:
+        a.rng_target = rng_target.data_ptr()
     if eos_offsets is not None and eos_ids is not None and eos_ids.numel() > 0:
         _require(eos_offsets, "eos_offsets", torch.int64, rows + 1)
         _require_cuda(eos_ids, "eos_ids")

@@ -232,6 +232,31 @@ __device__ __forceinline__ double pcg64_random(const uint64_t* st, uint64_t next
   return (double)(out >> 11) * 0x1.0p-53;
 }
 
+// The first n draws of a PCG64 state, in order (n <= 8); the state itself is
+// left as it is.
+__device__ __forceinline__ void pcg64_draws(const uint64_t* st, int n, double* u) {
+  uint64_t cur[4] = {st[0], st[1], st[2], st[3]}, next[4];
+  for (int i = 0; i < n && i < 8; ++i) {
+    u[i] = pcg64_random(cur, next);
+    cur[0] = next[0];
+    cur[1] = next[1];
+  }
+}
+
+// Advances a PCG64 state in place by n draws (one thread).
+__device__ __forceinline__ void pcg64_advance(uint64_t* st, int n) {
+  uint64_t cur[4] = {st[0], st[1], st[2], st[3]}, next[4];
+  for (int i = 0; i < n; ++i) {
+    pcg64_random(cur, next);
+    cur[0] = next[0];
+    cur[1] = next[1];
+  }
+  if (n > 0) {
+    st[0] = cur[0];
+    st[1] = cur[1];
+  }
+}
+
 // A row's draw source: its PCG64 state (rng_state) in the kernels
 // instantiated with RNG = true (launched when the caller gives states), else
 // its pre-drawn uniform.

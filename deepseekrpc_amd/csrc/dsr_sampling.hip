@@ -296,7 +296,8 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
 int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   if (!args) return DSR_ERR_ARG;
   const dsr_verify_args_t& a = *args;
-  if (!a.target || (a.K > 0 && (!a.draft || !a.draft_ids || !a.u_accept)) || !a.policy || !a.u_target ||
+  if (!a.target || (a.K > 0 && (!a.draft || !a.draft_ids || (!a.u_accept && !a.rng_accept))) || !a.policy ||
+      (!a.u_target && !a.rng_target) ||
       !a.output_limit || !a.out_accepted || !a.out_ids || !a.out_count || !a.out_pending || !a.out_stop ||
       !a.out_used_accept || !a.out_used_target || !a.out_status || !dtype_ok(a.dtype) || a.K < 0 ||
       a.K > DSR_MAX_DRAFTS || a.rows < 0 || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab)

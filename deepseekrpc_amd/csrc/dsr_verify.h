@@ -285,6 +285,12 @@ __device__ void write_decision(const dsr_verify_args_t& a, int64_t row, const De
   a.out_stop[row] = ok ? d.stop : DSR_STOP_NONE;
   a.out_used_accept[row] = ok ? d.ua : 0;
   a.out_used_target[row] = ok ? d.ut : 0;
+  // Device draws: each domain's state moves by exactly the draws reported
+  // (an error reports none, as the reference's aborted transaction restores
+  // its streams).  This is the decision's last step, so every draw above read
+  // the state as it was.
+  if (a.rng_accept) pcg64_advance(a.rng_accept + 4 * row, ok ? d.ua : 0);
+  if (a.rng_target) pcg64_advance(a.rng_target + 4 * row, ok ? d.ut : 0);
   if (a.out_flags) a.out_flags[row] = (uint8_t)d.flags;
 }
 
@@ -395,8 +401,11 @@ __device__ void general_decide(const dsr_verify_args_t& a, const VerifyLayout& L
   auto Prow = [&](int slot) { return L.W + (row * L.slots + slot) * L.stride; };
   auto status_of = [&](int slot) { return (int)info[slot * 4]; };
   const bool greedy = a.policy[row].temperature == 0.0;
-  const Request rq = request_of(a, row);
+  Request rq = request_of(a, row);
+  __shared__ double gua[DSR_MAX_DRAFTS];
+  if (a.rng_accept) rq.ua = gua;  // the accept domain's next K draws, consumed in order
   if (threadIdx.x == 0) {
+    if (a.rng_accept) pcg64_draws(a.rng_accept + 4 * row, K, gua);
     verify_precheck(a, rq, status_of, d);
     for (int j = 0; j < K; ++j) d.flags |= (unsigned)info[(K + 1 + j) * 4 + 2] & DSR_FLAG_MARGIN;
     if (d.status == DSR_OK)
@@ -415,7 +424,10 @@ __device__ void general_decide(const dsr_verify_args_t& a, const VerifyLayout& L
     if (greedy) {
       rep = info[j * 4 + 1];
     } else {
-      st = draw_from(Prow(j), d.next == 1 ? Prow(K + 1 + j) : nullptr, a.vocab, a.u_target[row], sh, rep, used, flags);
+      double ut = 0.0;
+      if (a.rng_target) pcg64_draws(a.rng_target + 4 * row, 1, &ut);
+      else ut = a.u_target[row];
+      st = draw_from(Prow(j), d.next == 1 ? Prow(K + 1 + j) : nullptr, a.vocab, ut, sh, rep, used, flags);
     }
     if (threadIdx.x == 0) {
       d.flags |= flags;
@@ -711,13 +723,14 @@ __global__ __launch_bounds__(kThreads) void k_verify_chain(dsr_verify_args_t a, 
       }
       if (t < K) {
         sids[t] = x;
-        sua[t] = a.u_accept[row * K + t];
+        if (!a.rng_accept) sua[t] = a.u_accept[row * K + t];
       }
     }
     sprob[t] = pr;
   }
   const int n_eos = a.eos_off ? (int)(a.eos_off[row + 1] - a.eos_off[row]) : 0;
   if (n_eos <= kEosCached && t >= 64 && t < 64 + n_eos) seos[t - 64] = a.eos_ids[a.eos_off[row] + (t - 64)];
+  if (a.rng_accept && t == 0) pcg64_draws(a.rng_accept + 4 * row, K, sua);  // the next K accept draws
   __syncthreads();
   if (t == 0) {
     Request rq = request_of(a, row);
@@ -905,7 +918,9 @@ __global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, Verif
   } else if (n == 1) {
     rep = f;  // a single positive token: no uniform is drawn (sampling.py:120-122)
   } else {
-    const double u = a.u_target[row];
+    double u = 0.0;
+    if (a.rng_target) pcg64_draws(a.rng_target + 4 * row, 1, &u);
+    else u = a.u_target[row];
     if (!(u >= 0.0 && u < 1.0)) {
       status = DSR_E_UNIFORM;
     } else {

@@ -148,7 +148,15 @@ typedef struct dsr_sample_args {
  * verify_drafts, terminal_sampling.py:170-183, sampling.py:247-294).
  * Target row j and draft row j of a request are both conditioned on the
  * accepted prefix draft_ids[:j] (each prefix token adds one to count and
- * generated count, terminal_sampling.py:127-136) and on allow mask j. */
+ * generated count, terminal_sampling.py:127-136) and on allow mask j.
+ *
+ * Draws: with rng_accept set, the accept test of position j uses the
+ * (j+1)-th Generator.random() of the request's accept-domain PCG64 state
+ * instead of u_accept; with rng_target set, the replacement / bonus draw
+ * uses the next draw of its target-domain state instead of u_target.  Each
+ * state is written back advanced by exactly out_used_accept /
+ * out_used_target draws (none when the request's status is an error), in the
+ * layout of dsr_sample_args_t.rng_state. */
 typedef struct dsr_verify_args {
   const void* target;          /* [rows, K+1, ld] logits */
   const void* draft;           /* [rows, K, ld] logits */
@@ -184,6 +192,8 @@ typedef struct dsr_verify_args {
   uint8_t* out_flags;          /* [rows] or NULL */
   void* workspace;             /* >= dsr_verify_workspace_bytes(rows, K, vocab) */
   size_t workspace_bytes;
+  uint64_t* rng_accept;        /* [rows, 4] PCG64 states of the accept domain, or NULL */
+  uint64_t* rng_target;        /* [rows, 4] PCG64 states of the target domain, or NULL */
 } dsr_verify_args_t;
 
 /* ABI gate, after the reference's abi_version() (native/bindings.cpp:25). */

@@ -97,3 +97,62 @@ def test_repeated_launches_continue_the_streams():
         assert torch.equal(got.tokens[got.consumed.bool()], want.tokens[got.consumed.bool()])
     batch.pcg64_restore(gens, states)
     assert [g.random() for g in gens] == [g.random() for g in ref]
+
+
+def verify_device_vs_host(tgt, drf, ids, pols, limit, seed, **kw):
+    rows, K = ids.shape
+    acc_dev = [np.random.default_rng(seed + 2 * r) for r in range(rows)]
+    tgt_dev = [np.random.default_rng(seed + 2 * r + 1) for r in range(rows)]
+    acc_host = [np.random.default_rng(seed + 2 * r) for r in range(rows)]
+    tgt_host = [np.random.default_rng(seed + 2 * r + 1) for r in range(rows)]
+    sa, st = batch.pcg64_states(acc_dev), batch.pcg64_states(tgt_dev)
+    sa0, st0 = sa.clone(), st.clone()
+    got = batch.verify_drafts(tgt, drf, ids, pols, None, None, limit, rng_accept=sa, rng_target=st, **kw)
+    ua = torch.tensor([[g.random() for _ in range(K)] for g in acc_host], dtype=torch.float64, device="cuda")
+    ut = torch.tensor([g.random() for g in tgt_host], dtype=torch.float64, device="cuda")
+    want = batch.verify_drafts(tgt, drf, ids, pols, ua.reshape(-1), ut, limit, **kw)
+    for f in ("accepted", "ids", "count", "pending", "stop", "used_accept", "used_target", "status", "flags"):
+        assert torch.equal(getattr(got, f), getattr(want, f)), f
+    used_a, used_t = got.used_accept.cpu().numpy(), got.used_target.cpu().numpy()
+    np.testing.assert_array_equal(sa.cpu().numpy().view(np.uint64), expected_states_n(sa0, used_a))
+    np.testing.assert_array_equal(st.cpu().numpy().view(np.uint64), expected_states_n(st0, used_t))
+    return got
+
+
+def expected_states_n(before, steps):
+    words = before.cpu().numpy().view(np.uint64)
+    out = words.copy()
+    for r, n in enumerate(steps):
+        s = int(words[r, 0]) | (int(words[r, 1]) << 64)
+        inc = int(words[r, 2]) | (int(words[r, 3]) << 64)
+        for _ in range(int(n)):
+            s, _ = P.random(s, inc)
+        out[r, 0], out[r, 1] = s & M64, s >> 64
+    return out
+
+
+def test_verifier_fast_path_device_draws():
+    w = workloads.c4(rows=16)
+    e = w.extra
+    R, K, V = e["target"].shape[0], e["K"], e["target"].shape[2]
+    tgt = torch.from_numpy(e["target"]).cuda()
+    drf = torch.from_numpy(e["draft"]).cuda()
+    draw = batch.sample_rows(drf.reshape(R * K, V), [dict()] * (R * K),
+                             uniforms=torch.from_numpy(e["u_draft"].reshape(-1)).cuda())
+    ids = draw.tokens.reshape(R, K).contiguous()
+    got = verify_device_vs_host(tgt, drf, ids, [dict()] * R, torch.from_numpy(e["limit"]).cuda(), 700)
+    assert int(got.used_accept.sum()) > R and int(got.used_target.sum()) > 0
+
+
+def test_verifier_general_path_and_greedy_device_draws():
+    # Filtered policies take the general verifier; greedy requests draw nothing.
+    rng = np.random.default_rng(31)
+    R, K, V = 6, 3, 1000
+    tgt = torch.from_numpy(rng.normal(0, 2, (R, K + 1, V)).astype(np.float32)).cuda()
+    drf = torch.from_numpy(rng.normal(0, 2, (R, K, V)).astype(np.float32)).cuda()
+    ids = torch.from_numpy(rng.integers(0, V, (R, K)).astype(np.int32)).cuda()
+    pols = [dict(top_k=50), dict(top_p=0.9), dict(temperature=0.0), dict(min_p=0.05), dict(), dict(temperature=0.0)]
+    limit = torch.full((R,), 10, dtype=torch.int32, device="cuda")
+    got = verify_device_vs_host(tgt, drf, ids, pols, limit, 800)
+    for r in (2, 5):
+        assert int(got.used_accept[r]) == 0 and int(got.used_target[r]) == 0
