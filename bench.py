@@ -40,7 +40,7 @@ WORKLOADS = {
     "c3": ("sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline", "rows/s", 5,
            "k_sample_bf16_fast"),
     "c1": ("sampled rows/sec at B=1×V=129,280 fp32 with fp32 probabilities out", "rows/s", 1000,
-           "k_sample_general"),
+           "k_split_select + k_split_finish"),
     "c2": ("sampled rows/sec at B=64×V=129,280 bf16 with 4,096-token histories", "rows/s", 20,
            "k_sample_bf16_full"),
     "c4": ("verify-rows/sec at B=32 requests × K=4 drafts × V=129,280 fp32", "verify-rows/s", 60,

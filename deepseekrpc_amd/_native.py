@@ -35,6 +35,7 @@ MAX_APPEND = 16384
 
 FLAG_MARGIN = 1
 FLAG_GENERAL = 2
+FLAG_SPLIT = 4
 STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 
 EXPORTS = (

@@ -19,6 +19,9 @@ namespace dsr {
 constexpr int kThreads = 1024;            // one workgroup per row
 constexpr int kWaves = kThreads / 64;     // 16 wave64s
 
+// Doubles per workspace row: the vocabulary rounded up to 32 tokens.
+__host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(int64_t)31; }
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 

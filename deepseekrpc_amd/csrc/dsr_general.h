@@ -545,6 +545,134 @@ struct DistOut {
   long long first;  // first positive index
 };
 
+struct IdentityMap {
+  __device__ __forceinline__ int64_t operator()(int64_t i) const { return i; }
+};
+
+// Steps 10-13 (sampling.py:92-106) over W[0, n), which holds s = (v - max) / T
+// and the top-k decision (`kth`, `cut` from radix_kth_largest and
+// nth_equal_index).  Position j of W is token map(j), positions in token
+// order, so index-order ties and the CDF keep the reference's order.  `vocab`
+// sizes the rounding band of a sum over the whole row.  On DSR_OK, W holds
+// the final probabilities (also written to the optional outputs).
+template <class Map>
+__device__ __forceinline__ int filter_tail(const RowSpec& r, double* W, int64_t n, int64_t vocab, bool topk,
+                                           uint64_t kth, int64_t cut, GenShared& sh, unsigned& flags, DistOut& out,
+                                           Map map) {
+  const dsr_policy_t& p = r.pol;
+  auto ldW = [&](int64_t i) { return W[i]; };
+  double acc = 0.0;  // sampling.py:92-93; removed tokens are exp(-inf) = 0
+  row_pass<double>(n, ldW, [&](int64_t i, double z) {
+    bool keep = z > -(double)INFINITY;
+    if (topk) {
+      const uint64_t key = order_key(z);
+      keep = keep && (key > kth || (key == kth && i <= cut));
+    }
+    double e = 0.0;
+    if (keep) e = exp(z);
+    W[i] = e;
+    acc += e;
+  });
+  const double s1 = block_sum(acc, sh.b);
+
+  double cur = 0.0;  // sum of what the last pass wrote
+  if (p.min_p != 0.0) {  // sampling.py:94-96
+    // max(r) = 1 / s1: the maximum's exp is exactly 1 and division is monotone.
+    const double cut_p = p.min_p * (1.0 / s1);
+    const double tol = cut_p * 0x1p-49;
+    int close = 0;
+    double acc2 = 0.0;
+    row_pass<double>(n, ldW, [&](int64_t i, double e) {
+      double x = e / s1;
+      if (x > 0.0 && fabs(x - cut_p) <= tol) close = 1;
+      if (x < cut_p) x = 0.0;
+      W[i] = x;
+      acc2 += x;
+    });
+    if (block_or(close, sh.b)) flags |= DSR_FLAG_MARGIN;
+    const double s2 = block_sum(acc2, sh.b);
+    row_pass<double>(n, ldW, [&](int64_t i, double x) {
+      x = x / s2;
+      W[i] = x;
+      cur += x;
+    });
+  } else {
+    row_pass<double>(n, ldW, [&](int64_t i, double e) {
+      const double x = e / s1;
+      W[i] = x;
+      cur += x;
+    });
+  }
+  __syncthreads();
+
+  if (p.top_p < 1.0) {  // sampling.py:97-102
+    uint64_t lbits;
+    if (radix_mass_crossing(W, n, p.top_p, sh, lbits)) {
+      const double rt = __longlong_as_double((long long)lbits);
+      double a = 0.0;
+      long long n_above = 0, n_tie = 0;
+      row_pass<double>(n, ldW, [&](int64_t, double x) {
+        a += x > rt ? x : 0.0;
+        n_above += x > rt ? 1 : 0;
+        n_tie += x == rt ? 1 : 0;
+      });
+      const double A = block_sum(a, sh.b);
+      n_above = block_sum_i64(n_above, sh.b);
+      n_tie = block_sum_i64(n_tie, sh.b);
+      // Tie member j (index order) has exclusive prefix A + j*rt; it is kept
+      // while that prefix is below top_p, and rank 0 always (sampling.py:99-102).
+      long long keep = 0;
+      {
+        double q = ceil((p.top_p - A) / rt);
+        keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
+        while (keep > 0 && A + (double)(keep - 1) * rt >= p.top_p) --keep;
+        while (keep < n_tie && A + (double)keep * rt < p.top_p) ++keep;
+      }
+      if (n_above == 0 && keep == 0) keep = 1;
+      // Rounding band of a float64 prefix over this many terms.
+      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51;
+      bool close = fabs(A + (double)keep * rt - p.top_p) <= tol;           // first removed
+      if (keep >= 1 && n_above + keep > 1)
+        close = close || fabs(A + (double)(keep - 1) * rt - p.top_p) <= tol;  // last kept
+      if (keep == 0 && n_above > 0) close = true;                          // crossing above this group
+      if (keep == n_tie && A + (double)n_tie * rt < p.top_p) close = true;  // crossing below it
+      if (close) flags |= DSR_FLAG_MARGIN;
+      const int64_t cutp = nth_equal_index(W, n, lbits, keep, [](double x) { return raw_bits(x); }, sh);
+      cur = 0.0;
+      row_pass<double>(n, ldW, [&](int64_t i, double x) {
+        if (x < rt || (x == rt && i > cutp)) {
+          x = 0.0;
+          W[i] = 0.0;
+        }
+        cur += x;
+      });
+      __syncthreads();
+    } else {
+      // The whole mass stays below top_p: nothing is removed.
+      const double tot = block_sum(cur, sh.b);
+      if (fabs(tot - p.top_p) <= ((double)vocab + 16.0) * 0x1p-51) flags |= DSR_FLAG_MARGIN;
+    }
+  }
+
+  const double total = block_sum(cur, sh.b);  // sampling.py:103-106
+  if (!(total > 0.0) || !isfinite(total)) return DSR_E_NO_MASS;
+  long long npos = 0, fpos = LLONG_MAX;
+  row_pass<double>(n, ldW, [&](int64_t i, double x) {
+    x = x / total;
+    W[i] = x;
+    if (r.probs_f32) r.probs_f32[map(i)] = (float)x;
+    if (r.probs_f64) r.probs_f64[map(i)] = x;
+    if (x > 0.0) {
+      ++npos;
+      if (i < fpos) fpos = i;
+    }
+  });
+  out.npos = block_sum_i64(npos, sh.b);
+  const long long f = block_min_i64(fpos, sh.b);
+  out.first = f == LLONG_MAX ? f : (long long)map(f);
+  return DSR_OK;
+}
+
 // Full distribution (sampling.py:48-106).  On DSR_OK, W holds the final
 // probabilities (also written to the optional outputs).
 __device__ __forceinline__ int general_distribution(const RowSpec& r, GenShared& sh, unsigned& flags, DistOut& out) {
@@ -598,115 +726,7 @@ __device__ __forceinline__ int general_distribution(const RowSpec& r, GenShared&
   }
   if (r.kept_bits) write_kept_bits(W, V, topk, kth, cut, r.kept_bits, r.kept_words);
 
-  double acc = 0.0;  // sampling.py:92-93; removed tokens are exp(-inf) = 0
-  row_pass<double>(V, ldW, [&](int64_t i, double z) {
-    bool keep = z > -(double)INFINITY;
-    if (topk) {
-      const uint64_t key = order_key(z);
-      keep = keep && (key > kth || (key == kth && i <= cut));
-    }
-    double e = 0.0;
-    if (keep) e = exp(z);
-    W[i] = e;
-    acc += e;
-  });
-  const double s1 = block_sum(acc, sh.b);
-
-  double cur = 0.0;  // sum of what the last pass wrote
-  if (p.min_p != 0.0) {  // sampling.py:94-96
-    // max(r) = 1 / s1: the maximum's exp is exactly 1 and division is monotone.
-    const double cut_p = p.min_p * (1.0 / s1);
-    const double tol = cut_p * 0x1p-49;
-    int close = 0;
-    double acc2 = 0.0;
-    row_pass<double>(V, ldW, [&](int64_t i, double e) {
-      double x = e / s1;
-      if (x > 0.0 && fabs(x - cut_p) <= tol) close = 1;
-      if (x < cut_p) x = 0.0;
-      W[i] = x;
-      acc2 += x;
-    });
-    if (block_or(close, sh.b)) flags |= DSR_FLAG_MARGIN;
-    const double s2 = block_sum(acc2, sh.b);
-    row_pass<double>(V, ldW, [&](int64_t i, double x) {
-      x = x / s2;
-      W[i] = x;
-      cur += x;
-    });
-  } else {
-    row_pass<double>(V, ldW, [&](int64_t i, double e) {
-      const double x = e / s1;
-      W[i] = x;
-      cur += x;
-    });
-  }
-  __syncthreads();
-
-  if (p.top_p < 1.0) {  // sampling.py:97-102
-    uint64_t lbits;
-    if (radix_mass_crossing(W, V, p.top_p, sh, lbits)) {
-      const double rt = __longlong_as_double((long long)lbits);
-      double a = 0.0;
-      long long n_above = 0, n_tie = 0;
-      row_pass<double>(V, ldW, [&](int64_t, double x) {
-        a += x > rt ? x : 0.0;
-        n_above += x > rt ? 1 : 0;
-        n_tie += x == rt ? 1 : 0;
-      });
-      const double A = block_sum(a, sh.b);
-      n_above = block_sum_i64(n_above, sh.b);
-      n_tie = block_sum_i64(n_tie, sh.b);
-      // Tie member j (index order) has exclusive prefix A + j*rt; it is kept
-      // while that prefix is below top_p, and rank 0 always (sampling.py:99-102).
-      long long keep = 0;
-      {
-        double q = ceil((p.top_p - A) / rt);
-        keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
-        while (keep > 0 && A + (double)(keep - 1) * rt >= p.top_p) --keep;
-        while (keep < n_tie && A + (double)keep * rt < p.top_p) ++keep;
-      }
-      if (n_above == 0 && keep == 0) keep = 1;
-      // Rounding band of a float64 prefix over this many terms.
-      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51;
-      bool close = fabs(A + (double)keep * rt - p.top_p) <= tol;           // first removed
-      if (keep >= 1 && n_above + keep > 1)
-        close = close || fabs(A + (double)(keep - 1) * rt - p.top_p) <= tol;  // last kept
-      if (keep == 0 && n_above > 0) close = true;                          // crossing above this group
-      if (keep == n_tie && A + (double)n_tie * rt < p.top_p) close = true;  // crossing below it
-      if (close) flags |= DSR_FLAG_MARGIN;
-      const int64_t cutp = nth_equal_index(W, V, lbits, keep, [](double x) { return raw_bits(x); }, sh);
-      cur = 0.0;
-      row_pass<double>(V, ldW, [&](int64_t i, double x) {
-        if (x < rt || (x == rt && i > cutp)) {
-          x = 0.0;
-          W[i] = 0.0;
-        }
-        cur += x;
-      });
-      __syncthreads();
-    } else {
-      // The whole mass stays below top_p: nothing is removed.
-      const double tot = block_sum(cur, sh.b);
-      if (fabs(tot - p.top_p) <= ((double)V + 16.0) * 0x1p-51) flags |= DSR_FLAG_MARGIN;
-    }
-  }
-
-  const double total = block_sum(cur, sh.b);  // sampling.py:103-106
-  if (!(total > 0.0) || !isfinite(total)) return DSR_E_NO_MASS;
-  long long npos = 0, fpos = LLONG_MAX;
-  row_pass<double>(V, ldW, [&](int64_t i, double x) {
-    x = x / total;
-    W[i] = x;
-    if (r.probs_f32) r.probs_f32[i] = (float)x;
-    if (r.probs_f64) r.probs_f64[i] = x;
-    if (x > 0.0) {
-      ++npos;
-      if (i < fpos) fpos = i;
-    }
-  });
-  out.npos = block_sum_i64(npos, sh.b);
-  out.first = block_min_i64(fpos, sh.b);
-  return DSR_OK;
+  return filter_tail(r, W, V, V, topk, kth, cut, sh, flags, out, IdentityMap());
 }
 
 // Number of positive entries and the first positive index.

@@ -17,6 +17,7 @@
 #include "dsr_full.h"
 #include "dsr_general.h"
 #include "dsr_history.h"
+#include "dsr_split.h"
 #include "dsr_verify.h"
 
 namespace dsr {
@@ -24,10 +25,10 @@ namespace dsr {
 // ---------------------------------------------------------------------------
 // dsr_sample_rows: general path.
 
-template <bool RNG>
-__device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int st, const DistOut& d,
-                           unsigned flags, GenShared& sh) {
-  const int64_t V = a.vocab;
+// W[0, n) holds the final probabilities; position j is token map(j).
+template <bool RNG, class Map = IdentityMap>
+__device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t row, const double* W, int64_t n, int st,
+                                           const DistOut& d, unsigned flags, GenShared& sh, Map map = Map()) {
   int64_t token = -1;
   int consumed = 0;
   if (st == DSR_OK && has_draws<RNG>(a)) {
@@ -39,7 +40,8 @@ __device__ __forceinline__ void finish_row(const dsr_sample_args_t& a, int64_t r
       if (!(u >= 0.0 && u < 1.0)) {
         st = DSR_E_UNIFORM;
       } else {
-        token = cdf_search(W, V, u, d.npos, sh, flags);
+        token = cdf_search(W, n, u, d.npos, sh, flags);
+        if (token >= 0) token = map(token);
         consumed = 1;
       }
       if (RNG) {
@@ -101,7 +103,36 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
   unsigned flags = DSR_FLAG_GENERAL;
   DistOut d;
   int st = general_distribution(r, sh, flags, d);
-  finish_row<RNG>(a, row, W, st, d, flags, sh);
+  finish_row<RNG>(a, row, W, a.vocab, st, d, flags, sh);
+}
+
+// Split-row path, stage two: one workgroup per row finishes from the slices'
+// candidates, or redoes the row on the general path in the same workgroup.
+template <bool RNG>
+__global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, int smax) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x;
+  double* W = (double*)a.workspace + row * ws_stride(a.vocab);
+  RowSpec r = sample_row_spec(a, row, W);
+  unsigned flags = DSR_FLAG_GENERAL;
+  SplitGeom g;
+  if (split_geom(r.pol, a.vocab, smax, g)) {
+    unsigned sflags = DSR_FLAG_SPLIT;
+    DistOut d;
+    int64_t n = 0;
+    int why = 0;
+    const int st = split_distribution(r, g, sh, sflags, d, n, why);
+    if (st >= 0) {
+      const int32_t* ids = (const int32_t*)((const char*)W + kSplitIdsOff);
+      finish_row<RNG>(a, row, W, n, st, d, sflags, sh, [ids](int64_t j) { return (int64_t)ids[j]; });
+      return;
+    }
+    __syncthreads();  // every thread is done with the candidate list
+    flags |= (unsigned)why << 4;
+  }
+  DistOut d;
+  int st = general_distribution(r, sh, flags, d);
+  finish_row<RNG>(a, row, W, a.vocab, st, d, flags, sh);
 }
 
 // Fast path for bf16 rows; rows it does not take are redone by the general
@@ -119,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
   DistOut d;
   int st = general_distribution(r, gs, flags, d);
-  finish_row<RNG>(a, row, W, st, d, flags, gs);
+  finish_row<RNG>(a, row, W, a.vocab, st, d, flags, gs);
 }
 
 // Full-vocabulary path for bf16 rows that carry a token history (no bias);
@@ -143,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t
   unsigned flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
   DistOut d;
   int st = general_distribution(r, sh.g, flags, d);
-  finish_row<RNG>(a, row, W, st, d, flags, sh.g);
+  finish_row<RNG>(a, row, W, a.vocab, st, d, flags, sh.g);
 }
 
 // ---------------------------------------------------------------------------
@@ -286,6 +317,11 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
   } else if (full_path_eligible(a)) {
     if (a.rng_state) hipLaunchKernelGGL(k_sample_bf16_full<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
     else hipLaunchKernelGGL(k_sample_bf16_full<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+  } else if (split_path_eligible(a)) {
+    const int smax = split_max_slices(a.rows);
+    hipLaunchKernelGGL(k_split_select, dim3((unsigned)(a.rows * smax)), dim3(kThreads), 0, s, a, smax);
+    if (a.rng_state) hipLaunchKernelGGL(k_split_finish<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, smax);
+    else hipLaunchKernelGGL(k_split_finish<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, smax);
   } else {
     if (a.rng_state) hipLaunchKernelGGL(k_sample_general<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
     else hipLaunchKernelGGL(k_sample_general<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);

@@ -1,0 +1,368 @@
+// Split-row top-k path: rows that the register-resident bf16 paths do not
+// take (float32 / float64 logits, or bf16 rows those paths cannot load) and
+// that carry a top-k filter (1 <= k <= 1024) or are greedy.
+//
+// One workgroup walking a whole row through the general path's passes uses
+// one CU of 256; a small batch (one fp32 row per call is the reference's own
+// calling pattern, sampling.py:108-128) then waits on that CU alone.  Here the
+// row is cut into S contiguous slices, one workgroup each:
+//
+//   k_split_select  reads its slice once (logits, allow bits), validates it,
+//                   and keeps the slice's k largest values (ranked by value,
+//                   then index) by 11-bit radix passes over registers, in
+//                   index order, at slice s * k of a candidate list in the
+//                   row's workspace.  It also zeroes the slice's probability
+//                   and kept-bit outputs.
+//   k_split_finish  one workgroup per row runs steps 8-13 of
+//                   SamplingPolicy.probabilities (sampling.py:86-106) over
+//                   the <= 8,192 candidates instead of the V tokens, then the
+//                   categorical draw (sampling.py:108-128).
+//
+// Why the candidates decide the row: s = (v - max) / T is non-decreasing in
+// v, so a token that is not among its slice's k largest values has s at most
+// t, the s of the slice's smallest kept value; and t is at most s_k, the
+// row's k-th largest s (the slice alone holds k values with s >= t).  If
+// t < s_k, no token outside the candidates survives top-k.  If t == s_k,
+// rounding may have merged distinct values into the k-th s, whose tie group
+// the reference cuts by index (sampling.py:89-91 argsort is stable); the
+// candidates cannot settle that, and the row goes to the general path in the
+// same workgroup, as do rows with NaN / +inf logits or no finite logit (the
+// general path reports their status in the reference's order).
+#pragma once
+
+#include "dsr_general.h"
+
+namespace dsr {
+
+constexpr int kSplitCap = 8192;                  // candidates per row
+constexpr int kSplitMaxK = 1024;
+constexpr int kSplitMinSlice = kThreads;         // tokens per slice, at least
+constexpr int kSplitPer = 16;                    // tokens per thread, at most
+constexpr int kSplitMaxSlices = 128;
+constexpr int kSplitMinSlices = 8;
+constexpr int kSplitTarget = 512;                // stage-one workgroups a launch aims for
+constexpr int64_t kSplitMinVocab = 16384;        // the candidate area must fit the row's workspace
+constexpr int kHandSplit = 7;                    // reason: a slice's last candidate ties the k-th value
+
+constexpr int kSliceBad = 1;     // NaN or +inf in the slice
+constexpr int kSliceFinite = 2;  // a finite value in the slice
+constexpr int kSliceTrunc = 4;   // the slice holds more than k tokens
+constexpr int kSliceOdd = 8;     // the selection did not come to k tokens (never expected)
+
+struct SplitSlice {
+  long long vmin;  // order key of the smallest kept value, sign bit flipped (so it orders as signed)
+  int flags;
+  int count;
+};
+
+// Per-row candidate area, at the start of the row's workspace row.
+constexpr size_t kSplitIdsOff = (size_t)kSplitCap * 8;   // values (float64), then token ids (int32)
+constexpr size_t kSplitRecOff = (size_t)kSplitCap * 12;  // then one SplitSlice per slice
+constexpr size_t kSplitBytes = kSplitRecOff + (size_t)kSplitMaxSlices * sizeof(SplitSlice);
+static_assert(kSplitBytes <= (size_t)kSplitMinVocab * 8, "candidate area exceeds the smallest workspace row");
+static_assert((int64_t)kSplitMinSlices * kSplitPer * kThreads >= DSR_MAX_VOCAB, "slices too short for the vocabulary");
+
+static inline bool split_path_eligible(const dsr_sample_args_t& a) {
+  return a.pen_off == nullptr && a.bias_off == nullptr && a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
+}
+
+// Slice budget per row: enough stage-one workgroups to cover the chip.
+static inline int split_max_slices(int64_t rows) {
+  const int64_t s = kSplitTarget / (rows > 0 ? rows : 1);
+  return (int)(s < kSplitMinSlices ? kSplitMinSlices : (s > kSplitMaxSlices ? kSplitMaxSlices : s));
+}
+
+struct SplitGeom {
+  int k;        // values kept per slice
+  int S;        // slices
+  int64_t len;  // tokens per slice (a multiple of 64; the last slice may be shorter)
+};
+
+// Both launches derive the same geometry from the policy.  With S <= 8192 / k
+// the list holds at most 8,192 candidates; each slice holds at least k tokens,
+// so every slice but the last contributes exactly k.
+__device__ __forceinline__ bool split_geom(const dsr_policy_t& p, int64_t V, int smax, SplitGeom& g) {
+  if (!policy_ok(p)) return false;
+  int k;
+  if (p.temperature == 0.0) k = 1;  // greedy: only the first maximum matters (sampling.py:82-85)
+  else if (p.top_k >= 1 && p.top_k <= kSplitMaxK && p.top_k < V) k = p.top_k;
+  else return false;
+  int s = kSplitCap / k;
+  if (s > smax) s = smax;
+  int64_t len = (V + s - 1) / s;
+  len = (len + 63) & ~(int64_t)63;
+  if (len < kSplitMinSlice) len = kSplitMinSlice;
+  g.k = k;
+  g.len = len;
+  g.S = (int)((V + len - 1) / len);
+  return true;
+}
+
+__device__ __forceinline__ double key_value(uint64_t key) {
+  const uint64_t b = (key >> 63) ? (key & 0x7FFFFFFFFFFFFFFFull) : ~key;
+  return __longlong_as_double((long long)b);
+}
+
+// The next representable logit above (or below) v in the row's input type;
+// NaN for bf16 (whose rows then take the general path on any such tie).
+__device__ __forceinline__ double next_input_value(double v, int dtype, bool up) {
+  if (dtype == DSR_F64) return nextafter(v, up ? (double)INFINITY : -(double)INFINITY);
+  if (dtype == DSR_F32) return (double)nextafterf((float)v, up ? INFINITY : -INFINITY);
+  return __longlong_as_double(0x7FF8000000000000ll);
+}
+
+// Stage one: grid rows * smax, blockIdx.x = row * smax + slice.
+__global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, int smax) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x / (unsigned)smax;
+  const int s = (int)(blockIdx.x % (unsigned)smax);
+  const int64_t V = a.vocab;
+  SplitGeom g;
+  if (!split_geom(a.policy[row], V, smax, g) || s >= g.S) return;
+  const int64_t lo = (int64_t)s * g.len;
+  const int64_t hi = lo + g.len < V ? lo + g.len : V;
+  const int64_t len = hi - lo;
+  char* ws = (char*)((double*)a.workspace + row * ws_stride(V));
+  double* Wc = (double*)ws;
+  int32_t* Ic = (int32_t*)(ws + kSplitIdsOff);
+  SplitSlice* rec = (SplitSlice*)(ws + kSplitRecOff);
+
+  // The slice's outputs start at zero; the finishing launch writes the kept tokens.
+  if (a.out_probs_f32)
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) a.out_probs_f32[row * a.probs_ld + i] = 0.0f;
+  if (a.out_probs_f64)
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) a.out_probs_f64[row * a.probs_ld + i] = 0.0;
+  if (a.out_kept_bits)
+    for (int64_t w = (lo >> 5) + threadIdx.x; w < ((hi + 31) >> 5); w += kThreads) a.out_kept_bits[row * a.kept_ld + w] = 0u;
+
+  // Thread t holds the contiguous tokens [lo + t*E, lo + (t+1)*E), so one scan of
+  // per-thread counts places the kept tokens in index order.
+  const size_t esz = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
+  const void* base = (const char*)a.logits + (size_t)row * (size_t)a.ld * esz;
+  const uint32_t* allow = a.allow_bits ? a.allow_bits + row * a.allow_ld : nullptr;
+  const int E = (int)((len + kThreads - 1) / kThreads);
+  const int64_t t0 = lo + (int64_t)threadIdx.x * E;
+  double v[kSplitPer];
+  uint64_t key[kSplitPer];
+  unsigned valid = 0;
+  int bad = 0, fin = 0;
+#pragma unroll
+  for (int j = 0; j < kSplitPer; ++j) {
+    const int64_t i = t0 + j;
+    const bool in = j < E && i < hi;
+    v[j] = in ? load_logit(base, a.dtype, i) : -(double)INFINITY;
+    if (in) valid |= 1u << j;
+  }
+#pragma unroll
+  for (int j = 0; j < kSplitPer; ++j) {
+    const int64_t i = t0 + j;
+    double x = v[j];
+    if ((valid >> j) & 1u) {
+      if (x != x || x == INFINITY) bad = 1;
+      if (allow && !((allow[i >> 5] >> (i & 31)) & 1u)) x = -(double)INFINITY;  // sampling.py:75-79
+      fin |= isfinite(x) ? 1 : 0;
+    }
+    v[j] = x;
+    key[j] = order_key(x);
+  }
+
+  // Radix selection of the slice's k largest keys.  A pass whose selected bin
+  // is taken whole ends the search; a tie group split by the last pass keeps
+  // its lowest indices.
+  const bool trunc = len > g.k;
+  uint64_t prefix = 0, pmask = 0;
+  long long rem = g.k;
+  bool whole = true;
+  if (trunc) {
+    for (int pass = 0; pass < kRadixPasses; ++pass) {
+      const int shift = radix_shift(pass);
+      const uint64_t dm = radix_mask(pass);
+      for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kSplitPer; ++j)
+        if (((valid >> j) & 1u) && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dm], 1u);
+      __syncthreads();
+      long long above;
+      const int b = select_from_top(sh.hist, rem, sh, above);
+      const long long cb = b >= 0 ? (long long)sh.hist[b] : 0;
+      __syncthreads();
+      rem -= above;
+      prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
+      pmask |= dm << shift;
+      if (cb == rem) break;
+      if (pass == kRadixPasses - 1) whole = false;
+    }
+  }
+  long long tb = 0;
+  if (trunc && !whole) {
+    int ties = 0;
+#pragma unroll
+    for (int j = 0; j < kSplitPer; ++j) ties += ((valid >> j) & 1u) && key[j] == prefix;
+    long long tt;
+    tb = block_exclusive_scan_i64(ties, sh.b, tt);
+  }
+  unsigned selm = 0;
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kSplitPer; ++j) {
+    bool sel = (valid >> j) & 1u;
+    if (trunc) {
+      const uint64_t km = key[j] & pmask;
+      if (whole) {
+        sel = sel && km >= prefix;
+      } else {
+        const bool tie = sel && km == prefix;
+        sel = sel && (km > prefix || (tie && tb < rem));
+        tb += tie ? 1 : 0;
+      }
+    }
+    if (sel) {
+      selm |= 1u << j;
+      ++cnt;
+    }
+  }
+  long long total;
+  const long long pos = block_exclusive_scan_i64(cnt, sh.b, total);
+  const long long expect = trunc ? g.k : len;
+  long long mn = LLONG_MAX;
+  long long q = pos;
+#pragma unroll
+  for (int j = 0; j < kSplitPer; ++j) {
+    if ((selm >> j) & 1u) {
+      if (q < expect) {
+        Wc[(int64_t)s * g.k + q] = v[j];
+        Ic[(int64_t)s * g.k + q] = (int32_t)(t0 + j);
+      }
+      ++q;
+      const long long sk = (long long)(key[j] ^ 0x8000000000000000ull);
+      mn = sk < mn ? sk : mn;
+    }
+  }
+  mn = block_min_i64(mn, sh.b);
+  bad = block_or(bad, sh.b);
+  fin = block_or(fin, sh.b);
+  if (threadIdx.x == 0) {
+    SplitSlice r;
+    r.vmin = mn;
+    r.flags = (bad ? kSliceBad : 0) | (fin ? kSliceFinite : 0) | (trunc ? kSliceTrunc : 0) |
+              (total != expect ? kSliceOdd : 0);
+    r.count = (int)total;
+    rec[s] = r;
+  }
+}
+
+// Stage two over the candidate list.  Returns a row status when the
+// candidates decide the row (W then holds the final probabilities of the n
+// candidates), or -1 with the reason in `why` when the general path must.
+__device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitGeom& g, GenShared& sh, unsigned& flags, DistOut& out,
+                                  int64_t& n, int& why) {
+  char* ws = (char*)r.W;
+  double* Wc = (double*)ws;
+  const int32_t* Ic = (const int32_t*)(ws + kSplitIdsOff);
+  const SplitSlice* rec = (const SplitSlice*)(ws + kSplitRecOff);
+  out.onehot = -1;
+  out.npos = 0;
+  out.first = -1;
+  const int f = (int)threadIdx.x < g.S ? rec[threadIdx.x].flags : 0;
+  const int odd = block_or(f & kSliceOdd, sh.b);
+  const int bad = block_or(f & kSliceBad, sh.b);
+  const int fin = block_or(f & kSliceFinite, sh.b);
+  if (odd) {
+    why = kHandSplit;
+    return -1;
+  }
+  if (bad || !fin) {
+    why = kHandInvalid;
+    return -1;
+  }
+  const int64_t last = r.V - (int64_t)(g.S - 1) * g.len;
+  n = (int64_t)(g.S - 1) * g.k + (last < g.k ? last : g.k);
+  auto ldW = [&](int64_t j) { return Wc[j]; };
+
+  RowMax mx;  // candidates are in index order, so the first maximum is the row's
+  row_pass<double>(n, ldW, [&](int64_t j, double x) { mx.add(j, x); });
+  const double M = block_max(mx.m, sh.b);
+  const long long fj = block_min_i64(mx.m == M ? mx.first : LLONG_MAX, sh.b);
+  if (!(fj >= 0 && fj < n && M > -(double)INFINITY)) {  // not reached: a slice with a finite value keeps its maximum
+    why = kHandSplit;
+    return -1;
+  }
+  const dsr_policy_t& p = r.pol;
+  if (p.temperature == 0.0) {  // sampling.py:82-85
+    const int64_t first = Ic[fj];
+    out.onehot = first;
+    out.npos = 1;
+    out.first = first;
+    if (threadIdx.x == 0) {
+      if (r.probs_f32) r.probs_f32[first] = 1.0f;
+      if (r.probs_f64) r.probs_f64[first] = 1.0;
+      if (r.kept_bits) r.kept_bits[first >> 5] = 1u << (first & 31);
+    }
+    __syncthreads();
+    return DSR_OK;
+  }
+  const double T = p.temperature;
+  row_pass<double>(n, ldW, [&](int64_t j, double x) { Wc[j] = (x - M) / T; });  // sampling.py:86-88
+  __syncthreads();
+  if (!(g.k < n)) {  // not reached: S >= 2 gives more than k candidates
+    why = kHandSplit;
+    return -1;
+  }
+  uint64_t kth;
+  long long need;
+  radix_kth_largest(Wc, n, g.k, sh, kth, need);
+  const int64_t cut = nth_equal_index(Wc, n, kth, need, [](double x) { return order_key(x); }, sh);
+  const double sk = key_value(kth);
+  // A truncated slice whose smallest kept value v maps onto s_k may have left
+  // out tokens of the k-th tie group.  When v's neighbours in the input type
+  // map strictly below and above s_k, that group's members in the slice are
+  // exactly its tokens equal to v, and the ones left out follow the slice's
+  // kept ones in index order: the candidates decide the row unless the cut
+  // passes the slice's last kept member.
+  int amb = 0, eq = 0;
+  if ((int)threadIdx.x < g.S) {
+    const SplitSlice q = rec[threadIdx.x];
+    if (q.flags & kSliceTrunc) {
+      const double v = key_value((uint64_t)q.vmin ^ 0x8000000000000000ull);
+      const double t = (v - M) / T;
+      if (!(t <= sk)) {
+        amb = 1;  // not reached: t <= s_k
+      } else if (t == sk) {
+        eq = 1;
+        const double dn = next_input_value(v, r.dtype, false), up = next_input_value(v, r.dtype, true);
+        if (!(v > -(double)INFINITY && (dn - M) / T < sk && (up - M) / T > sk)) amb = 1;
+      }
+    }
+  }
+  if (block_or(amb, sh.b)) {
+    why = kHandSplit;
+    return -1;
+  }
+  if (block_or(eq, sh.b)) {
+    int* last = (int*)sh.hist;  // per slice: the last candidate position holding s_k
+    if ((int)threadIdx.x < g.S) last[threadIdx.x] = -1;
+    __syncthreads();
+    row_pass<double>(n, ldW, [&](int64_t j, double z) {
+      if (order_key(z) == kth) atomicMax(&last[j / g.k], (int)j);
+    });
+    __syncthreads();
+    if (eq && last[threadIdx.x] < cut) amb = 1;
+    if (block_or(amb, sh.b)) {
+      why = kHandSplit;
+      return -1;
+    }
+  }
+  if (r.kept_bits) {  // finite after top-k (sampling.py:89-91); the slices zeroed the words
+    row_pass<double>(n, ldW, [&](int64_t j, double z) {
+      const uint64_t key = order_key(z);
+      if (z > -(double)INFINITY && (key > kth || (key == kth && j <= cut))) {
+        const int32_t i = Ic[j];
+        atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
+      }
+    });
+  }
+  return filter_tail(r, Wc, n, r.V, true, kth, cut, sh, flags, out, [Ic](int64_t j) { return (int64_t)Ic[j]; });
+}
+
+}  // namespace dsr

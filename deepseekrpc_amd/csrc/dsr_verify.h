@@ -75,8 +75,6 @@ struct VerifyLayout {
   int fast_inputs;   // no history, bias or allow mask
 };
 
-__host__ __device__ inline int64_t ws_stride(int64_t V) { return (V + 31) & ~(int64_t)31; }
-
 __host__ __device__ inline size_t verify_ws_bytes(int64_t rows, int32_t K, int64_t V) {
   const size_t slots = (size_t)(2 * K + 1);
   size_t b = (size_t)rows * slots * (size_t)ws_stride(V) * sizeof(double);

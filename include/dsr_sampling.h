@@ -71,7 +71,9 @@ extern "C" {
 /* Per-row flags. */
 #define DSR_FLAG_MARGIN 1u      /* a threshold decision sat inside the rounding band */
 #define DSR_FLAG_GENERAL 2u     /* decided by the general (workspace) path; bits 4-7 give
-                                   the reason a bf16 row left the register-resident path */
+                                   the reason a row left a faster path */
+#define DSR_FLAG_SPLIT 4u       /* decided from per-slice top-k candidates (rows split over
+                                   several workgroups) */
 
 /* Verifier stop reasons (sampling.py:286,289,294). */
 #define DSR_STOP_NONE 0
