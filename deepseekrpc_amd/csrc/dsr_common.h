@@ -44,110 +44,6 @@ struct OpMin {
   template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }
 };
 
-template <class T, class Op>
-__device__ __forceinline__ T wave_reduce(T x, Op op) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = op(x, __shfl_xor(x, o));
-  return x;
-}
-
-template <class T>
-__device__ __forceinline__ T wave_sum(T x) { return wave_reduce(x, OpSum()); }
-
-// Combines the per-wave partials slot[0..15]: lane l < 16 takes slot[l] and a
-// four-step butterfly leaves the result in every lane of every wave.
-template <class T, class Op>
-__device__ __forceinline__ T combine_waves(const T* slot, T identity, Op op) {
-  const int l = lane_id();
-  T y = l < kWaves ? slot[l] : identity;
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) y = op(y, __shfl_xor(y, o));
-  return __shfl(y, 0);
-}
-
-template <class T, class Op>
-__device__ __forceinline__ T block_reduce(T x, T* slot, T identity, Op op) {
-  x = wave_reduce(x, op);
-  if (lane_id() == 0) slot[wave_id()] = x;
-  __syncthreads();
-  const T r = combine_waves(slot, identity, op);
-  __syncthreads();
-  return r;
-}
-
-__device__ __forceinline__ double block_sum(double x, BlockScratch& s) {
-  return block_reduce(x, s.f64, 0.0, OpSum());
-}
-
-__device__ __forceinline__ double block_max(double x, BlockScratch& s) {
-  return block_reduce(x, s.f64, -(double)INFINITY, OpMax());
-}
-
-__device__ __forceinline__ long long block_sum_i64(long long x, BlockScratch& s) {
-  return block_reduce(x, s.i64, 0ll, OpSum());
-}
-
-__device__ __forceinline__ long long block_min_i64(long long x, BlockScratch& s) {
-  return block_reduce(x, s.i64, LLONG_MAX, OpMin());
-}
-
-__device__ __forceinline__ long long block_max_i64(long long x, BlockScratch& s) {
-  return block_reduce(x, s.i64, LLONG_MIN, OpMax());
-}
-
-__device__ __forceinline__ int block_or(int x, BlockScratch& s) {
-  return block_max_i64(x ? 1 : 0, s) != 0;
-}
-
-// Inclusive prefix over the lanes of a wave (fixed association order).
-template <class T>
-__device__ __forceinline__ T wave_incl_scan(T v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    T y = __shfl_up(v, o);
-    if (lane_id() >= o) v += y;
-  }
-  return v;
-}
-
-// Prefix of the 16 per-wave totals: exclusive base of this wave, and the total.
-template <class T>
-__device__ __forceinline__ void wave_bases(const T* slot, T& base, T& total) {
-  const int l = lane_id();
-  T y = l < kWaves ? slot[l] : (T)0;
-  T incl = y;
-#pragma unroll
-  for (int o = 1; o < kWaves; o <<= 1) {
-    T z = __shfl_up(incl, o);
-    if (l >= o) incl += z;
-  }
-  base = __shfl(incl - y, wave_id());
-  total = __shfl(incl, kWaves - 1);
-}
-
-// Exclusive prefix sum over threads in thread order; `total` gets the sum.
-__device__ __forceinline__ long long block_exclusive_scan_i64(long long x, BlockScratch& s, long long& total) {
-  const long long v = wave_incl_scan(x);
-  if (lane_id() == 63) s.i64[wave_id()] = v;
-  __syncthreads();
-  long long base;
-  wave_bases(s.i64, base, total);
-  __syncthreads();
-  return base + v - x;
-}
-
-// Exclusive prefix sum of doubles in thread order (fixed association order).
-__device__ __forceinline__ double block_exclusive_scan_f64(double x, BlockScratch& s, double& total) {
-  const double v = wave_incl_scan(x);
-  if (lane_id() == 63) s.f64[wave_id()] = v;
-  __syncthreads();
-  double base;
-  wave_bases(s.f64, base, total);
-  __syncthreads();
-  // v is the inclusive prefix inside the wave; drop this thread's own term.
-  return (base + v) - x;
-}
-
 // Order-preserving 64-bit key of a double: larger value -> larger key,
 // -0.0 and +0.0 share one key (NumPy sorts them as equal).
 __device__ __forceinline__ uint64_t order_key(double x) {

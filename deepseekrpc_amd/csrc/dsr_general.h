@@ -56,6 +56,7 @@ struct GenShared {
   unsigned long long hmass[kBins];
   int sel_bin;
   long long sel_above;
+  long long sel_count;
   long long bc[4];
 };
 
@@ -142,10 +143,12 @@ struct RunAdd {
 };
 
 // bins[] ranked from the top (largest digit first): the bin where the running
-// total reaches rem (1-based), or -1, and the total of the bins above it.
-// Thread t holds bins kBins-1-2t and kBins-2-2t.  Every thread calls.
+// total reaches rem (1-based), or -1, the total of the bins above it, and
+// counts[] of that bin (the token count when bins[] holds masses).  Thread t
+// holds bins kBins-1-2t and kBins-2-2t.  Every thread calls.
 template <class T>
-__device__ int select_from_top(const T* bins, long long rem, GenShared& sh, long long& above) {
+__device__ int select_from_top(const T* bins, long long rem, GenShared& sh, long long& above,
+                               const unsigned int* counts, long long& count) {
   const int t = threadIdx.x;
   const int b0 = kBins - 1 - 2 * t, b1 = b0 - 1;
   const long long c0 = (long long)bins[b0], c1 = (long long)bins[b1];
@@ -155,13 +158,16 @@ __device__ int select_from_top(const T* bins, long long rem, GenShared& sh, long
   if (ex < rem && rem <= ex + c0) {
     sh.sel_bin = b0;
     sh.sel_above = ex;
+    sh.sel_count = counts[b0];
   } else if (ex + c0 < rem && rem <= ex + c0 + c1) {
     sh.sel_bin = b1;
     sh.sel_above = ex + c0;
+    sh.sel_count = counts[b1];
   }
   __syncthreads();
   const int b = sh.sel_bin;
   above = sh.sel_above;
+  count = sh.sel_count;
   __syncthreads();
   return b;
 }
@@ -169,74 +175,6 @@ __device__ int select_from_top(const T* bins, long long rem, GenShared& sh, long
 __device__ __forceinline__ int radix_shift(int pass) { return pass < kRadixPasses - 1 ? 64 - kRadixBits * (pass + 1) : 0; }
 __device__ __forceinline__ uint64_t radix_mask(int pass) {
   return pass < kRadixPasses - 1 ? (uint64_t)(kBins - 1) : (1ull << (64 - kRadixBits * (kRadixPasses - 1))) - 1;
-}
-
-// Radix select: key of the k-th largest element (1-based, ties counted) and
-// `need`, how many elements carrying that key are ranked within the first k.
-__device__ void radix_kth_largest(const double* W, int64_t V, long long k, GenShared& sh, uint64_t& kth,
-                                  long long& need) {
-  uint64_t prefix = 0, pmask = 0;
-  long long rem = k;
-  for (int pass = 0; pass < kRadixPasses; ++pass) {
-    const int shift = radix_shift(pass);
-    const uint64_t dm = radix_mask(pass);
-    for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
-    __syncthreads();
-    RunAdd<unsigned int> ra;
-    row_pass<double>(
-        V, [&](int64_t i) { return W[i]; },
-        [&](int64_t, double x) {
-          const uint64_t key = order_key(x);
-          if ((key & pmask) == prefix) ra.add(sh.hist, (int)((key >> shift) & dm), 1u);
-        });
-    ra.flush(sh.hist);
-    __syncthreads();
-    long long above;
-    const int b = select_from_top(sh.hist, rem, sh, above);
-    rem -= above;
-    prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
-    pmask |= dm << shift;
-  }
-  kth = prefix;
-  need = rem;
-}
-
-// Radix search over probability mass.  W holds r >= 0; ranks run (r desc,
-// index asc).  Finds the bit pattern of r at L, the first ranked element
-// whose inclusive cumulative mass reaches `top_p`.  Masses are summed as
-// 60-bit fixed point (order-independent, so deterministic); the caller
-// re-derives the decision exactly in float64.  Returns false if the whole
-// mass stays below top_p.
-__device__ bool radix_mass_crossing(const double* W, int64_t V, double top_p, GenShared& sh, uint64_t& lbits) {
-  long long tgt = (long long)(top_p * 0x1p60);
-  if (tgt == 0) tgt = 1;  // top_p == 0: the first ranked element is L
-  uint64_t prefix = 0, pmask = 0;
-  long long above = 0;
-  for (int pass = 0; pass < kRadixPasses; ++pass) {
-    const int shift = radix_shift(pass);
-    const uint64_t dm = radix_mask(pass);
-    for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hmass[b] = 0;
-    __syncthreads();
-    RunAdd<unsigned long long> ra;
-    row_pass<double>(
-        V, [&](int64_t i) { return W[i]; },
-        [&](int64_t, double x) {
-          if (x > 0.0) {
-            const uint64_t key = raw_bits(x);
-            if ((key & pmask) == prefix) ra.add(sh.hmass, (int)((key >> shift) & dm), (unsigned long long)(x * 0x1p60));
-          }
-        });
-    ra.flush(sh.hmass);
-    __syncthreads();
-    long long ab;
-    const int b = select_from_top(sh.hmass, tgt - above, sh, ab);
-    if (b < 0) return false;
-    above += ab;
-    prefix |= (uint64_t)b << shift;
-    pmask |= dm << shift;
-  }
-  lbits = prefix;
-  return true;
 }
 
 // Index of the need-th (1-based, in index order) element with keyfn(W[i]) == key.
@@ -286,6 +224,115 @@ __device__ int64_t nth_equal_index(const double* W, int64_t V, uint64_t key, lon
   __syncthreads();
   return r;
 }
+
+// Radix select of the k-th largest element (1-based, ties counted) and its
+// tie group's cut: the first k elements in (key desc, index asc) order are
+// those with key > kth, and those with key == kth and index <= cut.  A pass
+// whose selected bin is taken whole ends the search: kth is then the bin's
+// smallest key and its whole tie group is kept (cut = INT64_MAX).
+__device__ void radix_top_k(const double* W, int64_t V, long long k, GenShared& sh, uint64_t& kth, int64_t& cut) {
+  uint64_t prefix = 0, pmask = 0;
+  long long rem = k;
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
+    const int shift = radix_shift(pass);
+    const uint64_t dm = radix_mask(pass);
+    for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
+    __syncthreads();
+    RunAdd<unsigned int> ra;
+    row_pass<double>(
+        V, [&](int64_t i) { return W[i]; },
+        [&](int64_t, double x) {
+          const uint64_t key = order_key(x);
+          if ((key & pmask) == prefix) ra.add(sh.hist, (int)((key >> shift) & dm), 1u);
+        });
+    ra.flush(sh.hist);
+    __syncthreads();
+    long long above, cb;
+    const int b = select_from_top(sh.hist, rem, sh, above, sh.hist, cb);
+    rem -= above;
+    prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
+    pmask |= dm << shift;
+    if (b >= 0 && cb == rem) {
+      cut = INT64_MAX;
+      if (pass == kRadixPasses - 1) {
+        kth = prefix;
+        return;
+      }
+      long long mn = LLONG_MAX;  // smallest key of the bin, sign bit flipped so it orders as signed
+      row_pass<double>(
+          V, [&](int64_t i) { return W[i]; },
+          [&](int64_t, double x) {
+            const uint64_t key = order_key(x);
+            const long long sk = (long long)(key ^ 0x8000000000000000ull);
+            if ((key & pmask) == prefix && sk < mn) mn = sk;
+          });
+      kth = (uint64_t)block_min_i64(mn, sh.b) ^ 0x8000000000000000ull;
+      return;
+    }
+  }
+  kth = prefix;
+  cut = nth_equal_index(W, V, kth, rem, [](double x) { return order_key(x); }, sh);
+}
+
+// Radix search over probability mass.  W holds r >= 0; ranks run (r desc,
+// index asc).  Finds the bit pattern of r at L, the first ranked element
+// whose inclusive cumulative mass reaches `top_p`.  Masses are summed as
+// 60-bit fixed point (order-independent, so deterministic); the caller
+// re-derives the decision exactly in float64.  A pass whose selected bin
+// holds one element ends the search (L is that element).  Returns false if
+// the whole mass stays below top_p.
+__device__ bool radix_mass_crossing(const double* W, int64_t V, double top_p, GenShared& sh, uint64_t& lbits) {
+  long long tgt = (long long)(top_p * 0x1p60);
+  if (tgt == 0) tgt = 1;  // top_p == 0: the first ranked element is L
+  uint64_t prefix = 0, pmask = 0;
+  long long above = 0;
+  for (int pass = 0; pass < kRadixPasses; ++pass) {
+    const int shift = radix_shift(pass);
+    const uint64_t dm = radix_mask(pass);
+    for (int b = threadIdx.x; b < kBins; b += kThreads) {
+      sh.hmass[b] = 0;
+      sh.hist[b] = 0;
+    }
+    __syncthreads();
+    RunAdd<unsigned long long> ra;
+    RunAdd<unsigned int> rc;
+    row_pass<double>(
+        V, [&](int64_t i) { return W[i]; },
+        [&](int64_t, double x) {
+          if (x > 0.0) {
+            const uint64_t key = raw_bits(x);
+            if ((key & pmask) == prefix) {
+              const int d = (int)((key >> shift) & dm);
+              ra.add(sh.hmass, d, (unsigned long long)(x * 0x1p60));
+              rc.add(sh.hist, d, 1u);
+            }
+          }
+        });
+    ra.flush(sh.hmass);
+    rc.flush(sh.hist);
+    __syncthreads();
+    long long ab, cb;
+    const int b = select_from_top(sh.hmass, tgt - above, sh, ab, sh.hist, cb);
+    if (b < 0) return false;
+    above += ab;
+    prefix |= (uint64_t)b << shift;
+    pmask |= dm << shift;
+    if (cb == 1 && pass < kRadixPasses - 1) {
+      long long mx = 0;  // the bin's one positive element
+      row_pass<double>(
+          V, [&](int64_t i) { return W[i]; },
+          [&](int64_t, double x) {
+            const uint64_t key = raw_bits(x);
+            if (x > 0.0 && (key & pmask) == prefix) mx = (long long)key;
+          });
+      lbits = (uint64_t)block_max_i64(mx, sh.b);
+      return true;
+    }
+  }
+  lbits = prefix;
+  return true;
+}
+
 
 // Wave 0 of the workgroup finishes a CDF search inside one contiguous slice
 // [lo, hi): the first element whose running sum (from `base`) exceeds thr.
@@ -550,11 +597,11 @@ struct IdentityMap {
 };
 
 // Steps 10-13 (sampling.py:92-106) over W[0, n), which holds s = (v - max) / T
-// and the top-k decision (`kth`, `cut` from radix_kth_largest and
-// nth_equal_index).  Position j of W is token map(j), positions in token
-// order, so index-order ties and the CDF keep the reference's order.  `vocab`
-// sizes the rounding band of a sum over the whole row.  On DSR_OK, W holds
-// the final probabilities (also written to the optional outputs).
+// and the top-k decision (`kth`, `cut` from radix_top_k).  Position j of W is
+// token map(j), positions in token order, so index-order ties and the CDF keep
+// the reference's order.  `vocab` sizes the rounding band of a sum over the
+// whole row.  On DSR_OK, W holds the final probabilities (also written to the
+// optional outputs).
 template <class Map>
 __device__ __forceinline__ int filter_tail(const RowSpec& r, double* W, int64_t n, int64_t vocab, bool topk,
                                            uint64_t kth, int64_t cut, GenShared& sh, unsigned& flags, DistOut& out,
@@ -720,9 +767,7 @@ __device__ __forceinline__ int general_distribution(const RowSpec& r, GenShared&
   uint64_t kth = 0;
   int64_t cut = -1;
   if (topk) {
-    long long need;
-    radix_kth_largest(W, V, p.top_k, sh, kth, need);
-    cut = nth_equal_index(W, V, kth, need, [](double x) { return order_key(x); }, sh);
+    radix_top_k(W, V, p.top_k, sh, kth, cut);
   }
   if (r.kept_bits) write_kept_bits(W, V, topk, kth, cut, r.kept_bits, r.kept_words);
 

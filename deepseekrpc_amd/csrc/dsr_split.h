@@ -183,10 +183,9 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
       for (int j = 0; j < kSplitPer; ++j)
         if (((valid >> j) & 1u) && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dm], 1u);
       __syncthreads();
-      long long above;
-      const int b = select_from_top(sh.hist, rem, sh, above);
-      const long long cb = b >= 0 ? (long long)sh.hist[b] : 0;
-      __syncthreads();
+      long long above, cb;
+      const int b = select_from_top(sh.hist, rem, sh, above, sh.hist, cb);
+      if (b < 0) cb = -1;
       rem -= above;
       prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
       pmask |= dm << shift;
@@ -310,9 +309,8 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
     return -1;
   }
   uint64_t kth;
-  long long need;
-  radix_kth_largest(Wc, n, g.k, sh, kth, need);
-  const int64_t cut = nth_equal_index(Wc, n, kth, need, [](double x) { return order_key(x); }, sh);
+  int64_t cut;
+  radix_top_k(Wc, n, g.k, sh, kth, cut);
   const double sk = key_value(kth);
   // A truncated slice whose smallest kept value v maps onto s_k may have left
   // out tokens of the k-th tie group.  When v's neighbours in the input type
@@ -347,7 +345,10 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
       if (order_key(z) == kth) atomicMax(&last[j / g.k], (int)j);
     });
     __syncthreads();
-    if (eq && last[threadIdx.x] < cut) amb = 1;
+    // A tie group kept whole (cut = INT64_MAX) ends at its last candidate.
+    const int64_t c = cut != INT64_MAX ? cut
+                                       : block_max_i64((int)threadIdx.x < g.S ? (long long)last[threadIdx.x] : -1, sh.b);
+    if (eq && last[threadIdx.x] < c) amb = 1;
     if (block_or(amb, sh.b)) {
       why = kHandSplit;
       return -1;

@@ -36,7 +36,7 @@ __device__ __forceinline__ uint64_t dpp64(uint64_t old, uint64_t x) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Bit-level carriers so one template serves u32, i64 and f64.
+// Bit-level carriers so one template serves u32, i64, u64 and f64.
 template <class T> struct Bits;
 template <> struct Bits<uint32_t> {
   static __device__ __forceinline__ uint32_t to(uint32_t x) { return x; }
@@ -61,6 +61,13 @@ template <> struct Bits<long long> {
 template <> struct Bits<double> {
   static __device__ __forceinline__ uint64_t to(double x) { return (uint64_t)__double_as_longlong(x); }
   static __device__ __forceinline__ double from(uint64_t x) { return __longlong_as_double((long long)x); }
+  template <int C, int RM = 0xF, int BM = 0xF, bool BC = true>
+  static __device__ __forceinline__ uint64_t dpp(uint64_t o, uint64_t x) { return dpp64<C, RM, BM, BC>(o, x); }
+  static __device__ __forceinline__ uint64_t readlane(uint64_t x, int l) { return Bits<long long>::readlane(x, l); }
+};
+template <> struct Bits<unsigned long long> {
+  static __device__ __forceinline__ uint64_t to(unsigned long long x) { return (uint64_t)x; }
+  static __device__ __forceinline__ unsigned long long from(uint64_t x) { return (unsigned long long)x; }
   template <int C, int RM = 0xF, int BM = 0xF, bool BC = true>
   static __device__ __forceinline__ uint64_t dpp(uint64_t o, uint64_t x) { return dpp64<C, RM, BM, BC>(o, x); }
   static __device__ __forceinline__ uint64_t readlane(uint64_t x, int l) { return Bits<long long>::readlane(x, l); }
@@ -270,6 +277,74 @@ template <> __device__ __forceinline__ uint32_t* BlockSync::slots<uint32_t>(int 
 // Position of this lane among the set lanes of a ballot.
 __device__ __forceinline__ uint32_t lanes_below(unsigned long long b) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup reductions and scans over BlockScratch slots.  Each call is
+// bracketed by full barriers (__syncthreads, which also orders global
+// memory): the workspace passes that call them re-read rows other threads
+// wrote.  The wave parts run on DPP.
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T x) { return wave_reduce_dpp(x, OpSum()); }
+
+template <class T, class Op>
+__device__ __forceinline__ T block_reduce(T x, T* slot, T identity, Op op) {
+  x = wave_reduce_dpp(x, op);
+  if (lane_id() == 0) slot[wave_id()] = x;
+  __syncthreads();
+  T y = lane_id() < kWaves ? slot[lane_id()] : identity;
+  y = row_reduce(y, op);
+  const T r = lane_value(y, 0);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ double block_sum(double x, BlockScratch& s) {
+  return block_reduce(x, s.f64, 0.0, OpSum());
+}
+
+__device__ __forceinline__ double block_max(double x, BlockScratch& s) {
+  return block_reduce(x, s.f64, -(double)INFINITY, OpMax());
+}
+
+__device__ __forceinline__ long long block_sum_i64(long long x, BlockScratch& s) {
+  return block_reduce(x, s.i64, 0ll, OpSum());
+}
+
+__device__ __forceinline__ long long block_min_i64(long long x, BlockScratch& s) {
+  return block_reduce(x, s.i64, LLONG_MAX, OpMin());
+}
+
+__device__ __forceinline__ long long block_max_i64(long long x, BlockScratch& s) {
+  return block_reduce(x, s.i64, LLONG_MIN, OpMax());
+}
+
+__device__ __forceinline__ int block_or(int x, BlockScratch& s) {
+  return block_max_i64(x ? 1 : 0, s) != 0;
+}
+
+// Exclusive prefix over threads in thread order (fixed association order);
+// `total` gets the workgroup total.
+template <class T>
+__device__ __forceinline__ T block_exclusive_scan(T x, T* slot, T& total) {
+  const T v = wave_scan_dpp(x);
+  if (lane_id() == 63) slot[wave_id()] = v;
+  __syncthreads();
+  const T y = lane_id() < kWaves ? slot[lane_id()] : (T)0;
+  const T wincl = row_scan_dpp(y);
+  total = lane_value(wincl, kWaves - 1);
+  const T base = lane_value(wincl - y, wave_id());
+  __syncthreads();
+  return (base + v) - x;
+}
+
+__device__ __forceinline__ long long block_exclusive_scan_i64(long long x, BlockScratch& s, long long& total) {
+  return block_exclusive_scan(x, s.i64, total);
+}
+
+__device__ __forceinline__ double block_exclusive_scan_f64(double x, BlockScratch& s, double& total) {
+  return block_exclusive_scan(x, s.f64, total);
 }
 
 }  // namespace dsr
