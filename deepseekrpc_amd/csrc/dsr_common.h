@@ -43,6 +43,9 @@ struct OpMax {
 struct OpMin {
   template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }
 };
+struct OpOr {
+  template <class T> __device__ __forceinline__ T operator()(T a, T b) const { return a | b; }
+};
 
 // Order-preserving 64-bit key of a double: larger value -> larger key,
 // -0.0 and +0.0 share one key (NumPy sorts them as equal).

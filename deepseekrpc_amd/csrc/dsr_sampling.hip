@@ -111,6 +111,9 @@ __global__ __launch_bounds__(kThreads) void k_sample_general(dsr_sample_args_t a
 template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, int smax) {
   __shared__ GenShared sh;
+  __shared__ double cz[kSplitCap];   // the candidates' values, then (v - max) / T
+  __shared__ double kz[kSplitMaxK];  // the kept tokens' values, then probabilities, in index order
+  __shared__ int32_t kid[kSplitMaxK];
   const int64_t row = blockIdx.x;
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
   RowSpec r = sample_row_spec(a, row, W);
@@ -121,10 +124,9 @@ __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, 
     DistOut d;
     int64_t n = 0;
     int why = 0;
-    const int st = split_distribution(r, g, sh, sflags, d, n, why);
+    const int st = split_distribution(r, g, sh, cz, kz, kid, sflags, d, n, why);
     if (st >= 0) {
-      const int32_t* ids = (const int32_t*)((const char*)W + kSplitIdsOff);
-      finish_row<RNG>(a, row, W, n, st, d, sflags, sh, [ids](int64_t j) { return (int64_t)ids[j]; });
+      finish_row<RNG>(a, row, kz, n, st, d, sflags, sh, [](int64_t j) { return (int64_t)kid[j]; });
       return;
     }
     __syncthreads();  // every thread is done with the candidate list

@@ -239,8 +239,9 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
     }
   }
   mn = block_min_i64(mn, sh.b);
-  bad = block_or(bad, sh.b);
-  fin = block_or(fin, sh.b);
+  const long long bf = block_reduce((long long)(bad | (fin << 1)), sh.b.i64, 0ll, OpOr());
+  bad = (int)(bf & 1);
+  fin = (int)((bf >> 1) & 1);
   if (threadIdx.x == 0) {
     SplitSlice r;
     r.vmin = mn;
@@ -252,21 +253,20 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
 }
 
 // Stage two over the candidate list.  Returns a row status when the
-// candidates decide the row (W then holds the final probabilities of the n
-// candidates), or -1 with the reason in `why` when the general path must.
-__device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitGeom& g, GenShared& sh, unsigned& flags, DistOut& out,
-                                  int64_t& n, int& why) {
+// candidates decide the row (kz then holds the final probabilities of the n
+// kept tokens in index order, kid their token ids), or -1 with the reason in
+// `why` when the general path must.  Wc is LDS for kSplitCap values.
+__device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitGeom& g, GenShared& sh, double* Wc,
+                                                  double* kz, int32_t* kid, unsigned& flags, DistOut& out, int64_t& n,
+                                                  int& why) {
   char* ws = (char*)r.W;
-  double* Wc = (double*)ws;
   const int32_t* Ic = (const int32_t*)(ws + kSplitIdsOff);
   const SplitSlice* rec = (const SplitSlice*)(ws + kSplitRecOff);
   out.onehot = -1;
   out.npos = 0;
   out.first = -1;
-  const int f = (int)threadIdx.x < g.S ? rec[threadIdx.x].flags : 0;
-  const int odd = block_or(f & kSliceOdd, sh.b);
-  const int bad = block_or(f & kSliceBad, sh.b);
-  const int fin = block_or(f & kSliceFinite, sh.b);
+  const long long f = block_reduce((int)threadIdx.x < g.S ? (long long)rec[threadIdx.x].flags : 0ll, sh.b.i64, 0ll, OpOr());
+  const bool odd = f & kSliceOdd, bad = f & kSliceBad, fin = f & kSliceFinite;
   if (odd) {
     why = kHandSplit;
     return -1;
@@ -277,10 +277,16 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
   }
   const int64_t last = r.V - (int64_t)(g.S - 1) * g.len;
   n = (int64_t)(g.S - 1) * g.k + (last < g.k ? last : g.k);
+  // The candidates' values move to LDS (Wc, kSplitCap doubles): every pass
+  // below re-reads them.  Candidates are in index order, so their first
+  // maximum is the row's.
+  const double* cand = (const double*)ws;
+  RowMax mx;
+  row_pass<double>(n, [&](int64_t j) { return cand[j]; }, [&](int64_t j, double x) {
+    Wc[j] = x;
+    mx.add(j, x);
+  });
   auto ldW = [&](int64_t j) { return Wc[j]; };
-
-  RowMax mx;  // candidates are in index order, so the first maximum is the row's
-  row_pass<double>(n, ldW, [&](int64_t j, double x) { mx.add(j, x); });
   const double M = block_max(mx.m, sh.b);
   const long long fj = block_min_i64(mx.m == M ? mx.first : LLONG_MAX, sh.b);
   if (!(fj >= 0 && fj < n && M > -(double)INFINITY)) {  // not reached: a slice with a finite value keeps its maximum
@@ -354,16 +360,36 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
       return -1;
     }
   }
-  if (r.kept_bits) {  // finite after top-k (sampling.py:89-91); the slices zeroed the words
-    row_pass<double>(n, ldW, [&](int64_t j, double z) {
-      const uint64_t key = order_key(z);
-      if (z > -(double)INFINITY && (key > kth || (key == kth && j <= cut))) {
-        const int32_t i = Ic[j];
-        atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
-      }
-    });
+  // The k tokens that survive top-k (sampling.py:89-91) move to LDS in index
+  // order, with their kept bits set (the slices zeroed the words); steps
+  // 10-13 and the draw then run over them alone.
+  auto kept = [&](int64_t j, double z) {
+    const uint64_t key = order_key(z);
+    return z > -(double)INFINITY && (key > kth || (key == kth && j <= cut));
+  };
+  int64_t lo, hi;
+  slice_of(threadIdx.x, n, lo, hi);
+  long long cnt = 0;
+  for (int64_t j = lo; j < hi; ++j) cnt += kept(j, Wc[j]) ? 1 : 0;
+  long long nk;
+  long long pos = block_exclusive_scan_i64(cnt, sh.b, nk);
+  if (nk > kSplitMaxK) {  // not reached: top-k keeps k tokens
+    why = kHandSplit;
+    return -1;
   }
-  return filter_tail(r, Wc, n, r.V, true, kth, cut, sh, flags, out, [Ic](int64_t j) { return (int64_t)Ic[j]; });
+  for (int64_t j = lo; j < hi; ++j) {
+    const double z = Wc[j];
+    if (kept(j, z)) {
+      const int32_t i = Ic[j];
+      kz[pos] = z;
+      kid[pos] = i;
+      ++pos;
+      if (r.kept_bits) atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  n = nk;
+  return filter_tail(r, kz, nk, r.V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; });
 }
 
 }  // namespace dsr
