@@ -1,7 +1,9 @@
 // Kernels and C ABI of the token-sampling hot path (gfx950).
 //
 //   dsr_sample_rows    -> SamplingPolicy.probabilities + categorical
-//                         (sampling.py:48-128), one workgroup per row.
+//                         (sampling.py:48-128), one workgroup per row; fp32 /
+//                         f64 top-k rows are first cut into slices, one
+//                         workgroup each (dsr_split.h).
 //   dsr_verify_drafts  -> SamplingWork.verify -> verify_drafts
 //                         (terminal_sampling.py:170-183, sampling.py:247-294):
 //                         one workgroup per conditional distribution, then
