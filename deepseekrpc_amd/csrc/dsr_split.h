@@ -1,14 +1,16 @@
 // Split-row top-k path: rows that the register-resident bf16 paths do not
-// take (float32 / float64 logits, or bf16 rows those paths cannot load) and
-// that carry a top-k filter (1 <= k <= 1024) or are greedy.
+// take (float32 / float64 logits, or bf16 rows those paths cannot load), with
+// or without a token history but no bias, that carry a top-k filter
+// (1 <= k <= 1024) or are greedy.
 //
 // One workgroup walking a whole row through the general path's passes uses
 // one CU of 256; a small batch (one fp32 row per call is the reference's own
 // calling pattern, sampling.py:108-128) then waits on that CU alone.  Here the
 // row is cut into S contiguous slices, one workgroup each:
 //
-//   k_split_select  reads its slice once (logits, allow bits), validates it,
-//                   and keeps the slice's k largest values (ranked by value,
+//   k_split_select  reads its slice once (logits, allow bits, the history
+//                   entries that fall in it), validates it, applies the
+//                   penalties, and keeps the slice's k largest values (ranked by value,
 //                   then index) by 11-bit radix passes over registers, in
 //                   index order, at slice s * k of a candidate list in the
 //                   row's workspace.  It also zeroes the slice's probability
@@ -63,7 +65,7 @@ static_assert(kSplitBytes <= (size_t)kSplitMinVocab * 8, "candidate area exceeds
 static_assert((int64_t)kSplitMinSlices * kSplitPer * kThreads >= DSR_MAX_VOCAB, "slices too short for the vocabulary");
 
 static inline bool split_path_eligible(const dsr_sample_args_t& a) {
-  return a.pen_off == nullptr && a.bias_off == nullptr && a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
+  return a.bias_off == nullptr && a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
 }
 
 // Slice budget per row: enough stage-one workgroups to cover the chip.
@@ -114,11 +116,13 @@ __device__ __forceinline__ double next_input_value(double v, int dtype, bool up)
 // Stage one: grid rows * smax, blockIdx.x = row * smax + slice.
 __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, int smax) {
   __shared__ GenShared sh;
+  __shared__ int32_t emap[kSplitPer * kThreads];  // slice position -> history entry, or -1
   const int64_t row = blockIdx.x / (unsigned)smax;
   const int s = (int)(blockIdx.x % (unsigned)smax);
   const int64_t V = a.vocab;
+  const dsr_policy_t pol = a.policy[row];
   SplitGeom g;
-  if (!split_geom(a.policy[row], V, smax, g) || s >= g.S) return;
+  if (!split_geom(pol, V, smax, g) || s >= g.S) return;
   const int64_t lo = (int64_t)s * g.len;
   const int64_t hi = lo + g.len < V ? lo + g.len : V;
   const int64_t len = hi - lo;
@@ -160,10 +164,74 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
     if ((valid >> j) & 1u) {
       if (x != x || x == INFINITY) bad = 1;
       if (allow && !((allow[i >> 5] >> (i & 31)) & 1u)) x = -(double)INFINITY;  // sampling.py:75-79
-      fin |= isfinite(x) ? 1 : 0;
     }
     v[j] = x;
-    key[j] = order_key(x);
+  }
+
+  // Repetition / presence / frequency penalties (sampling.py:59-66) from the
+  // row's history table, in the general path's float64 operation order
+  // (masking first is equivalent: -inf is a fixed point of both steps).
+  // Slice 0 checks the whole table with the general path's rules
+  // (sampling.py:55-58,62-65); a table it would reject hands the row over,
+  // and the general path reports the status.  Each slice finds its entries by
+  // counting the (sorted) ids below its bounds.
+  int64_t pen_n = 0;
+  const int32_t *pid = nullptr, *pcnt = nullptr, *pgen = nullptr;
+  if (a.pen_off) {
+    const int64_t o = a.pen_off[row];
+    pen_n = a.pen_off[row + 1] - o;
+    pid = a.pen_ids + o;
+    pcnt = a.pen_count + o;
+    pgen = a.pen_gen + o;
+  }
+  if (pen_n > V) {
+    bad = 1;  // more entries than tokens: not a valid table
+  } else if (pen_n > 0) {
+    long long below = 0;  // entries with id < lo (low half) and id < hi (high half)
+    long long csum = 0;
+    int tbad = 0;
+    for (int64_t e = threadIdx.x; e < pen_n; e += kThreads) {
+      const int32_t id = pid[e];
+      below += (id < lo ? 1ll : 0ll) + (id < hi ? (1ll << 32) : 0ll);
+      if (s == 0) {
+        const long long c = pcnt[e], gg = pgen[e];
+        if (id < 0 || id >= V || (e > 0 && pid[e - 1] >= id) || c < 0 || c > DSR_MAX_COUNT || gg < 0 || gg > c)
+          tbad = 1;
+        csum += c;
+      }
+    }
+    below = block_sum_i64(below, sh.b);
+    if (s == 0) {
+      const long long tb = block_or(tbad, sh.b);
+      csum = block_sum_i64(csum, sh.b);
+      if (tb || csum > DSR_MAX_COUNT) bad = 1;
+    }
+    const int64_t e0 = below & 0xFFFFFFFFll, e1 = below >> 32;
+    for (int64_t q = threadIdx.x; q < len; q += kThreads) emap[q] = -1;
+    __syncthreads();
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += kThreads) {
+      const int32_t id = pid[e];
+      if (id >= lo && id < hi) emap[id - lo] = (int32_t)e;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSplitPer; ++j) {
+      if ((valid >> j) & 1u) {
+        const int32_t e = emap[t0 + j - lo];
+        if (e >= 0) {
+          const long long c = pcnt[e], gg = pgen[e];
+          double x = v[j];
+          if (c > 0) x = x >= 0.0 ? x / pol.repetition_penalty : x * pol.repetition_penalty;
+          const double pen = pol.presence_penalty * (gg > 0 ? 1.0 : 0.0) + pol.frequency_penalty * (double)gg;
+          v[j] = x - pen;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kSplitPer; ++j) {
+    if ((valid >> j) & 1u) fin |= isfinite(v[j]) ? 1 : 0;
+    key[j] = order_key(v[j]);
   }
 
   // Radix selection of the slice's k largest keys.  A pass whose selected bin
@@ -334,7 +402,9 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
         amb = 1;  // not reached: t <= s_k
       } else if (t == sk) {
         eq = 1;
-        const double dn = next_input_value(v, r.dtype, false), up = next_input_value(v, r.dtype, true);
+        // Penalised values are float64, off the input type's grid.
+        const int vt = r.pen_n > 0 ? DSR_F64 : r.dtype;
+        const double dn = next_input_value(v, vt, false), up = next_input_value(v, vt, true);
         if (!(v > -(double)INFINITY && (dn - M) / T < sk && (up - M) / T > sk)) amb = 1;
       }
     }

@@ -226,3 +226,73 @@ def test_device_draws_on_the_split_path():
         now = int(words[r, 0]) | (int(words[r, 1]) << 64)
         assert now == (s_next if ref.consumed else st0[r]["state"])
         assert int(res.flags[r]) & N.FLAG_SPLIT
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_rows_with_histories_match_oracle(dtype):
+    """Penalised rows: each slice applies the history entries that fall in it."""
+    rng = np.random.default_rng(31 if dtype == torch.float32 else 32)
+    B, V = 6, 129280
+    logits = rng.normal(0, 2, (B, V))
+    if dtype == torch.float32:
+        logits = logits.astype(np.float32)
+    counts = np.zeros((B, V), np.int32)
+    gens = np.zeros((B, V), np.int32)
+    for r, n in enumerate((0, 10, 300, 4096, 16384, 60000)):
+        h = rng.integers(0, V, n)
+        counts[r] = np.bincount(h, minlength=V)
+        gens[r] = np.minimum(counts[r], np.bincount(h[n // 3:], minlength=V))
+    ks = (1, 50, 1024, 7, 300, 0)
+    pols = []
+    for r in range(B):
+        pol = dict(temperature=float(rng.choice([0.5, 1.0, 1.4])), top_k=ks[r], top_p=float(rng.choice([1.0, 0.9])),
+                   repetition_penalty=float(rng.uniform(0.5, 2)), presence_penalty=float(rng.uniform(-2, 2)),
+                   frequency_penalty=float(rng.uniform(-2, 2)))
+        if ks[r] == 0:
+            pol["temperature"] = 0.0  # greedy over the penalised logits
+        pols.append(pol)
+    allowed = rng.random((B, V)) < 0.9
+    u = rng.random(B)
+    x = torch.from_numpy(np.ascontiguousarray(logits)).to(DEV).to(dtype)
+    res = batch.sample_rows(x, pols, history=batch.HistoryTable.from_dense(counts, gens, device=DEV),
+                            allow_bits=torch.from_numpy(batch.pack_allow(allowed).view(np.int32)).to(DEV),
+                            uniforms=torch.from_numpy(u).to(DEV), probs="f64", kept=True)
+    torch.cuda.synchronize()
+    kept = batch.unpack_bits(res.kept_bits.cpu().numpy().view(np.uint32), V)
+    probs = res.probs.cpu().numpy()
+    flags = res.flags.cpu().numpy()
+    for r in range(B):
+        ref = O.sample_row(logits[r], O.Policy(**pols[r]), float(u[r]), counts[r], gens[r], None, allowed[r])
+        assert int(res.status[r]) == ref.status == 0
+        if not (flags[r] & 1 or ref.margin < MARGIN):
+            assert int(res.tokens[r]) == ref.token and bool(res.consumed[r]) == ref.consumed, r
+        np.testing.assert_array_equal(kept[r], ref.topk_kept)
+        np.testing.assert_allclose(probs[r], ref.probs, rtol=1e-12, atol=1e-300)
+    assert (flags & N.FLAG_SPLIT).all(), flags
+
+
+def test_invalid_history_tables_take_the_general_path():
+    V = 20000
+    rng = np.random.default_rng(33)
+    logits = rng.normal(0, 1, (3, V)).astype(np.float32)
+    d = DEV
+    # Row 0: generated above counts; row 1: counts summing past the limit; row 2: valid.
+    off = torch.tensor([0, 1, 3, 4], device=d)
+    ids = torch.tensor([5, 7, 9, 11], dtype=torch.int32, device=d)
+    cnt = torch.tensor([1, 600_000, 600_000, 2], dtype=torch.int32, device=d)
+    gen = torch.tensor([2, 0, 0, 1], dtype=torch.int32, device=d)
+    h = batch.HistoryTable(off, ids, cnt, gen)
+    pols = [dict(top_k=5)] * 3
+    res = batch.sample_rows(torch.from_numpy(logits).to(d), pols, history=h,
+                            uniforms=torch.tensor([0.5] * 3, dtype=torch.float64, device=d))
+    torch.cuda.synchronize()
+    st = res.status.cpu().numpy()
+    flags = res.flags.cpu().numpy()
+    assert list(st) == [N.E_GENERATED, N.E_COUNTS, 0]
+    assert reason(flags[0]) == 6 and reason(flags[1]) == 6 and flags[2] & N.FLAG_SPLIT
+    c2 = np.zeros(V, np.int32)
+    c2[11] = 2
+    g2 = np.zeros(V, np.int32)
+    g2[11] = 1
+    ref = O.sample_row(logits[2], O.Policy(top_k=5), 0.5, c2, g2)
+    assert int(res.tokens[2]) == ref.token
