@@ -1,6 +1,6 @@
 // Split-row top-k path: rows that the register-resident bf16 paths do not
 // take (float32 / float64 logits, or bf16 rows those paths cannot load), with
-// or without a token history but no bias, that carry a top-k filter
+// or without a token history and a logit bias, that carry a top-k filter
 // (1 <= k <= 1024) or are greedy.
 //
 // One workgroup walking a whole row through the general path's passes uses
@@ -9,8 +9,8 @@
 // row is cut into S contiguous slices, one workgroup each:
 //
 //   k_split_select  reads its slice once (logits, allow bits, the history
-//                   entries that fall in it), validates it, applies the
-//                   penalties, and keeps the slice's k largest values (ranked by value,
+//                   and bias entries that fall in it), validates it, applies
+//                   the penalties and bias, and keeps the slice's k largest values (ranked by value,
 //                   then index) by 11-bit radix passes over registers, in
 //                   index order, at slice s * k of a candidate list in the
 //                   row's workspace.  It also zeroes the slice's probability
@@ -65,7 +65,7 @@ static_assert(kSplitBytes <= (size_t)kSplitMinVocab * 8, "candidate area exceeds
 static_assert((int64_t)kSplitMinSlices * kSplitPer * kThreads >= DSR_MAX_VOCAB, "slices too short for the vocabulary");
 
 static inline bool split_path_eligible(const dsr_sample_args_t& a) {
-  return a.bias_off == nullptr && a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
+  return a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
 }
 
 // Slice budget per row: enough stage-one workgroups to cover the chip.
@@ -117,6 +117,7 @@ __device__ __forceinline__ double next_input_value(double v, int dtype, bool up)
 __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, int smax) {
   __shared__ GenShared sh;
   __shared__ int32_t emap[kSplitPer * kThreads];  // slice position -> history entry, or -1
+  __shared__ uint16_t bmap[kSplitPer * kThreads];  // slice position -> bias entry - first entry, or 0xFFFF
   const int64_t row = blockIdx.x / (unsigned)smax;
   const int s = (int)(blockIdx.x % (unsigned)smax);
   const int64_t V = a.vocab;
@@ -225,6 +226,49 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
           const double pen = pol.presence_penalty * (gg > 0 ? 1.0 : 0.0) + pol.frequency_penalty * (double)gg;
           v[j] = x - pen;
         }
+      }
+    }
+  }
+
+  // Logit bias (sampling.py:69-74), added after the penalties as the general
+  // path does; slice 0 checks the whole sorted list with that path's rules.
+  int64_t bias_n = 0;
+  const int32_t* bid = nullptr;
+  const double* bval = nullptr;
+  if (a.bias_off) {
+    const int64_t o = a.bias_off[row];
+    bias_n = a.bias_off[row + 1] - o;
+    bid = a.bias_ids + o;
+    bval = a.bias_val + o;
+  }
+  if (bias_n > V) {
+    bad = 1;  // more entries than tokens: not a valid list
+  } else if (bias_n > 0) {
+    long long below = 0;
+    int bbad = 0;
+    for (int64_t e = threadIdx.x; e < bias_n; e += kThreads) {
+      const int32_t id = bid[e];
+      below += (id < lo ? 1ll : 0ll) + (id < hi ? (1ll << 32) : 0ll);
+      if (s == 0) {
+        const double b = bval[e];
+        if (id < 0 || id >= V || (e > 0 && bid[e - 1] >= id) || !(b >= -100.0 && b <= 100.0)) bbad = 1;
+      }
+    }
+    below = block_sum_i64(below, sh.b);
+    if (s == 0 && block_or(bbad, sh.b)) bad = 1;
+    const int64_t e0 = below & 0xFFFFFFFFll, e1 = below >> 32;
+    for (int64_t q = threadIdx.x; q < len; q += kThreads) bmap[q] = 0xFFFF;
+    __syncthreads();
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += kThreads) {
+      const int32_t id = bid[e];
+      if (id >= lo && id < hi && e - e0 < 0xFFFF) bmap[id - lo] = (uint16_t)(e - e0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSplitPer; ++j) {
+      if ((valid >> j) & 1u) {
+        const uint16_t q = bmap[t0 + j - lo];
+        if (q != 0xFFFF) v[j] += bval[e0 + q];
       }
     }
   }
@@ -402,8 +446,8 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
         amb = 1;  // not reached: t <= s_k
       } else if (t == sk) {
         eq = 1;
-        // Penalised values are float64, off the input type's grid.
-        const int vt = r.pen_n > 0 ? DSR_F64 : r.dtype;
+        // Penalised or biased values are float64, off the input type's grid.
+        const int vt = (r.pen_n > 0 || r.bias_n > 0) ? DSR_F64 : r.dtype;
         const double dn = next_input_value(v, vt, false), up = next_input_value(v, vt, true);
         if (!(v > -(double)INFINITY && (dn - M) / T < sk && (up - M) / T > sk)) amb = 1;
       }

@@ -230,7 +230,8 @@ def test_device_draws_on_the_split_path():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_rows_with_histories_match_oracle(dtype):
-    """Penalised rows: each slice applies the history entries that fall in it."""
+    """Penalised and biased rows: each slice applies the history and bias
+    entries that fall in it."""
     rng = np.random.default_rng(31 if dtype == torch.float32 else 32)
     B, V = 6, 129280
     logits = rng.normal(0, 2, (B, V))
@@ -252,9 +253,14 @@ def test_rows_with_histories_match_oracle(dtype):
             pol["temperature"] = 0.0  # greedy over the penalised logits
         pols.append(pol)
     allowed = rng.random((B, V)) < 0.9
+    biases = [{int(t): float(rng.uniform(-100, 100)) for t in rng.choice(V, int(rng.integers(1, 40)), replace=False)}
+              for _ in range(B)]
+    biases[0] = {}
+    biases[1][int(np.argmin(logits[1]))] = 100.0  # lifts the row's smallest logit into its top-k
     u = rng.random(B)
     x = torch.from_numpy(np.ascontiguousarray(logits)).to(DEV).to(dtype)
     res = batch.sample_rows(x, pols, history=batch.HistoryTable.from_dense(counts, gens, device=DEV),
+                            bias=batch.BiasTable.from_dicts(biases, device=DEV),
                             allow_bits=torch.from_numpy(batch.pack_allow(allowed).view(np.int32)).to(DEV),
                             uniforms=torch.from_numpy(u).to(DEV), probs="f64", kept=True)
     torch.cuda.synchronize()
@@ -262,7 +268,7 @@ def test_rows_with_histories_match_oracle(dtype):
     probs = res.probs.cpu().numpy()
     flags = res.flags.cpu().numpy()
     for r in range(B):
-        ref = O.sample_row(logits[r], O.Policy(**pols[r]), float(u[r]), counts[r], gens[r], None, allowed[r])
+        ref = O.sample_row(logits[r], O.Policy(**pols[r]), float(u[r]), counts[r], gens[r], biases[r], allowed[r])
         assert int(res.status[r]) == ref.status == 0
         if not (flags[r] & 1 or ref.margin < MARGIN):
             assert int(res.tokens[r]) == ref.token and bool(res.consumed[r]) == ref.consumed, r
@@ -295,4 +301,24 @@ def test_invalid_history_tables_take_the_general_path():
     g2 = np.zeros(V, np.int32)
     g2[11] = 1
     ref = O.sample_row(logits[2], O.Policy(top_k=5), 0.5, c2, g2)
+    assert int(res.tokens[2]) == ref.token
+
+
+def test_invalid_bias_lists_take_the_general_path():
+    V = 20000
+    rng = np.random.default_rng(34)
+    logits = rng.normal(0, 1, (3, V)).astype(np.float32)
+    d = DEV
+    # Row 0: ids out of order; row 1: a bias above 100; row 2: valid.
+    b = batch.BiasTable(torch.tensor([0, 2, 3, 4], device=d), torch.tensor([9, 3, 5, 17], dtype=torch.int32, device=d),
+                        torch.tensor([1.0, 2.0, 150.0, -3.5], dtype=torch.float64, device=d))
+    pols = [dict(top_k=5, temperature=0.8)] * 3
+    res = batch.sample_rows(torch.from_numpy(logits).to(d), pols, bias=b,
+                            uniforms=torch.tensor([0.25] * 3, dtype=torch.float64, device=d))
+    torch.cuda.synchronize()
+    st = res.status.cpu().numpy()
+    flags = res.flags.cpu().numpy()
+    assert list(st) == [N.E_BIAS, N.E_BIAS, 0]
+    assert reason(flags[0]) == 6 and reason(flags[1]) == 6 and flags[2] & N.FLAG_SPLIT
+    ref = O.sample_row(logits[2], O.Policy(**pols[2]), 0.25, None, None, {17: -3.5})
     assert int(res.tokens[2]) == ref.token
