@@ -600,12 +600,14 @@ struct IdentityMap {
 // and the top-k decision (`kth`, `cut` from radix_top_k).  Position j of W is
 // token map(j), positions in token order, so index-order ties and the CDF keep
 // the reference's order.  `vocab` sizes the rounding band of a sum over the
-// whole row.  On DSR_OK, W holds the final probabilities (also written to the
-// optional outputs).
+// whole row.  `s1_row`, when not NaN, is the sum of exp(s) over the whole
+// row (W then holds only part of the row's tokens, and the rest are removed
+// by min-p or top-p).  On DSR_OK, W holds the final probabilities (also
+// written to the optional outputs).
 template <class Map>
 __device__ __forceinline__ int filter_tail(const RowSpec& r, double* W, int64_t n, int64_t vocab, bool topk,
                                            uint64_t kth, int64_t cut, GenShared& sh, unsigned& flags, DistOut& out,
-                                           Map map) {
+                                           Map map, double s1_row = __longlong_as_double(0x7FF8000000000000ll)) {
   const dsr_policy_t& p = r.pol;
   auto ldW = [&](int64_t i) { return W[i]; };
   double acc = 0.0;  // sampling.py:92-93; removed tokens are exp(-inf) = 0
@@ -620,7 +622,8 @@ __device__ __forceinline__ int filter_tail(const RowSpec& r, double* W, int64_t 
     W[i] = e;
     acc += e;
   });
-  const double s1 = block_sum(acc, sh.b);
+  const double s1_own = block_sum(acc, sh.b);
+  const double s1 = s1_row == s1_row ? s1_row : s1_own;
 
   double cur = 0.0;  // sum of what the last pass wrote
   if (p.min_p != 0.0) {  // sampling.py:94-96

@@ -45,6 +45,8 @@ constexpr int kSplitMinSlices = 8;
 constexpr int kSplitTarget = 512;                // stage-one workgroups a launch aims for
 constexpr int64_t kSplitMinVocab = 16384;        // the candidate area must fit the row's workspace
 constexpr int kHandSplit = 7;                    // reason: a slice's last candidate ties the k-th value
+constexpr int kHandMass = 8;                     // reason: top-p / min-p keep tokens beyond the candidates
+constexpr int kSplitNoTopK = 512;                // candidates kept for a row without top-k
 
 constexpr int kSliceBad = 1;     // NaN or +inf in the slice
 constexpr int kSliceFinite = 2;  // a finite value in the slice
@@ -55,6 +57,8 @@ struct SplitSlice {
   long long vmin;  // order key of the smallest kept value, sign bit flipped (so it orders as signed)
   int flags;
   int count;
+  double smax;     // rows without top-k: the slice's largest value (-inf if none is finite)
+  double ssum;     // and the sum of exp((v - smax) / T) over its tokens
 };
 
 // Per-row candidate area, at the start of the row's workspace row.
@@ -78,6 +82,7 @@ struct SplitGeom {
   int k;        // values kept per slice
   int S;        // slices
   int64_t len;  // tokens per slice (a multiple of 64; the last slice may be shorter)
+  bool nok;     // a row without top-k (top-p and / or min-p decide it)
 };
 
 // Both launches derive the same geometry from the policy.  With S <= 8192 / k
@@ -86,9 +91,17 @@ struct SplitGeom {
 __device__ __forceinline__ bool split_geom(const dsr_policy_t& p, int64_t V, int smax, SplitGeom& g) {
   if (!policy_ok(p)) return false;
   int k;
-  if (p.temperature == 0.0) k = 1;  // greedy: only the first maximum matters (sampling.py:82-85)
-  else if (p.top_k >= 1 && p.top_k <= kSplitMaxK && p.top_k < V) k = p.top_k;
-  else return false;
+  g.nok = false;
+  if (p.temperature == 0.0) {
+    k = 1;  // greedy: only the first maximum matters (sampling.py:82-85)
+  } else if (p.top_k >= 1 && p.top_k <= kSplitMaxK && p.top_k < V) {
+    k = p.top_k;
+  } else if ((p.top_k == 0 || p.top_k >= V) && (p.top_p < 1.0 || p.min_p != 0.0)) {
+    k = kSplitNoTopK;  // the row's largest values, if top-p / min-p keep no more
+    g.nok = true;
+  } else {
+    return false;
+  }
   int s = kSplitCap / k;
   if (s > smax) s = smax;
   int64_t len = (V + s - 1) / s;
@@ -272,6 +285,42 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
       }
     }
   }
+  // A row without top-k: the slice's maximum and sum of exp((v - max) / T),
+  // from which the finishing launch forms the row's sum; every finite token
+  // survives top-k, so its kept bit is set here.
+  double vmax = -(double)INFINITY, ssum = 0.0;
+  if (g.nok) {
+    double m = -(double)INFINITY;
+#pragma unroll
+    for (int j = 0; j < kSplitPer; ++j)
+      if (((valid >> j) & 1u) && v[j] > m) m = v[j];
+    vmax = block_max(m, sh.b);
+    double acc = 0.0;
+    if (vmax > -(double)INFINITY) {
+#pragma unroll
+      for (int j = 0; j < kSplitPer; ++j)
+        if (((valid >> j) & 1u) && v[j] > -(double)INFINITY) acc += exp((v[j] - vmax) / pol.temperature);
+    }
+    ssum = block_sum(acc, sh.b);
+    if (a.out_kept_bits) {
+      uint32_t* bits = a.out_kept_bits + row * a.kept_ld;
+      int64_t w = -1;
+      uint32_t mask = 0;
+#pragma unroll
+      for (int j = 0; j < kSplitPer; ++j) {
+        const int64_t i = t0 + j;
+        if (((valid >> j) & 1u) && isfinite(v[j])) {
+          if ((i >> 5) != w) {
+            if (mask) atomicOr(&bits[w], mask);
+            w = i >> 5;
+            mask = 0;
+          }
+          mask |= 1u << (i & 31);
+        }
+      }
+      if (mask) atomicOr(&bits[w], mask);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kSplitPer; ++j) {
     if ((valid >> j) & 1u) fin |= isfinite(v[j]) ? 1 : 0;
@@ -356,6 +405,8 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
   fin = (int)((bf >> 1) & 1);
   if (threadIdx.x == 0) {
     SplitSlice r;
+    r.smax = vmax;
+    r.ssum = ssum;
     r.vmin = mn;
     r.flags = (bad ? kSliceBad : 0) | (fin ? kSliceFinite : 0) | (trunc ? kSliceTrunc : 0) |
               (total != expect ? kSliceOdd : 0);
@@ -425,6 +476,16 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
   if (!(g.k < n)) {  // not reached: S >= 2 gives more than k candidates
     why = kHandSplit;
     return -1;
+  }
+  // A row without top-k: the row's sum of exp(s), from the slices' sums.
+  double s1_row = __longlong_as_double(0x7FF8000000000000ll);
+  if (g.nok) {
+    double term = 0.0;
+    if ((int)threadIdx.x < g.S) {
+      const SplitSlice q = rec[threadIdx.x];
+      if (q.smax > -(double)INFINITY) term = q.ssum * exp((q.smax - M) / T);
+    }
+    s1_row = block_sum(term, sh.b);
   }
   uint64_t kth;
   int64_t cut;
@@ -498,12 +559,32 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
       kz[pos] = z;
       kid[pos] = i;
       ++pos;
-      if (r.kept_bits) atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
+      if (r.kept_bits && !g.nok) atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
     }
   }
   __syncthreads();
   n = nk;
-  return filter_tail(r, kz, nk, r.V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; });
+  if (g.nok) {
+    // Every token outside the candidates has exp(s) <= exp(s_k).  With min-p,
+    // all of them must fall below min_p * max (max(r) = 1 / sum, sampling.py:
+    // 94-96); without it, the candidates' own mass must reach top_p
+    // (sampling.py:97-102).  Both with a margin far above the rounding band.
+    int ok;
+    if (p.min_p != 0.0) {
+      ok = exp(sk) < p.min_p * (1.0 - 0x1p-40);
+    } else {
+      double e = 0.0;
+      for (int64_t j = threadIdx.x; j < nk; j += kThreads) e += exp(kz[j]);
+      const double mass = block_sum(e, sh.b) / s1_row;
+      ok = mass >= p.top_p * (1.0 + 0x1p-40) + 0x1p-50;
+    }
+    if (!ok) {
+      why = kHandMass;
+      return -1;
+    }
+  }
+  return filter_tail(r, kz, nk, r.V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; },
+                     s1_row);
 }
 
 }  // namespace dsr

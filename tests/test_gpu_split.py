@@ -322,3 +322,61 @@ def test_invalid_bias_lists_take_the_general_path():
     assert reason(flags[0]) == 6 and reason(flags[1]) == 6 and flags[2] & N.FLAG_SPLIT
     ref = O.sample_row(logits[2], O.Policy(**pols[2]), 0.25, None, None, {17: -3.5})
     assert int(res.tokens[2]) == ref.token
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_rows_without_top_k(dtype):
+    """Top-p / min-p rows with no top-k: decided from the row's 512 largest
+    values when the kept tokens lie among them (peaked rows), otherwise by the
+    general path (flat rows, reason 8)."""
+    rng = np.random.default_rng(41 if dtype == torch.float32 else 42)
+    B, V = 10, 129280
+    x = rng.normal(0, 1, (B, V))
+    for r in range(B - 2):
+        pos = rng.choice(V, 24, replace=False)
+        x[r, pos] += rng.uniform(8, 15, 24)
+    x[B - 2] = rng.normal(0, 0.1, V)   # flat: top-p keeps most of the row
+    x[B - 1] = rng.normal(0, 0.1, V)
+    logits = x.astype(np.float32) if dtype == torch.float32 else x
+    pols = [dict(temperature=0.7, top_p=0.9), dict(top_p=0.5), dict(temperature=1.3, top_p=0.95, min_p=0.02),
+            dict(min_p=0.05), dict(temperature=0.5, min_p=0.2, top_p=0.99), dict(top_p=0.8, top_k=V),
+            dict(temperature=0.9, top_p=0.0), dict(top_p=0.9, min_p=1.0),
+            dict(top_p=0.95), dict(min_p=0.5)]
+    allowed = rng.random((B, V)) < 0.9
+    u = rng.random(B)
+    res = run(logits, pols, u, allowed, dtype=dtype)
+    flags = check(logits, pols, u, res, allowed)
+    assert (flags[:B - 2] & N.FLAG_SPLIT).all(), flags
+    assert reason(flags[B - 2]) == 8
+
+
+def test_rows_without_top_k_with_history_and_bias():
+    rng = np.random.default_rng(43)
+    B, V = 4, 65536
+    x = rng.normal(0, 1, (B, V))
+    for r in range(B):
+        pos = rng.choice(V, 16, replace=False)
+        x[r, pos] += rng.uniform(14, 18, 16)  # peaked: the 0.9 top-p set lies among the spikes
+    logits = x.astype(np.float32)
+    counts = np.zeros((B, V), np.int32)
+    for r in range(B):
+        counts[r] = np.bincount(rng.integers(0, V, 3000), minlength=V)
+    biases = [{int(t): float(rng.uniform(-5, 5)) for t in rng.choice(V, 20, replace=False)} for _ in range(B)]
+    pols = [dict(top_p=0.9, repetition_penalty=1.2, presence_penalty=0.4, frequency_penalty=0.2)] * B
+    u = rng.random(B)
+    xt = torch.from_numpy(logits).to(DEV)
+    res = batch.sample_rows(xt, pols, history=batch.HistoryTable.from_dense(counts, counts, device=DEV),
+                            bias=batch.BiasTable.from_dicts(biases, device=DEV),
+                            uniforms=torch.from_numpy(u).to(DEV), probs="f64", kept=True)
+    torch.cuda.synchronize()
+    kept = batch.unpack_bits(res.kept_bits.cpu().numpy().view(np.uint32), V)
+    probs = res.probs.cpu().numpy()
+    flags = res.flags.cpu().numpy()
+    for r in range(B):
+        ref = O.sample_row(logits[r], O.Policy(**pols[r]), float(u[r]), counts[r], counts[r], biases[r])
+        assert int(res.status[r]) == ref.status == 0
+        if not (flags[r] & 1 or ref.margin < MARGIN):
+            assert int(res.tokens[r]) == ref.token, r
+        np.testing.assert_array_equal(kept[r], ref.topk_kept)
+        np.testing.assert_allclose(probs[r], ref.probs, rtol=1e-12, atol=1e-300)
+    assert (flags & N.FLAG_SPLIT).all(), flags
