@@ -1,7 +1,9 @@
-// Split-row top-k path: rows that the register-resident bf16 paths do not
-// take (float32 / float64 logits, or bf16 rows those paths cannot load), with
-// or without a token history and a logit bias, that carry a top-k filter
-// (1 <= k <= 1024) or are greedy.
+// Split-row path: rows that the register-resident bf16 paths do not take
+// (float32 / float64 logits, or bf16 rows those paths cannot load), with or
+// without a token history and a logit bias, that carry a top-k filter
+// (1 <= k <= 1024), are greedy, or carry top-p / min-p without top-k (those
+// are decided from the row's 512 largest values when the kept set provably
+// lies among them).
 //
 // One workgroup walking a whole row through the general path's passes uses
 // one CU of 256; a small batch (one fp32 row per call is the reference's own
@@ -17,7 +19,8 @@
 //                   and kept-bit outputs.
 //   k_split_finish  one workgroup per row runs steps 8-13 of
 //                   SamplingPolicy.probabilities (sampling.py:86-106) over
-//                   the <= 8,192 candidates instead of the V tokens, then the
+//                   the <= 8,192 candidates instead of the V tokens (and over
+//                   the <= 1,024 that survive top-k from there on), then the
 //                   categorical draw (sampling.py:108-128).
 //
 // Why the candidates decide the row: s = (v - max) / T is non-decreasing in

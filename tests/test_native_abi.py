@@ -39,6 +39,16 @@ def test_status_messages_match_reference_texts():
     assert "unknown" in N.status_message(999)
 
 
+def test_flag_and_status_constants_match_header():
+    text = open(HEADER).read()
+    defs = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (DSR_\w+) \(?(-?\d+)u?\)?", text)}
+    for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
+                 "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
+                 "E_GENERATED", "E_HISTORY", "E_APPEND", "MAX_APPEND"):
+        assert getattr(N, name) == defs["DSR_" + name], name
+    assert N.ABI_VERSION == defs["DSR_ABI_VERSION"]
+
+
 def test_workspace_queries():
     lib = N.load()
     assert lib.dsr_sample_workspace_bytes(256, 129280) == 256 * 129280 * 8
