@@ -85,16 +85,24 @@ struct SplitGeom {
   int k;        // values kept per slice
   int S;        // slices
   int64_t len;  // tokens per slice (a multiple of 64; the last slice may be shorter)
-  bool nok;     // a row without top-k (top-p and / or min-p decide it)
+  bool nok;     // a row without top-k (top-p and / or min-p decide it, or no filter at all)
+  bool nof;     // a row with no filter at all: no candidates, only the slices' sums
 };
+
+// The row carries neither history entries nor bias entries.
+__device__ __forceinline__ bool row_plain(const dsr_sample_args_t& a, int64_t row) {
+  return (a.pen_off == nullptr || a.pen_off[row + 1] - a.pen_off[row] <= 0) &&
+         (a.bias_off == nullptr || a.bias_off[row + 1] - a.bias_off[row] <= 0);
+}
 
 // Both launches derive the same geometry from the policy.  With S <= 8192 / k
 // the list holds at most 8,192 candidates; each slice holds at least k tokens,
 // so every slice but the last contributes exactly k.
-__device__ __forceinline__ bool split_geom(const dsr_policy_t& p, int64_t V, int smax, SplitGeom& g) {
+__device__ __forceinline__ bool split_geom(const dsr_policy_t& p, int64_t V, int smax, bool plain, SplitGeom& g) {
   if (!policy_ok(p)) return false;
   int k;
   g.nok = false;
+  g.nof = false;
   if (p.temperature == 0.0) {
     k = 1;  // greedy: only the first maximum matters (sampling.py:82-85)
   } else if (p.top_k >= 1 && p.top_k <= kSplitMaxK && p.top_k < V) {
@@ -102,6 +110,10 @@ __device__ __forceinline__ bool split_geom(const dsr_policy_t& p, int64_t V, int
   } else if ((p.top_k == 0 || p.top_k >= V) && (p.top_p < 1.0 || p.min_p != 0.0)) {
     k = kSplitNoTopK;  // the row's largest values, if top-p / min-p keep no more
     g.nok = true;
+  } else if ((p.top_k == 0 || p.top_k >= V) && plain) {
+    k = kSplitNoTopK;  // no filter (the default policy, sampling.py:30-33): slice sums only
+    g.nok = true;
+    g.nof = true;
   } else {
     return false;
   }
@@ -139,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
   const int64_t V = a.vocab;
   const dsr_policy_t pol = a.policy[row];
   SplitGeom g;
-  if (!split_geom(pol, V, smax, g) || s >= g.S) return;
+  if (!split_geom(pol, V, smax, row_plain(a, row), g) || s >= g.S) return;
   const int64_t lo = (int64_t)s * g.len;
   const int64_t hi = lo + g.len < V ? lo + g.len : V;
   const int64_t len = hi - lo;
@@ -330,79 +342,81 @@ __global__ __launch_bounds__(kThreads) void k_split_select(dsr_sample_args_t a, 
     key[j] = order_key(v[j]);
   }
 
-  // Radix selection of the slice's k largest keys.  A pass whose selected bin
-  // is taken whole ends the search; a tie group split by the last pass keeps
-  // its lowest indices.
-  const bool trunc = len > g.k;
-  uint64_t prefix = 0, pmask = 0;
-  long long rem = g.k;
-  bool whole = true;
-  if (trunc) {
-    for (int pass = 0; pass < kRadixPasses; ++pass) {
-      const int shift = radix_shift(pass);
-      const uint64_t dm = radix_mask(pass);
-      for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < kSplitPer; ++j)
-        if (((valid >> j) & 1u) && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dm], 1u);
-      __syncthreads();
-      long long above, cb;
-      const int b = select_from_top(sh.hist, rem, sh, above, sh.hist, cb);
-      if (b < 0) cb = -1;
-      rem -= above;
-      prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
-      pmask |= dm << shift;
-      if (cb == rem) break;
-      if (pass == kRadixPasses - 1) whole = false;
-    }
-  }
-  long long tb = 0;
-  if (trunc && !whole) {
-    int ties = 0;
-#pragma unroll
-    for (int j = 0; j < kSplitPer; ++j) ties += ((valid >> j) & 1u) && key[j] == prefix;
-    long long tt;
-    tb = block_exclusive_scan_i64(ties, sh.b, tt);
-  }
-  unsigned selm = 0;
-  int cnt = 0;
-#pragma unroll
-  for (int j = 0; j < kSplitPer; ++j) {
-    bool sel = (valid >> j) & 1u;
+  // A row with no filter keeps no candidates.
+  const bool trunc = !g.nof && len > g.k;
+  long long total = 0, mn = LLONG_MAX;
+  const long long expect = g.nof ? 0 : (trunc ? g.k : len);
+  if (!g.nof) {
+    // Radix selection of the slice's k largest keys.  A pass whose selected bin
+    // is taken whole ends the search; a tie group split by the last pass keeps
+    // its lowest indices.
+    uint64_t prefix = 0, pmask = 0;
+    long long rem = g.k;
+    bool whole = true;
     if (trunc) {
-      const uint64_t km = key[j] & pmask;
-      if (whole) {
-        sel = sel && km >= prefix;
-      } else {
-        const bool tie = sel && km == prefix;
-        sel = sel && (km > prefix || (tie && tb < rem));
-        tb += tie ? 1 : 0;
+      for (int pass = 0; pass < kRadixPasses; ++pass) {
+        const int shift = radix_shift(pass);
+        const uint64_t dm = radix_mask(pass);
+        for (int b = threadIdx.x; b < kBins; b += kThreads) sh.hist[b] = 0;
+        __syncthreads();
+  #pragma unroll
+        for (int j = 0; j < kSplitPer; ++j)
+          if (((valid >> j) & 1u) && (key[j] & pmask) == prefix) atomicAdd(&sh.hist[(key[j] >> shift) & dm], 1u);
+        __syncthreads();
+        long long above, cb;
+        const int b = select_from_top(sh.hist, rem, sh, above, sh.hist, cb);
+        if (b < 0) cb = -1;
+        rem -= above;
+        prefix |= (uint64_t)(b < 0 ? 0 : b) << shift;
+        pmask |= dm << shift;
+        if (cb == rem) break;
+        if (pass == kRadixPasses - 1) whole = false;
       }
     }
-    if (sel) {
-      selm |= 1u << j;
-      ++cnt;
+    long long tb = 0;
+    if (trunc && !whole) {
+      int ties = 0;
+  #pragma unroll
+      for (int j = 0; j < kSplitPer; ++j) ties += ((valid >> j) & 1u) && key[j] == prefix;
+      long long tt;
+      tb = block_exclusive_scan_i64(ties, sh.b, tt);
     }
-  }
-  long long total;
-  const long long pos = block_exclusive_scan_i64(cnt, sh.b, total);
-  const long long expect = trunc ? g.k : len;
-  long long mn = LLONG_MAX;
-  long long q = pos;
-#pragma unroll
-  for (int j = 0; j < kSplitPer; ++j) {
-    if ((selm >> j) & 1u) {
-      if (q < expect) {
-        Wc[(int64_t)s * g.k + q] = v[j];
-        Ic[(int64_t)s * g.k + q] = (int32_t)(t0 + j);
+    unsigned selm = 0;
+    int cnt = 0;
+  #pragma unroll
+    for (int j = 0; j < kSplitPer; ++j) {
+      bool sel = (valid >> j) & 1u;
+      if (trunc) {
+        const uint64_t km = key[j] & pmask;
+        if (whole) {
+          sel = sel && km >= prefix;
+        } else {
+          const bool tie = sel && km == prefix;
+          sel = sel && (km > prefix || (tie && tb < rem));
+          tb += tie ? 1 : 0;
+        }
       }
-      ++q;
-      const long long sk = (long long)(key[j] ^ 0x8000000000000000ull);
-      mn = sk < mn ? sk : mn;
+      if (sel) {
+        selm |= 1u << j;
+        ++cnt;
+      }
     }
+    const long long pos = block_exclusive_scan_i64(cnt, sh.b, total);
+    long long q = pos;
+  #pragma unroll
+    for (int j = 0; j < kSplitPer; ++j) {
+      if ((selm >> j) & 1u) {
+        if (q < expect) {
+          Wc[(int64_t)s * g.k + q] = v[j];
+          Ic[(int64_t)s * g.k + q] = (int32_t)(t0 + j);
+        }
+        ++q;
+        const long long sk = (long long)(key[j] ^ 0x8000000000000000ull);
+        mn = sk < mn ? sk : mn;
+      }
+    }
+    mn = block_min_i64(mn, sh.b);
   }
-  mn = block_min_i64(mn, sh.b);
   const long long bf = block_reduce((long long)(bad | (fin << 1)), sh.b.i64, 0ll, OpOr());
   bad = (int)(bf & 1);
   fin = (int)((bf >> 1) & 1);
@@ -588,6 +602,107 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
   }
   return filter_tail(r, kz, nk, r.V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; },
                      s1_row);
+}
+
+// A row with no filter (top-k, top-p and min-p all off): the final
+// distribution is exp((v - max) / T) / sum over the whole row (sampling.py:
+// 86-93; the second normalisation, :103-106, divides by a sum that the first
+// made 1 up to rounding).  The row's maximum and sum come from the slices;
+// one pass over the row recomputes each probability from its logit, writes
+// it, and sums per-thread index ranges; the draw then walks one range, as the
+// general path's CDF search does (sampling.py:108-128).  Returns false, with
+// the reason in `why`, when the general path must decide the row.
+template <bool RNG>
+__device__ __forceinline__ bool split_no_filter(const dsr_sample_args_t& a, int64_t row, const RowSpec& r,
+                                                const SplitGeom& g, GenShared& sh, int& why) {
+  const SplitSlice* rec = (const SplitSlice*)((const char*)r.W + kSplitRecOff);
+  const bool mine = (int)threadIdx.x < g.S;
+  const long long f = block_reduce(mine ? (long long)rec[threadIdx.x].flags : 0ll, sh.b.i64, 0ll, OpOr());
+  if ((f & kSliceBad) || !(f & kSliceFinite)) {
+    why = kHandInvalid;
+    return false;
+  }
+  const double T = r.pol.temperature;
+  const double M = block_max(mine ? rec[threadIdx.x].smax : -(double)INFINITY, sh.b);
+  double term = 0.0;
+  if (mine && rec[threadIdx.x].smax > -(double)INFINITY)
+    term = rec[threadIdx.x].ssum * exp((rec[threadIdx.x].smax - M) / T);
+  const double s1 = block_sum(term, sh.b);
+  const int64_t V = r.V;
+  auto pf = [&](int64_t i) -> double {
+    double x = load_logit(r.logits, r.dtype, i);
+    if (r.allow && !((r.allow[i >> 5] >> (i & 31)) & 1u)) x = -(double)INFINITY;
+    return exp((x - M) / T) / s1;
+  };
+  int64_t lo, hi;
+  thread_slice(V, lo, hi);
+  double part = 0.0;
+  long long np = 0, fp = LLONG_MAX;
+  slice_pass<double>(lo, hi, pf, [&](int64_t i, double q) {
+    if (r.probs_f32) r.probs_f32[i] = (float)q;
+    if (r.probs_f64) r.probs_f64[i] = q;
+    part += q;
+    if (q > 0.0) {
+      ++np;
+      if (i < fp) fp = i;
+    }
+  });
+  double total;
+  const double base = block_exclusive_scan_f64(part, sh.b, total);
+  const long long npos = block_sum_i64(np, sh.b);
+  const long long first = block_min_i64(fp, sh.b);
+  if (!(total > 0.0) || !isfinite(total) || npos < 1) {  // not reached: the maximum's exp is 1
+    why = kHandInvalid;
+    return false;
+  }
+  int st = DSR_OK;
+  int64_t token = -1;
+  int consumed = 0;
+  unsigned flags = DSR_FLAG_SPLIT;
+  if (has_draws<RNG>(a)) {
+    if (npos == 1) {
+      token = first;  // sampling.py:120-122: no uniform is drawn
+    } else {
+      uint64_t next[4];
+      const double u = RNG ? pcg64_random(a.rng_state + 4 * row, next) : a.uniforms[row];
+      if (!(u >= 0.0 && u < 1.0)) {
+        st = DSR_E_UNIFORM;
+      } else {
+        const double thr = u * total;
+        const long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
+        const long long owner = block_max_i64(cand, sh.b);
+        if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(base);
+        __syncthreads();
+        if (wave_id() == 0 && owner >= 0) {
+          int64_t olo, ohi;
+          slice_of(owner, V, olo, ohi);
+          const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
+          int64_t tok;
+          int margin;
+          wave_slice_cdf(pf, olo, ohi, __longlong_as_double(sh.bc[0]), thr, tol, tok, margin);
+          if (lane_id() == 0) {
+            sh.bc[1] = tok;
+            sh.bc[2] = margin;
+          }
+        }
+        __syncthreads();
+        token = owner >= 0 ? (int64_t)sh.bc[1] : -1;
+        if (owner < 0 || sh.bc[2]) flags |= DSR_FLAG_MARGIN;
+        consumed = 1;
+      }
+      if (RNG) {
+        __syncthreads();  // every thread has read the state
+        if (threadIdx.x == 0) store_rng(a, row, next);
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.out_token[row] = st == DSR_OK ? (int32_t)token : -1;
+    a.out_consumed[row] = (uint8_t)(st == DSR_OK ? consumed : 0);
+    a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = (uint8_t)flags;
+  }
+  return true;
 }
 
 }  // namespace dsr

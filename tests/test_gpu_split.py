@@ -380,3 +380,48 @@ def test_rows_without_top_k_with_history_and_bias():
         np.testing.assert_array_equal(kept[r], ref.topk_kept)
         np.testing.assert_allclose(probs[r], ref.probs, rtol=1e-12, atol=1e-300)
     assert (flags & N.FLAG_SPLIT).all(), flags
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("V", [129280, 20000])
+def test_rows_without_any_filter(dtype, V):
+    """The default policy (T 1, no top-k / top-p / min-p) and temperature-only
+    rows: the slices' sums and one pass over the row decide them."""
+    rng = np.random.default_rng(V + (51 if dtype == torch.float32 else 52))
+    B = 6
+    logits = rng.normal(0, 2, (B, V))
+    logits[3] = rng.normal(0, 0.01, V)  # nearly flat
+    if dtype == torch.float32:
+        logits = logits.astype(np.float32)
+    pols = [dict(), dict(temperature=0.5), dict(temperature=2.0), dict(), dict(temperature=1e-3), dict(top_k=V)]
+    allowed = rng.random((B, V)) < 0.9
+    allowed[4] = False
+    allowed[4, [17, 18]] = True  # two tokens left
+    u = rng.random(B)
+    res = run(logits, pols, u, allowed, dtype=dtype)
+    flags = check(logits, pols, u, res, allowed)
+    assert (flags & N.FLAG_SPLIT).all(), flags
+
+
+def test_rows_without_any_filter_draw_on_device_and_skip_history_rows():
+    from oracle import pcg64_oracle as P
+    rng = np.random.default_rng(53)
+    B, V = 3, 129280
+    logits = rng.normal(0, 2, (B, V)).astype(np.float32)
+    gens = [np.random.default_rng(200 + r) for r in range(B)]
+    st0 = [g.bit_generator.state["state"] for g in gens]
+    states = batch.pcg64_states(gens, DEV)
+    counts = np.zeros((B, V), np.int32)
+    counts[2, :50] = 1  # row 2 has a history: the general path decides it
+    res = batch.sample_rows(torch.from_numpy(logits).to(DEV), [dict()] * B,
+                            history=batch.HistoryTable.from_dense(counts, counts, device=DEV), rng_state=states)
+    torch.cuda.synchronize()
+    words = states.cpu().numpy().view(np.uint64)
+    flags = res.flags.cpu().numpy()
+    for r in range(B):
+        s_next, u = P.random(st0[r]["state"], st0[r]["inc"])
+        ref = O.sample_row(logits[r], O.Policy(), u, counts[r], counts[r])
+        assert int(res.tokens[r]) == ref.token or flags[r] & 1 or ref.margin < MARGIN
+        assert int(words[r, 0]) | (int(words[r, 1]) << 64) == s_next
+    assert flags[0] & N.FLAG_SPLIT and flags[1] & N.FLAG_SPLIT
+    assert flags[2] & N.FLAG_GENERAL and not flags[2] & N.FLAG_SPLIT
