@@ -607,10 +607,12 @@ __device__ __forceinline__ int split_distribution(const RowSpec& r, const SplitG
 // A row with no filter (top-k, top-p and min-p all off): the final
 // distribution is exp((v - max) / T) / sum over the whole row (sampling.py:
 // 86-93; the second normalisation, :103-106, divides by a sum that the first
-// made 1 up to rounding).  The row's maximum and sum come from the slices;
-// one pass over the row recomputes each probability from its logit, writes
-// it, and sums per-thread index ranges; the draw then walks one range, as the
-// general path's CDF search does (sampling.py:108-128).  Returns false, with
+// made 1 up to rounding).  The row's maximum and sum come from the slices.
+// One coalesced pass over the row recomputes each probability from its logit,
+// writes it, and sums it per wave (each wave owns a contiguous range); the
+// draw finds the wave range that holds u * total, sums that range in
+// contiguous per-thread chunks and walks one chunk, as the general path's CDF
+// search walks its per-thread ranges (sampling.py:108-128).  Returns false, with
 // the reason in `why`, when the general path must decide the row.
 template <bool RNG>
 __device__ __forceinline__ bool split_no_filter(const dsr_sample_args_t& a, int64_t row, const RowSpec& r,
@@ -634,21 +636,38 @@ __device__ __forceinline__ bool split_no_filter(const dsr_sample_args_t& a, int6
     if (r.allow && !((r.allow[i >> 5] >> (i & 31)) & 1u)) x = -(double)INFINITY;
     return exp((x - M) / T) / s1;
   };
-  int64_t lo, hi;
-  thread_slice(V, lo, hi);
+  // Level 1: wave w owns the contiguous range [w*cw, (w+1)*cw), read 64
+  // tokens at a time (coalesced); it writes the probabilities and sums them.
+  const int64_t cw = (V + kWaves - 1) / kWaves;
+  const int64_t wlo = (int64_t)wave_id() * cw < V ? (int64_t)wave_id() * cw : V;
+  const int64_t whi = wlo + cw < V ? wlo + cw : V;
   double part = 0.0;
   long long np = 0, fp = LLONG_MAX;
-  slice_pass<double>(lo, hi, pf, [&](int64_t i, double q) {
-    if (r.probs_f32) r.probs_f32[i] = (float)q;
-    if (r.probs_f64) r.probs_f64[i] = q;
-    part += q;
-    if (q > 0.0) {
-      ++np;
-      if (i < fp) fp = i;
+  for (int64_t b = wlo; b < whi; b += 64 * kUnroll) {
+    double q[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const int64_t i = b + 64 * k + lane_id();
+      q[k] = i < whi ? pf(i) : 0.0;
     }
-  });
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const int64_t i = b + 64 * k + lane_id();
+      if (i < whi) {
+        if (r.probs_f32) r.probs_f32[i] = (float)q[k];
+        if (r.probs_f64) r.probs_f64[i] = q[k];
+        part += q[k];
+        if (q[k] > 0.0) {
+          ++np;
+          if (i < fp) fp = i;
+        }
+      }
+    }
+  }
+  const double wsum = wave_sum(part);
   double total;
-  const double base = block_exclusive_scan_f64(part, sh.b, total);
+  // Wave totals in wave order: each wave's lane 0 contributes its total.
+  const double wbase = block_exclusive_scan_f64(lane_id() == 0 ? wsum : 0.0, sh.b, total);
   const long long npos = block_sum_i64(np, sh.b);
   const long long first = block_min_i64(fp, sh.b);
   if (!(total > 0.0) || !isfinite(total) || npos < 1) {  // not reached: the maximum's exp is 1
@@ -669,25 +688,48 @@ __device__ __forceinline__ bool split_no_filter(const dsr_sample_args_t& a, int6
         st = DSR_E_UNIFORM;
       } else {
         const double thr = u * total;
-        const long long cand = (part > 0.0 && base <= thr) ? (long long)threadIdx.x : -1;
-        const long long owner = block_max_i64(cand, sh.b);
-        if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(base);
+        // The wave whose range holds the crossing: the last with mass whose base is <= thr.
+        const long long wc = (lane_id() == 0 && wsum > 0.0 && wbase <= thr) ? (long long)wave_id() : -1;
+        const long long ow = block_max_i64(wc, sh.b);
+        if (lane_id() == 0 && (long long)wave_id() == ow) sh.bc[3] = __double_as_longlong(wbase);
         __syncthreads();
-        if (wave_id() == 0 && owner >= 0) {
-          int64_t olo, ohi;
-          slice_of(owner, V, olo, ohi);
-          const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
-          int64_t tok;
-          int margin;
-          wave_slice_cdf(pf, olo, ohi, __longlong_as_double(sh.bc[0]), thr, tol, tok, margin);
-          if (lane_id() == 0) {
-            sh.bc[1] = tok;
-            sh.bc[2] = margin;
+        int64_t tok = -1;
+        int margin = 1;
+        if (ow >= 0) {
+          // Level 2: that range in contiguous per-thread chunks, then one walk.
+          const double ob = __longlong_as_double(sh.bc[3]);
+          const int64_t rlo = ow * cw, rhi = rlo + cw < V ? rlo + cw : V;
+          const int64_t ch = (rhi - rlo + kThreads - 1) / kThreads;
+          const int64_t clo = rlo + (int64_t)threadIdx.x * ch < rhi ? rlo + (int64_t)threadIdx.x * ch : rhi;
+          const int64_t chi = clo + ch < rhi ? clo + ch : rhi;
+          double cp = 0.0;
+          slice_pass<double>(clo, chi, pf, [&](int64_t, double q) { cp += q; });
+          double rt;
+          const double cb = ob + block_exclusive_scan_f64(cp, sh.b, rt);
+          const long long cc = (cp > 0.0 && cb <= thr) ? (long long)threadIdx.x : -1;
+          const long long owner = block_max_i64(cc, sh.b);
+          if ((long long)threadIdx.x == owner) sh.bc[0] = __double_as_longlong(cb);
+          __syncthreads();
+          if (wave_id() == 0 && owner >= 0) {
+            const int64_t olo = rlo + owner * ch < rhi ? rlo + owner * ch : rhi;
+            const int64_t ohi = olo + ch < rhi ? olo + ch : rhi;
+            const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
+            int64_t t;
+            int m;
+            wave_slice_cdf(pf, olo, ohi, __longlong_as_double(sh.bc[0]), thr, tol, t, m);
+            if (lane_id() == 0) {
+              sh.bc[1] = t;
+              sh.bc[2] = m;
+            }
+          }
+          __syncthreads();
+          if (owner >= 0) {
+            tok = (int64_t)sh.bc[1];
+            margin = (int)sh.bc[2];
           }
         }
-        __syncthreads();
-        token = owner >= 0 ? (int64_t)sh.bc[1] : -1;
-        if (owner < 0 || sh.bc[2]) flags |= DSR_FLAG_MARGIN;
+        token = tok;
+        if (tok < 0 || margin) flags |= DSR_FLAG_MARGIN;
         consumed = 1;
       }
       if (RNG) {
