@@ -73,8 +73,9 @@ extern "C" {
 #define DSR_FLAG_GENERAL 2u     /* decided by the general (workspace) path; bits 4-7 give
                                    the reason a row left a faster path */
 #define DSR_FLAG_SPLIT 4u       /* decided from per-slice candidates (rows split over several
-                                   workgroups: top-k <= 1024, greedy, or top-p / min-p whose
-                                   kept set lies among the row's 512 largest values) */
+                                   workgroups: top-k <= 1024, greedy, top-p / min-p whose
+                                   kept set lies among the row's 512 largest values, or no
+                                   filter with no history or bias) */
 
 /* Verifier stop reasons (sampling.py:286,289,294). */
 #define DSR_STOP_NONE 0
