@@ -3,7 +3,8 @@
 // without a token history and a logit bias, that carry a top-k filter
 // (1 <= k <= 1024), are greedy, or carry top-p / min-p without top-k (those
 // are decided from the row's 512 largest values when the kept set provably
-// lies among them).
+// lies among them); and rows with no filter at all and no history or bias,
+// decided from the slices' sums (split_no_filter).
 //
 // One workgroup walking a whole row through the general path's passes uses
 // one CU of 256; a small batch (one fp32 row per call is the reference's own
