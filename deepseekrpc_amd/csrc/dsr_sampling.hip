@@ -121,12 +121,13 @@ __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, 
   RowSpec r = sample_row_spec(a, row, W);
   unsigned flags = DSR_FLAG_GENERAL;
   SplitGeom g;
-  if (split_geom(r.pol, a.vocab, smax, row_plain(a, row), g) && g.nof) {
+  const bool split = split_geom(r.pol, a.vocab, smax, row_plain(a, row), g);
+  if (split && g.nof) {
     int why = 0;
     if (split_no_filter<RNG>(a, row, r, g, sh, why)) return;
     __syncthreads();
     flags |= (unsigned)why << 4;
-  } else if (split_geom(r.pol, a.vocab, smax, row_plain(a, row), g)) {
+  } else if (split) {
     unsigned sflags = DSR_FLAG_SPLIT;
     DistOut d;
     int64_t n = 0;
