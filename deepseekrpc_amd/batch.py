@@ -286,15 +286,26 @@ class SampleResult:
 
 
 class Workspace:
-    """Caller-owned scratch for the library (it never allocates)."""
+    """Caller-owned scratch for the library (it never allocates).
+
+    One buffer per (device, stream): calls on different streams never share
+    scratch memory.  A buffer is allocated while its stream is current, so
+    torch's caching allocator orders its reuse after that stream's work when
+    it is replaced by a larger one."""
 
     def __init__(self):
-        self._buf = None
+        self._bufs = {}
 
     def get(self, nbytes: int, device) -> torch.Tensor:
-        if self._buf is None or self._buf.numel() < nbytes or self._buf.device != torch.device(device):
-            self._buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        return self._buf
+        device = torch.device(device)
+        if device.index is None:
+            device = torch.device(device.type, torch.cuda.current_device())
+        stream = torch.cuda.current_stream(device)
+        key = (device.index, stream.cuda_stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = self._bufs[key] = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return buf
 
 
 _default_ws = Workspace()

@@ -19,10 +19,13 @@
 #include "dsr_full.h"
 #include "dsr_general.h"
 #include "dsr_history.h"
+#include "dsr_numpy.h"
 #include "dsr_split.h"
 #include "dsr_verify.h"
 
 namespace dsr {
+
+static_assert(DSR_MAX_VOCAB <= kNpMaxLength, "NumPy-order sums cover at most 16 buffers");
 
 // ---------------------------------------------------------------------------
 // dsr_sample_rows: general path.
@@ -193,20 +196,20 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t
 __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_t n, double* out_sum,
                                                          int32_t* out) {
   __shared__ GenShared sh;
-  double acc = 0.0;
+  __shared__ NpSumShared np;
   int bad = 0;
   long long npos = 0, first = LLONG_MAX;
   RowMax mx;
   row_pass<double>(n, [&](int64_t i) { return p[i]; }, [&](int64_t i, double x) {
     if (!isfinite(x) || x < 0.0) bad = 1;
-    acc += x;
     if (x > 0.0) {
       ++npos;
       if (i < first) first = i;
     }
     mx.add(i, x);
   });
-  const double s = block_sum(acc, sh.b);
+  // The sum the reference tests against 1 +- 1e-10 (sampling.py:111-113), in NumPy's order.
+  const double s = np_sum([&](int64_t i) { return p[i]; }, n, np);
   bad = block_or(bad, sh.b);
   npos = block_sum_i64(npos, sh.b);
   first = block_min_i64(first, sh.b);
@@ -221,12 +224,28 @@ __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_
   }
 }
 
+// First i with c_i / c_last > u for the sequential running sum c of p
+// (np.cumsum, then searchsorted "right"; sampling.py:126-128), by one lane.
+__device__ int64_t sequential_cdf_search(const double* p, int64_t n, double u) {
+  double last = 0.0;
+  for (int64_t i = 0; i < n; ++i) last += p[i];
+  double c = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    c += p[i];
+    if (c / last > u) return i;
+  }
+  return n - 1;  // not reached: c_last / c_last = 1 > u
+}
+
 __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, int64_t n, double u, int32_t* out) {
   __shared__ GenShared sh;
   long long npos, first;
   positive_support(p, n, sh, npos, first);
   unsigned flags = 0;
   int64_t tok = cdf_search(p, n, u, npos, sh, flags);
+  // The workgroup scan sums in another order than np.cumsum; where u sits
+  // within that rounding band of a cell edge the sequential sum decides.
+  if ((flags & DSR_FLAG_MARGIN) && threadIdx.x == 0) tok = sequential_cdf_search(p, n, u);
   if (threadIdx.x == 0) {
     out[0] = (int32_t)tok;
     out[1] = (int32_t)flags;
@@ -235,14 +254,12 @@ __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, 
 
 __global__ __launch_bounds__(kThreads) void k_prob_correction(const double* p, const double* q, int64_t n,
                                                               double* out, int32_t* st) {
-  __shared__ GenShared sh;
-  double acc = 0.0;
-  row_pass<ProbPair>(n, [&](int64_t i) { return ProbPair{p[i], q[i]}; }, [&](int64_t i, ProbPair v) {
-    const double r = fmax(v.p - v.q, 0.0);
-    out[i] = r;
-    acc += r;
-  });
-  const double total = block_sum(acc, sh.b);
+  __shared__ NpSumShared np;
+  row_pass<ProbPair>(n, [&](int64_t i) { return ProbPair{p[i], q[i]}; },
+                     [&](int64_t i, ProbPair v) { out[i] = fmax(v.p - v.q, 0.0); });
+  __syncthreads();  // the residual is read back across threads (global memory, one workgroup)
+  // residual.sum() in NumPy's order, then residual / total (sampling.py:134-139).
+  const double total = np_sum([&](int64_t i) { return out[i]; }, n, np);
   const bool ok = total > 0.0 && isfinite(total);
   if (ok) row_pass<double>(n, [&](int64_t i) { return out[i]; }, [&](int64_t i, double x) { out[i] = x / total; });
   if (threadIdx.x == 0) st[0] = ok ? DSR_OK : DSR_E_CORRECTION;

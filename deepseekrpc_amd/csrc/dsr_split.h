@@ -72,10 +72,6 @@ constexpr size_t kSplitBytes = kSplitRecOff + (size_t)kSplitMaxSlices * sizeof(S
 static_assert(kSplitBytes <= (size_t)kSplitMinVocab * 8, "candidate area exceeds the smallest workspace row");
 static_assert((int64_t)kSplitMinSlices * kSplitPer * kThreads >= DSR_MAX_VOCAB, "slices too short for the vocabulary");
 
-static inline bool split_path_eligible(const dsr_sample_args_t& a) {
-  return a.vocab >= kSplitMinVocab && a.rows <= (1 << 22);
-}
-
 // Slice budget per row.  More slices shorten the first launch but lengthen
 // the finishing workgroup's passes over S * k candidates; for a one-row call
 // with k = 50 (V = 129,280) 32 slices measured fastest (43.8 us, against 48.2
@@ -83,6 +79,13 @@ static inline bool split_path_eligible(const dsr_sample_args_t& a) {
 static inline int split_max_slices(int64_t rows) {
   const int64_t s = kSplitTarget / (rows > 0 ? rows : 1);
   return (int)(s < kSplitMinSlices ? kSplitMinSlices : (s > kSplitMaxSlices ? kSplitMaxSlices : s));
+}
+
+// The first launch's grid (rows x slices workgroups of kThreads) must stay
+// below 2^32 work-items; larger batches take the general path.
+static inline bool split_path_eligible(const dsr_sample_args_t& a) {
+  return a.vocab >= kSplitMinVocab && a.rows > 0 &&
+         a.rows * (int64_t)split_max_slices(a.rows) * kThreads < ((int64_t)1 << 32);
 }
 
 struct SplitGeom {

@@ -102,32 +102,44 @@ class SamplingPolicy:
             table = _history_table(counts, generated_counts, n)
         elif generated_counts is not None:
             raise ValidationError("generated counts require complete repetition-penalty history")
-        return self._probabilities_with(logits, n, device_input, table, logit_bias, allowed)
-
-    def _probabilities_with(self, logits, n, device_input, table, logit_bias, allowed):
-        """The rest of probabilities, with the history already a device table."""
-        bias = None
-        if logit_bias is not None:
-            if not isinstance(logit_bias, dict) or len(logit_bias) > n:
-                raise ValidationError("invalid logit bias mapping")
-            checked = {}
-            for token, value in logit_bias.items():
-                integer(token, "biased token", 0, n - 1)
-                checked[token] = _real(value, "logit bias", -100, 100)
-            bias = batch.BiasTable.from_dicts([checked], device=_device())
-        allow = None
-        if allowed is not None:
-            mask = np.asarray(allowed.cpu() if isinstance(allowed, torch.Tensor) else allowed)
-            if mask.shape != (n,) or mask.dtype != np.bool_:
-                raise ValidationError("sampling grammar/token mask does not match the vocabulary")
-            allow = torch.from_numpy(batch.pack_allow(mask[None]).astype(np.int32)).to(_device())
-        x, _ = _on_device(logits)
-        res = batch.sample_rows(x.reshape(1, n), [self], history=table, bias=bias, allow_bits=allow, probs="f64")
+        res = self._launch_row(logits, n, table, _bias_table(logit_bias, n), _allow_row(allowed, n))
         status = int(res.status.item())
         if status != N.OK:
             _raise_status(status)
         out = res.probs[0]
         return out if device_input else out.cpu().numpy()
+
+    def _launch_row(self, logits, n, table, bias, allow, uniform=None):
+        """One ``dsr_sample_rows`` launch over a single validated row: its
+        float64 probabilities, and with a pre-drawn ``uniform`` (a float64
+        device tensor of one element) also its categorical draw and whether
+        the draw consumed the uniform.  Nothing is synchronised."""
+        x, _ = _on_device(logits)
+        return batch.sample_rows(x.reshape(1, n), [self], history=table, bias=bias, allow_bits=allow,
+                                 uniforms=uniform, probs="f64")
+
+
+def _bias_table(logit_bias, n):
+    """A validated logit-bias mapping as a one-row device table (sampling.py:69-74)."""
+    if logit_bias is None:
+        return None
+    if not isinstance(logit_bias, dict) or len(logit_bias) > n:
+        raise ValidationError("invalid logit bias mapping")
+    checked = {}
+    for token, value in logit_bias.items():
+        integer(token, "biased token", 0, n - 1)
+        checked[token] = _real(value, "logit bias", -100, 100)
+    return batch.BiasTable.from_dicts([checked], device=_device())
+
+
+def _allow_row(allowed, n):
+    """A validated boolean token mask as one packed device row of allow bits (sampling.py:75-79)."""
+    if allowed is None:
+        return None
+    mask = np.asarray(allowed.cpu() if isinstance(allowed, torch.Tensor) else allowed)
+    if mask.shape != (n,) or mask.dtype != np.bool_:
+        raise ValidationError("sampling grammar/token mask does not match the vocabulary")
+    return torch.from_numpy(batch.pack_allow(mask[None]).astype(np.int32)).to(_device())
 
 
 def _logit_vector(logits):
@@ -323,6 +335,16 @@ class RandomTransaction:
             raise ValidationError("terminal RNG domain is closed, invalid or exceeds its bounded window")
         self.draws[domain] += 1
         return float(self.owner._streams[domain].random())
+
+    def _preview(self, domain):
+        """The value the next ``random(domain)`` will return, read from a copy
+        of the domain's generator: the live stream does not move.  A kernel
+        takes it pre-drawn and ``random(domain)`` is called only if the kernel
+        reports the draw consumed, so the stream advances exactly as a lazy
+        ``uniform()`` callback would advance it."""
+        copy = np.random.Generator(np.random.PCG64(0))
+        copy.bit_generator.state = self.owner._streams[domain].bit_generator.state
+        return float(copy.random())
 
     def commit(self):
         if self.closed:

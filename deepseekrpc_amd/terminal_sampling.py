@@ -1,38 +1,68 @@
-"""Drop-in replacement of the reference's terminal sampling transaction.
+"""Terminal sampling transactions whose rows never leave the GPU.
 
-Same classes and behaviour as src/deepseekrpc/terminal_sampling.py:
-``TerminalSampler`` (:48-106), ``SamplingWork`` (:109-231), ``SeedDecision``
-(:30-45) and the lazy ``_ConditionalTargets`` (:234-244).  The difference is
-where the rows live: the reference copies every FP32 logit row to the host
-(``_logits_cpu``, :16-27); here logits stay on the GPU and every
-distribution, draw and verification runs through the HIP library.  Host
-logic (counts bookkeeping, the RNG transaction, grammar callbacks, digests)
-is unchanged.
+Public surface of the reference's src/deepseekrpc/terminal_sampling.py:
+``TerminalSampler`` (begin_seed / begin_verification, :48-106),
+``SamplingWork`` (distribution / propose / use_normal_decode / verify /
+prepared / apply_stop / commit / abort, :109-231) and ``SeedDecision``
+(:30-45), with the same validation order, messages, RNG consumption and
+decision digest.
+
+How it is built here:
+
+* ``_Controls`` is the transaction's frozen input record.  ``_check_controls``
+  validates it once, in the reference's order, and the counts become one
+  device history table when the first row needs them.
+* A ``SamplingWork`` walks a small stage machine (``_Stage``): seeded, awaiting
+  proposals, proposed, decided.  Every guard reads the stage, and the
+  reference's error messages name the guard that fails.
+* Every draw (the seed, each proposal) is one fused ``dsr_sample_rows`` launch
+  on the current stream: the row's float64 distribution and its categorical
+  draw together.  The uniform is the domain's next value, read from a copy of
+  the generator (``RandomTransaction._preview``); the live domain advances
+  only when the kernel reports the draw consumed.  That is the draw sequence
+  of the reference's lazy ``uniform()`` callback, with one host round trip
+  per row in place of a device-to-host copy of the row and three passes over
+  it.
+* Proposal distributions stay on the device for the verifier, and target
+  rows are conditioned on the accepted prefix when the verifier first asks
+  for them (``_LazyRows``).
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import asdict, dataclass, replace
+import enum
 import hashlib
 
 import numpy as np
 import torch
 
+from . import _native as N
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
-from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _history_table, _logit_vector, _on_device,
-                       _raise_status, categorical, verify_drafts)
+from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _history_table,
+                       _logit_vector, _on_device, _raise_status, verify_drafts)
+
+_HISTORY_LIMIT = 1048576
+_MAX_PROPOSALS = 5
+
+_MSG_WINDOW = "terminal logits do not match the complete bounded vocabulary window"
+_MSG_HEAD = "terminal logits must come from the actual FP32 CUDA vocabulary head"
 
 
 def _logits_device(logits, rows, vocabulary):
-    """A bounded logit window on the GPU: ``[rows, vocabulary]`` FP32, all finite."""
+    """``[rows, vocabulary]`` FP32 finite logits as a device tensor.
+
+    The reference copies CUDA rows to the host here (terminal_sampling.py:16-27);
+    they stay on the device instead, and NumPy windows are uploaded.  The
+    same inputs are rejected with the same messages."""
     if isinstance(logits, np.ndarray):
         if logits.dtype != np.float32 or logits.shape != (rows, vocabulary) or not np.isfinite(logits).all():
-            raise ValidationError("terminal logits do not match the complete bounded vocabulary window")
-        result, _ = _on_device(logits)
-        return result
-    if not isinstance(logits, torch.Tensor) or not logits.is_cuda or logits.dtype != torch.float32:
-        raise ValidationError("terminal logits must come from the actual FP32 CUDA vocabulary head")
+            raise ValidationError(_MSG_WINDOW)
+        return _on_device(logits)[0]
+    if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32):
+        raise ValidationError(_MSG_HEAD)
     if tuple(logits.shape) != (rows, vocabulary) or not bool(torch.isfinite(logits).all()):
-        raise ValidationError("terminal logits do not match the complete bounded vocabulary window")
+        raise ValidationError(_MSG_WINDOW)
     return logits.detach().contiguous()
 
 
@@ -51,220 +81,328 @@ class SeedDecision:
 
     @property
     def accepted_target_rows(self):
+        # A seed decision consumed no verification row.
         return 0
 
 
+@dataclass(frozen=True)
+class _Controls:
+    """The frozen inputs of one transaction (copies: callers cannot mutate them)."""
+    policy: SamplingPolicy
+    counts: np.ndarray
+    generated: np.ndarray
+    remaining: int
+    eos_ids: frozenset
+    logit_bias: dict | None
+    allowed: object
+    grammar_identity: str | None
+    stop_identity: str | None
+
+
+def _valid_count_vector(values, vocabulary):
+    return (values.shape == (vocabulary,) and values.dtype in (np.int32, np.int64) and not (values < 0).any())
+
+
+def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_counts, logit_bias, allowed,
+                    grammar_identity, stop_identity) -> _Controls:
+    """Validation of terminal_sampling.py:54-81, in its order and with its messages."""
+    integer(remaining, "remaining output capacity", 1, _HISTORY_LIMIT)
+    if sampler.active is not None or not isinstance(policy, SamplingPolicy):
+        raise ValidationError("terminal sampling is active or its policy is invalid")
+    counts = np.asarray(counts)
+    if not _valid_count_vector(counts, sampler.vocabulary) or counts.sum(dtype=np.int64) > _HISTORY_LIMIT:
+        raise ValidationError("terminal counts differ from the exact published token history")
+    for token in eos_ids:
+        integer(token, "terminal EOS token", 0, sampler.vocabulary - 1)
+    if allowed is not None and not callable(allowed):
+        raise ValidationError("grammar mask provider must evaluate a bounded tentative token prefix")
+    if (allowed is None) != (grammar_identity is None):
+        raise ValidationError("a grammar mask requires its frozen grammar/prefix identity")
+    for identity, what in ((grammar_identity, "frozen grammar and committed-prefix identity"),
+                           (stop_identity, "frozen original detokenizer and stop-prefix identity")):
+        if identity is not None:
+            hex_id(identity, 64, what)
+    generated = counts if generated_counts is None else np.asarray(generated_counts)
+    if (generated.shape != counts.shape or not _valid_count_vector(generated, sampler.vocabulary)
+            or (generated > counts).any()):
+        raise ValidationError("generated sampling counts must be a subset of the complete history")
+    return _Controls(policy, counts.copy(), generated.copy(), remaining, frozenset(eos_ids),
+                     None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity)
+
+
 class TerminalSampler:
+    """Owns the three RNG domains and at most one open ``SamplingWork``."""
+
     def __init__(self, seed, *, vocabulary=129280):
         self.random = RandomStreams(seed)
         self.vocabulary = integer(vocabulary, "sampling vocabulary", 1, 129280)
         self.active = None
 
-    def _begin(self, policy, counts, remaining, eos_ids, *, generated_counts, logit_bias, allowed, grammar_identity,
-               stop_identity):
-        integer(remaining, "remaining output capacity", 1, 1048576)
-        if self.active is not None or not isinstance(policy, SamplingPolicy):
-            raise ValidationError("terminal sampling is active or its policy is invalid")
-        counts = np.asarray(counts)
-        if (counts.shape != (self.vocabulary,) or counts.dtype not in (np.int32, np.int64) or (counts < 0).any()
-                or counts.sum(dtype=np.int64) > 1048576):
-            raise ValidationError("terminal counts differ from the exact published token history")
-        for token in eos_ids:
-            integer(token, "terminal EOS token", 0, self.vocabulary - 1)
-        if allowed is not None and not callable(allowed):
-            raise ValidationError("grammar mask provider must evaluate a bounded tentative token prefix")
-        if (allowed is None) != (grammar_identity is None):
-            raise ValidationError("a grammar mask requires its frozen grammar/prefix identity")
-        if grammar_identity is not None:
-            hex_id(grammar_identity, 64, "frozen grammar and committed-prefix identity")
-        if stop_identity is not None:
-            hex_id(stop_identity, 64, "frozen original detokenizer and stop-prefix identity")
-        generated = counts if generated_counts is None else np.asarray(generated_counts)
-        if (generated.shape != counts.shape or generated.dtype not in (np.int32, np.int64) or (generated < 0).any()
-                or (generated > counts).any()):
-            raise ValidationError("generated sampling counts must be a subset of the complete history")
-        # The caller cannot mutate the controls of a running transaction.
-        bias = None if logit_bias is None else dict(logit_bias)
-        work = SamplingWork(self, self.random.begin(), policy, counts.copy(), generated.copy(), remaining,
-                            frozenset(eos_ids), bias, allowed, grammar_identity, stop_identity)
+    def _open_work(self, stage, *controls):
+        checked = _check_controls(self, *controls)   # nothing starts unless every control is valid
+        work = SamplingWork(self, self.random.begin(), checked, stage)
         self.active = work
         return work
 
     def begin_seed(self, logits, *, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
                    logit_bias=None, allowed=None, grammar_identity=None, stop_identity=None):
-        work = self._begin(policy, counts, remaining, eos_ids, generated_counts=generated_counts, logit_bias=logit_bias,
-                           allowed=allowed, grammar_identity=grammar_identity, stop_identity=stop_identity)
-        try:
-            values = _logits_device(logits, 1, self.vocabulary)[0]
-            distribution = work.distribution(values, ())
-            token = categorical(distribution, lambda: work.transaction.random("target"))
-            work.decision = SeedDecision(token, "eos" if token in work.eos_ids else "length" if remaining == 1 else None)
-            return work
-        except BaseException:
-            work.abort()
-            raise
+        """Sample the first token of a request from one row of target logits."""
+        work = self._open_work(_Stage.SEEDING, policy, counts, remaining, eos_ids, generated_counts, logit_bias,
+                               allowed, grammar_identity, stop_identity)
+        with work._aborting_on_error():
+            row = _logits_device(logits, 1, self.vocabulary)[0]
+            token, _ = work._draw(row, (), "target")
+            stop = "eos" if token in work.eos_ids else "length" if remaining == 1 else None
+            work._decide(SeedDecision(token, stop))
+        return work
 
     def begin_verification(self, *, seed_token, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
                            logit_bias=None, allowed=None, grammar_identity=None, stop_identity=None):
+        """Open a speculative step after ``seed_token``, which must already be in the history."""
         integer(seed_token, "pending verification seed", 0, self.vocabulary - 1)
-        work = self._begin(policy, counts, remaining, eos_ids, generated_counts=generated_counts, logit_bias=logit_bias,
-                           allowed=allowed, grammar_identity=grammar_identity, stop_identity=stop_identity)
-        if work.counts[seed_token] < 1 or work.generated_counts[seed_token] < 1:
+        work = self._open_work(_Stage.AWAITING_PROPOSALS, policy, counts, remaining, eos_ids, generated_counts,
+                               logit_bias, allowed, grammar_identity, stop_identity)
+        if min(work.counts[seed_token], work.generated_counts[seed_token]) < 1:
             work.abort()
             raise ValidationError("pending seed must already belong to published sampling history")
         work.seed_token = seed_token
         return work
 
 
-class SamplingWork:
-    def __init__(self, owner, transaction, policy, counts, generated_counts, remaining, eos_ids, logit_bias, allowed,
-                 grammar_identity, stop_identity):
-        self.owner, self.transaction, self.policy = owner, transaction, policy
-        self.counts, self.remaining, self.eos_ids = counts, remaining, eos_ids
-        self.generated_counts = generated_counts
-        self.logit_bias, self.allowed = logit_bias, allowed
-        self.grammar_identity = grammar_identity
-        self.stop_identity = stop_identity
-        self._stop_checked = stop_identity is None
-        self.seed_token = None
-        self.proposal_ids, self.proposal_rows = [], []
-        self.decision, self.closed = None, False
-        self._proposal_ready = False
-        self._table = None  # device history table of counts / generated_counts, built on first use
+class _Stage(enum.Enum):
+    SEEDING = "seeding"                        # begin_seed: decided when the seed is drawn
+    AWAITING_PROPOSALS = "awaiting proposals"  # begin_verification: propose or use_normal_decode next
+    PROPOSED = "proposed"                      # verify next
+    DECIDED = "decided"                        # apply_stop (if a stop identity is frozen), prepared, commit
 
-    def _open(self):
+
+class _LazyRows:
+    """A sequence whose items are built on first access and kept."""
+
+    def __init__(self, count, build):
+        self._slots = [None] * count
+        self._build = build
+
+    def __len__(self):
+        return len(self._slots)
+
+    def __getitem__(self, index):
+        item = self._slots[index]
+        if item is None:
+            item = self._slots[index] = self._build(index)
+        return item
+
+
+class SamplingWork:
+    """One open sampling transaction of a ``TerminalSampler``."""
+
+    def __init__(self, owner, transaction, controls: _Controls, stage: _Stage):
+        self.owner, self.transaction, self._controls = owner, transaction, controls
+        self._stage = stage
+        self._stop_pending = controls.stop_identity is not None
+        self.closed = False
+        self.seed_token = None
+        self.decision = None
+        self.proposal_ids, self.proposal_rows = [], []
+        self._device_history = None   # the counts as a device table, built for the first row
+
+    # -- the frozen controls, under the reference's attribute names --------
+    policy = property(lambda self: self._controls.policy)
+    counts = property(lambda self: self._controls.counts)
+    generated_counts = property(lambda self: self._controls.generated)
+    remaining = property(lambda self: self._controls.remaining)
+    eos_ids = property(lambda self: self._controls.eos_ids)
+    logit_bias = property(lambda self: self._controls.logit_bias)
+    allowed = property(lambda self: self._controls.allowed)
+    grammar_identity = property(lambda self: self._controls.grammar_identity)
+    stop_identity = property(lambda self: self._controls.stop_identity)
+
+    @property
+    def _proposal_ready(self):
+        return self._stage in (_Stage.PROPOSED, _Stage.DECIDED)
+
+    @_proposal_ready.setter
+    def _proposal_ready(self, ready):
+        # Callers that supply proposals themselves mark them complete this way.
+        if ready and self._stage is _Stage.AWAITING_PROPOSALS:
+            self._stage = _Stage.PROPOSED
+
+    # -- guards -------------------------------------------------------------
+    def _require_open(self):
         if self.closed or self.owner.active is not self:
             raise ValidationError("terminal sampling transaction is closed or stale")
 
-    def distribution(self, logits, prefix):
-        """Device distribution of one row conditioned on a tentative prefix
-        (terminal_sampling.py:127-136): the transaction's counts live in one
-        device history table, and each prefix token is appended to it on the
-        device (one more count and generated count each) instead of copying
-        and updating the dense vectors on the host."""
-        self._open()
-        n, device_input = _logit_vector(logits)
-        if n != len(self.counts):
-            raise ValidationError(_COUNTS_MSG)
-        table = self._history(prefix)
-        mask = None if self.allowed is None else self.allowed(tuple(prefix))
-        return self.policy._probabilities_with(logits, n, device_input, table, self.logit_bias, mask)
+    def _require_stage(self, stage, message):
+        self._require_open()
+        if self._stage is not stage:
+            raise ValidationError(message)
 
+    @contextmanager
+    def _aborting_on_error(self):
+        """A failing step ends the transaction and restores every RNG domain."""
+        try:
+            yield
+        except BaseException:
+            self.abort()
+            raise
+
+    def _decide(self, decision):
+        self.decision = decision
+        self._stage = _Stage.DECIDED
+
+    # -- rows -----------------------------------------------------------------
     def _history(self, prefix):
-        if self._table is None:
-            self._table = _history_table(self.counts, self.generated_counts, len(self.counts))
+        """The device history table with each prefix token counted once more,
+        as generated output (terminal_sampling.py:127-133)."""
+        if self._device_history is None:
+            self._device_history = _history_table(self.counts, self.generated_counts, len(self.counts))
         if not prefix:
-            return self._table
-        dev = self._table.offsets.device
-        tokens = torch.tensor([int(t) for t in prefix], dtype=torch.int32, device=dev)
-        off = torch.tensor([0, len(prefix)], dtype=torch.int64, device=dev)
-        table, status = self._table.append(tokens, off, vocab=len(self.counts))
-        if int(status.item()) != 0:
-            _raise_status(int(status.item()))
+            return self._device_history
+        dev = self._device_history.offsets.device
+        tokens = torch.tensor(list(prefix), dtype=torch.int32, device=dev)
+        bounds = torch.tensor([0, len(prefix)], dtype=torch.int64, device=dev)
+        table, status = self._device_history.append(tokens, bounds, vocab=len(self.counts))
+        code = int(status.item())
+        if code != N.OK:
+            _raise_status(code)
         return table
 
+    def _row_launch(self, logits, prefix, uniform=None):
+        """Validate one row and launch its distribution (and draw, given a
+        uniform).  The grammar is asked for its mask first, then the row and
+        controls are checked in the order of sampling.py:50-79."""
+        mask = None if self.allowed is None else self.allowed(tuple(prefix))
+        size, device_input = _logit_vector(logits)
+        if size != len(self.counts):
+            raise ValidationError(_COUNTS_MSG)
+        table = self._history(prefix)
+        bias = _bias_table(self.logit_bias, size)
+        allow = _allow_row(mask, size)
+        return self.policy._launch_row(logits, size, table, bias, allow, uniform), device_input
+
+    def distribution(self, logits, prefix):
+        """Float64 distribution of one row given a tentative accepted prefix
+        (terminal_sampling.py:127-136); device rows in, device rows out."""
+        self._require_open()
+        result, device_input = self._row_launch(logits, prefix)
+        code = int(result.status.item())
+        if code != N.OK:
+            _raise_status(code)
+        row = result.probs[0]
+        return row if device_input else row.cpu().numpy()
+
+    def _draw(self, logits, prefix, domain):
+        """(token, distribution): one fused launch draws from the row's
+        distribution with the domain's next uniform; the domain advances
+        only if the kernel consumed it."""
+        self._require_open()
+        upcoming = self.transaction._preview(domain)
+        uniform = torch.tensor([upcoming], dtype=torch.float64, device=logits.device)
+        result, _ = self._row_launch(logits, prefix, uniform)
+        token, consumed, code = torch.stack(
+            [result.tokens.long(), result.consumed.long(), result.status.long()]).view(-1).tolist()
+        if code != N.OK:
+            _raise_status(code)
+        if consumed and self.transaction.random(domain) != upcoming:
+            raise RuntimeError("RNG domain moved between the preview and the draw")
+        return token, result.probs[0]
+
+    # -- the transaction's steps ------------------------------------------------
     def propose(self, graph, result):
-        """Sequential Markov-conditioned proposals over the five-row draft graph."""
-        self._open()
-        if self.seed_token is None or self._proposal_ready or self.decision is not None:
-            raise ValidationError("proposal generation is duplicate or lacks a committed pending seed")
-        try:
+        """Up to five draft tokens, each row conditioned on the previous token
+        by the graph (terminal_sampling.py:138-161); an EOS ends the chain."""
+        self._require_stage(_Stage.AWAITING_PROPOSALS,
+                            "proposal generation is duplicate or lacks a committed pending seed")
+        with self._aborting_on_error():
             previous = self.seed_token
-            for row in range(min(5, self.remaining)):
-                # The graph applies the conditional Markov bias; its confidence never prunes.
-                logits, _confidence = graph.draft_conditional_logits(result, row, previous)
-                values = _logits_device(logits, 1, self.owner.vocabulary)[0]
-                distribution = self.distribution(values, self.proposal_ids)
-                token = categorical(distribution, lambda: self.transaction.random("draft"))
-                self.proposal_rows.append(distribution)
-                self.proposal_ids.append(token)
-                previous = token
-                if token in self.eos_ids:
+            for position in range(min(_MAX_PROPOSALS, self.remaining)):
+                # The graph's confidence output is diagnostic only.
+                logits, _ = graph.draft_conditional_logits(result, position, previous)
+                row = _logits_device(logits, 1, self.owner.vocabulary)[0]
+                previous, dist = self._draw(row, tuple(self.proposal_ids), "draft")
+                self.proposal_ids.append(previous)
+                self.proposal_rows.append(dist)
+                if previous in self.eos_ids:
                     break
-            self._proposal_ready = True
-            return tuple(self.proposal_ids)
-        except BaseException:
-            self.abort()
-            raise
+            self._stage = _Stage.PROPOSED
+        return tuple(self.proposal_ids)
 
     def use_normal_decode(self):
-        """Explicit no-proposal path, including the end of context."""
-        self._open()
-        if self.seed_token is None or self._proposal_ready:
-            raise ValidationError("normal decode is duplicate or lacks its pending seed")
-        self._proposal_ready = True
+        """Verify with no proposals: the target row's draw is the bonus token."""
+        self._require_stage(_Stage.AWAITING_PROPOSALS, "normal decode is duplicate or lacks its pending seed")
+        self._stage = _Stage.PROPOSED
 
     def verify(self, target_logits):
-        self._open()
-        if self.seed_token is None or not self._proposal_ready or self.decision is not None:
-            raise ValidationError("target verification is duplicate or proposals are not complete")
-        try:
-            values = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
-            targets = _ConditionalTargets(self, values)
-            self.decision = verify_drafts(targets, self.proposal_rows, self.proposal_ids, self.transaction,
-                                          greedy=self.policy.temperature == 0, output_limit=self.remaining,
-                                          eos_ids=self.eos_ids)
-            return self.decision
-        except BaseException:
-            self.abort()
-            raise
+        """Exact sampled verification of the proposals against ``K + 1`` target rows."""
+        self._require_stage(_Stage.PROPOSED, "target verification is duplicate or proposals are not complete")
+        with self._aborting_on_error():
+            rows = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
+            ids = list(self.proposal_ids)
+            targets = _LazyRows(len(rows), lambda j: self.distribution(rows[j], ids[:j]))
+            self._decide(verify_drafts(targets, self.proposal_rows, ids, self.transaction,
+                                       greedy=self.policy.temperature == 0, output_limit=self.remaining,
+                                       eos_ids=self.eos_ids))
+        return self.decision
+
+    def _digest_record(self):
+        """The fields the decision digest covers (terminal_sampling.py:189-196)."""
+        def vector_sha(values):
+            return hashlib.sha256(values.astype("<i8").tobytes()).hexdigest()
+        decision = asdict(self.decision)
+        return {
+            "decision": decision, "accepted_target_rows": self.decision.accepted_target_rows,
+            "policy": self.policy.as_dict(), "RNG": self.transaction.prepared_state(),
+            "seed": self.seed_token, "proposals": self.proposal_ids,
+            "counts_sha256": vector_sha(self.counts), "generated_counts_sha256": vector_sha(self.generated_counts),
+            "logit_bias": self.logit_bias, "grammar_identity": self.grammar_identity,
+            "stop_identity": self.stop_identity, "remaining": self.remaining, "eos_ids": sorted(self.eos_ids),
+        }
 
     def prepared(self):
-        self._open()
-        if self.decision is None or not self._stop_checked:
+        """The decision and the SHA-256 digest every stage must commit against."""
+        self._require_open()
+        if self._stage is not _Stage.DECIDED or self._stop_pending:
             raise ValidationError("terminal decision has not been computed")
-        data = {"decision": asdict(self.decision), "accepted_target_rows": self.decision.accepted_target_rows,
-                "policy": self.policy.as_dict(), "RNG": self.transaction.prepared_state(),
-                "seed": self.seed_token, "proposals": self.proposal_ids,
-                "counts_sha256": hashlib.sha256(self.counts.astype("<i8").tobytes()).hexdigest(),
-                "generated_counts_sha256": hashlib.sha256(self.generated_counts.astype("<i8").tobytes()).hexdigest(),
-                "logit_bias": self.logit_bias, "grammar_identity": self.grammar_identity,
-                "stop_identity": self.stop_identity, "remaining": self.remaining, "eos_ids": sorted(self.eos_ids)}
         return {"decision": asdict(self.decision), "accepted_target_rows": self.decision.accepted_target_rows,
-                "digest": fingerprint(data)}
+                "digest": fingerprint(self._digest_record())}
 
     def apply_stop(self, tracker):
-        """Trim a stop string inside accepted proposals before any target GPU finish."""
-        self._open()
-        if self.decision is None or self._stop_checked or self.stop_identity != tracker.identity:
+        """Cut the decision at a stop string the frozen tracker finds in its output."""
+        self._require_open()
+        if self._stage is not _Stage.DECIDED or not self._stop_pending or self.stop_identity != tracker.identity:
             raise ValidationError("stop processing lacks the exact frozen terminal decision/prefix")
-        preview = tracker.preview(self.decision.output_ids)
-        if preview.matched is not None:
-            count = preview.token_count
-            if isinstance(self.decision, SeedDecision):
-                self.decision = replace(self.decision, stop_reason="stop")
-            elif count <= self.decision.accepted_drafts:
-                self.decision = replace(self.decision, accepted_drafts=count, output_ids=self.decision.output_ids[:count],
-                                        pending_token=None, stop_reason="stop")
-            else:
-                self.decision = replace(self.decision, output_ids=self.decision.output_ids[:count], stop_reason="stop")
-        self._stop_checked = True
+        found = tracker.preview(self.decision.output_ids)
+        if found.matched is not None:
+            self.decision = _cut_at_stop(self.decision, found.token_count)
+        self._stop_pending = False
         return self.decision
 
     def commit(self, expected_digest):
-        self._open()
+        self._require_open()
         if self.prepared()["digest"] != expected_digest:
             raise ValidationError("all-stage commit does not match the prepared terminal decision/RNG")
         self.transaction.commit()
-        self.closed, self.owner.active = True, None
+        self._close()
         return self.decision
 
     def abort(self):
-        self._open()
+        self._require_open()
         self.transaction.abort()
-        self.closed, self.owner.active = True, None
+        self._close()
+
+    def _close(self):
+        self.closed = True
+        self.owner.active = None
 
 
-class _ConditionalTargets:
-    """Lazy, cached target distributions; row j sees the accepted prefix proposal_ids[:j]."""
-
-    def __init__(self, work, values):
-        self.work, self.values, self.cache = work, values, {}
-
-    def __len__(self):
-        return len(self.values)
-
-    def __getitem__(self, index):
-        if index not in self.cache:
-            self.cache[index] = self.work.distribution(self.values[index], self.work.proposal_ids[:index])
-        return self.cache[index]
+def _cut_at_stop(decision, kept):
+    """The decision with its output cut to ``kept`` tokens by a stop string
+    (terminal_sampling.py:200-216).  A seed keeps its token as the pending
+    one; a cut inside the accepted drafts drops the pending token and the
+    later drafts; a cut at the replacement or bonus token keeps it pending."""
+    if isinstance(decision, SeedDecision):
+        return replace(decision, stop_reason="stop")
+    cut = {"output_ids": decision.output_ids[:kept], "stop_reason": "stop"}
+    if kept <= decision.accepted_drafts:
+        cut.update(accepted_drafts=kept, pending_token=None)
+    return replace(decision, **cut)

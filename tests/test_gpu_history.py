@@ -221,8 +221,9 @@ def test_prefix_distribution_equals_dense_prefix_counts():
                          frequency_penalty=0.2)
     logits = torch.from_numpy(rng.normal(0, 2, V).astype(np.float32)).to(DEV)
     sampler = TerminalSampler(seed=7, vocabulary=V)
-    work = sampler._begin(pol, counts, 8, frozenset(), generated_counts=gen, logit_bias=None, allowed=None,
-                          grammar_identity=None, stop_identity=None)
+    seed = int(ids[2])
+    gen[seed] = counts[seed]          # the pending seed is published, generated history
+    work = sampler.begin_verification(seed_token=seed, policy=pol, counts=counts, remaining=8, generated_counts=gen)
     for prefix in ([], [int(ids[0])], [5, 5, int(ids[1]), V - 1]):
         got = work.distribution(logits, prefix)
         c, g = counts.copy(), gen.copy()

@@ -4,8 +4,9 @@ Token ids, consumption flags, top-k index sets and statuses must be bit-exact;
 fp32 probabilities within 1e-5 relative (exactly zero where the oracle is
 zero).  The only tolerated token difference is a decision that the oracle
 itself places inside the float64 rounding band (its margin below 1e-11, where
-a different exp or summation order may legitimately pick the neighbour); such
-rows, and rows the kernel flags with DSR_FLAG_MARGIN, must be rare.
+a different exp or summation order may legitimately pick the neighbour); the
+kernel's own rounding-band flag excuses nothing.  The benchmark
+configurations assert the observed count of such rows: zero.
 """
 import json
 import os
@@ -24,14 +25,14 @@ pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def check(rep, max_margin_frac=0.01):
+def check(rep, margin_rows=0):
+    """No mismatch, and at most ``margin_rows`` rows whose token differs
+    where the oracle's own decision sat within 1e-11 of its threshold."""
     print(f"rows={rep.rows} exact={rep.exact} margin={rep.margin_rows} flagged={rep.flagged} "
           f"max_rel={rep.max_rel:.3g}", flush=True)
     assert not rep.mismatches, rep.mismatches[:10]
-    assert len(rep.margin_rows) <= max(1, int(max_margin_frac * rep.rows))
-    # The rounding-band flag must stay rare: it marks decisions within a few
-    # ulps of a threshold, which random inputs almost never produce.
-    assert rep.flagged <= max(1, int(max_margin_frac * rep.rows))
+    assert len(rep.margin_rows) <= margin_rows, rep.margin_rows
+    assert rep.exact + len(rep.margin_rows) == rep.rows
 
 
 def test_c1_single_row_fp32():
@@ -61,17 +62,17 @@ def test_c5_stress_rows():
         c = np.bincount(w.histories[r], minlength=V).astype(np.int32)
         v = O.adjusted_logits(w.logits[r], O.Policy(**w.policies[r]), c, c)
         assert gpu["tokens"][r] == int(np.argmax(v)) and gpu["consumed"][r] == 0 and gpu["status"][r] == 0
-    # Sampled rows from both families against the full oracle.
-    rows = [r for r in list(range(1, 96, 2)) + list(range(513, 608, 2))]
+    # Every sampled row, from both families, against the full oracle.
+    rows = list(range(1, w.rows, 2))
     sub = workloads.select_rows(w, rows)
     gpu_sub = {k: v[rows] for k, v in gpu.items()}
-    check(compare(sub, gpu_sub), max_margin_frac=0.05)
+    check(compare(sub, gpu_sub))
 
 
 def test_c5_near_tie_rows_with_probs_and_sets():
     w = workloads.select_rows(workloads.c5(), list(range(512, 544)))
     gpu = run_gpu(w)
-    check(compare(w, gpu), max_margin_frac=0.1)
+    check(compare(w, gpu))
 
 
 GOLD = np.load(os.path.join(HERE, "golden", "sampling_golden.npz"))
@@ -239,7 +240,7 @@ def test_penalties_bias_mask_match_oracle_on_mixed_rows():
         assert int(res.status[r]) == ref.status
         if ref.status:
             continue
-        if not (int(res.flags[r]) & 1 or ref.margin < 1e-11):
+        if ref.margin >= MARGIN:
             assert int(res.tokens[r]) == ref.token and bool(res.consumed[r]) == ref.consumed, r
         np.testing.assert_array_equal(kept[r], ref.topk_kept)
         np.testing.assert_allclose(probs[r], ref.probs, rtol=1e-12, atol=1e-300)
@@ -283,18 +284,17 @@ def test_verify_c4_against_oracle():
                None if int(res.pending[r]) < 0 else int(res.pending[r]), int(res.used_accept[r]),
                int(res.used_target[r]))
         want = (ref.accepted, ref.output_ids, ref.pending, ref.used_accept, ref.used_target)
-        if got == want:
-            hits += 1
-        else:
-            assert int(res.flags[r]) & 1 or ref.margin < 1e-11, (r, got, want)
-    assert hits >= R - 1
+        assert got == want, (r, got, want, ref.margin)
+        hits += 1
+    assert hits == R == 32
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_verify_fast_path_matches_general_path(dtype):
+def test_verify_fast_and_general_paths_match_the_oracle(dtype):
     """Filter-free requests take the statistics-only verifier; an all-ones
     allow mask sends the same requests through the full-distribution path.
-    Decisions must agree except where either side flags the rounding band."""
+    Both must equal the oracle on every request; a decision may differ only
+    where the oracle's own margin is below 1e-11."""
     rng = np.random.default_rng(11)
     R, K, V = 24, 3, 5003
     tgt_np = rng.normal(0, 2, (R, K + 1, V)).astype(np.float32)
@@ -302,7 +302,8 @@ def test_verify_fast_path_matches_general_path(dtype):
     dev = "cuda"
     tgt = torch.from_numpy(tgt_np).to(dev).to(dtype)
     drf = torch.from_numpy(drf_np).to(dev).to(dtype)
-    pols = [dict(temperature=[1.0, 0.7, 1.3, 0.0][r % 4]) for r in range(R)]
+    temps = [1.0, 0.7, 1.3, 0.0]
+    pols = [dict(temperature=temps[r % 4]) for r in range(R)]
     # Draft ids from the draft rows themselves, so most are plausible.
     draw = batch.sample_rows(drf.reshape(R * K, V).contiguous(), [dict()] * (R * K),
                              uniforms=torch.from_numpy(rng.random(R * K)).to(dev))
@@ -311,9 +312,10 @@ def test_verify_fast_path_matches_general_path(dtype):
     # proposals have probability one.
     greedy = torch.arange(R, device=dev) % 4 == 3
     ids[greedy] = drf.float().argmax(dim=-1).to(torch.int32)[greedy]
-    ua = torch.from_numpy(rng.random((R, K))).to(dev)
-    ut = torch.from_numpy(rng.random(R)).to(dev)
-    lim = torch.from_numpy(np.array([10, 2, 3, 10] * (R // 4), dtype=np.int32)).to(dev)
+    ua_np, ut_np = rng.random((R, K)), rng.random(R)
+    ua, ut = torch.from_numpy(ua_np).to(dev), torch.from_numpy(ut_np).to(dev)
+    limits = np.array([10, 2, 3, 10] * (R // 4), dtype=np.int32)
+    lim = torch.from_numpy(limits).to(dev)
     eos_ids = ids[:, 1].contiguous()  # the second draft of each request is an EOS token
     eos_off = torch.arange(0, R + 1, dtype=torch.int64, device=dev)
     words = (V + 31) // 32
@@ -322,16 +324,25 @@ def test_verify_fast_path_matches_general_path(dtype):
     fast = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim, **kw)
     gen = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim, allow_bits=ones, **kw)
     torch.cuda.synchronize()
-    fields = ("status", "accepted", "count", "pending", "stop", "used_accept", "used_target")
-    same = 0
+    # The oracle sees the logits the device sees (bf16 rows rounded once).
+    tgt_seen = tgt.float().cpu().numpy()
+    drf_seen = drf.float().cpu().numpy()
+    ids_np, eos_np = ids.cpu().numpy(), eos_ids.cpu().numpy()
+    waived = 0
     for r in range(R):
-        a = tuple(int(getattr(fast, f)[r]) for f in fields) + (tuple(fast.ids[r].tolist()),)
-        b = tuple(int(getattr(gen, f)[r]) for f in fields) + (tuple(gen.ids[r].tolist()),)
-        if a == b:
-            same += 1
-        else:
-            assert (int(fast.flags[r]) | int(gen.flags[r])) & 1, (r, a, b)
-    assert same >= R - 1
+        ref = O.verify(tgt_seen[r], drf_seen[r], list(ids_np[r]), O.Policy(**pols[r]), ua_np[r], float(ut_np[r]),
+                       eos_ids=(int(eos_np[r]),), output_limit=int(limits[r]))
+        want = (ref.status, ref.accepted, ref.output_ids, ref.pending, ref.stop, ref.used_accept, ref.used_target)
+        for res in (fast, gen):
+            n = int(res.count[r])
+            got = (int(res.status[r]), int(res.accepted[r]), tuple(res.ids[r, :n].tolist()),
+                   None if int(res.pending[r]) < 0 else int(res.pending[r]),
+                   {0: None, 1: "eos", 2: "length"}[int(res.stop[r])], int(res.used_accept[r]),
+                   int(res.used_target[r]))
+            if got != want:
+                assert ref.margin < MARGIN, (r, got, want, ref.margin)
+                waived += 1
+    assert waived == 0
     assert int(fast.status.abs().sum()) == 0
 
 

@@ -84,12 +84,8 @@ def test_policy_bounds_and_types():
 
 def test_jsonutil():
     assert jsonutil.canonical({"b": 1, "a": [1.5, None]}) == b'{"a":[1.5,null],"b":1}'
-    with pytest.raises(ValidationError):
-        jsonutil.loads('{"a":1,"a":2}', limit=100)
-    with pytest.raises(ValidationError):
-        jsonutil.loads("NaN", limit=100)
-    with pytest.raises(ValidationError):
-        jsonutil.loads("[" * 10, limit=5)
+    with pytest.raises(ValueError):
+        jsonutil.canonical({"x": float("nan")})
     with pytest.raises(ValidationError):
         jsonutil.integer(True, "x", 0, 5)
     with pytest.raises(ValidationError):

@@ -17,157 +17,44 @@ import pytest
 from oracle import sampling_oracle as O
 
 
+import sampling_law as law
+
+
 def P(**kw):
     return O.Policy(**kw)
 
 
-class Draws:
-    """Interval-midpoint uniforms (tests/test_sampling.py:13-19)."""
+class OracleImpl:
+    """The ``sampling_law`` adapter over the oracle."""
+    Rejected = O.OracleError
 
-    def __init__(self, accept, target=0.5):
-        self.accept, self.target = iter(accept), target
-        self.calls = []
+    def probs(self, logits, counts=None, generated=None, bias=None, allowed=None, **policy):
+        return O.probabilities(np.asarray(logits), O.Policy(**policy), counts, generated, logit_bias=bias,
+                               allowed=allowed)
 
-    def __call__(self, domain):
-        self.calls.append(domain)
-        return next(self.accept) if domain == "accept" else self.target
+    def draw(self, p, u):
+        return O.categorical(np.asarray(p), u)[0]
 
+    def residual(self, p, q):
+        return O.correction(np.asarray(p), np.asarray(q))
 
-def test_temperature_filters_known_answers():
-    # tests/test_sampling.py:22-32
-    logits = np.log(np.array([.5, .3, .2], np.float64))
-    np.testing.assert_allclose(O.probabilities(logits, P()), [.5, .3, .2], rtol=1e-15)
-    np.testing.assert_array_equal(O.probabilities(logits, P(temperature=0)), [1, 0, 0])
-    np.testing.assert_array_equal(O.probabilities(logits, P(temperature=1e-320)), [1, 0, 0])
-    np.testing.assert_allclose(O.probabilities(logits, P(top_k=2)), [.625, .375, 0], rtol=1e-15)
-    np.testing.assert_allclose(O.probabilities(logits, P(top_p=.7)), [.625, .375, 0], rtol=1e-15)
-    np.testing.assert_array_equal(O.probabilities(logits, P(top_p=0)), [1, 0, 0])
-    np.testing.assert_array_equal(O.probabilities(logits, P(min_p=.7)), [1, 0, 0])
-    np.testing.assert_array_equal(O.probabilities(logits, P(min_p=.5, top_p=.6)), [1, 0, 0])
+    def verify(self, targets, proposals, ids, draws, *, greedy, limit, eos=()):
+        return O.verify_probs(targets, proposals, ids, draws.random, greedy=greedy, output_limit=limit, eos_ids=eos)
 
 
-def test_penalties_bias_mask_closed_form():
-    # tests/test_sampling.py:35-44
-    logits = np.array([2., -1., 3., 0.], np.float32)
-    counts = np.array([2, 1, 0, 0], np.int32)
-    pol = P(repetition_penalty=2, presence_penalty=.25, frequency_penalty=.5)
-    got = O.probabilities(logits, pol, counts, logit_bias={3: .2}, allowed=np.array([True, True, False, True]))
-    adj = np.array([1 - .25 - 1, -2 - .25 - .5, -np.inf, .2])
-    want = np.exp(adj - adj.max())
-    np.testing.assert_allclose(got, want / want.sum(), rtol=1e-15)
-    with pytest.raises(O.OracleError, match="every"):
-        O.probabilities(logits, pol, allowed=np.zeros(4, bool))
+@pytest.mark.parametrize("name", sorted(law.LAWS))
+def test_reference_law(name):
+    # The reference's known answers and laws (tests/sampling_law.py cites each source).
+    law.LAWS[name](OracleImpl())
 
 
-def test_categorical_cdf_boundaries():
-    # tests/test_sampling.py:49-53
-    p = np.array([0., .25, 0., .75, 0.], np.float64)
-    assert O.categorical(p, 0.)[0] == 1
-    assert O.categorical(p, .25)[0] == 3
-    assert O.categorical(p, np.nextafter(1., 0.).item())[0] == 3
+def test_two_token_joint_law_at_full_resolution():
+    law.check_two_token_joint_law(OracleImpl(), accept_cells=4, target_cells=8)
 
 
-def test_categorical_single_support_draws_nothing():
-    # sampling.py:120-122
-    def never():
-        raise AssertionError("uniform requested for a one-point support")
-    assert O.categorical(np.array([0., 1., 0.]), never) == (1, False, math.inf)
-
-
-def test_exact_rejection_marginal():
-    # tests/test_sampling.py:56-69
-    target, proposal = np.array([.3, .7]), np.array([.8, .2])
-    np.testing.assert_array_equal(O.correction(target, proposal), [0, 1])
-    mass = [Fraction(0), Fraction(0)]
-    q = (Fraction(4, 5), Fraction(1, 5))
-    for token in (0, 1):
-        for u in (np.arange(8) + .5) / 8:
-            _, out, _, _ = O.verify_probs((target, target), (proposal,), (token,), Draws([float(u)]),
-                                          greedy=False, output_limit=2)
-            mass[out[0]] += q[token] / 8
-    assert mass == [Fraction(3, 10), Fraction(7, 10)]
-
-
-@pytest.mark.parametrize("rejected", range(6))
-def test_every_rejection_length(rejected):
-    # tests/test_sampling.py:72-84
-    proposal = np.array([.5, .5])
-    targets = [np.array([.75, .25]) for _ in range(6)]
-    if rejected < 5:
-        targets[rejected] = np.array([.25, .75])
-    acc, out, pending, stop = O.verify_probs(targets, [proposal] * 5, [0] * 5, Draws([.75] * 5),
-                                             greedy=False, output_limit=10)
-    assert acc == rejected and len(out) == rejected + 1 and pending == out[-1] and stop is None
-
-
-def test_eos_or_limit_inside_drafts_has_no_bonus():
-    # tests/test_sampling.py:87-95
-    target, proposal = np.array([.9, .1]), np.array([.5, .5])
-    d = Draws([.1])
-    assert O.verify_probs([target] * 6, [proposal] * 5, [0] * 5, d, greedy=False, output_limit=10,
-                          eos_ids={0}) == (1, (0,), None, "eos")
-    assert d.calls == ["accept"]
-    assert O.verify_probs([target] * 6, [proposal] * 5, [0] * 5, Draws([.1, .1]), greedy=False,
-                          output_limit=2) == (2, (0, 0), None, "length")
-
-
-def test_greedy_draws_nothing():
-    # tests/test_sampling.py:98-107
-    d = Draws([])
-    out = O.verify_probs([np.array([.2, .8])] * 6, [np.array([.5, .5])] * 5, [0] * 5, d, greedy=True,
-                         output_limit=5)
-    assert out[1] == (1,) and d.calls == []
-
-
-def test_two_token_joint_law_exact():
-    # tests/test_sampling_reference_law.py:15-42
-    q0 = (Fraction(1, 2), Fraction(1, 4), Fraction(1, 4))
-    p0 = (Fraction(1, 4), Fraction(3, 8), Fraction(3, 8))
-    q1 = [tuple(q0[(t - prev - 1) % 3] for t in range(3)) for prev in range(3)]
-    p1 = [tuple(p0[(t - prev - 2) % 3] for t in range(3)) for prev in range(3)]
-    seen = [[Fraction(0)] * 3 for _ in range(3)]
-    arr = lambda rows: [np.array([float(x) for x in r]) for r in rows]
-    for first, second, a, b, c, d in product(range(3), range(3), range(4), range(4), range(8), range(8)):
-        _, out, _, _ = O.verify_probs(arr((p0, p1[first], p0)), arr((q0, q1[first])), (first, second),
-                                      Draws(((a + .5) / 4, (b + .5) / 4), (c + .5) / 8), greedy=False,
-                                      output_limit=2)
-        if len(out) == 1:
-            out += (O.categorical(np.array([float(x) for x in p1[out[0]]]), (d + .5) / 8)[0],)
-        seen[out[0]][out[1]] += q0[first] * q1[first][second] / (16 * 64)
-    assert seen == [[p0[f] * p1[f][s] for s in range(3)] for f in range(3)]
-
-
-def test_equal_coordinates_get_no_correction_mass():
-    # tests/test_sampling_reference_law.py:45-50
-    np.testing.assert_array_equal(O.correction(np.array([.125, .625, .25]), np.array([.5, .25, .25])), [0., 1., 0.])
-
-
-def test_cluster_probe_verifier_checks():
-    # src/deepseekrpc/cluster_probe.py:22-56 (13 checks)
-    point = np.eye(3)
-    for rejected in range(6):
-        targets = [point[0] if r < rejected else point[1] for r in range(5)] + [point[2]]
-        acc, out, _, _ = O.verify_probs(targets, [point[0]] * 5, [0] * 5, Draws([]), greedy=True, output_limit=64)
-        assert acc == rejected and out == (0,) * rejected + ((1,) if rejected < 5 else (2,))
-    for limit in range(1, 6):
-        acc, out, pending, stop = O.verify_probs([point[0]] * 6, [point[0]] * 5, [0] * 5, Draws([.5] * 5),
-                                                 greedy=False, output_limit=limit)
-        assert out == (0,) * limit and stop == "length" and pending is None
-    acc, out, pending, stop = O.verify_probs([point[0]] * 6, [point[0]] * 5, [0] * 5, Draws([.5] * 5),
-                                             greedy=False, output_limit=64, eos_ids={0})
-    assert (out, acc, stop, pending) == ((0,), 1, "eos", None)
-    p, q = np.array([.1, .6, .3]), np.array([.5, .2, .3])
-    m = np.minimum(p, q)
-    np.testing.assert_allclose(m + (1 - m.sum()) * O.correction(p, q), p, rtol=0, atol=2e-16)
-
-
-def test_presence_frequency_use_generated_counts_only():
-    # tests/test_sampling.py:236-243
-    counts, gen = np.array([5, 1, 0], np.int32), np.array([0, 1, 0], np.int32)
-    got = O.probabilities(np.array([2., 2., 0.], np.float32),
-                          P(repetition_penalty=2, presence_penalty=.5, frequency_penalty=.25), counts, gen)
-    want = np.exp(np.array([1., .25, 0.]) - 1)
-    np.testing.assert_allclose(got, want / want.sum(), rtol=1e-15, atol=0)
+def test_categorical_reports_no_draw_for_one_point_support():
+    # sampling.py:120-122: no uniform, so no margin either.
+    assert O.categorical(np.array([0., 1., 0.]), lambda: 0.5) == (1, False, math.inf)
 
 
 def test_negative_logits_are_multiplied_by_repetition():
