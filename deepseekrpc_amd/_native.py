@@ -41,8 +41,9 @@ STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 EXPORTS = (
     "dsr_abi_version", "dsr_status_message", "dsr_sample_workspace_bytes", "dsr_verify_workspace_bytes",
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
-    "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append",
+    "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append", "dsr_sample_rows_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 268435456
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -109,6 +110,8 @@ def load(path: str = LIB_PATH):
     lib.dsr_verify_workspace_bytes.argtypes = [_i64, _i32, _i64]
     lib.dsr_sample_rows.restype = _i32
     lib.dsr_sample_rows.argtypes = [ctypes.POINTER(SampleArgs), _p]
+    lib.dsr_sample_rows_noalloc.restype = _i32
+    lib.dsr_sample_rows_noalloc.argtypes = [ctypes.POINTER(SampleArgs), _p]
     lib.dsr_verify_drafts.restype = _i32
     lib.dsr_verify_drafts.argtypes = [ctypes.POINTER(VerifyArgs), _p]
     lib.dsr_prob_stats.restype = _i32

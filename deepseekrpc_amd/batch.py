@@ -283,6 +283,7 @@ class SampleResult:
     probs: torch.Tensor | None = None
     kept_bits: torch.Tensor | None = None
     args: object = None       # the marshalled dsr_sample_args_t of this call
+    keep: tuple = ()          # every tensor ``args`` points into, kept alive with it
 
 
 class Workspace:
@@ -314,7 +315,7 @@ _default_ws = Workspace()
 def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None = None, bias: BiasTable | None = None,
                 allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
                 rng_state: torch.Tensor | None = None, probs: str | None = None, kept: bool = False,
-                workspace: Workspace | None = None) -> SampleResult:
+                workspace: Workspace | None = None, noalloc: bool = False) -> SampleResult:
     """Sample every row of ``logits [rows, V]`` on the current stream.
 
     ``policies`` is a device tensor made by ``policy_tensor`` or a list of
@@ -323,7 +324,10 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     ``pcg64_states``) instead lets each row that needs a draw take it on the
     device from its PCG64 state, which is advanced in place.  With neither,
     only the distribution is computed.  ``probs`` may be ``"f32"`` or
-    ``"f64"`` to return the final probabilities.
+    ``"f64"`` to return the final probabilities.  ``noalloc`` launches
+    through ``dsr_sample_rows_noalloc``, whose workspace is the library's own
+    device array (at most ``N.NOALLOC_SCRATCH_BYTES``; calls on one device
+    share it, so overlapping calls race).
     """
     lib = N.load()
     _require_cuda(logits, "logits", rows_strided=True)
@@ -355,7 +359,11 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         _require_cuda(allow_bits, "allow_bits")
         if allow_bits.dim() != 2 or allow_bits.shape[0] != rows or allow_bits.element_size() != 4:
             raise ValueError("allow_bits must be [rows, words] 32-bit")
-    ws = (workspace or _default_ws).get(lib.dsr_sample_workspace_bytes(rows, V), dev)
+    need = lib.dsr_sample_workspace_bytes(rows, V)
+    if noalloc and need > N.NOALLOC_SCRATCH_BYTES:
+        raise ValueError(f"{rows} rows of {V} tokens need {need} bytes of scratch; the allocation-free entry point "
+                         f"holds {N.NOALLOC_SCRATCH_BYTES}")
+    ws = None if noalloc else (workspace or _default_ws).get(need, dev)
     a = N.SampleArgs()
     a.logits = logits.data_ptr()
     a.dtype = _DTYPES[logits.dtype]
@@ -382,9 +390,13 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         a.probs_ld = V
     if res.kept_bits is not None:
         a.out_kept_bits, a.kept_ld = res.kept_bits.data_ptr(), res.kept_bits.stride(0)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    N.check(lib.dsr_sample_rows(ctypes.byref(a), _stream()), "dsr_sample_rows")
+    if noalloc:
+        N.check(lib.dsr_sample_rows_noalloc(ctypes.byref(a), _stream()), "dsr_sample_rows_noalloc")
+    else:
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        N.check(lib.dsr_sample_rows(ctypes.byref(a), _stream()), "dsr_sample_rows")
     res.args = a
+    res.keep = (logits, policies, history, bias, allow_bits, uniforms, rng_state, ws)
     return res
 
 
@@ -485,6 +497,7 @@ class VerifyResult:
     status: torch.Tensor
     flags: torch.Tensor
     args: object = None  # the marshalled dsr_verify_args_t
+    keep: tuple = ()     # every tensor ``args`` points into, kept alive with it
 
 
 def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, policies, u_accept: torch.Tensor,
@@ -561,6 +574,8 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     res.args = a
+    res.keep = (target, draft, draft_ids, policies, u_accept, u_target, output_limit, history, bias, allow_bits,
+                eos_offsets, eos_ids, rng_accept, rng_target, ws)
     N.check(lib.dsr_verify_drafts(ctypes.byref(a), _stream()), "dsr_verify_drafts")
     return res
 

@@ -12,6 +12,7 @@
 //                         test on float64 probability vectors.
 #include <hip/hip_runtime.h>
 #include <limits.h>
+#include <mutex>
 #include <math.h>
 #include <stdint.h>
 
@@ -354,6 +355,50 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
     else hipLaunchKernelGGL(k_sample_general<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   }
   return launched();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of dsr_sample_rows.  Its workspace is a file-scope
+// device array, one copy per device, held until the process ends.  Host code
+// never passes the array's name to a kernel (on the host that name is only a
+// stand-in): each device's address is looked up once, with that device
+// current, and kept.
+
+static __device__ __align__(256) unsigned char scratch[DSR_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex scratch_lock;
+void* scratch_address[kMaxScratchDevices];  // per device; null until looked up
+}  // namespace
+
+// The scratch array of the current device; 0 or DSR_ERR_LAUNCH.
+static int32_t current_scratch(void** out) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxScratchDevices) return DSR_ERR_LAUNCH;
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (!scratch_address[device]) {
+    void* address = nullptr;
+    if (hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)) != hipSuccess || !address) return DSR_ERR_LAUNCH;
+    scratch_address[device] = address;
+  }
+  *out = scratch_address[device];
+  return 0;
+}
+
+int32_t dsr_sample_rows_noalloc(const dsr_sample_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  if (args->workspace || args->workspace_bytes) return DSR_ERR_ARG;  // the device array is the workspace
+  if (args->rows < 0 || args->vocab < 1) return DSR_ERR_ARG;
+  if (dsr_sample_workspace_bytes(args->rows, args->vocab) > (size_t)DSR_NOALLOC_SCRATCH_BYTES)
+    return DSR_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int32_t rc = current_scratch(&ws);
+  if (rc) return rc;
+  dsr_sample_args_t a = *args;
+  a.workspace = ws;
+  a.workspace_bytes = DSR_NOALLOC_SCRATCH_BYTES;
+  return dsr_sample_rows(&a, stream);
 }
 
 int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {

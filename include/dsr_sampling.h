@@ -68,6 +68,9 @@ extern "C" {
 #define DSR_ERR_LAUNCH (-2)
 #define DSR_ERR_WORKSPACE (-3)
 
+/* Device scratch of dsr_sample_rows_noalloc, in bytes (256 MiB). */
+#define DSR_NOALLOC_SCRATCH_BYTES (268435456u)
+
 /* Per-row flags. */
 #define DSR_FLAG_MARGIN 1u      /* a threshold decision sat inside the rounding band */
 #define DSR_FLAG_GENERAL 2u     /* decided by the general (workspace) path; bits 4-7 give
@@ -215,6 +218,23 @@ size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab);
  * Replaces SamplingPolicy.probabilities + categorical (sampling.py:48-128),
  * as called by TerminalSampler.begin_seed (terminal_sampling.py:83-95). */
 int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream);
+
+/* Allocation-free dsr_sample_rows.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).
+ * Arguments as dsr_sample_rows, except that workspace and workspace_bytes
+ * must be 0: the workspace is a device array of DSR_NOALLOC_SCRATCH_BYTES
+ * inside the library, one per device, allocated when the library is loaded
+ * on that device and held until the process ends.  The call uses the current
+ * device's array (the stream must belong to the current device) and calls
+ * no allocating routine.  A call needing more than the array, that is
+ * dsr_sample_workspace_bytes(rows, vocab) > DSR_NOALLOC_SCRATCH_BYTES (more
+ * than 259 rows at vocab 129,280), returns DSR_ERR_WORKSPACE and launches
+ * nothing.
+ * The kernels need no cleared workspace.  Calls on one device share its
+ * array: calls whose work overlaps on that device (two streams, or two host
+ * threads) race and must be ordered by the caller. */
+int32_t dsr_sample_rows_noalloc(const dsr_sample_args_t* args, void* stream);
 
 /* Exact sampled verifier; replaces SamplingWork.verify (terminal_sampling.py
  * :170-183) with verify_drafts (sampling.py:247-294) and the lazy
