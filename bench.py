@@ -15,11 +15,16 @@ mixed greedy, 16,384-token histories) and hist (1,024 rows x 16,384 token
 ids built into device history tables; one step is one
 ``dsr_history_append`` call).
 
+Distinct input batches rotate through the timed region: the workload's rows
+with their vocabulary positions rolled by a different shift each
+(``workloads.rolled``), enough of them to exceed 256 MB together, so no step
+reads its inputs from the 256 MB Infinity Cache a previous step filled.
+
 Prints one JSON line: the throughput, the roofline of the step (algorithmic
 HBM bytes / HIP-event time of the launches on their stream, against 8 TB/s)
 and the CPU baseline: the float64 oracle (a restatement of the reference's
-NumPy sampler) timed on the host cores over a bounded sample of the same
-workload, on every core and per core.
+NumPy sampler) timed on the host over a bounded sample of the same workload,
+on 16 worker processes (the GPU box's CPU share) and on one process alone.
 """
 from __future__ import annotations
 
@@ -119,12 +124,28 @@ def _cpu_rows(span):
     return hi - lo, time.perf_counter() - t0
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# Worker processes of the CPU baseline: the GPU box's CPU share for one GPU
+# (its process limits size pools by that share, not by os.cpu_count()).
+CPU_WORKERS = 16
+
+
 def cpu_baseline(name, w, passes):
-    """Oracle throughput on the host cores: one forked worker per core (at
-    most 16), the sample split evenly; run before the GPU is initialised."""
+    """Oracle throughput on the host: CPU_WORKERS forked workers with the
+    sample split evenly, then one worker alone on an eighth of the sample
+    (the single-core figure); run before the GPU is initialised."""
     _CPU.update(w=w, name=name)
     os.environ["OMP_NUM_THREADS"] = "1"
-    cores = min(16, os.cpu_count() or 1)
+    cores = max(1, min(CPU_WORKERS, os.cpu_count() or 1))
     total = _units(name, w) * passes
     edges = np.linspace(0, total, cores + 1).astype(int)
     spans = [(int(a), int(b)) for a, b in zip(edges[:-1], edges[1:]) if b > a]
@@ -133,14 +154,19 @@ def cpu_baseline(name, w, passes):
         t0 = time.perf_counter()
         done = pool.map(_cpu_rows, spans, chunksize=1)
         wall = time.perf_counter() - t0
+    with mp.get_context("fork").Pool(1) as pool:   # one process alone: the single-core figure
+        pool.map(_cpu_rows, [(0, 1)])
+        one_n, one_wall = pool.map(_cpu_rows, [(0, max(1, total // 8))])[0]
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
     unit = WORKLOADS[name][1]
-    return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port", "value_per_core": n / busy,
-            "sample": f"{n} {'requests' if name == 'c4' else 'rows'} ({passes} pass(es) over the {_units(name, w)} of the "
-                      f"same workload, {busy:.1f} s of CPU work) with the "
-                      f"{'NumPy history oracle (np.add.at on dense counts)' if name == 'hist' else 'float64 NumPy oracle'}"
-                      f" on {cores} worker processes; {n / busy:.2f} {unit} per core"}
+    what = "requests" if name == "c4" else "rows"
+    oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
+    return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
+            "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
+            "sample": f"{n} {what} ({passes} pass(es) over the {_units(name, w)} of the same workload, "
+                      f"{busy:.1f} s of CPU work) with the {oracle} on {cores} worker processes; "
+                      f"{one_n} {what} on one process alone: {one_n / one_wall:.2f} {unit}"}
 
 
 class _HistResult:
@@ -150,6 +176,27 @@ class _HistResult:
         import torch
         self.status = status
         self.flags = torch.zeros_like(status)
+
+
+# Inputs rotated through the timed region exceed this many bytes together.
+ROTATION_BYTES = 300 * 2**20
+
+
+def _batch_bytes(name, w):
+    if name == "hist":
+        return w.extra["tokens"].nbytes
+    if name == "c4":
+        return w.extra["target"].nbytes + w.extra["draft"].nbytes
+    return w.logits.shape[0] * w.logits.shape[1] * (2 if w.dtype == "bf16" else 4)
+
+
+def variants(name, w):
+    """Distinct input batches of the workload (vocabulary layouts rolled by
+    different shifts), at least 4 and together above ROTATION_BYTES."""
+    from deepseekrpc_amd import workloads
+    count = max(4, -(-ROTATION_BYTES // max(1, _batch_bytes(name, w))))
+    V = w.logits.shape[1]
+    return [w] + [workloads.rolled(w, (i * 7919) % V) for i in range(1, count)]
 
 
 def _prepare(name, w, device_rng=False):
@@ -215,33 +262,41 @@ def main():
     N.load()
     if args.device_rng and name in ("c4", "hist"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
-    prep, alg_bytes, units = _prepare(name, w, args.device_rng)
+    batches = variants(name, w)
+    preps = []
+    for v in batches:
+        prep, alg_bytes, units = _prepare(name, v, args.device_rng)
+        preps.append(prep)
     torch.cuda.synchronize()
-    res = prep.result
-    status = res.status.cpu().numpy()
-    if (status != 0).any():
-        raise SystemExit(f"kernel reported row errors: {np.unique(status)}")
+    for prep in preps:
+        status = prep.result.status.cpu().numpy()
+        if (status != 0).any():
+            raise SystemExit(f"kernel reported row errors: {np.unique(status)}")
 
-    for _ in range(args.warmup):
-        prep.launch()
+    for i in range(args.warmup):
+        preps[i % len(preps)].launch()
     torch.cuda.synchronize()
-    # The timed region: K back-to-back steps on the launch stream, bracketed by
-    # synchronisation (host wall clock) and by HIP events on that stream
-    # (average duration of one step's launches).
+    # The timed region: K back-to-back steps on the launch stream, each on the
+    # next of the rotated input batches, bracketed by synchronisation (host
+    # wall clock) and by HIP events on that stream (average duration of one
+    # step's launches).
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(args.steps):
-        prep.launch()
+    for i in range(args.steps):
+        preps[i % len(preps)].launch()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kern_ms = ev0.elapsed_time(ev1) / args.steps
-    status = res.status.cpu().numpy()
-    if (status != 0).any():
-        raise SystemExit("kernel reported row errors in the timed region")
-    general = int(((res.flags.cpu().numpy() & N.FLAG_GENERAL) != 0).sum())
+    general = 0
+    for prep in preps:
+        res = prep.result
+        if (res.status.cpu().numpy() != 0).any():
+            raise SystemExit("kernel reported row errors in the timed region")
+        general = max(general, int(((res.flags.cpu().numpy() & N.FLAG_GENERAL) != 0).sum()))
+    prep = preps[0]
     if args.copy_calibration:
         # A plain read-N/write-N kernel over the batch's logit bytes, for
         # scaling the FETCH_SIZE / WRITE_SIZE counters.
@@ -255,22 +310,29 @@ def main():
 
     ms_per_step = wall * 1e3 / args.steps
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
-    traffic = None
+    # HBM traffic per launch is not measurable from inside the run (counters
+    # need their own rocprofv3 pass); it is read from the committed counter
+    # summary of the same command and labelled as such.
+    traffic, traffic_source = None, None
     tf = os.path.join(ROOT, "profiles", f"{kernels.split(' ')[0]}_{name}_traffic.json")
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("bytes_per_launch")
-    cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]),
-           "general_path_rows": general, "kernels": kernels}
+        traffic_source = os.path.relpath(tf, ROOT) + " (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)"
+    cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]), "input_dtype": w.dtype,
+           "general_path_rows": general, "kernels": kernels,
+           "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
     if name not in ("c4", "hist"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": {"bf16": "bf16", "i32": "int32"}.get(w.dtype, "f32"), "data": "synthetic",
+        # Every decision is taken in float64 (the reference's arithmetic) and
+        # fixed-point integers; the input type is reported in the config.
+        "vs_baseline": None, "dtype": "int32" if name == "hist" else "f64", "data": "synthetic",
         "config": cfg,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel_ms": kern_ms,
-                     "algorithmic_bytes": alg_bytes},
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": traffic_source,
+                     "kernel_ms": kern_ms, "algorithmic_bytes": alg_bytes},
     }
     if cpu is not None:
         line["cpu_baseline"] = cpu
