@@ -54,6 +54,8 @@ WORKLOADS = {
            "k_sample_bf16_full"),
     "hist": ("history rows/sec: 1,024 rows x 16,384 token ids -> sparse count tables over V=129,280", "rows/s", 10,
              "k_history_append (count) + k_history_offsets + k_history_append (write)"),
+    "propose": ("5-row draft proposal chains/sec at V=129,280 fp32, one host synchronisation per chain",
+                "chains/s", 100, "k_split_select + k_split_finish (5x) + k_history_append (4x)"),
 }
 
 DESCRIPTIONS = {
@@ -66,6 +68,8 @@ DESCRIPTIONS = {
           "top-p 0.9, rep 1.1 / pres 0.5 / freq 0.3 over 16384-token histories",
     "hist": "hist: 1024 rows x 16384 token ids U{0..129279}, all generated, appended into an empty history table "
             "(one dsr_history_append call)",
+    "propose": "propose: 5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the "
+               "device, T 0.7 / top-k 50 / top-p 0.9, 64-token history, draft PCG64 draws on the device",
 }
 
 _CPU = {}
@@ -75,6 +79,8 @@ def _units(name, w):
     """Rows of a sampling or history workload; requests of the verifier workload."""
     if name == "c4":
         return w.extra["target"].shape[0]
+    if name == "propose":
+        return 1
     return w.extra["tokens"].shape[0] if name == "hist" else w.rows
 
 
@@ -101,6 +107,8 @@ def _cpu_rows(span):
         for row in rows:
             H.append(None, None, None, None, [row], V)
         return hi - lo, time.perf_counter() - t0
+    if name == "propose":
+        return hi - lo, _cpu_chains(w, hi - lo)
     jobs = []
     for r in range(lo, hi):
         r = r % _units(name, w)
@@ -122,6 +130,30 @@ def _cpu_rows(span):
             O.sample_row(w.logits[r], O.Policy(**w.policies[r]), float(w.uniforms[r]), x, x, None, allowed,
                          keep_probs=name == "c1")
     return hi - lo, time.perf_counter() - t0
+
+
+def _cpu_chains(w, n):
+    """n proposal chains by the oracle: each row conditioned on the previous
+    token (the +4 bias) and on the prefix counts, the draft uniform drawn only
+    when needed (terminal_sampling.py:138-161)."""
+    from oracle import sampling_oracle as O
+    V = w.logits.shape[1]
+    counts0 = np.bincount(np.asarray(w.histories[0]), minlength=V).astype(np.int32)
+    gen = np.random.default_rng(w.extra["rng_seed"])
+    t0 = time.perf_counter()
+    for _ in range(n):
+        counts, previous = counts0.copy(), w.extra["seed_token"]
+        for j in range(w.extra["steps"]):
+            row = w.logits[j].copy()
+            row[previous] += np.float32(w.extra["bump"])
+            probe = np.random.Generator(np.random.PCG64(0))
+            probe.bit_generator.state = gen.bit_generator.state
+            ref = O.sample_row(row, O.Policy(**w.policies[0]), float(probe.random()), counts, counts, keep_probs=True)
+            if ref.consumed:
+                gen.random()
+            counts[ref.token] += 1
+            previous = ref.token
+    return time.perf_counter() - t0
 
 
 def _cpu_model():
@@ -160,7 +192,7 @@ def cpu_baseline(name, w, passes):
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
     unit = WORKLOADS[name][1]
-    what = "requests" if name == "c4" else "rows"
+    what = {"c4": "requests", "propose": "chains"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
@@ -185,6 +217,8 @@ ROTATION_BYTES = 300 * 2**20
 def _batch_bytes(name, w):
     if name == "hist":
         return w.extra["tokens"].nbytes
+    if name == "propose":
+        return w.logits.nbytes
     if name == "c4":
         return w.extra["target"].nbytes + w.extra["draft"].nbytes
     return w.logits.shape[0] * w.logits.shape[1] * (2 if w.dtype == "bf16" else 4)
@@ -199,11 +233,49 @@ def variants(name, w):
     return [w] + [workloads.rolled(w, (i * 7919) % V) for i in range(1, count)]
 
 
+class _Chain:
+    """One proposal chain per launch: five rows drawn on the device, then the
+    chain's one synchronisation."""
+
+    def __init__(self, w):
+        import torch
+
+        from deepseekrpc_amd import batch
+        self.batch, self.w = batch, w
+        dev = "cuda"
+        self.base = torch.from_numpy(w.logits).to(dev)
+        self.bump = torch.full((1,), float(w.extra["bump"]), device=dev)
+        self.seed = torch.tensor([w.extra["seed_token"]], dtype=torch.int32, device=dev)
+        self.state = batch.pcg64_states([np.random.default_rng(w.extra["rng_seed"])], dev)
+        self.table, st = batch.HistoryTable.from_token_lists_device(w.histories, device=dev)
+        assert int(st.abs().sum()) == 0
+        self.inputs = (self.base,)
+        self.launch()
+
+    def _row(self, j, previous):
+        out = self.base[j].clone()
+        out.index_add_(0, previous.long(), self.bump)
+        return out
+
+    def launch(self):
+        import torch
+        chain = self.batch.propose_rows(self._row, self.seed, self.w.extra["steps"], self.w.policies[0], self.state,
+                                        history=self.table)
+        ids, rows, draws, final, failed = self.batch.finish_proposals(chain)
+        if failed is not None:
+            raise SystemExit(f"proposal chain failed at row {failed}")
+        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        return self
+
+
 def _prepare(name, w, device_rng=False):
     """Device inputs and a launch closure for one step of the workload."""
     import torch
 
     from deepseekrpc_amd import batch, workloads
+    if name == "propose":
+        per_row = w.logits.shape[1] * (4 + 8) + 64 + 4   # logits in, float64 distribution out, controls, token
+        return _Chain(w), w.extra["steps"] * per_row + 4 * len(w.histories[0]), 1
     if name == "hist":
         toks = w.extra["tokens"]
         off = np.arange(toks.shape[0] + 1, dtype=np.int64) * toks.shape[1]
@@ -260,7 +332,7 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    if args.device_rng and name in ("c4", "hist"):
+    if args.device_rng and name in ("c4", "hist", "propose"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
     batches = variants(name, w)
     preps = []
@@ -321,7 +393,7 @@ def main():
     cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]), "input_dtype": w.dtype,
            "general_path_rows": general, "kernels": kernels,
            "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
-    if name not in ("c4", "hist"):
+    if name not in ("c4", "hist", "propose"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,

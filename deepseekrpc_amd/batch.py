@@ -485,6 +485,125 @@ class PreparedHistoryAppend:
         return HistoryTable(self.off, *(o[:total] for o in self.out))
 
 
+def _append_one(table: HistoryTable, token: torch.Tensor, bounds: torch.Tensor,
+                vocab: int) -> tuple[HistoryTable, torch.Tensor]:
+    """One device token appended to a one-row table (counted and generated),
+    without synchronising: the outputs keep their capacity (old capacity + 1)
+    and only ``offsets`` says how many entries are real, which is all the
+    sampling kernels read."""
+    dev = token.device
+    old = table.ids.numel()
+    cap = old + 1
+    off = torch.empty(2, dtype=torch.int64, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    out = [torch.empty(cap, dtype=torch.int32, device=dev) for _ in range(3)]
+    rc = N.load().dsr_history_append(_ptr(table.offsets), _ptr(table.ids), _ptr(table.counts),
+                                     _ptr(table.generated), _ptr(token), _ptr(bounds), None, 1, vocab, _ptr(off),
+                                     *(_ptr(o) for o in out), cap, _ptr(status), _stream())
+    N.check(rc, "dsr_history_append")
+    return HistoryTable(off, *out), status
+
+
+@dataclass
+class Proposals:
+    """Draft proposals drawn on the device by ``propose_rows``; rows after the
+    first stop token are speculative until ``finish_proposals`` cuts them."""
+    tokens: torch.Tensor      # int32 [steps]
+    rows: torch.Tensor        # float64 [steps, V]: each row's distribution
+    consumed: torch.Tensor    # uint8 [steps]
+    status: torch.Tensor      # int32 [steps]: sampling status, then history-append status
+    finite: torch.Tensor      # bool [steps]: the row's logits were all finite
+    states: torch.Tensor      # int64 [steps + 1, 4]: PCG64 state before row 0 and after each row
+    keep: tuple = ()
+
+
+def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_state: torch.Tensor, *,
+                 history: HistoryTable | None = None, bias: BiasTable | None = None,
+                 allow_bits: torch.Tensor | None = None, vocab: int = VOCAB) -> Proposals:
+    """Up to ``steps`` draft tokens drawn one row at a time with no host
+    synchronisation (terminal_sampling.py:138-161).
+
+    ``row_logits(position, previous)`` returns row ``position``'s FP32 logits
+    on the device, conditioned on ``previous``, the previous token as a device
+    int32 tensor of one element (``seed_token`` first, always a valid id): the
+    caller's Markov bias step reads the token the sampling kernel wrote.  Each row is
+    one ``dsr_sample_rows`` launch that draws its uniform from the ``draft``
+    domain's PCG64 state in ``rng_state`` (int64 ``[1, 4]``, advanced in
+    place) and sees the history with every earlier proposal appended, as
+    ``SamplingWork.distribution`` conditions it (:127-133).  Every row is
+    drawn speculatively; ``finish_proposals`` keeps them up to the first stop
+    token and restores the state saved after that row."""
+    if steps < 0 or steps > 5:
+        raise ValueError("at most five proposals")
+    _require(rng_state, "rng_state", torch.int64, 4)
+    _require(seed_token, "seed_token", torch.int32, 1)
+    dev = rng_state.device
+    pol = policy_tensor([policy], dev)
+    tokens = torch.empty(steps, dtype=torch.int32, device=dev)
+    rows = torch.empty(steps, vocab, dtype=torch.float64, device=dev)
+    consumed = torch.empty(steps, dtype=torch.uint8, device=dev)
+    status = torch.zeros(steps, dtype=torch.int32, device=dev)
+    finite = torch.empty(steps, dtype=torch.bool, device=dev)
+    states = torch.empty(steps + 1, 4, dtype=torch.int64, device=dev)
+    bounds = torch.tensor([0, 1], dtype=torch.int64, device=dev)  # one token per append
+    keep = [pol, bounds]
+    table, previous = history, seed_token
+    for j in range(steps):
+        logits = row_logits(j, previous)
+        if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
+                and logits.numel() == vocab):
+            raise ValueError("row_logits must return FP32 device logits of the vocabulary")
+        logits = logits.reshape(1, vocab).contiguous()
+        finite[j] = torch.isfinite(logits).all()
+        if j > 0:
+            if table is None:
+                table = HistoryTable(torch.zeros(2, dtype=torch.int64, device=dev),
+                                     *(torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(3)))
+            table, app = _append_one(table, previous, bounds, vocab)
+            keep.append(app)
+        states[j].copy_(rng_state.reshape(4))
+        res = sample_rows(logits, pol, history=table, bias=bias, allow_bits=allow_bits, rng_state=rng_state,
+                          probs="f64")
+        tokens[j:j + 1].copy_(res.tokens)
+        consumed[j:j + 1].copy_(res.consumed)
+        rows[j].copy_(res.probs[0])
+        if j > 0:
+            status[j:j + 1].copy_(torch.where(res.status != 0, res.status, app))
+        else:
+            status[j:j + 1].copy_(res.status)
+        keep.append((logits, table, res))
+        # A failed row writes token -1; the chain is rejected at its end, but
+        # the caller's bias step and the history only ever see a valid id.
+        previous = torch.clamp(res.tokens, min=0)
+    states[steps].copy_(rng_state.reshape(4))
+    return Proposals(tokens, rows, consumed, status, finite, states, tuple(keep))
+
+
+def finish_proposals(p: Proposals, eos_ids=()):
+    """The one synchronisation of a proposal chain: the kept proposals (up
+    to and including the first stop token), their distributions, the number
+    of ``draft`` draws they consumed, the PCG64 state after the last kept row
+    (int64 ``[1, 4]`` on the device, for ``pcg64_restore``), and the first row
+    whose status or logits failed
+    (``(position, status)`` with status -1 for non-finite logits, or None)."""
+    toks, used, st, fin = (t.cpu().numpy() for t in (p.tokens, p.consumed, p.status, p.finite))
+    count = len(toks)
+    for j, t in enumerate(toks):
+        if int(t) in eos_ids:
+            count = j + 1
+            break
+    failed = None
+    for j in range(count):
+        if not fin[j]:
+            failed = (j, -1)
+        elif st[j] != 0:
+            failed = (j, int(st[j]))
+        if failed:
+            break
+    return tuple(int(t) for t in toks[:count]), p.rows[:count], int(used[:count].sum()), p.states[count:count + 1], \
+        failed
+
+
 @dataclass
 class VerifyResult:
     accepted: torch.Tensor

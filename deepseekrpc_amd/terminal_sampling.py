@@ -38,6 +38,7 @@ import numpy as np
 import torch
 
 from . import _native as N
+from . import batch
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
 from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _history_table,
                        _logit_vector, _on_device, _raise_status, verify_drafts)
@@ -205,6 +206,7 @@ class SamplingWork:
         self.decision = None
         self.proposal_ids, self.proposal_rows = [], []
         self._device_history = None   # the counts as a device table, built for the first row
+        self._counts_sha = None       # SHA-256 of the frozen count vectors, for the digest
 
     # -- the frozen controls, under the reference's attribute names --------
     policy = property(lambda self: self._controls.policy)
@@ -314,18 +316,61 @@ class SamplingWork:
         self._require_stage(_Stage.AWAITING_PROPOSALS,
                             "proposal generation is duplicate or lacks a committed pending seed")
         with self._aborting_on_error():
-            previous = self.seed_token
-            for position in range(min(_MAX_PROPOSALS, self.remaining)):
-                # The graph's confidence output is diagnostic only.
-                logits, _ = graph.draft_conditional_logits(result, position, previous)
-                row = _logits_device(logits, 1, self.owner.vocabulary)[0]
-                previous, dist = self._draw(row, tuple(self.proposal_ids), "draft")
-                self.proposal_ids.append(previous)
-                self.proposal_rows.append(dist)
-                if previous in self.eos_ids:
-                    break
+            steps = min(_MAX_PROPOSALS, self.remaining)
+            device_step = getattr(graph, "draft_conditional_logits_device", None)
+            if device_step is not None and self.allowed is None:
+                self._propose_on_device(device_step, result, steps)
+            else:
+                previous = self.seed_token
+                for position in range(steps):
+                    # The graph's confidence output is diagnostic only.
+                    logits, _ = graph.draft_conditional_logits(result, position, previous)
+                    row = _logits_device(logits, 1, self.owner.vocabulary)[0]
+                    previous, dist = self._draw(row, tuple(self.proposal_ids), "draft")
+                    self.proposal_ids.append(previous)
+                    self.proposal_rows.append(dist)
+                    if previous in self.eos_ids:
+                        break
             self._stage = _Stage.PROPOSED
         return tuple(self.proposal_ids)
+
+    def _propose_on_device(self, device_step, result, steps):
+        """The proposal chain without a host round trip per row.  A graph that
+        offers ``draft_conditional_logits_device(result, row, previous)``
+        takes the previous token as a device int32 tensor of one element and
+        returns the row's ``(1, V)`` FP32 logits on the device; each row is one
+        launch that draws from the ``draft`` domain's PCG64 state on the
+        device.  Rows after a stop token are computed speculatively and
+        dropped at the one synchronisation, where the domain takes the state
+        saved after the last kept row and the draws it consumed are counted
+        in the transaction's window, exactly as the host loop draws them."""
+        vocab = self.owner.vocabulary
+        device = torch.device("cuda", torch.cuda.current_device())
+        generator = self.transaction.owner._streams["draft"]
+        state = batch.pcg64_states([generator], device)
+        seed = torch.tensor([self.seed_token], dtype=torch.int32, device=device)
+
+        def row_logits(position, previous):
+            logits, _confidence = device_step(result, position, previous)
+            if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32):
+                raise ValidationError(_MSG_HEAD)
+            if tuple(logits.shape) != (1, vocab):
+                raise ValidationError(_MSG_WINDOW)
+            return logits
+
+        chain = batch.propose_rows(row_logits, seed, steps, self.policy, state, history=self._history(()),
+                                   bias=_bias_table(self.logit_bias, vocab), vocab=vocab)
+        ids, rows, draws, final, failed = batch.finish_proposals(chain, self.eos_ids)
+        if failed is not None:
+            if failed[1] == -1:
+                raise ValidationError(_MSG_WINDOW)
+            _raise_status(failed[1])
+        if self.transaction.draws["draft"] + draws > 64:
+            raise ValidationError("terminal RNG domain is closed, invalid or exceeds its bounded window")
+        batch.pcg64_restore([generator], final)
+        self.transaction.draws["draft"] += draws
+        self.proposal_ids.extend(ids)
+        self.proposal_rows.extend(rows[j] for j in range(len(ids)))
 
     def use_normal_decode(self):
         """Verify with no proposals: the target row's draw is the bonus token."""
@@ -345,15 +390,19 @@ class SamplingWork:
         return self.decision
 
     def _digest_record(self):
-        """The fields the decision digest covers (terminal_sampling.py:189-196)."""
-        def vector_sha(values):
-            return hashlib.sha256(values.astype("<i8").tobytes()).hexdigest()
+        """The fields the decision digest covers (terminal_sampling.py:189-196).
+        The two count hashes cover the transaction's frozen copies, so they
+        are computed once per transaction (prepared() runs at prepare and
+        again at commit)."""
+        if self._counts_sha is None:
+            self._counts_sha = tuple(hashlib.sha256(v.astype("<i8").tobytes()).hexdigest()
+                                     for v in (self.counts, self.generated_counts))
         decision = asdict(self.decision)
         return {
             "decision": decision, "accepted_target_rows": self.decision.accepted_target_rows,
             "policy": self.policy.as_dict(), "RNG": self.transaction.prepared_state(),
             "seed": self.seed_token, "proposals": self.proposal_ids,
-            "counts_sha256": vector_sha(self.counts), "generated_counts_sha256": vector_sha(self.generated_counts),
+            "counts_sha256": self._counts_sha[0], "generated_counts_sha256": self._counts_sha[1],
             "logit_bias": self.logit_bias, "grammar_identity": self.grammar_identity,
             "stop_identity": self.stop_identity, "remaining": self.remaining, "eos_ids": sorted(self.eos_ids),
         }
