@@ -11,9 +11,11 @@ launch over the batch.
 deepseekrpc_amd/workloads.py): c1 (1 fp32 row with probabilities out), c2 (64
 bf16 rows with 4,096-token histories), c4 (32 verifier requests x 4 fp32
 drafts; one step is one ``dsr_verify_drafts`` call), c5 (1,024 bf16 rows,
-mixed greedy, 16,384-token histories) and hist (1,024 rows x 16,384 token
-ids built into device history tables; one step is one
-``dsr_history_append`` call).
+mixed greedy, 16,384-token histories), whole (256 bf16 rows whose policies
+set no top-k: the reference's default, top-p only, min-p only), hist (1,024
+rows x 16,384 token ids built into device history tables; one step is one
+``dsr_history_append`` call) and propose (one 5-row draft proposal chain
+drawn on the device).
 
 Distinct input batches rotate through the timed region: the workload's rows
 with their vocabulary positions rolled by a different shift each
@@ -54,6 +56,8 @@ WORKLOADS = {
            "k_sample_bf16_full"),
     "hist": ("history rows/sec: 1,024 rows x 16,384 token ids -> sparse count tables over V=129,280", "rows/s", 10,
              "k_history_append (count) + k_history_offsets + k_history_append (write)"),
+    "whole": ("sampled rows/sec at B=256×V=129,280 bf16 with no top-k (default / top-p / min-p policies)", "rows/s",
+              5, "k_sample_bf16_full"),
     "propose": ("5-row draft proposal chains/sec at V=129,280 fp32, one host synchronisation per chain",
                 "chains/s", 100, "k_split_select + k_split_finish (5x) + k_history_append (4x)"),
 }
@@ -68,6 +72,8 @@ DESCRIPTIONS = {
           "top-p 0.9, rep 1.1 / pres 0.5 / freq 0.3 over 16384-token histories",
     "hist": "hist: 1024 rows x 16384 token ids U{0..129279}, all generated, appended into an empty history table "
             "(one dsr_history_append call)",
+    "whole": "whole: 256 rows x 129280 bf16 heavy-tail logits, 10% allow mask, no top-k: default policy, "
+             "top-p ~ U[0.8,0.99], min-p 0.05, top-p 0.95 + min-p 0.01 (by row mod 4)",
     "propose": "propose: 5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the "
                "device, T 0.7 / top-k 50 / top-p 0.9, 64-token history, draft PCG64 draws on the device",
 }
@@ -372,9 +378,8 @@ def main():
     if args.copy_calibration:
         # A plain read-N/write-N kernel over the batch's logit bytes, for
         # scaling the FETCH_SIZE / WRITE_SIZE counters.
-        src = prep.inputs[0].view(torch.int32).reshape(-1) if name != "c4" else prep.inputs[0][0].reshape(-1)
-        if name == "hist":
-            src = prep.inputs[0]
+        src = prep.inputs[0] if name == "hist" else prep.inputs[0][0] if name == "c4" else prep.inputs[0]
+        src = src.reshape(-1).view(torch.int32)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
             torch.bitwise_not(src, out=dst)

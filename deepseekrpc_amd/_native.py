@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_NAME = "libdsr_sampling.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -31,11 +31,16 @@ E_POLICY = 11
 E_GENERATED = 12
 E_HISTORY = 13
 E_APPEND = 14
+E_HINT = 15
 MAX_APPEND = 16384
 
 FLAG_MARGIN = 1
 FLAG_GENERAL = 2
 FLAG_SPLIT = 4
+# Kernel-choice hints (statements about a batch's policies; results never depend on them).
+HINT_WHOLE_SOME = 1
+HINT_WHOLE_ALL = 2
+HINT_VERIFY_FAST = 4
 STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 
 EXPORTS = (
@@ -62,7 +67,7 @@ POLICY_DTYPE_FIELDS = [(name, "<f8") for name, _ in Policy._fields_[:6]] + [("to
 
 class SampleArgs(ctypes.Structure):
     _fields_ = [
-        ("logits", _p), ("dtype", _i32), ("reserved0", _i32), ("rows", _i64), ("vocab", _i64), ("ld", _i64),
+        ("logits", _p), ("dtype", _i32), ("hints", ctypes.c_uint32), ("rows", _i64), ("vocab", _i64), ("ld", _i64),
         ("policy", _p), ("pen_off", _p), ("pen_ids", _p), ("pen_count", _p), ("pen_gen", _p),
         ("bias_off", _p), ("bias_ids", _p), ("bias_val", _p), ("allow_bits", _p), ("allow_ld", _i64),
         ("uniforms", _p), ("out_token", _p), ("out_consumed", _p), ("out_status", _p), ("out_flags", _p),
@@ -80,6 +85,7 @@ class VerifyArgs(ctypes.Structure):
         ("out_accepted", _p), ("out_ids", _p), ("out_count", _p), ("out_pending", _p), ("out_stop", _p),
         ("out_used_accept", _p), ("out_used_target", _p), ("out_status", _p), ("out_flags", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_accept", _p), ("rng_target", _p),
+        ("hints", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
     ]
 
 

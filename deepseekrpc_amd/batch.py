@@ -68,8 +68,37 @@ def policy_array(policies) -> np.ndarray:
 
 
 def policy_tensor(policies, device) -> torch.Tensor:
+    """The packed policies on ``device``; the tensor keeps its host copy as
+    ``dsr_policies``, from which ``sample_rows`` and ``verify_drafts`` derive
+    their kernel-choice hints (a tensor without one gets no hints)."""
     arr = policies if isinstance(policies, np.ndarray) and policies.dtype == POLICY_DTYPE else policy_array(policies)
-    return torch.from_numpy(arr.view(np.uint8).copy()).to(device)
+    t = torch.from_numpy(arr.view(np.uint8).copy()).to(device)
+    t.dsr_policies = arr.copy()
+    return t
+
+
+FAST_MAX_K = 1024   # the largest top-k the bf16 register kernel cuts to
+
+
+def sample_hints(arr: np.ndarray | None, vocab: int) -> int:
+    """DSR_HINT_WHOLE_* bits for packed policies: whole rows are sampled
+    (0 < T <= 100) with no top-k or one above ``FAST_MAX_K`` (the kernels'
+    ``whole_row``).  The bits only choose launches; results never depend on them."""
+    if arr is None or len(arr) == 0:
+        return 0
+    T, k = arr["temperature"], arr["top_k"]
+    whole = (T > 0) & (T <= 100) & ~((k >= 1) & (k <= FAST_MAX_K) & (k < vocab))
+    return (N.HINT_WHOLE_SOME if whole.any() else 0) | (N.HINT_WHOLE_ALL if whole.all() else 0)
+
+
+def verify_hints(arr: np.ndarray | None, vocab: int, plain: bool) -> int:
+    """DSR_HINT_VERIFY_FAST when every request's policy has no filter and the
+    call carries no history, bias or allow mask (``plain``)."""
+    if arr is None or len(arr) == 0 or not plain:
+        return 0
+    k = arr["top_k"]
+    ok = ((k == 0) | (k >= vocab)) & (arr["top_p"] >= 1.0) & (arr["min_p"] == 0.0)
+    return N.HINT_VERIFY_FAST if ok.all() else 0
 
 
 @dataclass
@@ -315,7 +344,7 @@ _default_ws = Workspace()
 def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None = None, bias: BiasTable | None = None,
                 allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
                 rng_state: torch.Tensor | None = None, probs: str | None = None, kept: bool = False,
-                workspace: Workspace | None = None, noalloc: bool = False) -> SampleResult:
+                workspace: Workspace | None = None, noalloc: bool = False, hints: int | None = None) -> SampleResult:
     """Sample every row of ``logits [rows, V]`` on the current stream.
 
     ``policies`` is a device tensor made by ``policy_tensor`` or a list of
@@ -327,7 +356,8 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     ``"f64"`` to return the final probabilities.  ``noalloc`` launches
     through ``dsr_sample_rows_noalloc``, whose workspace is the library's own
     device array (at most ``N.NOALLOC_SCRATCH_BYTES``; calls on one device
-    share it, so overlapping calls race).
+    share it, so overlapping calls race).  ``hints`` overrides the
+    DSR_HINT_* bits derived from the policies (they choose launches only).
     """
     lib = N.load()
     _require_cuda(logits, "logits", rows_strided=True)
@@ -367,6 +397,7 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     a = N.SampleArgs()
     a.logits = logits.data_ptr()
     a.dtype = _DTYPES[logits.dtype]
+    a.hints = sample_hints(getattr(policies, "dsr_policies", None), V) if hints is None else hints
     a.rows, a.vocab, a.ld = rows, V, logits.stride(0)
     a.policy = policies.data_ptr()
     if _nonempty(history, "ids"):
@@ -624,7 +655,7 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
                   bias: BiasTable | None = None, allow_bits: torch.Tensor | None = None,
                   eos_offsets: torch.Tensor | None = None, eos_ids: torch.Tensor | None = None,
                   rng_accept: torch.Tensor | None = None, rng_target: torch.Tensor | None = None,
-                  workspace: Workspace | None = None) -> VerifyResult:
+                  workspace: Workspace | None = None, hints: int | None = None) -> VerifyResult:
     """Exact sampled verification of ``rows`` requests with ``K`` drafts each.
 
     ``target [rows, K+1, V]`` and ``draft [rows, K, V]`` are logits; row ``j``
@@ -632,7 +663,8 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     ``u_target`` are pre-drawn uniforms; ``rng_accept`` / ``rng_target``
     (int64 ``[rows, 4]``, see ``pcg64_states``) instead draw them on the
     device from each request's accept / target PCG64 state, which is advanced
-    by exactly the draws the decision uses.
+    by exactly the draws the decision uses.  ``hints`` overrides the
+    DSR_HINT_VERIFY_FAST bit derived from the policies.
     """
     lib = N.load()
     _require_cuda(target, "target")
@@ -676,6 +708,9 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     if allow_bits is not None:
         _require_cuda(allow_bits, "allow_bits")
         a.allow_bits, a.allow_ld = allow_bits.data_ptr(), allow_bits.shape[-1]
+    a.hints = verify_hints(getattr(policies, "dsr_policies", None), V,
+                           not _nonempty(history, "ids") and not _nonempty(bias, "ids") and allow_bits is None) \
+        if hints is None else hints
     a.u_accept = u_accept.data_ptr() if K > 0 and u_accept is not None else None
     a.u_target = u_target.data_ptr() if u_target is not None else None
     if rng_accept is not None and rows > 0:

@@ -62,6 +62,20 @@ constexpr int kHandCapacity = 4;   // too many chunks reach tau, or tau lies out
 constexpr int kHandOrder = 5;      // bf16 key order may differ from float64 order at a boundary
 constexpr int kHandInvalid = 6;    // invalid or fully masked logits (reported in the reference's order)
 
+// Launch modes the host writes into dsr_sample_args_t.hints of the kernel's
+// copy of the arguments (the caller's DSR_HINT_* bits are not passed on).
+constexpr uint32_t kModeDeferWhole = 1u << 8;  // top-k register kernel: leave whole rows untouched
+constexpr uint32_t kModeOnlyWhole = 1u << 9;   // full-vocabulary kernel: decide whole rows only
+
+// A whole row: sampled (0 < T <= 100) without a top-k the register kernel
+// takes, so its filters keep the whole vocabulary or a top-k above 1024.  In
+// a call that launches both bf16 kernels, the top-k register kernel leaves
+// exactly these rows (its kHandTopK hand-over) to the full-vocabulary kernel,
+// which decides exactly these rows.
+__host__ __device__ __forceinline__ bool whole_row(double T, int top_k, int64_t V) {
+  return T > 0.0 && T <= 100.0 && !(top_k >= 1 && top_k <= kFastMaxK && top_k < V);
+}
+
 struct FastLists {
   union {
     uint32_t lut[256][4];                  // allow byte -> four 2 x 16-bit "disallowed" masks (pass 1)
@@ -347,7 +361,7 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
   const int top_k = pol.top_k;
   const bool greedy = T == 0.0;
   if (!(T >= 0.0 && T <= 100.0)) return kHandPolicy;
-  if (!greedy && !(top_k >= 1 && top_k <= kFastMaxK && top_k < V)) return kHandTopK;
+  if (whole_row(T, top_k, V)) return kHandTopK;
 
   const uint32_t bad = max((int)(short)(vmax_s & 0xFFFFu), (int)(short)(vmax_s >> 16)) >= 0x7F80 ||
                        max(vmax_u & 0xFFFFu, vmax_u >> 16) >= 0xFF81u;

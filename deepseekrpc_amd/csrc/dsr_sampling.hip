@@ -156,7 +156,8 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t
   __shared__ FastShared sh;
   const int64_t row = blockIdx.x;
   const int why = fast_sample_row<RNG>(a, row, sh);
-  if (why == 0) return;
+  // A whole row under kModeDeferWhole is the next launch's (k_sample_bf16_full).
+  if (why == 0 || (why == kHandTopK && (a.hints & kModeDeferWhole))) return;
   __syncthreads();
   GenShared& gs = *reinterpret_cast<GenShared*>(&sh);
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
@@ -180,6 +181,9 @@ template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t a) {
   __shared__ FullKernelShared sh;
   const int64_t row = blockIdx.x;
+  // After the top-k register kernel: only the rows it left (uniform; read
+  // before the row's loads are issued, so other rows cost no HBM traffic).
+  if ((a.hints & kModeOnlyWhole) && !whole_row(a.policy[row].temperature, a.policy[row].top_k, a.vocab)) return;
   const int why = full_sample_row<RNG>(a, row, sh.f);
   if (why == 0) return;
   __syncthreads();
@@ -306,6 +310,7 @@ const char* dsr_status_message(int32_t code) {
     case DSR_E_GENERATED: return "generated token counts must be a subset of complete sampling history";
     case DSR_E_HISTORY: return "history needs bounded exact integer token IDs";
     case DSR_E_APPEND: return "a history append holds at most 16384 tokens per row";
+    case DSR_E_HINT: return "request contradicts the call's DSR_HINT_VERIFY_FAST promise";
     default: return "unknown sampling status";
   }
 }
@@ -339,12 +344,32 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
     return DSR_ERR_WORKSPACE;
   if (a.rows == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)a.rows);
+  auto launch_fast = [&](uint32_t mode) {
+    dsr_sample_args_t k = a;
+    k.hints = mode;
+    if (k.rng_state) hipLaunchKernelGGL(k_sample_bf16_fast<true>, grid, dim3(kThreads), 0, s, k);
+    else hipLaunchKernelGGL(k_sample_bf16_fast<false>, grid, dim3(kThreads), 0, s, k);
+  };
+  auto launch_full = [&](uint32_t mode) {
+    dsr_sample_args_t k = a;
+    k.hints = mode;
+    if (k.rng_state) hipLaunchKernelGGL(k_sample_bf16_full<true>, grid, dim3(kThreads), 0, s, k);
+    else hipLaunchKernelGGL(k_sample_bf16_full<false>, grid, dim3(kThreads), 0, s, k);
+  };
   if (fast_path_eligible(a)) {
-    if (a.rng_state) hipLaunchKernelGGL(k_sample_bf16_fast<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL(k_sample_bf16_fast<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    // A bf16 batch with no history or bias: whole rows (no top-k register
+    // cut) go to the full-vocabulary kernel when the caller says it has some.
+    if (a.hints & DSR_HINT_WHOLE_ALL) {
+      launch_full(0u);
+    } else if (a.hints & DSR_HINT_WHOLE_SOME) {
+      launch_fast(kModeDeferWhole);
+      launch_full(kModeOnlyWhole);
+    } else {
+      launch_fast(0u);
+    }
   } else if (full_path_eligible(a)) {
-    if (a.rng_state) hipLaunchKernelGGL(k_sample_bf16_full<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL(k_sample_bf16_full<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    launch_full(0u);
   } else if (split_path_eligible(a)) {
     const int smax = split_max_slices(a.rows);
     hipLaunchKernelGGL(k_split_select, dim3((unsigned)(a.rows * smax)), dim3(kThreads), 0, s, a, smax);
@@ -423,8 +448,13 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   VerifyLayout L = verify_layout(a.workspace, a.rows, a.K, a.vocab);
   L.fast_inputs = !a.pen_off && !a.bias_off && !a.allow_bits;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_verify_dists, dim3((unsigned)(a.rows * slots)), dim3(kThreads), 0, s, a, L);
-  if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  // A call whose requests all take the fast path needs no general-path
+  // distributions; a request breaking that promise gets DSR_E_HINT.
+  L.dists_built = !(L.fast_inputs && (a.hints & DSR_HINT_VERIFY_FAST));
+  if (L.dists_built) {
+    hipLaunchKernelGGL(k_verify_dists, dim3((unsigned)(a.rows * slots)), dim3(kThreads), 0, s, a, L);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  }
   if (L.fast_inputs) {
     const dim3 grid((unsigned)(a.rows * slots * kVerifySplit));
     // 16-byte loads when every row starts on a 16-byte boundary.

@@ -73,6 +73,7 @@ struct VerifyLayout {
   struct Decision* dec;  // [rows] chain outcome handed to the draw kernels
   int64_t rows;
   int fast_inputs;   // no history, bias or allow mask
+  int dists_built;   // k_verify_dists ran before k_verify_chain
 };
 
 __host__ __device__ inline size_t verify_ws_bytes(int64_t rows, int32_t K, int64_t V) {
@@ -107,6 +108,7 @@ __host__ inline VerifyLayout verify_layout(void* ws, int64_t rows, int32_t K, in
   L.dec = (struct Decision*)p;
   L.rows = rows;
   L.fast_inputs = 0;
+  L.dists_built = 1;
   return L;
 }
 
@@ -173,11 +175,10 @@ __device__ __forceinline__ Request request_of(const dsr_verify_args_t& a, int64_
 // ---------------------------------------------------------------------------
 // General path.
 
-__global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ GenShared sh;
-  const int64_t row = blockIdx.x / L.slots;
-  const int slot = (int)(blockIdx.x % L.slots);
-  if (verify_fast_row(a, L, row)) return;
+// Distribution `slot` of general-path request `row`, built in full into its
+// workspace row, its status / one-hot / flags into L.info.
+__device__ __forceinline__ void verify_build_dist(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row, int slot,
+                                  GenShared& sh) {
   const int K = a.K;
   const bool is_target = slot <= K;
   const int j = is_target ? slot : slot - (K + 1);
@@ -221,6 +222,15 @@ __global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, 
     info[1] = (int32_t)d.onehot;
     info[2] = (int32_t)flags;
   }
+}
+
+// One workgroup per distribution of every general-path request.
+__global__ __launch_bounds__(kThreads) void k_verify_dists(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ GenShared sh;
+  const int64_t row = blockIdx.x / L.slots;
+  const int slot = (int)(blockIdx.x % L.slots);
+  if (verify_fast_row(a, L, row)) return;
+  verify_build_dist(a, L, row, slot, sh);
 }
 
 // Categorical draw over max(p - q, 0) / sum (correction_distribution,
@@ -562,69 +572,127 @@ struct StatItem {
       }
     }
   }
-  // Element u (-inf outside [lo, hi); VEC: after mask()).
-  __device__ __forceinline__ double value(const Raw* r, int u) const {
-    X y;
+  // Element u in the logits' own type (float for bf16 / f32, exactly):
+  // -inf outside [lo, hi) (VEC: after mask()).
+  __device__ __forceinline__ X elem(const Raw* r, int u) const {
     if constexpr (VEC) {
       const uint4 v = r[u / W];
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
       const int e = u % W;
-      if constexpr (DT == DSR_BF16) y = __uint_as_float(((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
-      else if constexpr (DT == DSR_F32) y = __uint_as_float(w4[e]);
-      else y = __longlong_as_double((long long)(((unsigned long long)w4[2 * e + 1] << 32) | w4[2 * e]));
-      return (double)y;
+      if constexpr (DT == DSR_BF16) return __uint_as_float(((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
+      else if constexpr (DT == DSR_F32) return __uint_as_float(w4[e]);
+      else return __longlong_as_double((long long)(((unsigned long long)w4[2 * e + 1] << 32) | w4[2 * e]));
     } else {
-      y = r[u];
-      return index_of(u) < hi ? (double)y : -(double)INFINITY;
+      return index_of(u) < hi ? r[u] : -X(INFINITY);
     }
   }
 };
 
-// One share held in registers -> its maximum, the first index holding it,
-// sum exp((v - max) / T) and the NaN/+inf / finite flags.  Each thread sums
-// its exps against its own maximum and rescales once by exp((m_t - M) / T),
-// so the exps need no workgroup step before them.  The exp pass is
-// branch-free: a -inf element adds exactly 0 (exp_nonpos clamps its argument
-// at -746, which underflows), and a NaN or +inf marks the row invalid, whose
-// statistics are then never used.  The first maximum is kept as the slot of
-// the first strict increase, its index formed once.
+// exp((v - m) * iT) for v <= m (or -inf), as 2^(y / 64) with
+// y = (v - m) * iT * 64 / ln 2 clamped at -68,900 (below it the result is
+// 0): k = rint(y), 2^(k / 64) = 2^(k >> 6) * 2^((k & 63) / 64) from the
+// table, and 2^((y - k) / 64) = exp(r), r = (y - k) ln 2 / 64, |r| <= 0.0055,
+// by its degree-4 Taylor polynomial (truncation below 4e-14 relative).  v - m
+// is exact for float inputs; the result is within about 1e-13 relative of
+// exp, far inside the accept tests' 2^-40 band.  k & 63 indexes the table
+// for every input, NaN included.
+struct ExpTerm {
+  double m, c1;  // c1 = iT * 64 / ln 2
+  const double* etab;
+  __device__ __forceinline__ double operator()(double v) const {
+    constexpr double L = 0x1.62e42fefa39efp-7;  // ln 2 / 64
+    constexpr double a2 = L * L / 2, a3 = L * L * L / 6, a4 = L * L * L * L / 24;
+    const double y = fmax((v - m) * c1, -68900.0);
+    const double kd = rint(y);
+    const double f = y - kd;  // exact, |f| <= 1/2
+    double p = fma(a4, f, a3);
+    p = fma(p, f, a2);
+    p = fma(p, f, L);
+    p = fma(p, f, 1.0);
+    const int k = (int)kd;
+    return ldexp(etab[k & 63] * p, k >> 6);
+  }
+};
+
+// Order key of a float (increasing with the value; -inf -> 0x007FFFFF).
+__device__ __forceinline__ uint32_t float_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// One share held in registers -> its maximum, the first index holding it
+// (greedy rows only), sum exp((v - max) / T) and the NaN/+inf / finite flags.
+// The maximum pass works in the logits' own type: for bf16 / f32 a float
+// maximum plus the signed and unsigned maxima of the raw bits, which reveal
+// +inf / +NaN (signed >= 0x7F800000) and -NaN (unsigned > 0xFF800000); the
+// workgroup then needs one 32-bit key reduction for both.  Each thread sums
+// its exps against its own maximum (ExpTerm) as soon as its loads land and
+// rescales once by exp((m_t - M) / T).  A -inf element adds exactly 0; a NaN
+// or +inf marks the row invalid, whose statistics are then never used.
 template <int DT, bool VEC>
 __device__ __forceinline__ void stat_share(const dsr_verify_args_t& a, const VerifyLayout& L,
                                            const StatItem<DT, VEC>& it, typename StatItem<DT, VEC>::Raw* x,
                                            StatShared& sm) {
+  using X = typename LogitT<DT>::T;
   const double* etab = sm.etab;
   const int64_t row = it.rs / L.slots;
   if (!verify_fast_row(a, L, row)) return;  // uniform over the workgroup
   const double T = policy_of(a, row).temperature;
   const bool greedy = T == 0.0;
   it.mask(x);
-  double m = -INFINITY;
-  bool nan = false;
-  int mu = -1;  // slot of the first maximum (a strict comparison in increasing index order)
+  X m = -X(INFINITY);
+  double Mg;
+  uint32_t flags;
+  if constexpr (DT == DSR_F64) {
+    bool nan = false;
 #pragma unroll
-  for (int u = 0; u < kStatPer; ++u) {
-    const double v = it.value(x, u);
-    nan |= v != v;
-    if (v > m) {
-      m = v;
-      mu = u;
+    for (int u = 0; u < kStatPer; ++u) {
+      const double v = it.elem(x, u);
+      nan |= v != v;
+      m = fmax(m, v);  // a NaN operand is ignored; the flag covers it
     }
-  }
-  // 1: a NaN or +inf logit; 2: a finite one.
-  const uint32_t fl = ((nan || m == (double)INFINITY) ? 1u : 0u) | (m > -(double)INFINITY ? 2u : 0u);
-  const double iT = greedy ? 0.0 : 1.0 / T;
-  double s = 0.0;
-  if (!greedy) {
-    const double mm = m > -(double)INFINITY ? m : 0.0;  // a thread with no finite value sums exact zeros
+    const uint32_t fl = ((nan || m == (double)INFINITY) ? 1u : 0u) | (m > -(double)INFINITY ? 2u : 0u);
+    Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
+    flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
+  } else {
+    int32_t smax = INT_MIN;
+    uint32_t umax = 0u;
 #pragma unroll
-    for (int u = 0; u < kStatPer; ++u) s += exp_nonpos((it.value(x, u) - mm) * iT, etab);
+    for (int u = 0; u < kStatPer; ++u) {
+      const float v = it.elem(x, u);
+      const uint32_t b = __float_as_uint(v);
+      smax = max(smax, (int32_t)b);
+      umax = max(umax, b);
+      m = fmaxf(m, v);
+    }
+    const bool bad = smax >= 0x7F800000 || umax > 0xFF800000u;
+    const uint32_t K = stat_reduce(bad ? 0xFFFFFFFFu : float_key(m), sm.su, 0u, OpMax());
+    Mg = K == 0xFFFFFFFFu ? (double)INFINITY : (double)key_float(K);
+    flags = (K == 0xFFFFFFFFu ? 1u : 0u) | (K > 0x007FFFFFu && K != 0xFFFFFFFFu ? 2u : 0u);
   }
-  const double Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
-  const uint32_t flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
-  const long long amg =
-      stat_reduce(m == Mg && mu >= 0 ? it.index_of(mu) : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
-  const double sc = s > 0.0 ? s * exp_nonpos((m - Mg) * iT, etab) : 0.0;
-  const double Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
+  long long amg = LLONG_MAX;
+  double Sg = 0.0;
+  if (greedy) {
+    // The first index holding the maximum: the thread's first slot equal to
+    // its own maximum, then the smallest such index over the threads at Mg.
+    int mu = -1;
+#pragma unroll
+    for (int u = kStatPer - 1; u >= 0; --u)
+      if ((double)it.elem(x, u) == (double)m) mu = u;
+    amg = stat_reduce((double)m == Mg && mu >= 0 ? it.index_of(mu) : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
+  } else {
+    const double iT = 1.0 / T;
+    const double mm = (double)m > -(double)INFINITY ? (double)m : 0.0;  // no finite value: exact zeros
+    const ExpTerm term{mm, iT * 92.33248261689366, etab};
+    double s = 0.0;
+#pragma unroll
+    for (int u = 0; u < kStatPer; ++u) s += term((double)it.elem(x, u));
+    const double sc = s > 0.0 ? s * exp_nonpos(((double)m - Mg) * iT, etab) : 0.0;
+    Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
+  }
   if (threadIdx.x == 0) {
     VerifyPart p;
     p.m = Mg;
@@ -690,6 +758,14 @@ __global__ __launch_bounds__(kThreads) void k_verify_chain(dsr_verify_args_t a, 
   __shared__ int32_t seos[kEosCached];
   const int64_t row = blockIdx.x;
   if (!verify_fast_row(a, L, row)) {
+    if (!L.dists_built) {  // the call promised every request is fast (DSR_HINT_VERIFY_FAST); this one is not
+      if (threadIdx.x == 0) {
+        d.status = DSR_E_HINT;
+        d.flags = 0;
+        write_decision(a, row, d);
+      }
+      return;
+    }
     general_decide(a, L, row, sh, d);
     return;
   }

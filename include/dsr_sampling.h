@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSR_ABI_VERSION 2
+#define DSR_ABI_VERSION 3
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
@@ -62,6 +62,7 @@ extern "C" {
 #define DSR_E_HISTORY 13        /* history.py:30-36: token id outside the vocabulary, or a
                                    malformed history table */
 #define DSR_E_APPEND 14         /* more than DSR_MAX_APPEND new tokens for one row */
+#define DSR_E_HINT 15           /* a verifier request breaks the call's DSR_HINT_VERIFY_FAST */
 
 /* Launch / argument errors (return values). */
 #define DSR_ERR_ARG (-1)
@@ -79,6 +80,28 @@ extern "C" {
                                    workgroups: top-k <= 1024, greedy, top-p / min-p whose
                                    kept set lies among the row's 512 largest values, or no
                                    filter with no history or bias) */
+
+/* Kernel-choice hints (dsr_sample_args_t.hints, dsr_verify_args_t.hints):
+ * statements about the batch's policies that let the library choose its
+ * launches on the host, where the device-resident policies cannot be read.
+ * 0 makes no statement.
+ *
+ * DSR_HINT_WHOLE_SOME: at least one row is sampled (temperature > 0) with
+ *   no top-k or a top-k above 1024; in a bf16 batch with no history or bias
+ *   such rows then run the full-vocabulary kernel in a second launch instead
+ *   of the general path.
+ * DSR_HINT_WHOLE_ALL: every row is such a row; that batch runs the
+ *   full-vocabulary kernel alone.
+ *   The two WHOLE hints change no result: a row that contradicts them is
+ *   still decided exactly, by a slower path.
+ * DSR_HINT_VERIFY_FAST: a promise that every request has a policy with no
+ *   filter (top_k 0 or >= vocab, top_p 1, min_p 0) and that the call passes
+ *   no history, bias or allow mask, so the launch that builds general-path
+ *   distributions is left out.  A request that breaks the promise is not
+ *   decided: its status is DSR_E_HINT (the others are unaffected). */
+#define DSR_HINT_WHOLE_SOME 1u
+#define DSR_HINT_WHOLE_ALL 2u
+#define DSR_HINT_VERIFY_FAST 4u
 
 /* Verifier stop reasons (sampling.py:286,289,294). */
 #define DSR_STOP_NONE 0
@@ -121,7 +144,7 @@ typedef struct dsr_policy {
 typedef struct dsr_sample_args {
   const void* logits;          /* [rows, ld] of dtype */
   int32_t dtype;               /* DSR_BF16 | DSR_F32 | DSR_F64 */
-  int32_t reserved0;
+  uint32_t hints;              /* DSR_HINT_* bits, or 0 */
   int64_t rows;
   int64_t vocab;               /* 1 .. 129280 */
   int64_t ld;                  /* elements between rows, >= vocab */
@@ -201,6 +224,8 @@ typedef struct dsr_verify_args {
   size_t workspace_bytes;
   uint64_t* rng_accept;        /* [rows, 4] PCG64 states of the accept domain, or NULL */
   uint64_t* rng_target;        /* [rows, 4] PCG64 states of the target domain, or NULL */
+  uint32_t hints;              /* DSR_HINT_* bits, or 0 */
+  uint32_t reserved;           /* must be 0 */
 } dsr_verify_args_t;
 
 /* ABI gate, after the reference's abi_version() (native/bindings.cpp:25). */

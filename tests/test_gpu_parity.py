@@ -346,6 +346,35 @@ def test_verify_fast_and_general_paths_match_the_oracle(dtype):
     assert int(fast.status.abs().sum()) == 0
 
 
+def test_verify_hint_broken_by_a_filter_is_reported():
+    """DSR_HINT_VERIFY_FAST forced on requests that carry filters: the
+    general-path launch is left out, so those requests get DSR_E_HINT and
+    consume no draws, and every filter-free request decides as without the
+    hint."""
+    rng = np.random.default_rng(12)
+    R, K, V = 8, 3, 5003
+    dev = "cuda"
+    tgt = torch.from_numpy(rng.normal(0, 2, (R, K + 1, V)).astype(np.float32)).to(dev)
+    drf = (tgt[:, :K] + torch.from_numpy(rng.normal(0, 0.5, (R, K, V)).astype(np.float32)).to(dev)).contiguous()
+    pols = [[dict(), dict(top_k=50), dict(top_p=0.9, temperature=0.8), dict(min_p=0.02)][r % 4] for r in range(R)]
+    draw = batch.sample_rows(drf.reshape(R * K, V).contiguous(), [dict(top_k=50)] * (R * K),
+                             uniforms=torch.from_numpy(rng.random(R * K)).to(dev))
+    ids = draw.tokens.reshape(R, K).contiguous()
+    ua, ut = torch.from_numpy(rng.random((R, K))).to(dev), torch.from_numpy(rng.random(R)).to(dev)
+    lim = torch.full((R,), 10, dtype=torch.int32, device=dev)
+    plain = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim)
+    forced = batch.verify_drafts(tgt, drf, ids, pols, ua, ut, lim, hints=N.HINT_VERIFY_FAST)
+    torch.cuda.synchronize()
+    assert plain.args.hints == 0
+    fast = torch.arange(R, device=dev) % 4 == 0
+    for k in ("status", "accepted", "ids", "count", "pending", "stop", "used_accept", "used_target", "flags"):
+        assert torch.equal(getattr(plain, k)[fast], getattr(forced, k)[fast]), k
+    assert (plain.status[fast] == 0).all() and (plain.status[1::4] == 0).all()
+    assert (forced.status[~fast] == N.E_HINT).all()
+    assert (forced.used_accept[~fast] == 0).all() and (forced.used_target[~fast] == 0).all()
+    assert (forced.ids[~fast] == -1).all() and (forced.count[~fast] == 0).all()
+
+
 @pytest.mark.parametrize("case", META["verify"], ids=lambda c: c["name"])
 def test_verify_golden_on_gpu(case):
     dev = "cuda"

@@ -7,7 +7,8 @@ import os
 import numpy as np
 import pytest
 
-from deepseekrpc_amd import batch, jsonutil
+from deepseekrpc_amd import _native as N
+from deepseekrpc_amd import batch, jsonutil, workloads
 from deepseekrpc_amd.jsonutil import ValidationError
 from deepseekrpc_amd.sampling import DOMAINS, RandomStreams, SamplingPolicy
 
@@ -125,3 +126,27 @@ def test_policy_packing_layout():
     assert arr.dtype.itemsize == 56
     assert arr[0]["temperature"] == 0.5 and arr[0]["top_k"] == 7 and arr[0]["top_p"] == 1.0
     assert arr[1]["top_p"] == 0.25 and arr[1]["repetition_penalty"] == 1.0
+
+
+def _mixed_policies(rows=96):
+    wp, cp = workloads.whole().policies, workloads.c3().policies
+    return [wp[r] if r % 3 == 0 else cp[r] for r in range(rows)]
+
+
+def test_hints_follow_the_policies():
+    arr = batch.policy_array(workloads.whole().policies)
+    assert batch.sample_hints(arr, 129280) == N.HINT_WHOLE_SOME | N.HINT_WHOLE_ALL
+    assert batch.sample_hints(batch.policy_array(workloads.c3().policies), 129280) == 0
+    assert batch.sample_hints(batch.policy_array(_mixed_policies()), 129280) == N.HINT_WHOLE_SOME
+    # Greedy rows and rows with a top-k the register kernel takes are not whole.
+    arr = batch.policy_array([dict(temperature=0.0), dict(top_k=1024), dict(top_k=1025), dict(top_k=8, top_p=0.5)])
+    assert batch.sample_hints(arr, 129280) == N.HINT_WHOLE_SOME
+    assert batch.sample_hints(batch.policy_array([dict(top_k=8)]), 8) == N.HINT_WHOLE_ALL | N.HINT_WHOLE_SOME
+
+
+def test_verify_hint_needs_filter_free_policies_and_plain_inputs():
+    arr = batch.policy_array([dict(), dict(temperature=0.5), dict(top_k=129280)])
+    assert batch.verify_hints(arr, 129280, True) == N.HINT_VERIFY_FAST
+    assert batch.verify_hints(arr, 129280, False) == 0
+    for bad in (dict(top_k=50), dict(top_p=0.9), dict(min_p=0.1)):
+        assert batch.verify_hints(batch.policy_array([dict(), bad]), 129280, True) == 0

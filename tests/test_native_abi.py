@@ -44,7 +44,8 @@ def test_flag_and_status_constants_match_header():
     defs = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (DSR_\w+) \(?(-?\d+)u?\)?", text)}
     for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
                  "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
-                 "E_GENERATED", "E_HISTORY", "E_APPEND", "MAX_APPEND"):
+                 "E_GENERATED", "E_HISTORY", "E_APPEND", "E_HINT", "MAX_APPEND", "HINT_WHOLE_SOME", "HINT_WHOLE_ALL",
+                 "HINT_VERIFY_FAST"):
         assert getattr(N, name) == defs["DSR_" + name], name
     assert N.ABI_VERSION == defs["DSR_ABI_VERSION"]
 
