@@ -455,12 +455,12 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
     hipLaunchKernelGGL(k_verify_dists, dim3((unsigned)(a.rows * slots)), dim3(kThreads), 0, s, a, L);
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
   }
+  // 16-byte loads when every row starts on a 16-byte boundary.
+  const size_t elt = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
+  const bool vec = ((uintptr_t)a.target & 15u) == 0 && (a.K == 0 || ((uintptr_t)a.draft & 15u) == 0) &&
+                   ((size_t)a.ld * elt) % 16 == 0;
   if (L.fast_inputs) {
     const dim3 grid((unsigned)(a.rows * slots * kVerifySplit));
-    // 16-byte loads when every row starts on a 16-byte boundary.
-    const size_t elt = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
-    const bool vec = ((uintptr_t)a.target & 15u) == 0 && (a.K == 0 || ((uintptr_t)a.draft & 15u) == 0) &&
-                     ((size_t)a.ld * elt) % 16 == 0;
     if (a.dtype == DSR_BF16) {
       if (vec) hipLaunchKernelGGL((k_verify_stats<DSR_BF16, true>), grid, dim3(kStatThreads), 0, s, a, L);
       else hipLaunchKernelGGL((k_verify_stats<DSR_BF16, false>), grid, dim3(kStatThreads), 0, s, a, L);
@@ -477,9 +477,16 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   if (L.fast_inputs) {
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
     const dim3 dgrid((unsigned)(a.rows * kDrawSplit));
-    if (a.dtype == DSR_BF16) hipLaunchKernelGGL(k_verify_draw<DSR_BF16>, dgrid, dim3(kStatThreads), 0, s, a, L);
-    else if (a.dtype == DSR_F32) hipLaunchKernelGGL(k_verify_draw<DSR_F32>, dgrid, dim3(kStatThreads), 0, s, a, L);
-    else hipLaunchKernelGGL(k_verify_draw<DSR_F64>, dgrid, dim3(kStatThreads), 0, s, a, L);
+    if (a.dtype == DSR_BF16) {
+      if (vec) hipLaunchKernelGGL((k_verify_draw<DSR_BF16, true>), dgrid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_draw<DSR_BF16, false>), dgrid, dim3(kStatThreads), 0, s, a, L);
+    } else if (a.dtype == DSR_F32) {
+      if (vec) hipLaunchKernelGGL((k_verify_draw<DSR_F32, true>), dgrid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_draw<DSR_F32, false>), dgrid, dim3(kStatThreads), 0, s, a, L);
+    } else {
+      if (vec) hipLaunchKernelGGL((k_verify_draw<DSR_F64, true>), dgrid, dim3(kStatThreads), 0, s, a, L);
+      else hipLaunchKernelGGL((k_verify_draw<DSR_F64, false>), dgrid, dim3(kStatThreads), 0, s, a, L);
+    }
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
     hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
   }

@@ -523,16 +523,18 @@ struct StatItem {
     else return lo + t + (int64_t)u * kStatThreads;
   }
   // The raw words of this thread's elements: 16-byte vectors (VEC) or one
-  // element per slot at a clamped index; decoded and masked by value().
+  // element per slot at a clamped index; decoded (and masked) by elem().
   static constexpr int kRaw = VEC ? kStatPer / W : kStatPer;
   using Raw = typename std::conditional<VEC, uint4, X>::type;
   // Issues this thread's loads; nothing here waits for them.
   __device__ __forceinline__ void load(const dsr_verify_args_t& a, const VerifyLayout& L, Raw* r) const {
     const char* base = verify_logits(a, rs / L.slots, (int)(rs % L.slots));
     if constexpr (VEC) {
-      // The row as a buffer: out-of-range vectors read as 0 and are masked by value().
-      const __amdgpu_buffer_rsrc_t rsrc =
-          __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(a.vocab * kElt), 0x00020000);
+      // The row as a buffer of whole 16-byte vectors (V rounded up to W
+      // elements, inside the row since ld is a multiple of W): vectors past
+      // it read as 0, and every element at or past hi is masked by mask().
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)base, (short)0, (int)(((a.vocab + W - 1) / W) * W * kElt), 0x00020000);
 #pragma unroll
       for (int q = 0; q < kRaw; ++q) {
         const int64_t e0 = index_of(q * W);
@@ -549,7 +551,7 @@ struct StatItem {
   }
   // VEC: elements at or past hi become -inf in the raw words, once, after
   // the loads have landed (a vector is wholly in range except at the end of
-  // a share), so value() needs no index test.
+  // a share), so elem() needs no index test.
   __device__ __forceinline__ void mask(Raw* r) const {
     if constexpr (VEC) {
 #pragma unroll
@@ -613,6 +615,9 @@ struct ExpTerm {
     return ldexp(etab[k & 63] * p, k >> 6);
   }
 };
+
+// ExpTerm's c1 for temperature T (every user forms it this one way).
+__device__ __forceinline__ double exp_scale(double T) { return (1.0 / T) * 92.33248261689366; }
 
 // Order key of a float (increasing with the value; -inf -> 0x007FFFFF).
 __device__ __forceinline__ uint32_t float_key(float v) {
@@ -686,7 +691,7 @@ __device__ __forceinline__ void stat_share(const dsr_verify_args_t& a, const Ver
   } else {
     const double iT = 1.0 / T;
     const double mm = (double)m > -(double)INFINITY ? (double)m : 0.0;  // no finite value: exact zeros
-    const ExpTerm term{mm, iT * 92.33248261689366, etab};
+    const ExpTerm term{mm, exp_scale(T), etab};
     double s = 0.0;
 #pragma unroll
     for (int u = 0; u < kStatPer; ++u) s += term((double)it.elem(x, u));
@@ -827,19 +832,23 @@ __global__ __launch_bounds__(kThreads) void k_verify_chain(dsr_verify_args_t a, 
 }
 
 // The draw's weights at token i: p_j (bonus) or max(p_j - q_j, 0)
-// (replacement, correction_distribution, sampling.py:131-139).
+// (replacement, correction_distribution, sampling.py:131-139), each
+// probability exp((v - M) / T) / s1 by ExpTerm.  The share sums of the draw
+// kernel and the token walk of the finish use this same function.
 struct DrawWeights {
   const char* P;
   const char* Q;
   int dt;
   bool resid;
-  double Mp, iTp, isp, Mq, isq;
-  const double* etab;
-  __device__ __forceinline__ double operator()(int64_t i) const {
-    const double p = exp_nonpos((load_logit(P, dt, i) - Mp) * iTp, etab) * isp;
+  double isp, isq;
+  ExpTerm ep, eq;
+  __device__ __forceinline__ double weight(double vp, double vq) const {
+    const double p = ep(vp) * isp;
     if (!resid) return p;
-    const double q = exp_nonpos((load_logit(Q, dt, i) - Mq) * iTp, etab) * isq;
-    return fmax(p - q, 0.0);
+    return fmax(p - eq(vq) * isq, 0.0);
+  }
+  __device__ __forceinline__ double operator()(int64_t i) const {
+    return weight(load_logit(P, dt, i), resid ? load_logit(Q, dt, i) : 0.0);
   }
 };
 
@@ -847,87 +856,17 @@ __device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, 
                                                     const Decision& d, const double* etab) {
   const int K = a.K;
   const VerifyStat* st = L.stat + row * L.slots;
+  const double c1 = exp_scale(a.policy[row].temperature);
   DrawWeights w;
   w.resid = d.next == 1;
   w.P = verify_logits(a, row, d.draw_j);
   w.Q = w.resid ? verify_logits(a, row, K + 1 + d.draw_j) : nullptr;
   w.dt = a.dtype;
-  w.iTp = 1.0 / a.policy[row].temperature;
-  w.Mp = st[d.draw_j].M;
   w.isp = 1.0 / st[d.draw_j].s1;
-  w.Mq = w.resid ? st[K + 1 + d.draw_j].M : 0.0;
   w.isq = w.resid ? 1.0 / st[K + 1 + d.draw_j].s1 : 0.0;
-  w.etab = etab;
+  w.ep = ExpTerm{st[d.draw_j].M, c1, etab};
+  w.eq = ExpTerm{w.resid ? st[K + 1 + d.draw_j].M : 0.0, c1, etab};
   return w;
-}
-
-// Step 3: share g of a pending draw, 64-token blocks in index order, one
-// per wave step (lane l takes token l of the block, so each load is
-// coalesced): each block's weight sum is kept for step 4's search; the
-// share's sum, positive count and first positive index go to its DrawPart.
-// Instantiated per logit type, so every load of the share is issued before
-// the first weight needs one.
-template <int DT>
-__global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ double etab[64];
-  __shared__ double sf[kStatWaves];
-  __shared__ long long si[2][kStatWaves];
-  const int64_t row = blockIdx.x / kDrawSplit;
-  const int g = (int)(blockIdx.x % kDrawSplit);
-  if (!verify_fast_row(a, L, row)) return;
-  const Decision d = L.dec[row];
-  if (d.status != DSR_OK || d.next == 0) return;
-  exp_table_init(etab);
-  __syncthreads();
-  const DrawWeights wf = draw_weights(a, L, row, d, etab);
-  const int64_t V = a.vocab;
-  const int l = lane_id(), w = wave_id();
-  using X = typename LogitT<DT>::T;
-  X pv[kStatPer], qv[kStatPer];
-#pragma unroll
-  for (int u = 0; u < kStatPer; ++u) {
-    const int64_t i = ((int64_t)g * kDrawBlocks + w * kStatPer + u) * 64 + l;
-    const int64_t ic = i < V ? i : V - 1;  // past the row: any in-range element, weight forced to 0 below
-    pv[u] = logit_as<DT>(wf.P, ic);
-    qv[u] = wf.resid ? logit_as<DT>(wf.Q, ic) : X(0);
-  }
-  double acc = 0.0;
-  long long npos = 0, first = LLONG_MAX;
-  double* bs = L.bsum + row * kDrawParts + (int64_t)g * kDrawBlocks;
-#pragma unroll
-  for (int u = 0; u < kStatPer; ++u) {
-    const int blk = w * kStatPer + u;                     // block within the share
-    const int64_t i = ((int64_t)g * kDrawBlocks + blk) * 64 + l;  // token of this lane
-    double x = exp_nonpos(((double)pv[u] - wf.Mp) * wf.iTp, etab) * wf.isp;
-    if (wf.resid) x = fmax(x - exp_nonpos(((double)qv[u] - wf.Mq) * wf.iTp, etab) * wf.isq, 0.0);
-    x = i < V ? x : 0.0;
-    const double sum = wave_reduce_dpp(x, OpSum());
-    const unsigned long long pb = __ballot(x > 0.0);
-    if (l == 0) bs[blk] = sum;
-    acc += sum;
-    npos += __popcll(pb);
-    if (pb && first == LLONG_MAX) first = i - l + (__ffsll((long long)pb) - 1);
-  }
-  // Blocks in index order: wave w holds blocks 16w .. 16w+15.
-  if (l == 0) {
-    sf[w] = acc;
-    si[0][w] = npos;
-    si[1][w] = first;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    DrawPart p;
-    p.sum = 0.0;
-    p.npos = 0;
-    p.first = LLONG_MAX;
-    for (int q = 0; q < kStatWaves; ++q) {
-      p.sum += sf[q];
-      p.npos += si[0][q];
-      if (si[1][q] < p.first) p.first = si[1][q];
-    }
-    p.pad = 0;
-    L.dpart[row * kDrawSplit + g] = p;
-  }
 }
 
 // The 64-token block of share `owner` that holds the crossing of thr: one
@@ -962,16 +901,12 @@ __device__ void block_cdf_search(int64_t V, const double* bsum, int owner, WF wf
   margin = m | m2;
 }
 
-// Step 4, one wave per request with a pending draw: combine the shares in
-// index order, then search the share that holds the crossing of u * total.
-__global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, VerifyLayout L) {
-  __shared__ double etab[64];
-  const int64_t row = blockIdx.x;
-  if (!verify_fast_row(a, L, row)) return;
-  Decision d = L.dec[row];
-  if (d.status != DSR_OK || d.next == 0) return;
-  exp_table_init(etab);
-  __syncthreads();
+// The end of a pending draw, run by one wave: combine the kDrawSplit shares
+// in index order, then search the share that holds the crossing of
+// u * total, and write the decision.  d is the workgroup's LDS copy of the
+// request's decision (lane 0 completes it).
+__device__ void verify_finish_wave(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row, Decision& d,
+                                   const double* etab) {
   const DrawWeights wf = draw_weights(a, L, row, d, etab);
   // Lane q holds share q; sums and the share prefix come from fixed-order
   // wave reductions and scans.
@@ -1021,7 +956,7 @@ __global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, Verif
       margin |= m2;
     }
   }
-  if (threadIdx.x == 0) {
+  if (lane_id() == 0) {
     if (margin) d.flags |= DSR_FLAG_MARGIN;
     if (status != DSR_OK) {
       d.status = status;
@@ -1031,6 +966,146 @@ __global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, Verif
     }
     write_decision(a, row, d);
   }
+}
+
+// Step 3: share g of a pending draw, 4,096 tokens, 1,024 per wave.  Lane l
+// of wave w holds kDrawPer tokens as kDrawPer / W groups of W consecutive
+// ones (W = 16 bytes of logits): group q is tokens
+// g * 4096 + w * 1024 + (64 q + l) W .. + W - 1, so each load instruction of
+// the wave reads 1 KB in one piece.  The 64-token block b of the wave
+// (q = b / W) is then held by the LB = 64 / W lanes l with l / LB = b % W:
+// each lane sums its W weights in index order, a butterfly over those lanes
+// gives the block sum (bitwise the same in each of them), and the block sums
+// go to L.bsum for the search.  The share's sum, positive count and first
+// positive index go to its DrawPart.  VEC (rows 16-byte aligned): buffer
+// loads, past the row reading as 0 and given weight 0.
+constexpr int kDrawPer = 16;  // tokens per lane
+static_assert(kStatThreads * kDrawPer == kDrawBlocks * 64, "a draw workgroup covers its blocks");
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ double etab[64];
+  __shared__ double sf[kStatWaves];
+  __shared__ long long si[2][kStatWaves];
+  __shared__ Decision sd;
+  using X = typename LogitT<DT>::T;
+  constexpr int kElt = DT == DSR_BF16 ? 2 : (int)sizeof(X);
+  constexpr int W = 16 / kElt;       // tokens per 16-byte group
+  constexpr int NQ = kDrawPer / W;   // groups per lane
+  constexpr int LB = 64 / W;         // lanes per 64-token block
+  static_assert(NQ * W == kDrawPer && LB * W == 64, "groups tile the lane's tokens and the blocks");
+  const int64_t row = blockIdx.x / kDrawSplit;
+  const int g = (int)(blockIdx.x % kDrawSplit);
+  if (!verify_fast_row(a, L, row)) return;
+  const int status = L.dec[row].status, next = L.dec[row].next;
+  if (status != DSR_OK || next == 0) return;
+  exp_table_init(etab);
+  if (threadIdx.x == 0) sd = L.dec[row];
+  __syncthreads();
+  const DrawWeights wf = draw_weights(a, L, row, sd, etab);
+  const int64_t V = a.vocab;
+  const int l = lane_id(), w = wave_id();
+  const int64_t wbase = (int64_t)g * (kDrawBlocks * 64) + (int64_t)w * 1024;  // this wave's first token
+  auto token = [&](int q, int e) { return wbase + (int64_t)(64 * q + l) * W + e; };
+  X pv[kDrawPer], qv[kDrawPer];
+  if constexpr (VEC) {
+    // Whole 16-byte groups (V rounded up to W elements, inside the row since
+    // ld is a multiple of W); elements past V get weight 0 below.
+    const int bytes = (int)(((V + W - 1) / W) * W * kElt);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)wf.P, (short)0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(wf.resid ? wf.Q : wf.P), (short)0, bytes, 0x00020000);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t e0 = token(q, 0);
+      const int off = e0 < V ? (int)(e0 * kElt) : 0x7FFFFFF0;
+      const auto vp = __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 0);
+      const auto vq = __builtin_amdgcn_raw_buffer_load_b128(rq, wf.resid ? off : 0x7FFFFFF0, 0, 0);
+      const uint32_t wp[4] = {vp[0], vp[1], vp[2], vp[3]}, wq[4] = {vq[0], vq[1], vq[2], vq[3]};
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        if constexpr (DT == DSR_BF16) {
+          pv[q * W + e] = __uint_as_float(((wp[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
+          qv[q * W + e] = __uint_as_float(((wq[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) << 16);
+        } else if constexpr (DT == DSR_F32) {
+          pv[q * W + e] = __uint_as_float(wp[e]);
+          qv[q * W + e] = __uint_as_float(wq[e]);
+        } else {
+          pv[q * W + e] = __longlong_as_double((long long)(((unsigned long long)wp[2 * e + 1] << 32) | wp[2 * e]));
+          qv[q * W + e] = __longlong_as_double((long long)(((unsigned long long)wq[2 * e + 1] << 32) | wq[2 * e]));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        const int64_t i = token(q, e);
+        const int64_t ic = i < V ? i : V - 1;  // past the row: any in-range element, weight forced to 0 below
+        pv[q * W + e] = logit_as<DT>(wf.P, ic);
+        qv[q * W + e] = wf.resid ? logit_as<DT>(wf.Q, ic) : X(0);
+      }
+    }
+  }
+  double lane_sum = 0.0;   // this lane's block sums, counted once per block (lanes l % LB == 0)
+  long long npos = 0, first = LLONG_MAX;
+  double* bs = L.bsum + row * kDrawParts + (int64_t)g * kDrawBlocks + w * 16;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    double part = 0.0;
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      const int64_t i = token(q, e);
+      const double x = i < V ? wf.weight((double)pv[q * W + e], (double)qv[q * W + e]) : 0.0;
+      part += x;
+      npos += x > 0.0 ? 1 : 0;
+      first = (first == LLONG_MAX && x > 0.0) ? i : first;
+    }
+    // Block sum over the LB lanes holding the block (unconditional butterfly).
+#pragma unroll
+    for (int off = 1; off < LB; off <<= 1) part += __shfl_xor(part, off);
+    if (l % LB == 0) {
+      bs[q * W + l / LB] = part;
+      lane_sum += part;
+    }
+  }
+  const double ws = wave_reduce_dpp(lane_sum, OpSum());
+  const long long wn = wave_reduce_dpp(npos, OpSum());
+  const long long wfst = wave_reduce_dpp(first, OpMin());
+  if (l == 0) {
+    sf[w] = ws;
+    si[0][w] = wn;
+    si[1][w] = wfst;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    DrawPart p;
+    p.sum = 0.0;
+    p.npos = 0;
+    p.first = LLONG_MAX;
+    for (int q = 0; q < kStatWaves; ++q) {
+      p.sum += sf[q];
+      p.npos += si[0][q];
+      if (si[1][q] < p.first) p.first = si[1][q];
+    }
+    p.pad = 0;
+    L.dpart[row * kDrawSplit + g] = p;
+  }
+}
+
+// Step 4, one wave per request with a pending draw (after k_verify_draw:
+// the kernel boundary orders every share's block sums and part before it).
+__global__ __launch_bounds__(64) void k_verify_finish(dsr_verify_args_t a, VerifyLayout L) {
+  __shared__ double etab[64];
+  __shared__ Decision sd;
+  const int64_t row = blockIdx.x;
+  if (!verify_fast_row(a, L, row)) return;
+  const int status = L.dec[row].status, next = L.dec[row].next;
+  if (status != DSR_OK || next == 0) return;
+  exp_table_init(etab);
+  if (threadIdx.x == 0) sd = L.dec[row];
+  __syncthreads();
+  verify_finish_wave(a, L, row, sd, etab);
 }
 
 }  // namespace dsr
