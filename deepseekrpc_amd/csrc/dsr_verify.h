@@ -31,10 +31,21 @@ namespace dsr {
 
 constexpr int kStatThreads = 256;   // statistics workgroups: 4 waves, several resident per CU
 constexpr int kStatWaves = kStatThreads / 64;
-constexpr int kStatPer = 16;        // logits per thread of one share
-constexpr int kVerifySplit = 32;    // shares per distribution row
+#ifndef DSR_STAT_PER
+#define DSR_STAT_PER 16
+#endif
+#ifndef DSR_VERIFY_SPLIT
+#define DSR_VERIFY_SPLIT 32
+#endif
+#ifndef DSR_STAT_AUX
+#define DSR_STAT_AUX 2  // non-temporal: each logit is read once by this pass
+#endif
+constexpr int kStatPer = DSR_STAT_PER;        // logits per thread of one share
+constexpr int kVerifySplit = DSR_VERIFY_SPLIT;  // shares per distribution row
+constexpr int kStatAux = DSR_STAT_AUX;        // cache policy bits of the statistics loads
 constexpr int kDrawSplit = 32;   // workgroups per request (replacement / bonus draw)
-constexpr int kDrawBlocks = kStatWaves * kStatPer;  // 64-token blocks per draw workgroup (one per wave step)
+constexpr int kDrawPer = 16;                         // tokens per lane of a draw workgroup
+constexpr int kDrawBlocks = kStatWaves * kDrawPer;   // 64-token blocks per draw workgroup
 constexpr int kDrawParts = kDrawSplit * kDrawBlocks;  // block partial sums per request
 static_assert((int64_t)kDrawParts * 64 >= DSR_MAX_VOCAB, "the draw blocks cover a row");
 constexpr size_t kDecisionBytes = 64;
@@ -538,7 +549,8 @@ struct StatItem {
 #pragma unroll
       for (int q = 0; q < kRaw; ++q) {
         const int64_t e0 = index_of(q * W);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(e0 < hi ? e0 * kElt : 0x7FFFFFF0), 0, 0);
+        const auto v =
+            __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(e0 < hi ? e0 * kElt : 0x7FFFFFF0), 0, kStatAux);
         r[q] = make_uint4(v[0], v[1], v[2], v[3]);
       }
     } else {
@@ -651,52 +663,80 @@ __device__ __forceinline__ void stat_share(const dsr_verify_args_t& a, const Ver
   X m = -X(INFINITY);
   double Mg;
   uint32_t flags;
-  if constexpr (DT == DSR_F64) {
+  long long amg = LLONG_MAX;
+  double Sg = 0.0;
+  if (!greedy && DT != DSR_F64) {
+    // Sampled rows: a float maximum (which passes over NaN) and a NaN test;
+    // +inf shows as the maximum.
     bool nan = false;
 #pragma unroll
     for (int u = 0; u < kStatPer; ++u) {
-      const double v = it.elem(x, u);
-      nan |= v != v;
-      m = fmax(m, v);  // a NaN operand is ignored; the flag covers it
-    }
-    const uint32_t fl = ((nan || m == (double)INFINITY) ? 1u : 0u) | (m > -(double)INFINITY ? 2u : 0u);
-    Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
-    flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
-  } else {
-    int32_t smax = INT_MIN;
-    uint32_t umax = 0u;
-#pragma unroll
-    for (int u = 0; u < kStatPer; ++u) {
       const float v = it.elem(x, u);
-      const uint32_t b = __float_as_uint(v);
-      smax = max(smax, (int32_t)b);
-      umax = max(umax, b);
+      nan |= v != v;
       m = fmaxf(m, v);
     }
-    const bool bad = smax >= 0x7F800000 || umax > 0xFF800000u;
-    const uint32_t K = stat_reduce(bad ? 0xFFFFFFFFu : float_key(m), sm.su, 0u, OpMax());
+    const bool bad = nan || m == INFINITY;
+    // The key reduction comes before the exp pass: its barrier keeps the
+    // compiler from interleaving the two passes (which costs registers).
+    const uint32_t K = stat_reduce(bad ? 0xFFFFFFFFu : float_key((float)m), sm.su, 0u, OpMax());
     Mg = K == 0xFFFFFFFFu ? (double)INFINITY : (double)key_float(K);
     flags = (K == 0xFFFFFFFFu ? 1u : 0u) | (K > 0x007FFFFFu && K != 0xFFFFFFFFu ? 2u : 0u);
-  }
-  long long amg = LLONG_MAX;
-  double Sg = 0.0;
-  if (greedy) {
-    // The first index holding the maximum: the thread's first slot equal to
-    // its own maximum, then the smallest such index over the threads at Mg.
-    int mu = -1;
-#pragma unroll
-    for (int u = kStatPer - 1; u >= 0; --u)
-      if ((double)it.elem(x, u) == (double)m) mu = u;
-    amg = stat_reduce((double)m == Mg && mu >= 0 ? it.index_of(mu) : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
-  } else {
     const double iT = 1.0 / T;
     const double mm = (double)m > -(double)INFINITY ? (double)m : 0.0;  // no finite value: exact zeros
     const ExpTerm term{mm, exp_scale(T), etab};
     double s = 0.0;
 #pragma unroll
     for (int u = 0; u < kStatPer; ++u) s += term((double)it.elem(x, u));
-    const double sc = s > 0.0 ? s * exp_nonpos(((double)m - Mg) * iT, etab) : 0.0;
+    const double sc = (s > 0.0 && K != 0xFFFFFFFFu) ? s * exp_nonpos(((double)m - Mg) * iT, etab) : 0.0;
     Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
+  } else {
+    if constexpr (DT == DSR_F64) {
+      bool nan = false;
+#pragma unroll
+      for (int u = 0; u < kStatPer; ++u) {
+        const double v = it.elem(x, u);
+        nan |= v != v;
+        m = fmax(m, v);  // a NaN operand is ignored; the flag covers it
+      }
+      const uint32_t fl = ((nan || m == (double)INFINITY) ? 1u : 0u) | (m > -(double)INFINITY ? 2u : 0u);
+      Mg = stat_reduce(m, sm.sf[0], -(double)INFINITY, OpMax());
+      flags = stat_reduce(fl, sm.su, 0u, [](uint32_t p, uint32_t q) { return p | q; });
+    } else {
+      // Greedy rows: the signed and unsigned maxima of the raw bits reveal
+      // +inf / +NaN (signed >= 0x7F800000) and -NaN (unsigned > 0xFF800000).
+      int32_t smax = INT_MIN;
+      uint32_t umax = 0u;
+#pragma unroll
+      for (int u = 0; u < kStatPer; ++u) {
+        const float v = it.elem(x, u);
+        const uint32_t b = __float_as_uint(v);
+        smax = max(smax, (int32_t)b);
+        umax = max(umax, b);
+        m = fmaxf(m, v);
+      }
+      const bool bad = smax >= 0x7F800000 || umax > 0xFF800000u;
+      const uint32_t K = stat_reduce(bad ? 0xFFFFFFFFu : float_key(m), sm.su, 0u, OpMax());
+      Mg = K == 0xFFFFFFFFu ? (double)INFINITY : (double)key_float(K);
+      flags = (K == 0xFFFFFFFFu ? 1u : 0u) | (K > 0x007FFFFFu && K != 0xFFFFFFFFu ? 2u : 0u);
+    }
+    if (greedy) {
+      // The first index holding the maximum: the thread's first slot equal to
+      // its own maximum, then the smallest such index over the threads at Mg.
+      int mu = -1;
+#pragma unroll
+      for (int u = kStatPer - 1; u >= 0; --u)
+        if ((double)it.elem(x, u) == (double)m) mu = u;
+      amg = stat_reduce((double)m == Mg && mu >= 0 ? it.index_of(mu) : LLONG_MAX, sm.si, LLONG_MAX, OpMin());
+    } else {  // f64 logits, sampled
+      const double iT = 1.0 / T;
+      const double mm = (double)m > -(double)INFINITY ? (double)m : 0.0;
+      const ExpTerm term{mm, exp_scale(T), etab};
+      double s = 0.0;
+#pragma unroll
+      for (int u = 0; u < kStatPer; ++u) s += term((double)it.elem(x, u));
+      const double sc = s > 0.0 ? s * exp_nonpos(((double)m - Mg) * iT, etab) : 0.0;
+      Sg = stat_reduce(sc, sm.sf[1], 0.0, OpSum());
+    }
   }
   if (threadIdx.x == 0) {
     VerifyPart p;
@@ -979,7 +1019,6 @@ __device__ void verify_finish_wave(const dsr_verify_args_t& a, const VerifyLayou
 // go to L.bsum for the search.  The share's sum, positive count and first
 // positive index go to its DrawPart.  VEC (rows 16-byte aligned): buffer
 // loads, past the row reading as 0 and given weight 0.
-constexpr int kDrawPer = 16;  // tokens per lane
 static_assert(kStatThreads * kDrawPer == kDrawBlocks * 64, "a draw workgroup covers its blocks");
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t a, VerifyLayout L) {

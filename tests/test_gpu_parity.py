@@ -346,6 +346,58 @@ def test_verify_fast_and_general_paths_match_the_oracle(dtype):
     assert int(fast.status.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("V", [5003, 5008])  # unaligned rows (element loads) and 16-byte aligned rows
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_fast_path_non_finite_and_masked_rows(V, dtype):
+    """Filter-free requests whose rows hold NaN, +inf, -NaN or only -inf:
+    every proposal row and the first target are checked up front, later
+    targets only when the chain reaches them (sampling.py:264-272).  The
+    kernel's statuses and decisions equal the oracle's on every request."""
+    rng = np.random.default_rng(23 + V)
+    R, K = 12, 3
+    dev = "cuda"
+    tgt_np = rng.normal(0, 2, (R, K + 1, V)).astype(np.float32)
+    drf_np = (tgt_np[:, :K] + rng.normal(0, 0.5, (R, K, V))).astype(np.float32)
+    greedy = np.arange(R) % 2 == 1
+    ids_np = rng.integers(0, V, (R, K)).astype(np.int32)
+    for r in np.flatnonzero(greedy):
+        drf_np[r] = tgt_np[r, :K]
+    pos = lambda: int(rng.integers(0, V))
+    drf_np[0, 1, pos()] = np.nan              # a proposal row: checked up front
+    tgt_np[1, 0, pos()] = np.inf              # the first target
+    tgt_np[2, 2, pos()] = np.inf              # a later target, not reached (sampled request, rejected early or not)
+    tgt_np[3, 2, pos()] = np.nan              # a later target, reached (greedy)
+    drf_np[4, 0, :] = -np.inf                 # a fully masked proposal
+    neg_nan = np.array([0xFFC00001], np.uint32).view(np.float32)[0]
+    tgt_np[5, 1, pos()] = neg_nan             # -NaN in a reached target (greedy)
+    tgt_np[6, 0, :V // 2] = -np.inf           # half masked: still a distribution
+    tgt = torch.from_numpy(tgt_np).to(dev).to(dtype)
+    drf = torch.from_numpy(drf_np).to(dev).to(dtype)
+    tgt_seen, drf_seen = tgt.float().cpu().numpy(), drf.float().cpu().numpy()
+    # Greedy requests propose the first argmax of the target rows as the
+    # device sees them, so their chains reach every target.
+    for r in np.flatnonzero(greedy):
+        ids_np[r] = np.nan_to_num(tgt_seen[r, :K], nan=-np.inf).argmax(axis=1)
+    pols = [dict(temperature=0.0) if greedy[r] else dict(temperature=1.0) for r in range(R)]
+    ua_np, ut_np = rng.random((R, K)), rng.random(R)
+    ids = torch.from_numpy(ids_np).to(dev)
+    res = batch.verify_drafts(tgt, drf, ids, pols, torch.from_numpy(ua_np).to(dev), torch.from_numpy(ut_np).to(dev),
+                              torch.full((R,), 10, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert res.args.hints == N.HINT_VERIFY_FAST
+    for r in range(R):
+        ref = O.verify(tgt_seen[r], drf_seen[r], list(ids_np[r]), O.Policy(**pols[r]), ua_np[r], float(ut_np[r]),
+                       output_limit=10)
+        assert int(res.status[r]) == ref.status, (r, int(res.status[r]), ref.status)
+        if ref.status == 0:
+            n = int(res.count[r])
+            got = (int(res.accepted[r]), tuple(res.ids[r, :n].tolist()), int(res.used_accept[r]), int(res.used_target[r]))
+            assert got == (ref.accepted, ref.output_ids, ref.used_accept, ref.used_target), (r, got, ref)
+    st = res.status.cpu().numpy()
+    assert st[0] == N.E_LOGITS and st[1] == N.E_LOGITS and st[3] == N.E_LOGITS and st[5] == N.E_LOGITS
+    assert st[4] == N.E_MASKED and st[6] == 0
+
+
 def test_verify_hint_broken_by_a_filter_is_reported():
     """DSR_HINT_VERIFY_FAST forced on requests that carry filters: the
     general-path launch is left out, so those requests get DSR_E_HINT and
