@@ -51,7 +51,7 @@ WORKLOADS = {
     "c2": ("sampled rows/sec at B=64×V=129,280 bf16 with 4,096-token histories", "rows/s", 20,
            "k_sample_bf16_full"),
     "c4": ("verify-rows/sec at B=32 requests × K=4 drafts × V=129,280 fp32", "verify-rows/s", 60,
-           "k_verify_dists + k_verify_stats + k_verify_chain + k_verify_draw + k_verify_finish"),
+           "k_verify_stats + k_verify_chain + k_verify_draw + k_verify_finish"),
     "c5": ("sampled rows/sec at B=1024×V=129,280 bf16, mixed greedy, 16,384-token histories", "rows/s", 2,
            "k_sample_bf16_full"),
     "hist": ("history rows/sec: 1,024 rows x 16,384 token ids -> sparse count tables over V=129,280", "rows/s", 10,
@@ -61,6 +61,9 @@ WORKLOADS = {
     "propose": ("5-row draft proposal chains/sec at V=129,280 fp32, one host synchronisation per chain",
                 "chains/s", 100, "k_split_select + k_split_finish (5x) + k_history_append (4x)"),
 }
+
+# Name prefix of a workload's committed profile summaries when it is not its first kernel's.
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split"}
 
 DESCRIPTIONS = {
     "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
@@ -391,7 +394,7 @@ def main():
     # need their own rocprofv3 pass); it is read from the committed counter
     # summary of the same command and labelled as such.
     traffic, traffic_source = None, None
-    tf = os.path.join(ROOT, "profiles", f"{kernels.split(' ')[0]}_{name}_traffic.json")
+    tf = os.path.join(ROOT, "profiles", f"{PROFILE_PREFIX.get(name, kernels.split(' ')[0])}_{name}_traffic.json")
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("bytes_per_launch")
         traffic_source = os.path.relpath(tf, ROOT) + " (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)"
