@@ -344,7 +344,8 @@ _default_ws = Workspace()
 def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None = None, bias: BiasTable | None = None,
                 allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
                 rng_state: torch.Tensor | None = None, probs: str | None = None, kept: bool = False,
-                workspace: Workspace | None = None, noalloc: bool = False, hints: int | None = None) -> SampleResult:
+                workspace: Workspace | None = None, noalloc: bool = False, hints: int | None = None,
+                out: dict | None = None) -> SampleResult:
     """Sample every row of ``logits [rows, V]`` on the current stream.
 
     ``policies`` is a device tensor made by ``policy_tensor`` or a list of
@@ -358,6 +359,9 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     device array (at most ``N.NOALLOC_SCRATCH_BYTES``; calls on one device
     share it, so overlapping calls race).  ``hints`` overrides the
     DSR_HINT_* bits derived from the policies (they choose launches only).
+    ``out`` may supply any of the result tensors (``tokens``, ``consumed``,
+    ``status``, ``flags``, ``probs``), contiguous and of the result's dtype
+    and shape, for the kernels to write in place.
     """
     lib = N.load()
     _require_cuda(logits, "logits", rows_strided=True)
@@ -369,14 +373,27 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         policies = policy_tensor(policies, dev)
     if policies.numel() != rows * POLICY_DTYPE.itemsize:
         raise ValueError("one policy per row is required")
-    res = SampleResult(torch.empty(rows, dtype=torch.int32, device=dev), torch.empty(rows, dtype=torch.uint8, device=dev),
-                       torch.empty(rows, dtype=torch.int32, device=dev), torch.empty(rows, dtype=torch.uint8, device=dev))
+    out = dict(out or {})
+
+    def result(key, shape, dtype):
+        t = out.pop(key, None)
+        if t is None:
+            return torch.empty(*shape, dtype=dtype, device=dev)
+        _require_cuda(t, key)
+        if t.dtype != dtype or tuple(t.shape) != tuple(shape) or not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"out['{key}'] must be a contiguous {dtype} {list(shape)} tensor on {dev}")
+        return t
+
+    res = SampleResult(result("tokens", (rows,), torch.int32), result("consumed", (rows,), torch.uint8),
+                       result("status", (rows,), torch.int32), result("flags", (rows,), torch.uint8))
     if probs == "f32":
-        res.probs = torch.empty(rows, V, dtype=torch.float32, device=dev)
+        res.probs = result("probs", (rows, V), torch.float32)
     elif probs == "f64":
-        res.probs = torch.empty(rows, V, dtype=torch.float64, device=dev)
+        res.probs = result("probs", (rows, V), torch.float64)
     elif probs is not None:
         raise ValueError("probs must be None, 'f32' or 'f64'")
+    if out:
+        raise ValueError(f"unused out tensors: {sorted(out)}")
     if kept:
         res.kept_bits = torch.empty(rows, allow_words(V), dtype=torch.int32, device=dev)
     if uniforms is not None:
@@ -542,8 +559,9 @@ class Proposals:
     tokens: torch.Tensor      # int32 [steps]
     rows: torch.Tensor        # float64 [steps, V]: each row's distribution
     consumed: torch.Tensor    # uint8 [steps]
-    status: torch.Tensor      # int32 [steps]: sampling status, then history-append status
-    finite: torch.Tensor      # bool [steps]: the row's logits were all finite
+    status: torch.Tensor      # int32 [steps]: each row's sampling status
+    appended: tuple           # int32 [1] history-append status of rows 1.. (the previous proposal)
+    logits: torch.Tensor      # float32 [steps, V]: each row's logits as sampled, checked for finiteness at the end
     states: torch.Tensor      # int64 [steps + 1, 4]: PCG64 state before row 0 and after each row
     keep: tuple = ()
 
@@ -560,10 +578,12 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
     caller's Markov bias step reads the token the sampling kernel wrote.  Each row is
     one ``dsr_sample_rows`` launch that draws its uniform from the ``draft``
     domain's PCG64 state in ``rng_state`` (int64 ``[1, 4]``, advanced in
-    place) and sees the history with every earlier proposal appended, as
+    place), writes its token and distribution straight into the chain's
+    tensors, and sees the history with every earlier proposal appended, as
     ``SamplingWork.distribution`` conditions it (:127-133).  Every row is
     drawn speculatively; ``finish_proposals`` keeps them up to the first stop
-    token and restores the state saved after that row."""
+    token, checks the rows' logits and statuses, and restores the state saved
+    after the last kept row."""
     if steps < 0 or steps > 5:
         raise ValueError("at most five proposals")
     _require(rng_state, "rng_state", torch.int64, 4)
@@ -573,11 +593,13 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
     tokens = torch.empty(steps, dtype=torch.int32, device=dev)
     rows = torch.empty(steps, vocab, dtype=torch.float64, device=dev)
     consumed = torch.empty(steps, dtype=torch.uint8, device=dev)
-    status = torch.zeros(steps, dtype=torch.int32, device=dev)
-    finite = torch.empty(steps, dtype=torch.bool, device=dev)
+    status = torch.empty(steps, dtype=torch.int32, device=dev)
+    flags = torch.empty(steps, dtype=torch.uint8, device=dev)
     states = torch.empty(steps + 1, 4, dtype=torch.int64, device=dev)
     bounds = torch.tensor([0, 1], dtype=torch.int64, device=dev)  # one token per append
-    keep = [pol, bounds]
+    # Each row's logits as sampled (the caller may reuse its buffer for the next row).
+    seen = torch.empty(steps, vocab, dtype=torch.float32, device=dev)
+    keep, appended = [pol, bounds, flags], []
     table, previous = history, seed_token
     for j in range(steps):
         logits = row_logits(j, previous)
@@ -585,29 +607,24 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
                 and logits.numel() == vocab):
             raise ValueError("row_logits must return FP32 device logits of the vocabulary")
         logits = logits.reshape(1, vocab).contiguous()
-        finite[j] = torch.isfinite(logits).all()
+        seen[j].copy_(logits[0])
         if j > 0:
             if table is None:
                 table = HistoryTable(torch.zeros(2, dtype=torch.int64, device=dev),
                                      *(torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(3)))
             table, app = _append_one(table, previous, bounds, vocab)
-            keep.append(app)
+            appended.append(app)
         states[j].copy_(rng_state.reshape(4))
         res = sample_rows(logits, pol, history=table, bias=bias, allow_bits=allow_bits, rng_state=rng_state,
-                          probs="f64")
-        tokens[j:j + 1].copy_(res.tokens)
-        consumed[j:j + 1].copy_(res.consumed)
-        rows[j].copy_(res.probs[0])
-        if j > 0:
-            status[j:j + 1].copy_(torch.where(res.status != 0, res.status, app))
-        else:
-            status[j:j + 1].copy_(res.status)
-        keep.append((logits, table, res))
+                          probs="f64", out=dict(tokens=tokens[j:j + 1], consumed=consumed[j:j + 1],
+                                                status=status[j:j + 1], flags=flags[j:j + 1],
+                                                probs=rows[j:j + 1]))
+        keep.append((table, res))
         # A failed row writes token -1; the chain is rejected at its end, but
         # the caller's bias step and the history only ever see a valid id.
-        previous = torch.clamp(res.tokens, min=0)
+        previous = torch.clamp(tokens[j:j + 1], min=0)
     states[steps].copy_(rng_state.reshape(4))
-    return Proposals(tokens, rows, consumed, status, finite, states, tuple(keep))
+    return Proposals(tokens, rows, consumed, status, tuple(appended), seen, states, tuple(keep))
 
 
 def finish_proposals(p: Proposals, eos_ids=()):
@@ -615,10 +632,17 @@ def finish_proposals(p: Proposals, eos_ids=()):
     to and including the first stop token), their distributions, the number
     of ``draft`` draws they consumed, the PCG64 state after the last kept row
     (int64 ``[1, 4]`` on the device, for ``pcg64_restore``), and the first row
-    whose status or logits failed
+    whose logits, sampling or history append failed
     (``(position, status)`` with status -1 for non-finite logits, or None)."""
-    toks, used, st, fin = (t.cpu().numpy() for t in (p.tokens, p.consumed, p.status, p.finite))
-    count = len(toks)
+    steps = p.tokens.numel()
+    if steps == 0:
+        return (), p.rows[:0], 0, p.states[0:1], None
+    dev = p.tokens.device
+    finite = torch.isfinite(p.logits).all(dim=1).to(torch.int32)
+    app = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), *p.appended])
+    info = torch.stack([p.tokens, p.consumed.to(torch.int32), p.status, app, finite]).cpu().numpy()
+    toks, used, st, ap, fin = info
+    count = steps
     for j, t in enumerate(toks):
         if int(t) in eos_ids:
             count = j + 1
@@ -627,8 +651,8 @@ def finish_proposals(p: Proposals, eos_ids=()):
     for j in range(count):
         if not fin[j]:
             failed = (j, -1)
-        elif st[j] != 0:
-            failed = (j, int(st[j]))
+        elif st[j] != 0 or ap[j] != 0:
+            failed = (j, int(st[j] if st[j] != 0 else ap[j]))
         if failed:
             break
     return tuple(int(t) for t in toks[:count]), p.rows[:count], int(used[:count].sum()), p.states[count:count + 1], \
