@@ -291,8 +291,9 @@ __device__ __forceinline__ int fast_sample_row(const dsr_sample_args_t& a, int64
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
     const uint32_t c = (uint32_t)wave * CW + cw;
     const bool mine = cw < CW;  // chunks past this wave's range belong to the next wave: read as 0
-    mb[j] = __builtin_amdgcn_raw_buffer_load_b8(mrs, (int)(mine ? c : 0x7FFFFFF0u), 0, 0);
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)(mine ? c * 16u : 0x7FFFFFF0u), 0, 0);
+    // Non-temporal (cache policy bit 2): each byte is read once.
+    mb[j] = __builtin_amdgcn_raw_buffer_load_b8(mrs, (int)(mine ? c : 0x7FFFFFF0u), 0, 2);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)(mine ? c * 16u : 0x7FFFFFF0u), 0, 2);
     d[j] = make_uint4(v[0], v[1], v[2], v[3]);
   }
   __builtin_amdgcn_sched_barrier(0);
