@@ -14,8 +14,9 @@ drafts; one step is one ``dsr_verify_drafts`` call), c5 (1,024 bf16 rows,
 mixed greedy, 16,384-token histories), whole (256 bf16 rows whose policies
 set no top-k: the reference's default, top-p only, min-p only), hist (1,024
 rows x 16,384 token ids built into device history tables; one step is one
-``dsr_history_append`` call) and propose (one 5-row draft proposal chain
-drawn on the device).
+``dsr_history_append`` call), propose (one 5-row draft proposal chain
+drawn on the device) and seed (one drop-in ``TerminalSampler.begin_seed``
+call as the reference's callers make it: host dense counts, one FP32 row).
 
 Distinct input batches rotate through the timed region: the workload's rows
 with their vocabulary positions rolled by a different shift each
@@ -58,12 +59,14 @@ WORKLOADS = {
              "k_history_append (count) + k_history_offsets + k_history_append (write)"),
     "whole": ("sampled rows/sec at B=256×V=129,280 bf16 with no top-k (default / top-p / min-p policies)", "rows/s",
               5, "k_sample_bf16_full"),
+    "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
+             300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
     "propose": ("5-row draft proposal chains/sec at V=129,280 fp32, one host synchronisation per chain",
                 "chains/s", 100, "k_split_select + k_split_finish (5x) + k_history_append (4x)"),
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
-PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split"}
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split"}
 
 DESCRIPTIONS = {
     "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
@@ -77,6 +80,8 @@ DESCRIPTIONS = {
             "(one dsr_history_append call)",
     "whole": "whole: 256 rows x 129280 bf16 heavy-tail logits, 10% allow mask, no top-k: default policy, "
              "top-p ~ U[0.8,0.99], min-p 0.05, top-p 0.95 + min-p 0.01 (by row mod 4)",
+    "seed": "seed: TerminalSampler.begin_seed then abort on 1 fp32 row x 129280 N(0,2^2), T 0.7 / top-k 50 / "
+            "top-p 0.9, dense int32 counts of a 64-token history (the reference's calling pattern)",
     "propose": "propose: 5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the "
                "device, T 0.7 / top-k 50 / top-p 0.9, 64-token history, draft PCG64 draws on the device",
 }
@@ -88,7 +93,7 @@ def _units(name, w):
     """Rows of a sampling or history workload; requests of the verifier workload."""
     if name == "c4":
         return w.extra["target"].shape[0]
-    if name == "propose":
+    if name in ("propose", "seed"):
         return 1
     return w.extra["tokens"].shape[0] if name == "hist" else w.rows
 
@@ -118,6 +123,15 @@ def _cpu_rows(span):
         return hi - lo, time.perf_counter() - t0
     if name == "propose":
         return hi - lo, _cpu_chains(w, hi - lo)
+    if name == "seed":
+        counts = np.bincount(np.asarray(w.histories[0]), minlength=V).astype(np.int32)
+        gen = np.random.default_rng(w.extra["rng_seed"])
+        t0 = time.perf_counter()
+        for _ in range(hi - lo):
+            probe = np.random.Generator(np.random.PCG64(0))
+            probe.bit_generator.state = gen.bit_generator.state
+            O.sample_row(w.logits[0], O.Policy(**w.policies[0]), float(probe.random()), counts, counts)
+        return hi - lo, time.perf_counter() - t0
     jobs = []
     for r in range(lo, hi):
         r = r % _units(name, w)
@@ -201,7 +215,7 @@ def cpu_baseline(name, w, passes):
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
     unit = WORKLOADS[name][1]
-    what = {"c4": "requests", "propose": "chains"}.get(name, "rows")
+    what = {"c4": "requests", "propose": "chains", "seed": "calls"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
@@ -226,7 +240,7 @@ ROTATION_BYTES = 300 * 2**20
 def _batch_bytes(name, w):
     if name == "hist":
         return w.extra["tokens"].nbytes
-    if name == "propose":
+    if name in ("propose", "seed"):
         return w.logits.nbytes
     if name == "c4":
         return w.extra["target"].nbytes + w.extra["draft"].nbytes
@@ -277,6 +291,31 @@ class _Chain:
         return self
 
 
+class _Seed:
+    """One drop-in call per launch: TerminalSampler.begin_seed on one FP32
+    CUDA row with dense count vectors, as the reference's callers make it,
+    then abort (which restores the RNG domains, so every call is the same)."""
+
+    def __init__(self, w):
+        import torch
+
+        from deepseekrpc_amd.sampling import SamplingPolicy
+        from deepseekrpc_amd.terminal_sampling import TerminalSampler
+        self.sampler = TerminalSampler(w.extra["rng_seed"])
+        self.policy = SamplingPolicy(**w.policies[0])
+        self.logits = torch.from_numpy(w.logits).cuda()
+        self.counts = np.bincount(np.asarray(w.histories[0]), minlength=w.logits.shape[1]).astype(np.int32)
+        self.inputs = (self.logits,)
+        self.launch()
+
+    def launch(self):
+        import torch
+        work = self.sampler.begin_seed(self.logits, policy=self.policy, counts=self.counts, remaining=9)
+        work.abort()
+        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        return self
+
+
 def _prepare(name, w, device_rng=False):
     """Device inputs and a launch closure for one step of the workload."""
     import torch
@@ -285,6 +324,9 @@ def _prepare(name, w, device_rng=False):
     if name == "propose":
         per_row = w.logits.shape[1] * (4 + 8) + 64 + 4   # logits in, float64 distribution out, controls, token
         return _Chain(w), w.extra["steps"] * per_row + 4 * len(w.histories[0]), 1
+    if name == "seed":
+        # The row's logits and its dense counts and generated counts in, the decision out.
+        return _Seed(w), w.logits.shape[1] * (4 + 4 + 4) + 64 + 4, 1
     if name == "hist":
         toks = w.extra["tokens"]
         off = np.arange(toks.shape[0] + 1, dtype=np.int64) * toks.shape[1]
@@ -341,7 +383,7 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    if args.device_rng and name in ("c4", "hist", "propose"):
+    if args.device_rng and name in ("c4", "hist", "propose", "seed"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
     batches = variants(name, w)
     preps = []
@@ -401,7 +443,7 @@ def main():
     cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]), "input_dtype": w.dtype,
            "general_path_rows": general, "kernels": kernels,
            "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
-    if name not in ("c4", "hist", "propose"):
+    if name not in ("c4", "hist", "propose", "seed"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,

@@ -149,6 +149,12 @@ class HistoryTable:
             offs.append(offs[-1] + len(nz))
         return cls._upload(offs, ids, cnt, gen, device)
 
+    @classmethod
+    def from_support(cls, ids, counts, generated, device="cuda"):
+        """One row from its positive entries: increasing ``ids`` with their
+        counts and generated counts, already validated by the caller."""
+        return cls._upload([0, len(ids)], [ids], [counts], [generated], device)
+
     @property
     def rows(self) -> int:
         return self.offsets.numel() - 1
@@ -254,11 +260,16 @@ class HistoryTable:
 
     @classmethod
     def _upload(cls, offs, ids, cnt, gen, device):
-        cat = lambda xs: np.concatenate(xs) if xs and sum(len(x) for x in xs) else np.zeros(0)
-        return cls(torch.tensor(np.asarray(offs, np.int64), device=device),
-                   torch.tensor(cat(ids).astype(np.int32), device=device),
-                   torch.tensor(cat(cnt).astype(np.int32), device=device),
-                   torch.tensor(cat(gen).astype(np.int32), device=device))
+        # ids, counts and generated counts travel in one int32 copy and are
+        # handed out as three contiguous slices of it.
+        n = int(offs[-1])
+        body = np.empty(3 * n, np.int32)
+        for part, xs in enumerate((ids, cnt, gen)):
+            if n:
+                body[part * n:(part + 1) * n] = np.concatenate(xs)
+        packed = torch.from_numpy(body).to(device)
+        return cls(torch.from_numpy(np.asarray(offs, np.int64)).to(device),
+                   packed[:n], packed[n:2 * n], packed[2 * n:])
 
 
 @dataclass

@@ -40,7 +40,7 @@ import torch
 from . import _native as N
 from . import batch
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
-from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _history_table,
+from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _device,
                        _logit_vector, _on_device, _raise_status, verify_drafts)
 
 _HISTORY_LIMIT = 1048576
@@ -65,6 +65,24 @@ def _logits_device(logits, rows, vocabulary):
     if tuple(logits.shape) != (rows, vocabulary) or not bool(torch.isfinite(logits).all()):
         raise ValidationError(_MSG_WINDOW)
     return logits.detach().contiguous()
+
+
+def _logits_deferred(logits, rows, vocabulary):
+    """``_logits_device`` with the finiteness test of a CUDA window left on
+    the device: ``(window, finite)``, ``finite`` a device bool the caller
+    reads with its next synchronisation (None when the window was checked
+    here).  Every other check runs at once, as in ``_logits_device``."""
+    if (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
+            and tuple(logits.shape) == (rows, vocabulary)):
+        window = logits.detach().contiguous()
+        return window, torch.isfinite(window).all()
+    return _logits_device(logits, rows, vocabulary), None
+
+
+def _require_finite(finite):
+    """Reports a deferred non-finite window, ahead of any later error."""
+    if finite is not None and not bool(finite):
+        raise ValidationError(_MSG_WINDOW)
 
 
 @dataclass(frozen=True)
@@ -98,10 +116,11 @@ class _Controls:
     allowed: object
     grammar_identity: str | None
     stop_identity: str | None
+    support: np.ndarray           # the token ids with a positive count, increasing
 
 
 def _valid_count_vector(values, vocabulary):
-    return (values.shape == (vocabulary,) and values.dtype in (np.int32, np.int64) and not (values < 0).any())
+    return values.shape == (vocabulary,) and values.dtype in (np.int32, np.int64) and values.min() >= 0
 
 
 def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_counts, logit_bias, allowed,
@@ -111,7 +130,9 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
     if sampler.active is not None or not isinstance(policy, SamplingPolicy):
         raise ValidationError("terminal sampling is active or its policy is invalid")
     counts = np.asarray(counts)
-    if not _valid_count_vector(counts, sampler.vocabulary) or counts.sum(dtype=np.int64) > _HISTORY_LIMIT:
+    support = np.flatnonzero(counts > 0) if _valid_count_vector(counts, sampler.vocabulary) else None
+    # Zero entries add nothing, so the int64 total (wrapping as a plain sum would) is taken over the support.
+    if support is None or counts[support].sum(dtype=np.int64) > _HISTORY_LIMIT:
         raise ValidationError("terminal counts differ from the exact published token history")
     for token in eos_ids:
         integer(token, "terminal EOS token", 0, sampler.vocabulary - 1)
@@ -124,11 +145,12 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
         if identity is not None:
             hex_id(identity, 64, what)
     generated = counts if generated_counts is None else np.asarray(generated_counts)
-    if (generated.shape != counts.shape or not _valid_count_vector(generated, sampler.vocabulary)
-            or (generated > counts).any()):
+    if generated is not counts and (generated.shape != counts.shape or not _valid_count_vector(
+            generated, sampler.vocabulary) or (generated > counts).any()):
         raise ValidationError("generated sampling counts must be a subset of the complete history")
     return _Controls(policy, counts.copy(), generated.copy(), remaining, frozenset(eos_ids),
-                     None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity)
+                     None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity,
+                     support)
 
 
 class TerminalSampler:
@@ -151,8 +173,14 @@ class TerminalSampler:
         work = self._open_work(_Stage.SEEDING, policy, counts, remaining, eos_ids, generated_counts, logit_bias,
                                allowed, grammar_identity, stop_identity)
         with work._aborting_on_error():
-            row = _logits_device(logits, 1, self.vocabulary)[0]
-            token, _ = work._draw(row, (), "target")
+            # Without a grammar provider nothing the caller sees happens
+            # between the window check and the draw, so the window's
+            # finiteness is read with the draw's result.
+            if work.allowed is None:
+                window, finite = _logits_deferred(logits, 1, self.vocabulary)
+            else:
+                window, finite = _logits_device(logits, 1, self.vocabulary), None
+            token, _ = work._draw(window[0], (), "target", finite)
             stop = "eos" if token in work.eos_ids else "length" if remaining == 1 else None
             work._decide(SeedDecision(token, stop))
         return work
@@ -257,7 +285,12 @@ class SamplingWork:
         """The device history table with each prefix token counted once more,
         as generated output (terminal_sampling.py:127-133)."""
         if self._device_history is None:
-            self._device_history = _history_table(self.counts, self.generated_counts, len(self.counts))
+            # The controls were checked on entry (no negative count, 2^20 in
+            # total, generated <= counts), so nothing here can be rejected and
+            # the table is built on the host from the positive entries.
+            ids = self._controls.support
+            self._device_history = batch.HistoryTable.from_support(
+                ids, self.counts[ids], self.generated_counts[ids], device=_device())
         if not prefix:
             return self._device_history
         dev = self._device_history.offsets.device
@@ -277,7 +310,13 @@ class SamplingWork:
         size, device_input = _logit_vector(logits)
         if size != len(self.counts):
             raise ValidationError(_COUNTS_MSG)
-        table = self._history(prefix)
+        # Repetition 1 and presence and frequency 0 leave every logit as it
+        # is, and the counts were checked on entry: a row with no prefix then
+        # needs no table.  A prefix still goes through the table, whose
+        # append checks the grown history.
+        policy = self.policy
+        penalised = policy.repetition_penalty != 1 or policy.presence_penalty != 0 or policy.frequency_penalty != 0
+        table = self._history(prefix) if prefix or penalised else None
         bias = _bias_table(self.logit_bias, size)
         allow = _allow_row(mask, size)
         return self.policy._launch_row(logits, size, table, bias, allow, uniform), device_input
@@ -293,16 +332,26 @@ class SamplingWork:
         row = result.probs[0]
         return row if device_input else row.cpu().numpy()
 
-    def _draw(self, logits, prefix, domain):
+    def _draw(self, logits, prefix, domain, finite=None):
         """(token, distribution): one fused launch draws from the row's
         distribution with the domain's next uniform; the domain advances
-        only if the kernel consumed it."""
+        only if the kernel consumed it.  ``finite`` is a deferred window
+        check (a device bool), read with the result and reported first."""
         self._require_open()
         upcoming = self.transaction._preview(domain)
-        uniform = torch.tensor([upcoming], dtype=torch.float64, device=logits.device)
-        result, _ = self._row_launch(logits, prefix, uniform)
-        token, consumed, code = torch.stack(
-            [result.tokens.long(), result.consumed.long(), result.status.long()]).view(-1).tolist()
+        # A fill kernel, not a host-to-device copy: nothing waits for it.
+        uniform = torch.full((1,), upcoming, dtype=torch.float64, device=logits.device)
+        try:
+            result, _ = self._row_launch(logits, prefix, uniform)
+        except Exception:
+            _require_finite(finite)
+            raise
+        parts = [result.tokens.long(), result.consumed.long(), result.status.long()]
+        if finite is not None:
+            parts.append(finite.long().view(1))
+        token, consumed, code, *window_ok = torch.stack(parts).view(-1).tolist()
+        if window_ok and not window_ok[0]:
+            raise ValidationError(_MSG_WINDOW)
         if code != N.OK:
             _raise_status(code)
         if consumed and self.transaction.random(domain) != upcoming:

@@ -248,6 +248,61 @@ def test_device_rows_stay_on_the_device():
         sampler.begin_seed(logits.cpu(), policy=SamplingPolicy(), counts=np.zeros(V, np.int32), remaining=1)
 
 
+@pytest.mark.parametrize("penalties", [dict(repetition_penalty=1.3, presence_penalty=0.4, frequency_penalty=0.2),
+                                       dict()])
+def test_seed_rows_read_the_frozen_history(penalties):
+    """A seed from CUDA logits with int64 counts and generated counts: its
+    draw and float64 distribution are the oracle's (sampling.py:54-66), and
+    a one-token prefix counts once more as generated output
+    (terminal_sampling.py:127-133).  Without penalties the history changes
+    nothing, and the rows are still the oracle's."""
+    from oracle import sampling_oracle as O
+    rng = np.random.default_rng(29)
+    vocab = 3001
+    counts = np.zeros(vocab, np.int64)
+    np.add.at(counts, rng.integers(0, vocab, 400), 1)
+    generated = np.where(np.arange(vocab) % 3 == 0, 0, counts)
+    logits = rng.normal(0, 2, (1, vocab)).astype(np.float32)
+    kw = dict(temperature=0.8, top_p=0.95, **penalties)
+    sampler = TerminalSampler(77, vocabulary=vocab)
+    device_logits = torch.from_numpy(logits).cuda()
+    work = sampler.begin_seed(device_logits, policy=SamplingPolicy(**kw), counts=counts, generated_counts=generated,
+                              remaining=5)
+    u = RandomStreams(77).begin().random("target")
+    ref = O.sample_row(logits[0], O.Policy(**kw), u, counts, generated)
+    assert ref.status == O.OK and work.decision.token == ref.token
+    np.testing.assert_allclose(work.distribution(device_logits[0], ()).cpu().numpy(), ref.probs, rtol=1e-12,
+                               atol=1e-300)
+    token = int(np.flatnonzero(counts == 0)[0])
+    grown, grown_generated = counts.copy(), generated.copy()
+    grown[token] += 1
+    grown_generated[token] += 1
+    want = O.probabilities(logits[0], O.Policy(**kw), grown, grown_generated)
+    np.testing.assert_allclose(work.distribution(device_logits[0], (token,)).cpu().numpy(), want, rtol=1e-12,
+                               atol=1e-300)
+    work.abort()
+    assert sampler.random.snapshot() == RandomStreams(77).snapshot()
+
+
+def test_a_non_finite_cuda_window_is_reported_before_later_errors():
+    """NaN, +inf and -inf in a CUDA seed window give the window message
+    (terminal_sampling.py:16-27), also when the logit bias is invalid too,
+    and the transaction is gone with the RNG untouched."""
+    sampler = TerminalSampler(3)
+    for bad in (float("nan"), float("inf"), -float("inf")):
+        logits = torch.zeros((1, V), dtype=torch.float32, device="cuda")
+        logits[0, 9] = bad
+        for bias in (None, {V + 5: 1.0}):
+            with pytest.raises(ValidationError, match="vocabulary window"):
+                sampler.begin_seed(logits, policy=SamplingPolicy(), counts=np.zeros(V, np.int32), remaining=2,
+                                   logit_bias=bias)
+            assert sampler.active is None and not sampler.random.active
+    with pytest.raises(ValidationError, match="biased token"):
+        sampler.begin_seed(torch.zeros((1, V), dtype=torch.float32, device="cuda"), policy=SamplingPolicy(),
+                           counts=np.zeros(V, np.int32), remaining=2, logit_bias={V + 5: 1.0})
+    assert sampler.random.snapshot() == RandomStreams(3).snapshot()
+
+
 def test_proposal_rows_are_kept_on_the_device_for_verification():
     sampler = TerminalSampler(99)
     history = np.zeros(V, np.int32)
