@@ -61,8 +61,9 @@ WORKLOADS = {
               5, "k_sample_bf16_full"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
              300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
-    "propose": ("5-row draft proposal chains/sec at V=129,280 fp32, one host synchronisation per chain",
-                "chains/s", 100, "k_split_select + k_split_finish (5x) + k_history_append (4x)"),
+    "propose": ("drop-in 5-row draft proposal steps/sec at V=129,280 fp32, one host synchronisation per step",
+                "chains/s", 100, "k_split_select + k_split_finish (5x; a policy without penalties carries no "
+                "history table)"),
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
@@ -82,8 +83,10 @@ DESCRIPTIONS = {
              "top-p ~ U[0.8,0.99], min-p 0.05, top-p 0.95 + min-p 0.01 (by row mod 4)",
     "seed": "seed: TerminalSampler.begin_seed then abort on 1 fp32 row x 129280 N(0,2^2), T 0.7 / top-k 50 / "
             "top-p 0.9, dense int32 counts of a 64-token history (the reference's calling pattern)",
-    "propose": "propose: 5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the "
-               "device, T 0.7 / top-k 50 / top-p 0.9, 64-token history, draft PCG64 draws on the device",
+    "propose": "propose: TerminalSampler.begin_verification, SamplingWork.propose over a device graph, then abort; "
+               "5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the device, "
+               "T 0.7 / top-k 50 / top-p 0.9, dense int32 counts of a 64-token history, draft PCG64 draws on the "
+               "device",
 }
 
 _CPU = {}
@@ -257,36 +260,40 @@ def variants(name, w):
 
 
 class _Chain:
-    """One proposal chain per launch: five rows drawn on the device, then the
-    chain's one synchronisation."""
+    """One drop-in proposal step per launch, as the reference's callers make
+    it: TerminalSampler.begin_verification with dense counts, then
+    SamplingWork.propose over a graph that makes each row on the device (the
+    Markov bias step reads the previous token the sampling kernel wrote), so
+    the five rows take one host synchronisation; then abort, which restores
+    the RNG domains, so every step is the same."""
 
     def __init__(self, w):
         import torch
 
-        from deepseekrpc_amd import batch
-        self.batch, self.w = batch, w
-        dev = "cuda"
-        self.base = torch.from_numpy(w.logits).to(dev)
-        self.bump = torch.full((1,), float(w.extra["bump"]), device=dev)
-        self.seed = torch.tensor([w.extra["seed_token"]], dtype=torch.int32, device=dev)
-        self.state = batch.pcg64_states([np.random.default_rng(w.extra["rng_seed"])], dev)
-        self.table, st = batch.HistoryTable.from_token_lists_device(w.histories, device=dev)
-        assert int(st.abs().sum()) == 0
+        from deepseekrpc_amd.sampling import SamplingPolicy
+        from deepseekrpc_amd.terminal_sampling import TerminalSampler
+        self.w = w
+        self.base = torch.from_numpy(w.logits).cuda()
+        self.bump = torch.full((1,), float(w.extra["bump"]), device="cuda")
+        self.sampler = TerminalSampler(w.extra["rng_seed"])
+        self.policy = SamplingPolicy(**w.policies[0])
+        self.counts = np.bincount(np.asarray(w.histories[0]), minlength=w.logits.shape[1]).astype(np.int32)
         self.inputs = (self.base,)
         self.launch()
 
-    def _row(self, j, previous):
-        out = self.base[j].clone()
+    def draft_conditional_logits_device(self, result, row, previous):
+        out = self.base[row].clone()
         out.index_add_(0, previous.long(), self.bump)
-        return out
+        return out.reshape(1, -1), None
 
     def launch(self):
         import torch
-        chain = self.batch.propose_rows(self._row, self.seed, self.w.extra["steps"], self.w.policies[0], self.state,
-                                        history=self.table)
-        ids, rows, draws, final, failed = self.batch.finish_proposals(chain)
-        if failed is not None:
-            raise SystemExit(f"proposal chain failed at row {failed}")
+        work = self.sampler.begin_verification(seed_token=self.w.extra["seed_token"], policy=self.policy,
+                                               counts=self.counts, remaining=9)
+        ids = work.propose(self, None)
+        if len(ids) != self.w.extra["steps"]:
+            raise SystemExit(f"the proposal chain stopped after {len(ids)} rows")
+        work.abort()
         self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
         return self
 

@@ -91,6 +91,18 @@ def sample_hints(arr: np.ndarray | None, vocab: int) -> int:
     return (N.HINT_WHOLE_SOME if whole.any() else 0) | (N.HINT_WHOLE_ALL if whole.all() else 0)
 
 
+def _policy_hints(policies, vocab: int) -> int:
+    """``sample_hints`` of a policy tensor, kept on the tensor per vocabulary size."""
+    cached = getattr(policies, "dsr_hints", None)
+    if cached is not None and cached[0] == vocab:
+        return cached[1]
+    arr = getattr(policies, "dsr_policies", None)
+    hints = sample_hints(arr, vocab)
+    if arr is not None:
+        policies.dsr_hints = (vocab, hints)
+    return hints
+
+
 def verify_hints(arr: np.ndarray | None, vocab: int, plain: bool) -> int:
     """DSR_HINT_VERIFY_FAST when every request's policy has no filter and the
     call carries no history, bias or allow mask (``plain``)."""
@@ -337,11 +349,12 @@ class Workspace:
     def __init__(self):
         self._bufs = {}
 
-    def get(self, nbytes: int, device) -> torch.Tensor:
+    def get(self, nbytes: int, device, stream=None) -> torch.Tensor:
         device = torch.device(device)
         if device.index is None:
             device = torch.device(device.type, torch.cuda.current_device())
-        stream = torch.cuda.current_stream(device)
+        if stream is None:
+            stream = torch.cuda.current_stream(device)
         key = (device.index, stream.cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -421,11 +434,12 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     if noalloc and need > N.NOALLOC_SCRATCH_BYTES:
         raise ValueError(f"{rows} rows of {V} tokens need {need} bytes of scratch; the allocation-free entry point "
                          f"holds {N.NOALLOC_SCRATCH_BYTES}")
-    ws = None if noalloc else (workspace or _default_ws).get(need, dev)
+    stream = torch.cuda.current_stream(dev)
+    ws = None if noalloc else (workspace or _default_ws).get(need, dev, stream)
     a = N.SampleArgs()
     a.logits = logits.data_ptr()
     a.dtype = _DTYPES[logits.dtype]
-    a.hints = sample_hints(getattr(policies, "dsr_policies", None), V) if hints is None else hints
+    a.hints = _policy_hints(policies, V) if hints is None else hints
     a.rows, a.vocab, a.ld = rows, V, logits.stride(0)
     a.policy = policies.data_ptr()
     if _nonempty(history, "ids"):
@@ -449,11 +463,12 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         a.probs_ld = V
     if res.kept_bits is not None:
         a.out_kept_bits, a.kept_ld = res.kept_bits.data_ptr(), res.kept_bits.stride(0)
+    handle = ctypes.c_void_p(stream.cuda_stream)
     if noalloc:
-        N.check(lib.dsr_sample_rows_noalloc(ctypes.byref(a), _stream()), "dsr_sample_rows_noalloc")
+        N.check(lib.dsr_sample_rows_noalloc(ctypes.byref(a), handle), "dsr_sample_rows_noalloc")
     else:
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        N.check(lib.dsr_sample_rows(ctypes.byref(a), _stream()), "dsr_sample_rows")
+        N.check(lib.dsr_sample_rows(ctypes.byref(a), handle), "dsr_sample_rows")
     res.args = a
     res.keep = (logits, policies, history, bias, allow_bits, uniforms, rng_state, ws)
     return res
@@ -579,7 +594,7 @@ class Proposals:
 
 def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_state: torch.Tensor, *,
                  history: HistoryTable | None = None, bias: BiasTable | None = None,
-                 allow_bits: torch.Tensor | None = None, vocab: int = VOCAB) -> Proposals:
+                 allow_bits: torch.Tensor | None = None, vocab: int = VOCAB, grow: bool = True) -> Proposals:
     """Up to ``steps`` draft tokens drawn one row at a time with no host
     synchronisation (terminal_sampling.py:138-161).
 
@@ -594,13 +609,15 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
     ``SamplingWork.distribution`` conditions it (:127-133).  Every row is
     drawn speculatively; ``finish_proposals`` keeps them up to the first stop
     token, checks the rows' logits and statuses, and restores the state saved
-    after the last kept row."""
+    after the last kept row.  With ``grow=False`` nothing is appended and
+    every row carries ``history`` as given: the caller's choice when no row's
+    distribution reads the prefix counts and no append could fail."""
     if steps < 0 or steps > 5:
         raise ValueError("at most five proposals")
     _require(rng_state, "rng_state", torch.int64, 4)
     _require(seed_token, "seed_token", torch.int32, 1)
     dev = rng_state.device
-    pol = policy_tensor([policy], dev)
+    pol = policy if isinstance(policy, torch.Tensor) else policy_tensor([policy], dev)
     tokens = torch.empty(steps, dtype=torch.int32, device=dev)
     rows = torch.empty(steps, vocab, dtype=torch.float64, device=dev)
     consumed = torch.empty(steps, dtype=torch.uint8, device=dev)
@@ -619,7 +636,7 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
             raise ValueError("row_logits must return FP32 device logits of the vocabulary")
         logits = logits.reshape(1, vocab).contiguous()
         seen[j].copy_(logits[0])
-        if j > 0:
+        if j > 0 and grow:
             if table is None:
                 table = HistoryTable(torch.zeros(2, dtype=torch.int64, device=dev),
                                      *(torch.zeros(1, dtype=torch.int32, device=dev) for _ in range(3)))
@@ -650,7 +667,8 @@ def finish_proposals(p: Proposals, eos_ids=()):
         return (), p.rows[:0], 0, p.states[0:1], None
     dev = p.tokens.device
     finite = torch.isfinite(p.logits).all(dim=1).to(torch.int32)
-    app = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), *p.appended])
+    # Row j > 0 carries the status of the append before it; a chain without appends has none.
+    app = torch.cat([torch.zeros(1 if p.appended else steps, dtype=torch.int32, device=dev), *p.appended])
     info = torch.stack([p.tokens, p.consumed.to(torch.int32), p.status, app, finite]).cpu().numpy()
     toks, used, st, ap, fin = info
     count = steps

@@ -94,6 +94,21 @@ class SamplingPolicy:
     def as_dict(self):
         return asdict(self)
 
+    def _device_tensor(self, device):
+        """The policy packed for the kernels on ``device``, made once per
+        device: the policy is immutable.  Copies and pickles leave it out."""
+        cache = self.__dict__.get("_packed")
+        if cache is None:
+            cache = {}
+            object.__setattr__(self, "_packed", cache)
+        packed = cache.get(device.index)
+        if packed is None:
+            packed = cache[device.index] = batch.policy_tensor([self], device)
+        return packed
+
+    def __getstate__(self):
+        return {k: v for k, v in self.__dict__.items() if k != "_packed"}
+
     def probabilities(self, logits, *, counts=None, generated_counts=None, logit_bias=None, allowed=None):
         """Adjusted, filtered and normalised float64 probabilities (sampling.py:48-106)."""
         n, device_input = _logit_vector(logits)
@@ -115,8 +130,8 @@ class SamplingPolicy:
         device tensor of one element) also its categorical draw and whether
         the draw consumed the uniform.  Nothing is synchronised."""
         x, _ = _on_device(logits)
-        return batch.sample_rows(x.reshape(1, n), [self], history=table, bias=bias, allow_bits=allow,
-                                 uniforms=uniform, probs="f64")
+        return batch.sample_rows(x.reshape(1, n), self._device_tensor(x.device), history=table, bias=bias,
+                                 allow_bits=allow, uniforms=uniform, probs="f64")
 
 
 def _bias_table(logit_bias, n):

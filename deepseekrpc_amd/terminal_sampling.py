@@ -117,6 +117,7 @@ class _Controls:
     grammar_identity: str | None
     stop_identity: str | None
     support: np.ndarray           # the token ids with a positive count, increasing
+    total: int | None             # the sum of the counts; None when a count exceeds 2^20
 
 
 def _valid_count_vector(values, vocabulary):
@@ -132,8 +133,11 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
     counts = np.asarray(counts)
     support = np.flatnonzero(counts > 0) if _valid_count_vector(counts, sampler.vocabulary) else None
     # Zero entries add nothing, so the int64 total (wrapping as a plain sum would) is taken over the support.
-    if support is None or counts[support].sum(dtype=np.int64) > _HISTORY_LIMIT:
+    total = None if support is None else int(counts[support].sum(dtype=np.int64))
+    if total is None or total > _HISTORY_LIMIT:
         raise ValidationError("terminal counts differ from the exact published token history")
+    if support.size and int(counts[support].max()) > _HISTORY_LIMIT:
+        total = None   # the int64 sum wrapped: every row's distribution rejects these counts
     for token in eos_ids:
         integer(token, "terminal EOS token", 0, sampler.vocabulary - 1)
     if allowed is not None and not callable(allowed):
@@ -150,7 +154,7 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
         raise ValidationError("generated sampling counts must be a subset of the complete history")
     return _Controls(policy, counts.copy(), generated.copy(), remaining, frozenset(eos_ids),
                      None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity,
-                     support)
+                     support, total)
 
 
 class TerminalSampler:
@@ -284,6 +288,8 @@ class SamplingWork:
     def _history(self, prefix):
         """The device history table with each prefix token counted once more,
         as generated output (terminal_sampling.py:127-133)."""
+        if self._controls.total is None:
+            raise ValidationError(_COUNTS_MSG)   # sampling.py:55-58 rejects a count above 2^20
         if self._device_history is None:
             # The controls were checked on entry (no negative count, 2^20 in
             # total, generated <= counts), so nothing here can be rejected and
@@ -302,6 +308,17 @@ class SamplingWork:
             _raise_status(code)
         return table
 
+    def _needs_history(self, grown):
+        """Whether rows whose prefix holds up to ``grown`` tokens carry the
+        history table.  Penalties read it; repetition 1 and presence and
+        frequency 0 leave every logit as it is, and then only a history that
+        the prefix could push past the count limit needs the table, whose
+        append reports the overflow at the row where it happens
+        (sampling.py:55-58)."""
+        p, total = self.policy, self._controls.total
+        return (p.repetition_penalty != 1 or p.presence_penalty != 0 or p.frequency_penalty != 0
+                or total is None or total + grown > _HISTORY_LIMIT)
+
     def _row_launch(self, logits, prefix, uniform=None):
         """Validate one row and launch its distribution (and draw, given a
         uniform).  The grammar is asked for its mask first, then the row and
@@ -310,13 +327,7 @@ class SamplingWork:
         size, device_input = _logit_vector(logits)
         if size != len(self.counts):
             raise ValidationError(_COUNTS_MSG)
-        # Repetition 1 and presence and frequency 0 leave every logit as it
-        # is, and the counts were checked on entry: a row with no prefix then
-        # needs no table.  A prefix still goes through the table, whose
-        # append checks the grown history.
-        policy = self.policy
-        penalised = policy.repetition_penalty != 1 or policy.presence_penalty != 0 or policy.frequency_penalty != 0
-        table = self._history(prefix) if prefix or penalised else None
+        table = self._history(prefix) if self._needs_history(len(prefix)) else None
         bias = _bias_table(self.logit_bias, size)
         allow = _allow_row(mask, size)
         return self.policy._launch_row(logits, size, table, bias, allow, uniform), device_input
@@ -367,7 +378,9 @@ class SamplingWork:
         with self._aborting_on_error():
             steps = min(_MAX_PROPOSALS, self.remaining)
             device_step = getattr(graph, "draft_conditional_logits_device", None)
-            if device_step is not None and self.allowed is None:
+            # Counts the first row rejects keep the host loop, which asks the
+            # graph for that row before rejecting it, as the reference does.
+            if device_step is not None and self.allowed is None and self._controls.total is not None:
                 self._propose_on_device(device_step, result, steps)
             else:
                 previous = self.seed_token
@@ -407,7 +420,9 @@ class SamplingWork:
                 raise ValidationError(_MSG_WINDOW)
             return logits
 
-        chain = batch.propose_rows(row_logits, seed, steps, self.policy, state, history=self._history(()),
+        grow = self._needs_history(max(steps - 1, 0))   # row j's prefix holds j proposals
+        chain = batch.propose_rows(row_logits, seed, steps, self.policy._device_tensor(device), state,
+                                   history=self._history(()) if grow else None, grow=grow,
                                    bias=_bias_table(self.logit_bias, vocab), vocab=vocab)
         ids, rows, draws, final, failed = batch.finish_proposals(chain, self.eos_ids)
         if failed is not None:

@@ -166,3 +166,54 @@ def test_chain_primitive_keeps_speculative_rows_and_states():
     for j in range(5):
         host.random()
         assert int(words[j + 1, 0]) | (int(words[j + 1, 1]) << 64) == host.bit_generator.state["state"]["state"]
+
+
+@pytest.mark.parametrize("cls", [DeviceMarkovRows, MarkovRows])
+def test_a_history_the_prefix_pushes_past_the_limit_fails_at_that_row(cls):
+    """Without penalties the rows carry no history table until the prefix
+    could push the counts past 2^20 (sampling.py:55-58): counts summing to
+    2^20 - 2 let rows 0-2 through, and row 3 fails with the counts message."""
+    limit = 1048576
+    counts = np.zeros(V, np.int32)
+    counts[77] = limit - 2
+    sampler = TerminalSampler(31)
+    initial = sampler.random.snapshot()
+    work = sampler.begin_verification(seed_token=77, policy=SamplingPolicy(**POLICIES[0]), counts=counts,
+                                      remaining=9)
+    graph = cls(31)
+    with pytest.raises(ValidationError, match="frequency counts"):
+        work.propose(graph, None)
+    assert sampler.active is None and sampler.random.snapshot() == initial
+    if cls is MarkovRows:
+        assert [row for row, _ in graph.host_calls] == [0, 1, 2, 3]
+
+
+def test_rows_below_the_limit_match_the_oracle_without_a_table():
+    """The same chain one count lower stays within 2^20 at every row: its
+    proposals and RNG state are the oracle's."""
+    limit = 1048576
+    counts = np.zeros(V, np.int32)
+    counts[77] = limit - 4
+    sampler = TerminalSampler(32)
+    work = sampler.begin_verification(seed_token=77, policy=SamplingPolicy(**POLICIES[0]), counts=counts,
+                                      remaining=9)
+    graph = DeviceMarkovRows(32)
+    proposals = work.propose(graph, None)
+    state = work.transaction.prepared_state()
+    work.abort()
+    txn = TerminalSampler(32).random.begin()
+    host = MarkovRows(32)
+    previous, want = 77, []
+    for position in range(5):
+        c = counts.copy()
+        for t in want:
+            c[t] += 1
+        upcoming = txn._preview("draft")
+        ref = O.sample_row(host.host_row(position, previous), O.Policy(**POLICIES[0]), upcoming, c, c)
+        assert ref.status == 0
+        if ref.consumed:
+            txn.random("draft")
+        want.append(ref.token)
+        previous = ref.token
+    assert proposals == tuple(want) and state == txn.prepared_state()
+    txn.abort()

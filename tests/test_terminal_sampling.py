@@ -284,6 +284,31 @@ def test_seed_rows_read_the_frozen_history(penalties):
     assert sampler.random.snapshot() == RandomStreams(77).snapshot()
 
 
+def test_counts_whose_int64_sum_wraps_pass_the_controls_and_fail_the_first_row():
+    """Four counts of 2^62 sum to 2^64, which wraps to 0 in int64: the
+    controls accept them (terminal_sampling.py:57-60) and the first row's
+    distribution rejects the counts (sampling.py:55-58).  The graph is asked
+    for that row first, on both graph kinds."""
+    counts = np.zeros(8, np.int64)
+    counts[:4] = 1 << 62
+    sampler = TerminalSampler(5, vocabulary=8)
+    with pytest.raises(ValidationError, match="frequency counts"):
+        sampler.begin_seed(np.zeros((1, 8), np.float32), policy=SamplingPolicy(), counts=counts, remaining=3)
+    assert sampler.active is None and not sampler.random.active
+
+    class DeviceGraph(MarkovGraph):
+        def draft_conditional_logits_device(self, result, row, previous):
+            raise AssertionError("rows whose counts fail go through the host loop")
+
+    for graph in (MarkovGraph(lambda row, prev: np.zeros(8, np.float32)),
+                  DeviceGraph(lambda row, prev: np.zeros(8, np.float32))):
+        work = sampler.begin_verification(seed_token=1, policy=SamplingPolicy(), counts=counts, remaining=3)
+        with pytest.raises(ValidationError, match="frequency counts"):
+            work.propose(graph, None)
+        assert graph.calls == [(0, 1)] and sampler.active is None
+    assert sampler.random.snapshot() == RandomStreams(5).snapshot()
+
+
 def test_a_non_finite_cuda_window_is_reported_before_later_errors():
     """NaN, +inf and -inf in a CUDA seed window give the window message
     (terminal_sampling.py:16-27), also when the logit bias is invalid too,
