@@ -22,8 +22,8 @@
 // below it plus absent new ids below it), its old entry and its slot in a
 // count table indexed by rank among the new ids, which carries each new id's
 // multiplicity and generated multiplicity (16 bits each).  In the write pass
-// each lane expands one word of the union of the two bitmaps, a wave 64
-// consecutive words, so a wave's stores stay within one stretch of the row.
+// a wave takes 64 consecutive words of the union of the two bitmaps and
+// writes their entries 64 consecutive entries per store.
 #pragma once
 
 #include "dsr_wave.h"
@@ -194,16 +194,19 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
     }
   }
   lds_barrier();
-  // The merged row is the union of both bitmaps in id order.  Lane = word:
-  // wave w takes the groups of 64 consecutive words g = w, w + 16, ..., and
-  // each lane writes its word's ids in bit order from the word's rank in the
-  // merged row (old ids below it plus absent new ids below it), so a wave's
-  // stores cover one contiguous stretch of the output.  An old id's entry is
-  // its rank in the old bitmap; a new id's multiplicities are at its rank in
-  // the new bitmap.
+  // The merged row is the union of both bitmaps in id order.  Wave w takes
+  // the groups of 64 consecutive words g0 = 64 w, 64 (w + 16), ...; the
+  // group's entries are contiguous in the output from word g0's rank in the
+  // merged row (old ids below it plus absent new ids below it), word s of the
+  // group holding entries [ex_s, ex_s + popc) of them.  The wave writes them
+  // 64 at a time with lane l taking entry i = i0 + l, so every store covers
+  // 64 consecutive entries: the word holding entry i is the last lane s with
+  // ex_s <= i (a binary search over the lanes), its id is that word's
+  // (i - ex_s)-th set bit.  An old id's entry is its rank in the old bitmap;
+  // a new id's multiplicities are at its rank in the new bitmap.
   const int lane = lane_id(), wave = wave_id();
   const int64_t base = a.out_off[row];
-  for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {
+  for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {  // uniform over the wave
     const int w = g0 + lane;
     uint32_t nwv = 0u, owv = 0u, nbw = 0u, obw = 0u, ubw = 0u;
     if (w < words) {
@@ -213,24 +216,47 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
       obw = sh.obase[w];
       ubw = sh.ubase[w];
     }
-    int64_t p = base + obw + ubw;
-    for (uint32_t left = nwv | owv; left; left &= left - 1u) {
-      const uint32_t b = (uint32_t)(__ffs(left) - 1);
-      int32_t c = 0, g = 0;
-      if ((owv >> b) & 1u) {
-        const int64_t e = o0 + obw + bits_below(owv, b);
-        c = a.count[e];
-        g = a.gen[e];
+    const uint32_t uw = nwv | owv;
+    const uint32_t n = (uint32_t)__popc(uw);
+    const uint32_t ex = wave_scan_dpp(n) - n;
+    const uint32_t total = lane_value(ex + n, 63);
+    const int64_t p0 = base + (int64_t)lane_value(obw + ubw, 0);  // lane 0 holds word g0 < words
+    for (uint32_t i0 = 0; i0 < total; i0 += 64) {  // uniform: every lane takes part in the shuffles
+      const uint32_t i = i0 + (uint32_t)lane;
+      int s = 0;
+#pragma unroll
+      for (int step = 32; step >= 1; step >>= 1)  // s + step <= 63 at every step
+        if ((uint32_t)__shfl((int)ex, s + step) <= i) s += step;
+      const uint32_t k = i - (uint32_t)__shfl((int)ex, s);
+      const uint32_t u = (uint32_t)__shfl((int)uw, s);
+      const uint32_t nws = (uint32_t)__shfl((int)nwv, s), ows = (uint32_t)__shfl((int)owv, s);
+      const uint32_t nbs = (uint32_t)__shfl((int)nbw, s), obs = (uint32_t)__shfl((int)obw, s);
+      uint32_t b = 0, kk = k;  // the k-th set bit of u, by halves
+#pragma unroll
+      for (uint32_t h = 16; h >= 1; h >>= 1) {
+        const uint32_t c = (uint32_t)__popc((u >> b) & ((1u << h) - 1u));
+        if (kk >= c) {
+          b += h;
+          kk -= c;
+        }
       }
-      if ((nwv >> b) & 1u) {
-        const uint32_t add = sh.cnt[nbw + bits_below(nwv, b)];
-        c += (int32_t)(add & 0xFFFFu);
-        g += (int32_t)(add >> 16);
+      if (i < total) {
+        int32_t c = 0, g = 0;
+        if ((ows >> b) & 1u) {
+          const int64_t e = o0 + obs + bits_below(ows, b);
+          c = a.count[e];
+          g = a.gen[e];
+        }
+        if ((nws >> b) & 1u) {
+          const uint32_t add = sh.cnt[nbs + bits_below(nws, b)];
+          c += (int32_t)(add & 0xFFFFu);
+          g += (int32_t)(add >> 16);
+        }
+        const int64_t p = p0 + i;
+        a.out_ids[p] = 32 * (g0 + s) + (int32_t)b;
+        a.out_count[p] = c;
+        a.out_gen[p] = g;
       }
-      a.out_ids[p] = 32 * w + (int32_t)b;
-      a.out_count[p] = c;
-      a.out_gen[p] = g;
-      ++p;
     }
   }
 }
