@@ -75,6 +75,18 @@ struct HistAppendShared {
   SyncSlots sync;
 };
 
+// The count pass needs only the two bitmaps: at 33 KB two of its
+// workgroups fit on a CU, where the write pass's 147 KB leave room for one.
+struct HistCountShared {
+  uint32_t nb[kHistWords];
+  uint32_t ob[kHistWords];
+  int bad;
+  SyncSlots sync;
+};
+
+template <bool WRITE> struct HistSharedOf { using T = HistCountShared; };
+template <> struct HistSharedOf<true> { using T = HistAppendShared; };
+
 __device__ __forceinline__ uint32_t bits_below(uint32_t w, uint32_t b) { return __popc(w & ((1u << b) - 1u)); }
 
 // One row of dsr_history_append.  WRITE = false: validate and count the
@@ -82,7 +94,7 @@ __device__ __forceinline__ uint32_t bits_below(uint32_t w, uint32_t b) { return 
 // rejected, and every row when the total exceeds cap, write nothing).
 template <bool WRITE>
 __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
-  __shared__ HistAppendShared sh;
+  __shared__ typename HistSharedOf<WRITE>::T sh;
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
@@ -106,11 +118,23 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
       return;
     }
   }
+  // The row's new tokens, all loaded before any is used (their loads overlap
+  // the set-up below): token q of this thread is at position tid + q * kThreads
+  // of the row's tokens.  A row of more than kMaxAppend tokens was rejected
+  // above; this reads inside [t0, t1) whatever m is.
+  int32_t tk[kTokPer];
+#pragma unroll
+  for (int q = 0; q < kTokPer; ++q) {
+    const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
+    tk[q] = i < m ? a.tokens[t0 + i] : 0;
+  }
   for (int w = tid; w < words; w += kThreads) {
     sh.nb[w] = 0u;
     sh.ob[w] = 0u;
   }
-  for (int64_t i = tid; i < m; i += kThreads) sh.cnt[i] = 0u;
+  if constexpr (WRITE) {
+    for (int64_t i = tid; i < m; i += kThreads) sh.cnt[i] = 0u;
+  }
   if (tid == 0) sh.bad = 0;
   lds_barrier();
   // Old ids: strictly increasing, in range, 1 <= count <= DSR_MAX_COUNT, 0 <= gen <= count.
@@ -120,14 +144,6 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
                     g <= c;
     if (ok) atomicOr(&sh.ob[id >> 5], 1u << (id & 31));
     else sh.bad = 1;
-  }
-  // The row's new tokens, all loaded before any is used: token q of this
-  // thread is at position tid + q * kThreads of the row's tokens.
-  int32_t tk[kTokPer];
-#pragma unroll
-  for (int q = 0; q < kTokPer; ++q) {
-    const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
-    tk[q] = i < m ? a.tokens[t0 + i] : 0;
   }
 #pragma unroll
   for (int q = 0; q < kTokPer; ++q) {
@@ -161,101 +177,102 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
   long long n_old;
   uint32_t bex, btot;
   const long long oex = bs.scan2(po, pn | (pu << 16), n_old, bex, btot);
-  if (!WRITE) {
+  if constexpr (!WRITE) {
     if (tid == 0) {
       a.out_status[row] = DSR_OK;
       a.out_off[row + 1] = n_old + (long long)(btot >> 16);
     }
     return;
-  }
-  {
-    uint32_t nb0 = bex & 0xFFFFu, ub0 = bex >> 16, ob0 = (uint32_t)oex;
+  } else {
+    {
+      uint32_t nb0 = bex & 0xFFFFu, ub0 = bex >> 16, ob0 = (uint32_t)oex;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int w = 4 * tid + q;
+      for (int q = 0; q < 4; ++q) {
+        const int w = 4 * tid + q;
+        if (w < words) {
+          sh.nbase[w] = nb0;
+          sh.obase[w] = ob0;
+          sh.ubase[w] = ub0;
+        }
+        nb0 += __popc(nw[q]);
+        ob0 += __popc(ow[q]);
+        ub0 += __popc(nw[q] & ~ow[q]);
+      }
+    }
+    lds_barrier();
+    // Multiplicities of the new ids (and of their generated occurrences).
+#pragma unroll
+    for (int q = 0; q < kTokPer; ++q) {
+      const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
+      if (i < m) {
+        const uint32_t t = (uint32_t)tk[q], w = t >> 5, b = t & 31u;
+        atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], i >= gf ? 0x10001u : 1u);
+      }
+    }
+    lds_barrier();
+    // The merged row is the union of both bitmaps in id order.  Wave w takes
+    // the groups of 64 consecutive words g0 = 64 w, 64 (w + 16), ...; the
+    // group's entries are contiguous in the output from word g0's rank in the
+    // merged row (old ids below it plus absent new ids below it), word s of the
+    // group holding entries [ex_s, ex_s + popc) of them.  The wave writes them
+    // 64 at a time with lane l taking entry i = i0 + l, so every store covers
+    // 64 consecutive entries: the word holding entry i is the last lane s with
+    // ex_s <= i (a binary search over the lanes), its id is that word's
+    // (i - ex_s)-th set bit.  An old id's entry is its rank in the old bitmap;
+    // a new id's multiplicities are at its rank in the new bitmap.
+    const int lane = lane_id(), wave = wave_id();
+    const int64_t base = a.out_off[row];
+    for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {  // uniform over the wave
+      const int w = g0 + lane;
+      uint32_t nwv = 0u, owv = 0u, nbw = 0u, obw = 0u, ubw = 0u;
       if (w < words) {
-        sh.nbase[w] = nb0;
-        sh.obase[w] = ob0;
-        sh.ubase[w] = ub0;
+        nwv = sh.nb[w];
+        owv = sh.ob[w];
+        nbw = sh.nbase[w];
+        obw = sh.obase[w];
+        ubw = sh.ubase[w];
       }
-      nb0 += __popc(nw[q]);
-      ob0 += __popc(ow[q]);
-      ub0 += __popc(nw[q] & ~ow[q]);
-    }
-  }
-  lds_barrier();
-  // Multiplicities of the new ids (and of their generated occurrences).
+      const uint32_t uw = nwv | owv;
+      const uint32_t n = (uint32_t)__popc(uw);
+      const uint32_t ex = wave_scan_dpp(n) - n;
+      const uint32_t total = lane_value(ex + n, 63);
+      const int64_t p0 = base + (int64_t)lane_value(obw + ubw, 0);  // lane 0 holds word g0 < words
+      for (uint32_t i0 = 0; i0 < total; i0 += 64) {  // uniform: every lane takes part in the shuffles
+        const uint32_t i = i0 + (uint32_t)lane;
+        int s = 0;
 #pragma unroll
-  for (int q = 0; q < kTokPer; ++q) {
-    const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
-    if (i < m) {
-      const uint32_t t = (uint32_t)tk[q], w = t >> 5, b = t & 31u;
-      atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], i >= gf ? 0x10001u : 1u);
-    }
-  }
-  lds_barrier();
-  // The merged row is the union of both bitmaps in id order.  Wave w takes
-  // the groups of 64 consecutive words g0 = 64 w, 64 (w + 16), ...; the
-  // group's entries are contiguous in the output from word g0's rank in the
-  // merged row (old ids below it plus absent new ids below it), word s of the
-  // group holding entries [ex_s, ex_s + popc) of them.  The wave writes them
-  // 64 at a time with lane l taking entry i = i0 + l, so every store covers
-  // 64 consecutive entries: the word holding entry i is the last lane s with
-  // ex_s <= i (a binary search over the lanes), its id is that word's
-  // (i - ex_s)-th set bit.  An old id's entry is its rank in the old bitmap;
-  // a new id's multiplicities are at its rank in the new bitmap.
-  const int lane = lane_id(), wave = wave_id();
-  const int64_t base = a.out_off[row];
-  for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {  // uniform over the wave
-    const int w = g0 + lane;
-    uint32_t nwv = 0u, owv = 0u, nbw = 0u, obw = 0u, ubw = 0u;
-    if (w < words) {
-      nwv = sh.nb[w];
-      owv = sh.ob[w];
-      nbw = sh.nbase[w];
-      obw = sh.obase[w];
-      ubw = sh.ubase[w];
-    }
-    const uint32_t uw = nwv | owv;
-    const uint32_t n = (uint32_t)__popc(uw);
-    const uint32_t ex = wave_scan_dpp(n) - n;
-    const uint32_t total = lane_value(ex + n, 63);
-    const int64_t p0 = base + (int64_t)lane_value(obw + ubw, 0);  // lane 0 holds word g0 < words
-    for (uint32_t i0 = 0; i0 < total; i0 += 64) {  // uniform: every lane takes part in the shuffles
-      const uint32_t i = i0 + (uint32_t)lane;
-      int s = 0;
+        for (int step = 32; step >= 1; step >>= 1)  // s + step <= 63 at every step
+          if ((uint32_t)__shfl((int)ex, s + step) <= i) s += step;
+        const uint32_t k = i - (uint32_t)__shfl((int)ex, s);
+        const uint32_t u = (uint32_t)__shfl((int)uw, s);
+        const uint32_t nws = (uint32_t)__shfl((int)nwv, s), ows = (uint32_t)__shfl((int)owv, s);
+        const uint32_t nbs = (uint32_t)__shfl((int)nbw, s), obs = (uint32_t)__shfl((int)obw, s);
+        uint32_t b = 0, kk = k;  // the k-th set bit of u, by halves
 #pragma unroll
-      for (int step = 32; step >= 1; step >>= 1)  // s + step <= 63 at every step
-        if ((uint32_t)__shfl((int)ex, s + step) <= i) s += step;
-      const uint32_t k = i - (uint32_t)__shfl((int)ex, s);
-      const uint32_t u = (uint32_t)__shfl((int)uw, s);
-      const uint32_t nws = (uint32_t)__shfl((int)nwv, s), ows = (uint32_t)__shfl((int)owv, s);
-      const uint32_t nbs = (uint32_t)__shfl((int)nbw, s), obs = (uint32_t)__shfl((int)obw, s);
-      uint32_t b = 0, kk = k;  // the k-th set bit of u, by halves
-#pragma unroll
-      for (uint32_t h = 16; h >= 1; h >>= 1) {
-        const uint32_t c = (uint32_t)__popc((u >> b) & ((1u << h) - 1u));
-        if (kk >= c) {
-          b += h;
-          kk -= c;
+        for (uint32_t h = 16; h >= 1; h >>= 1) {
+          const uint32_t c = (uint32_t)__popc((u >> b) & ((1u << h) - 1u));
+          if (kk >= c) {
+            b += h;
+            kk -= c;
+          }
         }
-      }
-      if (i < total) {
-        int32_t c = 0, g = 0;
-        if ((ows >> b) & 1u) {
-          const int64_t e = o0 + obs + bits_below(ows, b);
-          c = a.count[e];
-          g = a.gen[e];
+        if (i < total) {
+          int32_t c = 0, g = 0;
+          if ((ows >> b) & 1u) {
+            const int64_t e = o0 + obs + bits_below(ows, b);
+            c = a.count[e];
+            g = a.gen[e];
+          }
+          if ((nws >> b) & 1u) {
+            const uint32_t add = sh.cnt[nbs + bits_below(nws, b)];
+            c += (int32_t)(add & 0xFFFFu);
+            g += (int32_t)(add >> 16);
+          }
+          const int64_t p = p0 + i;
+          a.out_ids[p] = 32 * (g0 + s) + (int32_t)b;
+          a.out_count[p] = c;
+          a.out_gen[p] = g;
         }
-        if ((nws >> b) & 1u) {
-          const uint32_t add = sh.cnt[nbs + bits_below(nws, b)];
-          c += (int32_t)(add & 0xFFFFu);
-          g += (int32_t)(add >> 16);
-        }
-        const int64_t p = p0 + i;
-        a.out_ids[p] = 32 * (g0 + s) + (int32_t)b;
-        a.out_count[p] = c;
-        a.out_gen[p] = g;
       }
     }
   }
