@@ -988,8 +988,12 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   const uint32_t cw0 = (uint32_t)ow * CW + (uint32_t)js * 64u;  // first chunk of that slot
   // Kept penalised masses of that slot's chunks, per chunk and per element
   // (only the run of entries whose tokens lie in the wave's chunks).
+  // Each thread takes the entries of its own stride (e = tid mod kThreads),
+  // whose packed words it wrote itself: no other thread's global stores are
+  // read, so the LDS-only barriers above order everything this pass needs.
   const int64_t elo = sh.elo[ow], ehi = sh.elo[ow + 1];
-  pen_batches<1>(ehi, elo + tid, fetch_pk, [&](int64_t, PenPk x) {
+  const int64_t first = elo + (((int64_t)tid - elo) % kThreads + kThreads) % kThreads;
+  pen_batches<1>(ehi, first, fetch_pk, [&](int64_t, PenPk x) {
     const uint32_t cid = (uint32_t)(x.id >> 3);
     if (x.pk != 0 && cid >= cw0 && cid < cw0 + 64u && cid < (uint32_t)(ow + 1) * CW &&
         pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
