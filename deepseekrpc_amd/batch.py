@@ -809,14 +809,25 @@ class PreparedVerify:
 # Probability-vector kernels used by the drop-in API.
 
 
+def prob_stats_launch(p: torch.Tensor, slot: torch.Tensor):
+    """``dsr_prob_stats`` of a float64 device vector into ``slot``, a float64
+    ``[3]`` device view: the sum, then the four int32 results.  Nothing is
+    synchronised; ``prob_stats_read`` decodes the slot once it is on the host."""
+    lib = N.load()
+    N.check(lib.dsr_prob_stats(_ptr(p), p.numel(), _ptr(slot[0:1]), _ptr(slot[1:3]), _stream()), "dsr_prob_stats")
+
+
+def prob_stats_read(slot: torch.Tensor):
+    """(sum, valid, n_positive, first_positive, argmax) from a host copy of a slot."""
+    o = slot[1:3].view(torch.int32).tolist()
+    return float(slot[0]), bool(o[0]), int(o[1]), int(o[2]), int(o[3])
+
+
 def prob_stats(p: torch.Tensor):
     """(sum, valid, n_positive, first_positive, argmax) of a float64 device vector."""
-    lib = N.load()
-    out_sum = torch.empty(1, dtype=torch.float64, device=p.device)
-    out = torch.empty(4, dtype=torch.int32, device=p.device)
-    N.check(lib.dsr_prob_stats(_ptr(p), p.numel(), _ptr(out_sum), _ptr(out), _stream()), "dsr_prob_stats")
-    o = out.cpu().tolist()
-    return float(out_sum.item()), bool(o[0]), int(o[1]), int(o[2]), int(o[3])
+    slot = torch.empty(3, dtype=torch.float64, device=p.device)
+    prob_stats_launch(p, slot)
+    return prob_stats_read(slot.cpu())
 
 
 def prob_categorical(p: torch.Tensor, u: float):
@@ -827,12 +838,19 @@ def prob_categorical(p: torch.Tensor, u: float):
     return int(tok), int(flags)
 
 
-def prob_correction(p: torch.Tensor, q: torch.Tensor):
+def prob_correction_launch(p: torch.Tensor, q: torch.Tensor, status: torch.Tensor) -> torch.Tensor:
+    """The normalised residual of ``p`` and ``q`` as a new device vector, its
+    status into the int32 device view ``status``; nothing is synchronised."""
     lib = N.load()
     out = torch.empty_like(p)
-    st = torch.empty(1, dtype=torch.int32, device=p.device)
-    N.check(lib.dsr_prob_correction(_ptr(p), _ptr(q), p.numel(), _ptr(out), _ptr(st), _stream()),
+    N.check(lib.dsr_prob_correction(_ptr(p), _ptr(q), p.numel(), _ptr(out), _ptr(status), _stream()),
             "dsr_prob_correction")
+    return out
+
+
+def prob_correction(p: torch.Tensor, q: torch.Tensor):
+    st = torch.empty(1, dtype=torch.int32, device=p.device)
+    out = prob_correction_launch(p, q, st)
     return out, int(st.item())
 
 

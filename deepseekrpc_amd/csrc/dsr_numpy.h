@@ -17,121 +17,180 @@
 //  * np.cumsum is a sequential running sum.
 //
 // One workgroup handles a vector of at most 16 buffers: wave w owns buffer w.
-// Its lane 0 lists the buffer's leaves (ranges of at most 128 elements, each
-// at least 64 long when the buffer is), the lanes sum the leaves, and lane 0
-// adds them back up along the same tree.  Not on the sampling hot path.
+// A full buffer's tree is balanced (64 leaves of 128), so its wave sums it
+// with no list: 8 lanes per leaf keep the leaf's 8 strided running sums, and
+// xor butterflies over 1, 2, 4 lanes combine them in NumPy's order, then
+// over 8, 16, 32 lanes give the sums of 1,024 elements, which the tree's top
+// three levels add.  (Floating-point addition is commutative, so a lane
+// pair's two sums agree bit for bit.)  A shorter last buffer's wave lists
+// its tree level by level (a scan per level, no recursion), sums each leaf
+// the same way (8 lanes, leftovers after the butterfly) and adds the tree
+// back up level by level.
 #pragma once
 
-#include "dsr_common.h"
+#include "dsr_wave.h"
 
 namespace dsr {
 
 constexpr int kNpBuffer = 8192;   // NumPy's default iterator buffer, in elements
 constexpr int kNpLeaf = 128;      // pairwise-summation block
-constexpr int kNpMaxLeaves = 128; // leaves of one buffer: each leaf holds >= 64 elements
+constexpr int kNpMaxLeaves = 128; // leaves of a buffer shorter than 8,192: each holds >= 64 elements
+constexpr int kNpLevels = 8;      // a short buffer's tree: the root, then at most 7 levels of splits
 constexpr int64_t kNpMaxLength = (int64_t)kWaves * kNpBuffer;
 
 struct NpSumShared {
-  int32_t leaf_lo[kWaves][kNpMaxLeaves];
-  int32_t leaf_len[kWaves][kNpMaxLeaves];
-  double leaf_sum[kWaves][kNpMaxLeaves];
+  int32_t node_lo[kNpLevels][kNpMaxLeaves];   // a short buffer's tree, level by level, in order
+  int32_t node_len[kNpLevels][kNpMaxLeaves];
+  int32_t node_pos[kNpLevels][kNpMaxLeaves];  // where a node's range sits in the next level
+  int32_t nodes[kNpLevels];
+  double val[kNpLevels][kNpMaxLeaves];        // node sums, from the leaves up
   double buffer_sum[kWaves];
-  int leaves[kWaves];
 };
-
-// Leaves of the pairwise tree over [lo, lo + n), left to right.
-template <int D>
-__device__ __noinline__ void np_list_leaves(int lo, int n, int32_t* out_lo, int32_t* out_len, int& count) {
-  if (n <= kNpLeaf) {
-    out_lo[count] = lo;
-    out_len[count] = n;
-    ++count;
-    return;
-  }
-  int h = n / 2;
-  h -= h % 8;
-  np_list_leaves<D - 1>(lo, h, out_lo, out_len, count);
-  np_list_leaves<D - 1>(lo + h, n - h, out_lo, out_len, count);
-}
-template <>
-__device__ __noinline__ void np_list_leaves<0>(int lo, int n, int32_t* out_lo, int32_t* out_len, int& count) {
-  out_lo[count] = lo;
-  out_len[count] = n;
-  ++count;
-}
-
-// The tree's sum from its leaf sums, consumed left to right.
-template <int D>
-__device__ __noinline__ double np_tree_sum(int n, const double* leaf, int& next) {
-  if (n <= kNpLeaf) return leaf[next++];
-  int h = n / 2;
-  h -= h % 8;
-  const double a = np_tree_sum<D - 1>(h, leaf, next);
-  const double b = np_tree_sum<D - 1>(n - h, leaf, next);
-  return a + b;
-}
-template <>
-__device__ __noinline__ double np_tree_sum<0>(int, const double* leaf, int& next) {
-  return leaf[next++];
-}
-
-// A buffer of 8,192 splits at most 6 times before its ranges fit a leaf.
-constexpr int kNpDepth = 8;
-
-// One leaf: 8 strided running sums (n >= 8) or a plain running sum (n < 8).
-template <class Load>
-__device__ double np_leaf_sum(Load load, int64_t base, int n) {
-  if (n < 8) {
-    double r = 0.0;
-    for (int i = 0; i < n; ++i) r += load(base + i);
-    return r;
-  }
-  double r0 = load(base + 0), r1 = load(base + 1), r2 = load(base + 2), r3 = load(base + 3);
-  double r4 = load(base + 4), r5 = load(base + 5), r6 = load(base + 6), r7 = load(base + 7);
-  int i = 8;
-  for (; i < n - (n % 8); i += 8) {
-    r0 += load(base + i + 0);
-    r1 += load(base + i + 1);
-    r2 += load(base + i + 2);
-    r3 += load(base + i + 3);
-    r4 += load(base + i + 4);
-    r5 += load(base + i + 5);
-    r6 += load(base + i + 6);
-    r7 += load(base + i + 7);
-  }
-  double res = ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7));
-  for (; i < n; ++i) res += load(base + i);
-  return res;
-}
 
 // np.add.reduce of load(0 .. n-1), n <= kNpMaxLength, for the whole
 // workgroup (every thread must call it; every thread gets the result).
-template <class Load>
-__device__ double np_sum(Load load, int64_t n, NpSumShared& sh) {
+// load(i) is called exactly once per element, and visit(i, x) then sees it,
+// in some thread; within a thread the visits come in increasing i.  Inlined,
+// so that what the callbacks capture stays in registers.
+template <class Load, class Visit>
+__device__ __forceinline__ double np_sum(Load load, int64_t n, NpSumShared& sh, Visit visit) {
   const int w = wave_id(), lane = lane_id();
+  const int g = lane >> 3, k = lane & 7;  // leaf within a group of 8, running sum within the leaf
   const int64_t lo = (int64_t)w * kNpBuffer;
-  const int len = lo < n ? (int)((n - lo) < kNpBuffer ? (n - lo) : kNpBuffer) : 0;
-  if (len > 0 && lane == 0) {
-    int count = 0;
-    np_list_leaves<kNpDepth>(0, len, sh.leaf_lo[w], sh.leaf_len[w], count);
-    sh.leaves[w] = count;
+  const int len = lo < n ? (int)((n - lo) < kNpBuffer ? (n - lo) : kNpBuffer) : 0;  // uniform per wave
+  const bool listed = len >= 8 && len < kNpBuffer;  // at most one wave: the last buffer
+  // A short buffer's tree, breadth first: level l + 1 holds level l's ranges
+  // in order, each one longer than a leaf replaced by its two halves (the
+  // split rounded down to a multiple of 8), so the last level lists the
+  // leaves.  The loop runs a fixed number of levels: once every range is a
+  // leaf a level copies the one above it.
+  if (listed && lane == 0) {
+    sh.nodes[0] = 1;
+    sh.node_lo[0][0] = 0;
+    sh.node_len[0][0] = len;
   }
   __syncthreads();
-  if (len > 0) {
-    for (int j = lane; j < sh.leaves[w]; j += 64)
-      sh.leaf_sum[w][j] = np_leaf_sum(load, lo + sh.leaf_lo[w][j], sh.leaf_len[w][j]);
+  for (int l = 0; l + 1 < kNpLevels; ++l) {  // every thread takes part in the barriers
+    if (listed) {
+      const int cnt = sh.nodes[l];
+      const int i0 = lane, i1 = lane + 64;
+      const int m0 = i0 < cnt ? sh.node_len[l][i0] : 0, m1 = i1 < cnt ? sh.node_len[l][i1] : 0;
+      const uint32_t c0 = i0 < cnt ? (m0 > kNpLeaf ? 2u : 1u) : 0u;
+      const uint32_t c1 = i1 < cnt ? (m1 > kNpLeaf ? 2u : 1u) : 0u;
+      const uint32_t s0 = wave_scan_dpp(c0), s1 = wave_scan_dpp(c1);
+      const uint32_t t0 = lane_value(s0, 63), t1 = lane_value(s1, 63);
+      auto emit = [&](int i, int m, uint32_t c, uint32_t e) {
+        if (c == 0 || e + c > (uint32_t)kNpMaxLeaves) return;  // the bound never binds: leaves hold >= 64
+        const int a = sh.node_lo[l][i];
+        sh.node_pos[l][i] = (int)e;
+        if (c == 2) {
+          int h = m / 2;
+          h -= h % 8;
+          sh.node_lo[l + 1][e] = a;
+          sh.node_len[l + 1][e] = h;
+          sh.node_lo[l + 1][e + 1] = a + h;
+          sh.node_len[l + 1][e + 1] = m - h;
+        } else {
+          sh.node_lo[l + 1][e] = a;
+          sh.node_len[l + 1][e] = m;
+        }
+      };
+      emit(i0, m0, c0, s0 - c0);
+      emit(i1, m1, c1, t0 + s1 - c1);
+      if (lane == 0) sh.nodes[l + 1] = (int)(t0 + t1 < (uint32_t)kNpMaxLeaves ? t0 + t1 : kNpMaxLeaves);
+    }
+    __syncthreads();
+  }
+  if (len == kNpBuffer) {
+    // A full buffer's tree is balanced: 64 leaves of 128.  The sum of leaves
+    // 8q .. 8q + 7 (elements 1,024 q .. 1,024 q + 1,023):
+    auto group = [&](int q) -> double {
+      const int64_t base = lo + 128 * (8 * q + g) + k;  // leaf 8q + g, running sum k
+      double v[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) v[t] = load(base + 8 * t);
+      double r = v[0];
+      visit(base, v[0]);
+#pragma unroll
+      for (int t = 1; t < 16; ++t) {
+        r += v[t];
+        visit(base + 8 * t, v[t]);
+      }
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) r += __shfl_xor(r, m);
+      return r;
+    };
+    const double s0 = group(0), s1 = group(1), s2 = group(2), s3 = group(3);
+    const double s4 = group(4), s5 = group(5), s6 = group(6), s7 = group(7);
+    if (lane == 0) sh.buffer_sum[w] = ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7));
+  } else if (listed) {
+    constexpr int L = kNpLevels - 1;
+    const int leaves = sh.nodes[L];
+    for (int q0 = 0; q0 < leaves; q0 += 8) {  // uniform over the wave
+      const int j = q0 + g;
+      const bool has = j < leaves;
+      const int llo = has ? sh.node_lo[L][j] : 0, llen = has ? sh.node_len[L][j] : 0;
+      const int nb = llen >> 3;  // full 8-element rows of the leaf (every leaf here holds >= 8)
+      const int64_t base = lo + llo + k;
+      double v[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) v[t] = t < nb ? load(base + 8 * t) : 0.0;
+      double r = v[0];
+      if (nb > 0) visit(base, v[0]);
+#pragma unroll
+      for (int t = 1; t < 16; ++t) {
+        if (t < nb) {
+          r += v[t];
+          visit(base + 8 * t, v[t]);
+        }
+      }
+      r += __shfl_xor(r, 1);
+      r += __shfl_xor(r, 2);
+      r += __shfl_xor(r, 4);
+      if (has && k == 0) {
+        for (int i = 8 * nb; i < llen; ++i) {  // the leftovers, in order
+          const double x = load(lo + llo + i);
+          r += x;
+          visit(lo + llo + i, x);
+        }
+        sh.val[L][j] = r;
+      }
+    }
+  } else if (len > 0 && lane == 0) {  // fewer than 8 elements: a running sum from 0.0
+    double r = 0.0;
+    for (int i = 0; i < len; ++i) {
+      const double x = load(lo + i);
+      r += x;
+      visit(lo + i, x);
+    }
+    sh.buffer_sum[w] = r;
   }
   __syncthreads();
-  if (len > 0 && lane == 0) {
-    int next = 0;
-    sh.buffer_sum[w] = np_tree_sum<kNpDepth>(len, sh.leaf_sum[w], next);
+  // The short buffer's tree from the leaves up: a split range is its left
+  // half's sum plus its right half's.
+  for (int l = kNpLevels - 2; l >= 0; --l) {
+    if (listed) {
+      const int cnt = sh.nodes[l];
+      for (int i = lane; i < cnt; i += 64) {
+        const int p = sh.node_pos[l][i];
+        const double a = sh.val[l + 1][p];
+        sh.val[l][i] = sh.node_len[l][i] > kNpLeaf ? a + sh.val[l + 1][p + 1] : a;
+      }
+    }
+    __syncthreads();
   }
+  if (listed && lane == 0) sh.buffer_sum[w] = sh.val[0][0];
   __syncthreads();
   double total = 0.0;
   const int buffers = (int)((n + kNpBuffer - 1) / kNpBuffer);
   for (int b = 0; b < buffers; ++b) total = b == 0 ? sh.buffer_sum[0] : total + sh.buffer_sum[b];
   __syncthreads();
   return total;
+}
+
+template <class Load>
+__device__ __forceinline__ double np_sum(Load load, int64_t n, NpSumShared& sh) {
+  return np_sum(load, n, sh, [](int64_t, double) {});
 }
 
 }  // namespace dsr

@@ -204,8 +204,10 @@ __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_
   __shared__ NpSumShared np;
   int bad = 0;
   long long npos = 0, first = LLONG_MAX;
-  RowMax mx;
-  row_pass<double>(n, [&](int64_t i) { return p[i]; }, [&](int64_t i, double x) {
+  RowMax mx;  // every thread visits its elements in increasing index order
+  // The sum the reference tests against 1 +- 1e-10 (sampling.py:111-113), in
+  // NumPy's order, with the other statistics taken from the same loads.
+  const double s = np_sum([&](int64_t i) { return p[i]; }, n, np, [&](int64_t i, double x) {
     if (!isfinite(x) || x < 0.0) bad = 1;
     if (x > 0.0) {
       ++npos;
@@ -213,8 +215,6 @@ __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_
     }
     mx.add(i, x);
   });
-  // The sum the reference tests against 1 +- 1e-10 (sampling.py:111-113), in NumPy's order.
-  const double s = np_sum([&](int64_t i) { return p[i]; }, n, np);
   bad = block_or(bad, sh.b);
   npos = block_sum_i64(npos, sh.b);
   first = block_min_i64(first, sh.b);
@@ -260,11 +260,10 @@ __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, 
 __global__ __launch_bounds__(kThreads) void k_prob_correction(const double* p, const double* q, int64_t n,
                                                               double* out, int32_t* st) {
   __shared__ NpSumShared np;
-  row_pass<ProbPair>(n, [&](int64_t i) { return ProbPair{p[i], q[i]}; },
-                     [&](int64_t i, ProbPair v) { out[i] = fmax(v.p - v.q, 0.0); });
-  __syncthreads();  // the residual is read back across threads (global memory, one workgroup)
-  // residual.sum() in NumPy's order, then residual / total (sampling.py:134-139).
-  const double total = np_sum([&](int64_t i) { return out[i]; }, n, np);
+  // residual.sum() in NumPy's order as the residual is formed and stored,
+  // then residual / total (sampling.py:134-139).
+  const double total = np_sum([&](int64_t i) { return fmax(p[i] - q[i], 0.0); }, n, np,
+                              [&](int64_t i, double x) { out[i] = x; });
   const bool ok = total > 0.0 && isfinite(total);
   if (ok) row_pass<double>(n, [&](int64_t i) { return out[i]; }, [&](int64_t i, double x) { out[i] = x / total; });
   if (threadIdx.x == 0) st[0] = ok ? DSR_OK : DSR_E_CORRECTION;

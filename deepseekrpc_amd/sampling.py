@@ -216,20 +216,66 @@ def _history_table(counts, generated_counts, n):
     return table
 
 
-def _distribution(values):
-    """Validated float64 probability vector on the device (sampling.py:109-115)."""
+_DIST_MSG = "verifier requires a normalized complete FP64 probability vector"
+
+
+def _dist_input(values):
+    """A probability vector of the shape and dtype the reference accepts
+    (sampling.py:109-111), as a device tensor."""
     if isinstance(values, torch.Tensor):
         ok = values.dim() == 1 and 1 <= values.numel() <= VOCAB and values.dtype == torch.float64
     else:
         values = np.asarray(values)
         ok = values.ndim == 1 and 1 <= len(values) <= VOCAB and values.dtype == np.float64
     if not ok:
-        raise ValidationError("verifier requires a normalized complete FP64 probability vector")
-    t, _ = _on_device(values)
-    total, valid, npos, first, argmax = batch.prob_stats(t)
+        raise ValidationError(_DIST_MSG)
+    return _on_device(values)[0]
+
+
+def _dist_checked(t, stats):
+    """The vector's statistics checked as sampling.py:112-115 checks them."""
+    total, valid, npos, first, argmax = stats
     if not valid or not math.isclose(total, 1.0, rel_tol=0, abs_tol=1e-10):
-        raise ValidationError("verifier requires a normalized complete FP64 probability vector")
+        raise ValidationError(_DIST_MSG)
     return _Dist(t, npos, first, argmax)
+
+
+def _distribution(values):
+    """Validated float64 probability vector on the device (sampling.py:109-115)."""
+    t = _dist_input(values)
+    return _dist_checked(t, batch.prob_stats(t))
+
+
+def _distributions(rows):
+    """``_as_dist`` of every row, with one synchronisation for all the rows
+    that still need their statistics.  Every rejection carries the same
+    message, so checking the shapes first and the values after reports what
+    checking row by row would."""
+    items = [row if isinstance(row, _Dist) else _dist_input(row) for row in rows]
+    pending = [i for i, item in enumerate(items) if not isinstance(item, _Dist)]
+    if pending:
+        slots = torch.empty(len(pending), 3, dtype=torch.float64, device=items[pending[0]].device)
+        for n, i in enumerate(pending):
+            batch.prob_stats_launch(items[i], slots[n])
+        host = slots.cpu()
+        for n, i in enumerate(pending):
+            items[i] = _dist_checked(items[i], batch.prob_stats_read(host[n]))
+    return tuple(items)
+
+
+def _residual(target, proposal):
+    """The validated normalised residual of two distributions (sampling.py:131-139,
+    then :109-115) behind one synchronisation: the correction's status and the
+    residual's statistics come back together."""
+    if len(target) != len(proposal):
+        raise ValidationError("target and proposal vocabulary sizes differ")
+    buf = torch.empty(4, dtype=torch.float64, device=target.tensor.device)  # stats slot, then the status
+    out = batch.prob_correction_launch(target.tensor, proposal.tensor, buf[3:4].view(torch.int32)[0:1])
+    batch.prob_stats_launch(out, buf[0:3])
+    host = buf.cpu()
+    if int(host[3:4].view(torch.int32)[0]) != N.OK:
+        raise ValidationError("a rejected proposal has no positive correction distribution")
+    return _dist_checked(out, batch.prob_stats_read(host[0:3]))
 
 
 @dataclass
@@ -401,7 +447,7 @@ def verify_drafts(target_rows, proposal_rows, proposal_ids, transaction, *, gree
     integer(output_limit, "remaining output limit", 1, MAX_COUNT)
     if type(greedy) is not bool or len(proposal_rows) != len(proposal_ids) or len(target_rows) != len(proposal_ids) + 1:
         raise ValidationError("target/proposal verification row counts differ")
-    proposals = tuple(_as_dist(row) for row in proposal_rows)
+    proposals = _distributions(proposal_rows)
     first_target = _as_dist(target_rows[0])
     vocabulary = len(first_target)
     if any(len(row) != vocabulary for row in proposals):
@@ -425,16 +471,23 @@ def verify_drafts(target_rows, proposal_rows, proposal_ids, transaction, *, gree
                 raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")
             accepted = token == target.argmax
         else:
-            positive, _ = batch.prob_accept(target.tensor, proposal.tensor, token, 0.0)
+            preview = getattr(transaction, "_preview", None)
+            # One launch tests q(x) > 0 and the draw together when the draw can
+            # be read ahead; the domain still advances only after the test.
+            u = preview("accept") if preview is not None else 0.0
+            positive, accepted = batch.prob_accept(target.tensor, proposal.tensor, token, u)
             if not positive:
                 raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")
-            u = transaction.random("accept")
-            _, accepted = batch.prob_accept(target.tensor, proposal.tensor, token, u)
+            if preview is None:
+                u = transaction.random("accept")
+                _, accepted = batch.prob_accept(target.tensor, proposal.tensor, token, u)
+            elif transaction.random("accept") != u:
+                raise RuntimeError("RNG domain moved between the preview and the draw")
         if not accepted:
             if greedy:
                 replacement = target.argmax
             else:
-                residual = _distribution(_correction(target, proposal))
+                residual = _residual(target, proposal)
                 replacement = categorical(residual, lambda: transaction.random("target"))
             stop = "eos" if replacement in eos_ids else "length" if len(output) + 1 >= output_limit else None
             return VerificationDecision(index, tuple(output) + (replacement,), replacement, stop)

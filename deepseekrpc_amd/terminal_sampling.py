@@ -41,7 +41,7 @@ from . import _native as N
 from . import batch
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
 from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _device,
-                       _logit_vector, _on_device, _raise_status, verify_drafts)
+                       _dist_checked, _logit_vector, _on_device, _raise_status, verify_drafts)
 
 _HISTORY_LIMIT = 1048576
 _MAX_PROPOSALS = 5
@@ -118,6 +118,11 @@ class _Controls:
     stop_identity: str | None
     support: np.ndarray           # the token ids with a positive count, increasing
     total: int | None             # the sum of the counts; None when a count exceeds 2^20
+
+
+def _sha256_i8(values):
+    """SHA-256 hex digest of a count vector's little-endian int64 bytes."""
+    return hashlib.sha256(np.ascontiguousarray(values, dtype="<i8")).hexdigest()
 
 
 def _valid_count_vector(values, vocabulary):
@@ -343,6 +348,22 @@ class SamplingWork:
         row = result.probs[0]
         return row if device_input else row.cpu().numpy()
 
+    def _target(self, logits, prefix):
+        """A verifier target row: ``distribution`` of the row and the
+        verifier's check of it (sampling.py:109-115), with the kernel's status
+        and the row's statistics read back together."""
+        self._require_open()
+        result, _ = self._row_launch(logits, prefix)
+        row = result.probs[0]
+        buf = torch.empty(4, dtype=torch.float64, device=row.device)  # stats slot, then the status
+        batch.prob_stats_launch(row, buf[0:3])
+        buf[3:4].view(torch.int32)[0:1].copy_(result.status)
+        host = buf.cpu()
+        code = int(host[3:4].view(torch.int32)[0])
+        if code != N.OK:
+            _raise_status(code)
+        return _dist_checked(row, batch.prob_stats_read(host[0:3]))
+
     def _draw(self, logits, prefix, domain, finite=None):
         """(token, distribution): one fused launch draws from the row's
         distribution with the domain's next uniform; the domain advances
@@ -447,7 +468,7 @@ class SamplingWork:
         with self._aborting_on_error():
             rows = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
             ids = list(self.proposal_ids)
-            targets = _LazyRows(len(rows), lambda j: self.distribution(rows[j], ids[:j]))
+            targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
             self._decide(verify_drafts(targets, self.proposal_rows, ids, self.transaction,
                                        greedy=self.policy.temperature == 0, output_limit=self.remaining,
                                        eos_ids=self.eos_ids))
@@ -459,8 +480,10 @@ class SamplingWork:
         are computed once per transaction (prepared() runs at prepare and
         again at commit)."""
         if self._counts_sha is None:
-            self._counts_sha = tuple(hashlib.sha256(v.astype("<i8").tobytes()).hexdigest()
-                                     for v in (self.counts, self.generated_counts))
+            counts, generated = self.counts, self.generated_counts
+            sha = _sha256_i8(counts)
+            # Equal vectors (no separate generated counts) share one hash.
+            self._counts_sha = (sha, sha if np.array_equal(counts, generated) else _sha256_i8(generated))
         decision = asdict(self.decision)
         return {
             "decision": decision, "accepted_target_rows": self.decision.accepted_target_rows,
