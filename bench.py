@@ -14,9 +14,11 @@ drafts; one step is one ``dsr_verify_drafts`` call), c5 (1,024 bf16 rows,
 mixed greedy, 16,384-token histories), whole (256 bf16 rows whose policies
 set no top-k: the reference's default, top-p only, min-p only), hist (1,024
 rows x 16,384 token ids built into device history tables; one step is one
-``dsr_history_append`` call), propose (one 5-row draft proposal chain
-drawn on the device) and seed (one drop-in ``TerminalSampler.begin_seed``
-call as the reference's callers make it: host dense counts, one FP32 row).
+``dsr_history_append`` call), and three drop-in workloads that time the
+reference's API as its callers use it (host dense counts, FP32 CUDA rows):
+propose (one 5-row proposal step drawn on the device), seed (one
+``TerminalSampler.begin_seed`` call) and step (one speculative decode step:
+proposals, verification against six target rows, the prepared digest).
 
 Distinct input batches rotate through the timed region: the workload's rows
 with their vocabulary positions rolled by a different shift each
@@ -59,6 +61,9 @@ WORKLOADS = {
              "k_history_append (count) + k_history_offsets + k_history_append (write)"),
     "whole": ("sampled rows/sec at B=256×V=129,280 bf16 with no top-k (default / top-p / min-p policies)", "rows/s",
               5, "k_sample_bf16_full"),
+    "step": ("drop-in speculative steps/sec: propose 5 rows on the device, verify against 6 fp32 rows, digest",
+             "steps/s", 30, "k_split_select + k_split_finish (proposals and targets) + k_prob_stats / "
+             "k_prob_accept / k_prob_correction / k_prob_categorical"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
              300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
     "propose": ("drop-in 5-row draft proposal steps/sec at V=129,280 fp32, one host synchronisation per step",
@@ -67,7 +72,7 @@ WORKLOADS = {
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
-PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split"}
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split", "step": "k_split"}
 
 DESCRIPTIONS = {
     "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
@@ -81,6 +86,9 @@ DESCRIPTIONS = {
             "(one dsr_history_append call)",
     "whole": "whole: 256 rows x 129280 bf16 heavy-tail logits, 10% allow mask, no top-k: default policy, "
              "top-p ~ U[0.8,0.99], min-p 0.05, top-p 0.95 + min-p 0.01 (by row mod 4)",
+    "step": "step: TerminalSampler.begin_verification, SamplingWork.propose over a device graph (5 fp32 rows x "
+            "129280 N(0,2^2), previous token +4), verify against 6 fp32 target rows (base + N(0,0.25^2)), prepared "
+            "digest, then abort; T 0.7 / top-k 50 / top-p 0.9, dense int32 counts of a 64-token history",
     "seed": "seed: TerminalSampler.begin_seed then abort on 1 fp32 row x 129280 N(0,2^2), T 0.7 / top-k 50 / "
             "top-p 0.9, dense int32 counts of a 64-token history (the reference's calling pattern)",
     "propose": "propose: TerminalSampler.begin_verification, SamplingWork.propose over a device graph, then abort; "
@@ -96,7 +104,7 @@ def _units(name, w):
     """Rows of a sampling or history workload; requests of the verifier workload."""
     if name == "c4":
         return w.extra["target"].shape[0]
-    if name in ("propose", "seed"):
+    if name in ("propose", "seed", "step"):
         return 1
     return w.extra["tokens"].shape[0] if name == "hist" else w.rows
 
@@ -126,6 +134,8 @@ def _cpu_rows(span):
         return hi - lo, time.perf_counter() - t0
     if name == "propose":
         return hi - lo, _cpu_chains(w, hi - lo)
+    if name == "step":
+        return hi - lo, _cpu_steps(w, hi - lo)
     if name == "seed":
         counts = np.bincount(np.asarray(w.histories[0]), minlength=V).astype(np.int32)
         gen = np.random.default_rng(w.extra["rng_seed"])
@@ -182,6 +192,44 @@ def _cpu_chains(w, n):
     return time.perf_counter() - t0
 
 
+def _cpu_steps(w, n):
+    """n speculative steps by the oracle, as the reference runs them: the
+    proposal chain (each row conditioned on the previous token and the prefix
+    counts, its distribution kept), then verification with each target row's
+    distribution computed when the step first reaches it
+    (terminal_sampling.py:138-183, sampling.py:247-294)."""
+    from oracle import sampling_oracle as O
+    V = w.logits.shape[1]
+    pol = O.Policy(**w.policies[0])
+    counts0 = np.bincount(np.asarray(w.histories[0]), minlength=V).astype(np.int32)
+    gen = np.random.default_rng(w.extra["rng_seed"])
+    t0 = time.perf_counter()
+    for _ in range(n):
+        counts, previous, ids, rows = counts0.copy(), w.extra["seed_token"], [], []
+        for j in range(w.extra["steps"]):
+            row = w.logits[j].copy()
+            row[previous] += np.float32(w.extra["bump"])
+            ref = O.sample_row(row, pol, float(gen.random()), counts, counts, keep_probs=True)
+            counts[ref.token] += 1
+            ids.append(ref.token)
+            rows.append(ref.probs)
+            previous = ref.token
+
+        class Targets:
+            def __len__(self):
+                return len(ids) + 1
+
+            def __getitem__(self, j):
+                c = counts0.copy()
+                for t in ids[:j]:
+                    c[t] += 1
+                return O.probabilities(w.extra["target"][j], pol, c, c)
+
+        O.verify_probs(Targets(), rows, ids, lambda domain: float(gen.random()), greedy=False,
+                       output_limit=1048576)
+    return time.perf_counter() - t0
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -218,7 +266,7 @@ def cpu_baseline(name, w, passes):
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
     unit = WORKLOADS[name][1]
-    what = {"c4": "requests", "propose": "chains", "seed": "calls"}.get(name, "rows")
+    what = {"c4": "requests", "propose": "chains", "seed": "calls", "step": "steps"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
@@ -245,6 +293,8 @@ def _batch_bytes(name, w):
         return w.extra["tokens"].nbytes
     if name in ("propose", "seed"):
         return w.logits.nbytes
+    if name == "step":
+        return w.logits.nbytes + w.extra["target"].nbytes
     if name == "c4":
         return w.extra["target"].nbytes + w.extra["draft"].nbytes
     return w.logits.shape[0] * w.logits.shape[1] * (2 if w.dtype == "bf16" else 4)
@@ -298,6 +348,28 @@ class _Chain:
         return self
 
 
+class _Step(_Chain):
+    """One drop-in speculative decode step per launch: begin_verification,
+    propose over the device graph, verify against the target rows, the
+    prepared digest, then abort (which restores the RNG domains)."""
+
+    def __init__(self, w):
+        import torch
+        self.target = torch.from_numpy(w.extra["target"]).cuda()
+        super().__init__(w)
+
+    def launch(self):
+        import torch
+        work = self.sampler.begin_verification(seed_token=self.w.extra["seed_token"], policy=self.policy,
+                                               counts=self.counts, remaining=9)
+        ids = work.propose(self, None)
+        work.verify(self.target[: len(ids) + 1])
+        work.prepared()
+        work.abort()
+        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        return self
+
+
 class _Seed:
     """One drop-in call per launch: TerminalSampler.begin_seed on one FP32
     CUDA row with dense count vectors, as the reference's callers make it,
@@ -331,6 +403,10 @@ def _prepare(name, w, device_rng=False):
     if name == "propose":
         per_row = w.logits.shape[1] * (4 + 8) + 64 + 4   # logits in, float64 distribution out, controls, token
         return _Chain(w), w.extra["steps"] * per_row + 4 * len(w.histories[0]), 1
+    if name == "step":
+        # Proposal rows as in propose; each of the six target rows read and its distribution written.
+        per_row = w.logits.shape[1] * (4 + 8) + 64 + 4
+        return _Step(w), (w.extra["steps"] + w.extra["target"].shape[0]) * per_row + 4 * len(w.histories[0]), 1
     if name == "seed":
         # The row's logits and its dense counts and generated counts in, the decision out.
         return _Seed(w), w.logits.shape[1] * (4 + 4 + 4) + 64 + 4, 1
@@ -390,7 +466,7 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    if args.device_rng and name in ("c4", "hist", "propose", "seed"):
+    if args.device_rng and name in ("c4", "hist", "propose", "seed", "step"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
     batches = variants(name, w)
     preps = []
@@ -450,7 +526,7 @@ def main():
     cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]), "input_dtype": w.dtype,
            "general_path_rows": general, "kernels": kernels,
            "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
-    if name not in ("c4", "hist", "propose", "seed"):
+    if name not in ("c4", "hist", "propose", "seed", "step"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
