@@ -777,17 +777,4 @@ __device__ __forceinline__ int general_distribution(const RowSpec& r, GenShared&
   return filter_tail(r, W, V, V, topk, kth, cut, sh, flags, out, IdentityMap());
 }
 
-// Number of positive entries and the first positive index.
-__device__ void positive_support(const double* W, int64_t V, GenShared& sh, long long& npos, long long& first) {
-  long long n = 0, f = LLONG_MAX;
-  row_pass<double>(V, [&](int64_t i) { return W[i]; }, [&](int64_t i, double x) {
-    if (x > 0.0) {
-      ++n;
-      if (i < f) f = i;
-    }
-  });
-  npos = block_sum_i64(n, sh.b);
-  first = block_min_i64(f, sh.b);
-}
-
 }  // namespace dsr

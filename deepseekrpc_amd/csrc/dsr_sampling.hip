@@ -242,16 +242,101 @@ __device__ int64_t sequential_cdf_search(const double* p, int64_t n, double u) {
   return n - 1;  // not reached: c_last / c_last = 1 > u
 }
 
+// categorical (sampling.py:118-128) over one float64 vector, one workgroup.
+// Wave w owns elements [8192 w, 8192 (w + 1)) as 16 chunks of 512.  One
+// coalesced pass gives every chunk's sum (8 strided loads per lane, then a
+// wave sum) and the positive count; the crossing of u * total is then found
+// by wave, by chunk, and inside the chunk by its wave's running scan.  These
+// sums take another order than np.cumsum: where u sits within that rounding
+// band of a cell edge (or no crossing shows), the sequential sum decides.
+constexpr int kCatChunk = 512;
+constexpr int kCatChunks = 16;
+static_assert((int64_t)kWaves * kCatChunks * kCatChunk >= DSR_MAX_VOCAB, "one workgroup covers the vocabulary");
+
 __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, int64_t n, double u, int32_t* out) {
-  __shared__ GenShared sh;
-  long long npos, first;
-  positive_support(p, n, sh, npos, first);
-  unsigned flags = 0;
-  int64_t tok = cdf_search(p, n, u, npos, sh, flags);
-  // The workgroup scan sums in another order than np.cumsum; where u sits
-  // within that rounding band of a cell edge the sequential sum decides.
-  if ((flags & DSR_FLAG_MARGIN) && threadIdx.x == 0) tok = sequential_cdf_search(p, n, u);
+  __shared__ double csum[kWaves][kCatChunks];
+  __shared__ double wsum[kWaves];
+  __shared__ long long wpos[kWaves];
+  __shared__ long long found[2];
+  const int w = wave_id(), lane = lane_id();
+  const int64_t lo = (int64_t)w * kCatChunks * kCatChunk;
+  long long np = 0;
+  double wtot = 0.0;
+#pragma unroll 1
+  for (int c = 0; c < kCatChunks; c += 2) {  // two chunks' loads in flight at a time
+    double x[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int64_t i = lo + (int64_t)c * kCatChunk + 64 * q + lane;
+      x[q] = i < n ? p[i] : 0.0;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      double part = 0.0;
+#pragma unroll
+      for (int q = 8 * h; q < 8 * h + 8; ++q) {
+        part += x[q];
+        np += x[q] > 0.0 ? 1 : 0;
+      }
+      const double cs = wave_reduce_dpp(part, OpSum());  // the same value in every lane
+      if (lane == 0) csum[w][c + h] = cs;
+      wtot += cs;
+    }
+  }
+  const long long wnp = wave_reduce_dpp(np, OpSum());
+  if (lane == 0) {
+    wsum[w] = wtot;
+    wpos[w] = wnp;
+  }
+  if (threadIdx.x == 0) found[1] = 1;
+  __syncthreads();
+  double total = 0.0;
+  long long npos = 0;
+  for (int v = 0; v < kWaves; ++v) {
+    total += wsum[v];
+    npos += wpos[v];
+  }
+  const double thr = u * total;
+  int ow = -1;  // the last wave with mass whose running sum before it is at most thr
+  double obase = 0.0, base = 0.0;
+  for (int v = 0; v < kWaves; ++v) {
+    if (wsum[v] > 0.0 && base <= thr) {
+      ow = v;
+      obase = base;
+    }
+    base += wsum[v];
+  }
+  if (w == ow) {  // uniform over the wave
+    int oc = -1;  // the same over its chunks
+    double ocb = 0.0, cb = obase;
+    for (int c = 0; c < kCatChunks; ++c) {
+      const double cs = csum[w][c];
+      if (cs > 0.0 && cb <= thr) {
+        oc = c;
+        ocb = cb;
+      }
+      cb += cs;
+    }
+    int64_t tok = -1;
+    int margin = 1;
+    if (oc >= 0) {
+      const int64_t clo = lo + (int64_t)oc * kCatChunk, chi = clo + kCatChunk < n ? clo + kCatChunk : n;
+      const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
+      wave_slice_cdf([&](int64_t i) { return p[i]; }, clo, chi, ocb, thr, tol, tok, margin);
+    }
+    if (lane == 0) {
+      found[0] = tok;
+      found[1] = margin;
+    }
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    int64_t tok = found[0];
+    unsigned flags = 0;
+    if (found[1]) {
+      flags |= DSR_FLAG_MARGIN;
+      tok = sequential_cdf_search(p, n, u);
+    }
     out[0] = (int32_t)tok;
     out[1] = (int32_t)flags;
   }
