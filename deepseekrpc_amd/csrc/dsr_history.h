@@ -64,19 +64,27 @@ struct HistDenseArgs {
   int32_t* out_status;
 };
 
+constexpr int kHistGroups = (kHistWords + 63) / 64;  // groups of 64 bitmap words (one wave's stretch)
+static_assert(kMaxAppend < 65536, "new-id ranks and multiplicities fit 16 bits");
+
+// The write pass: both bitmaps, each word's rank base among the new ids,
+// each 64-word group's base among the old ids and among the new ids the
+// table lacks, and the new ids' multiplicities by rank.  ALLGEN (every new
+// token generated) needs the multiplicity alone, two to a word: at 74 KB two
+// such workgroups fit on a CU; with separate generated counts (106 KB) one.
+template <bool ALLGEN>
 struct HistAppendShared {
-  uint32_t nb[kHistWords];     // new ids present
-  uint32_t ob[kHistWords];     // old ids present
-  uint32_t nbase[kHistWords];  // new ids below the word
-  uint32_t obase[kHistWords];  // old ids below the word
-  uint32_t ubase[kHistWords];  // new ids absent from the table, below the word
-  uint32_t cnt[kMaxAppend];    // by rank among the new ids: multiplicity | generated << 16
+  uint32_t nb[kHistWords];       // new ids present
+  uint32_t ob[kHistWords];       // old ids present
+  uint16_t nbase[kHistWords];    // new ids below the word
+  uint32_t gob[kHistGroups];     // old ids below the group
+  uint32_t gub[kHistGroups];     // new ids absent from the table, below the group
+  uint32_t cnt[ALLGEN ? kMaxAppend / 2 : kMaxAppend];  // by rank: ALLGEN 16-bit pairs, else mult | gen << 16
   int bad;
   SyncSlots sync;
 };
 
-// The count pass needs only the two bitmaps: at 33 KB two of its
-// workgroups fit on a CU, where the write pass's 147 KB leave room for one.
+// The count pass needs only the two bitmaps (33 KB).
 struct HistCountShared {
   uint32_t nb[kHistWords];
   uint32_t ob[kHistWords];
@@ -84,17 +92,18 @@ struct HistCountShared {
   SyncSlots sync;
 };
 
-template <bool WRITE> struct HistSharedOf { using T = HistCountShared; };
-template <> struct HistSharedOf<true> { using T = HistAppendShared; };
+template <bool WRITE, bool ALLGEN> struct HistSharedOf { using T = HistCountShared; };
+template <bool ALLGEN> struct HistSharedOf<true, ALLGEN> { using T = HistAppendShared<ALLGEN>; };
 
 __device__ __forceinline__ uint32_t bits_below(uint32_t w, uint32_t b) { return __popc(w & ((1u << b) - 1u)); }
 
 // One row of dsr_history_append.  WRITE = false: validate and count the
 // merged row; WRITE = true: write it at out_off[row] (rows the count pass
 // rejected, and every row when the total exceeds cap, write nothing).
-template <bool WRITE>
+// ALLGEN (no gen_from): every new token counts as generated.
+template <bool WRITE, bool ALLGEN = false>
 __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
-  __shared__ typename HistSharedOf<WRITE>::T sh;
+  __shared__ typename HistSharedOf<WRITE, ALLGEN>::T sh;
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t V = a.vocab;
@@ -133,7 +142,8 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
     sh.ob[w] = 0u;
   }
   if constexpr (WRITE) {
-    for (int64_t i = tid; i < m; i += kThreads) sh.cnt[i] = 0u;
+    const int64_t cw = ALLGEN ? (m + 1) / 2 : m;  // count words in use
+    for (int64_t i = tid; i < cw; i += kThreads) sh.cnt[i] = 0u;
   }
   if (tid == 0) sh.bad = 0;
   lds_barrier();
@@ -185,18 +195,18 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
     return;
   } else {
     {
+      // Thread t holds words 4t .. 4t + 3; the group of 64 words starting at
+      // word 4t takes thread t's bases when t is a multiple of 16.
       uint32_t nb0 = bex & 0xFFFFu, ub0 = bex >> 16, ob0 = (uint32_t)oex;
+      if ((tid & 15) == 0 && 4 * tid < words) {
+        sh.gob[tid >> 4] = ob0;
+        sh.gub[tid >> 4] = ub0;
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int w = 4 * tid + q;
-        if (w < words) {
-          sh.nbase[w] = nb0;
-          sh.obase[w] = ob0;
-          sh.ubase[w] = ub0;
-        }
+        if (w < words) sh.nbase[w] = (uint16_t)nb0;
         nb0 += __popc(nw[q]);
-        ob0 += __popc(ow[q]);
-        ub0 += __popc(nw[q] & ~ow[q]);
       }
     }
     lds_barrier();
@@ -206,7 +216,9 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
       const int64_t i = (int64_t)tid + (int64_t)q * kThreads;
       if (i < m) {
         const uint32_t t = (uint32_t)tk[q], w = t >> 5, b = t & 31u;
-        atomicAdd(&sh.cnt[sh.nbase[w] + bits_below(sh.nb[w], b)], i >= gf ? 0x10001u : 1u);
+        const uint32_t r = (uint32_t)sh.nbase[w] + bits_below(sh.nb[w], b);
+        if constexpr (ALLGEN) atomicAdd(&sh.cnt[r >> 1], 1u << (16u * (r & 1u)));
+        else atomicAdd(&sh.cnt[r], i >= gf ? 0x10001u : 1u);
       }
     }
     lds_barrier();
@@ -223,20 +235,20 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
     const int lane = lane_id(), wave = wave_id();
     const int64_t base = a.out_off[row];
     for (int g0 = wave * 64; g0 < words; g0 += kWaves * 64) {  // uniform over the wave
-      const int w = g0 + lane;
-      uint32_t nwv = 0u, owv = 0u, nbw = 0u, obw = 0u, ubw = 0u;
+      const int w = g0 + lane, G = g0 >> 6;
+      uint32_t nwv = 0u, owv = 0u, nbw = 0u;
       if (w < words) {
         nwv = sh.nb[w];
         owv = sh.ob[w];
         nbw = sh.nbase[w];
-        obw = sh.obase[w];
-        ubw = sh.ubase[w];
       }
+      const uint32_t po = (uint32_t)__popc(owv);
+      const uint32_t obw = sh.gob[G] + wave_scan_dpp(po) - po;  // old ids below this lane's word
       const uint32_t uw = nwv | owv;
       const uint32_t n = (uint32_t)__popc(uw);
       const uint32_t ex = wave_scan_dpp(n) - n;
       const uint32_t total = lane_value(ex + n, 63);
-      const int64_t p0 = base + (int64_t)lane_value(obw + ubw, 0);  // lane 0 holds word g0 < words
+      const int64_t p0 = base + (int64_t)sh.gob[G] + (int64_t)sh.gub[G];  // word g0's rank in the merged row
       for (uint32_t i0 = 0; i0 < total; i0 += 64) {  // uniform: every lane takes part in the shuffles
         const uint32_t i = i0 + (uint32_t)lane;
         int s = 0;
@@ -264,9 +276,16 @@ __global__ __launch_bounds__(kThreads) void k_history_append(HistAppendArgs a) {
             g = a.gen[e];
           }
           if ((nws >> b) & 1u) {
-            const uint32_t add = sh.cnt[nbs + bits_below(nws, b)];
-            c += (int32_t)(add & 0xFFFFu);
-            g += (int32_t)(add >> 16);
+            const uint32_t r = nbs + bits_below(nws, b);
+            if constexpr (ALLGEN) {
+              const int32_t add = (int32_t)((sh.cnt[r >> 1] >> (16u * (r & 1u))) & 0xFFFFu);
+              c += add;
+              g += add;
+            } else {
+              const uint32_t add = sh.cnt[r];
+              c += (int32_t)(add & 0xFFFFu);
+              g += (int32_t)(add >> 16);
+            }
           }
           const int64_t p = p0 + i;
           a.out_ids[p] = 32 * (g0 + s) + (int32_t)b;

@@ -642,7 +642,10 @@ int32_t dsr_history_append(const int64_t* off, const int32_t* ids, const int32_t
   hipLaunchKernelGGL(k_history_offsets, dim3(1), dim3(kThreads), 0, s, out_off, rows);
   if (rows > 0) {
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_history_append<true>, dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+    if (gen_from)
+      hipLaunchKernelGGL(HIP_KERNEL_NAME(k_history_append<true, false>), dim3((unsigned)rows), dim3(kThreads), 0, s, h);
+    else
+      hipLaunchKernelGGL(HIP_KERNEL_NAME(k_history_append<true, true>), dim3((unsigned)rows), dim3(kThreads), 0, s, h);
   }
   return launched();
 }
