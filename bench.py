@@ -66,13 +66,17 @@ WORKLOADS = {
              "k_prob_accept / k_prob_correction / k_prob_categorical"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
              300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
+    "head": ("verify-rows/sec with the vocabulary projection: B=32 requests × K=4 drafts, 160 target rows × "
+             "dim 5,120 → V=129,280 fp32 logits", "verify-rows/s", 30,
+             "k_vocab_head + k_head_shares + k_verify_chain + k_verify_draw + k_verify_finish"),
     "propose": ("drop-in 5-row draft proposal steps/sec at V=129,280 fp32, one host synchronisation per step",
                 "chains/s", 100, "k_split_select + k_split_finish (5x; a policy without penalties carries no "
                 "history table)"),
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
-PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split", "step": "k_split"}
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split", "step": "k_split",
+                  "head": "k_vocab_head"}
 
 DESCRIPTIONS = {
     "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
@@ -91,6 +95,10 @@ DESCRIPTIONS = {
             "digest, then abort; T 0.7 / top-k 50 / top-p 0.9, dense int32 counts of a 64-token history",
     "seed": "seed: TerminalSampler.begin_seed then abort on 1 fp32 row x 129280 N(0,2^2), T 0.7 / top-k 50 / "
             "top-p 0.9, dense int32 counts of a 64-token history (the reference's calling pattern)",
+    "head": "head: the terminal stage's vocabulary projection of 32 requests x 5 target rows (bf16 hidden "
+            "[160, 5120] x bf16 weight [129280, 5120] -> fp32 logits with per-tile verifier records), then "
+            "verification of 4 drafts per request whose rows and records came from the same projection; default "
+            "policy, limit 10",
     "propose": "propose: TerminalSampler.begin_verification, SamplingWork.propose over a device graph, then abort; "
                "5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the device, "
                "T 0.7 / top-k 50 / top-p 0.9, dense int32 counts of a 64-token history, draft PCG64 draws on the "
@@ -101,9 +109,11 @@ _CPU = {}
 
 
 def _units(name, w):
-    """Rows of a sampling or history workload; requests of the verifier workload."""
+    """Rows of a sampling or history workload; requests of the verifier workloads."""
     if name == "c4":
         return w.extra["target"].shape[0]
+    if name == "head":
+        return w.extra["requests"]
     if name in ("propose", "seed", "step"):
         return 1
     return w.extra["tokens"].shape[0] if name == "hist" else w.rows
@@ -136,6 +146,14 @@ def _cpu_rows(span):
         return hi - lo, _cpu_chains(w, hi - lo)
     if name == "step":
         return hi - lo, _cpu_steps(w, hi - lo)
+    if name == "head":
+        e = w.extra
+        t0 = time.perf_counter()
+        for r in range(lo, hi):
+            r %= e["requests"]
+            O.verify(e["cpu_target"][r], e["cpu_draft"][r], e["cpu_ids"][r], O.Policy(), e["u_accept"][r],
+                     float(e["u_target"][r]), output_limit=int(e["limit"][r]))
+        return hi - lo, time.perf_counter() - t0
     if name == "seed":
         counts = np.bincount(np.asarray(w.histories[0]), minlength=V).astype(np.int32)
         gen = np.random.default_rng(w.extra["rng_seed"])
@@ -230,6 +248,24 @@ def _cpu_steps(w, n):
     return time.perf_counter() - t0
 
 
+def _head_cpu_rows(w):
+    """The head workload's logits for the CPU sample, by NumPy's float32
+    product of the same bf16 values, and draft ids drawn from the draft rows
+    by the oracle (both untimed: the reference projects on its GPU and
+    samples the copied rows on the host, so only the verification is timed)."""
+    from deepseekrpc_amd import workloads
+    from oracle import sampling_oracle as O
+    e = w.extra
+    R, K, V = e["requests"], e["K"], e["weight_q"].shape[0]
+    wt = e["weight_q"].astype(np.float32)
+    wt *= np.float32(workloads.head_weight_scale())
+    e["cpu_target"] = (e["hidden_target"] @ wt.T).reshape(R, K + 1, V)
+    e["cpu_draft"] = (e["hidden_draft"] @ wt.T).reshape(R, K, V)
+    del wt
+    e["cpu_ids"] = [[O.sample_row(e["cpu_draft"][r][j], O.Policy(), float(e["u_draft"][r][j]),
+                                  keep_probs=False).token for j in range(K)] for r in range(R)]
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -249,6 +285,8 @@ def cpu_baseline(name, w, passes):
     """Oracle throughput on the host: CPU_WORKERS forked workers with the
     sample split evenly, then one worker alone on an eighth of the sample
     (the single-core figure); run before the GPU is initialised."""
+    if name == "head":
+        _head_cpu_rows(w)
     _CPU.update(w=w, name=name)
     os.environ["OMP_NUM_THREADS"] = "1"
     cores = max(1, min(CPU_WORKERS, os.cpu_count() or 1))
@@ -266,7 +304,7 @@ def cpu_baseline(name, w, passes):
     n = sum(d[0] for d in done)
     busy = sum(d[1] for d in done)
     unit = WORKLOADS[name][1]
-    what = {"c4": "requests", "propose": "chains", "seed": "calls", "step": "steps"}.get(name, "rows")
+    what = {"c4": "requests", "head": "requests", "propose": "chains", "seed": "calls", "step": "steps"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
@@ -289,6 +327,8 @@ ROTATION_BYTES = 300 * 2**20
 
 
 def _batch_bytes(name, w):
+    if name == "head":
+        return w.extra["weight_q"].nbytes * 2   # the bf16 weight
     if name == "hist":
         return w.extra["tokens"].nbytes
     if name in ("propose", "seed"):
@@ -304,6 +344,8 @@ def variants(name, w):
     """Distinct input batches of the workload (vocabulary layouts rolled by
     different shifts), at least 4 and together above ROTATION_BYTES."""
     from deepseekrpc_amd import workloads
+    if name == "head":
+        return [w]   # its weight stream (1.3 GB per step) is read from HBM on every step
     count = max(4, -(-ROTATION_BYTES // max(1, _batch_bytes(name, w))))
     V = w.logits.shape[1]
     return [w] + [workloads.rolled(w, (i * 7919) % V) for i in range(1, count)]
@@ -395,11 +437,59 @@ class _Seed:
         return self
 
 
+class _Head:
+    """One verification step at the terminal stage: the vocabulary projection
+    of the 160 target rows with its records, then dsr_verify_drafts_head
+    against the draft rows and records projected at proposal time (setup).
+    ``fused=False`` is the same step without records: the projection alone,
+    then the verifier's statistics pass over the logits."""
+
+    def __init__(self, w, fused=True):
+        import torch
+
+        from deepseekrpc_amd import batch, workloads
+        e = w.extra
+        R, K = e["requests"], e["K"]
+        dev = "cuda"
+        self.weight = (torch.from_numpy(e["weight_q"]).to(dev).to(torch.bfloat16)
+                       * workloads.head_weight_scale()).contiguous()
+        xt = torch.from_numpy(e["hidden_target"]).to(dev).to(torch.bfloat16)
+        xd = torch.from_numpy(e["hidden_draft"]).to(dev).to(torch.bfloat16)
+        self.policies = batch.policy_tensor(w.policies, dev)
+        self.th = batch.vocab_head(xt, self.weight, policies=self.policies, rows_per_policy=K + 1, records=fused)
+        self.dh = batch.vocab_head(xd, self.weight, policies=self.policies, rows_per_policy=K, records=fused)
+        V = self.weight.shape[0]
+        draw = batch.sample_rows(self.dh.logits, [dict()] * (R * K),
+                                 uniforms=torch.from_numpy(e["u_draft"].reshape(-1)).to(dev))
+        ids = draw.tokens.reshape(R, K).contiguous()
+        self.verify = batch.PreparedVerify(
+            self.th.logits.view(R, K + 1, V), self.dh.logits.view(R, K, V), ids, self.policies,
+            torch.from_numpy(e["u_accept"]).to(dev), torch.from_numpy(e["u_target"]).to(dev),
+            torch.from_numpy(e["limit"]).to(dev), head=(self.th, self.dh) if fused else None)
+        self.result = self.verify.result
+        self.inputs = (self.weight,)
+        self._launch_head = batch.vocab_head_launch
+
+    def launch(self):
+        self._launch_head(self.th)
+        self.verify.launch()
+        return self
+
+
 def _prepare(name, w, device_rng=False):
     """Device inputs and a launch closure for one step of the workload."""
     import torch
 
     from deepseekrpc_amd import batch, workloads
+    if name == "head":
+        e = w.extra
+        R, K, V, D = e["requests"], e["K"], e["weight_q"].shape[0], e["dim"]
+        # The weight stream, the hidden rows, the target logits and records
+        # written, the draft records read, and the verifier's scalar inputs
+        # and decision (as c4).
+        tiles = V // batch.HEAD_TILE
+        alg = V * D * 2 + R * (K + 1) * (D * 2 + V * 4 + tiles * 16) + R * K * tiles * 16 + R * 120
+        return _Head(w), alg, R
     if name == "propose":
         per_row = w.logits.shape[1] * (4 + 8) + 64 + 4   # logits in, float64 distribution out, controls, token
         return _Chain(w), w.extra["steps"] * per_row + 4 * len(w.histories[0]), 1
@@ -466,7 +556,7 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    if args.device_rng and name in ("c4", "hist", "propose", "seed", "step"):
+    if args.device_rng and name in ("c4", "head", "hist", "propose", "seed", "step"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
     batches = variants(name, w)
     preps = []
@@ -513,6 +603,26 @@ def main():
             torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
 
+    if name == "head":
+        # The same step without the projection's records: the projection
+        # alone, then the verifier's statistics pass over the logits.
+        plain = _Head(w, fused=False)
+        for _ in range(args.warmup):
+            plain.launch()
+        ev2, ev3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev2.record(stream)
+        for _ in range(args.steps):
+            plain.launch()
+        ev3.record(stream)
+        torch.cuda.synchronize()
+        same = all(torch.equal(getattr(plain.result, f), getattr(prep.result, f))
+                   for f in ("accepted", "ids", "count", "pending", "stop", "used_accept", "used_target", "status"))
+        if not same:
+            raise SystemExit("the fused and unfused steps decided differently")
+        head_extra = {"unfused_step_ms": ev2.elapsed_time(ev3) / args.steps,
+                      "unfused_kernels": "k_vocab_head (no records) + k_verify_stats + k_verify_chain + "
+                                         "k_verify_draw + k_verify_finish", "decisions_equal": same}
+        del plain
     ms_per_step = wall * 1e3 / args.steps
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     # HBM traffic per launch is not measurable from inside the run (counters
@@ -526,8 +636,10 @@ def main():
     cfg = {"workload": DESCRIPTIONS[name], "rows": units, "vocab": int(w.logits.shape[1]), "input_dtype": w.dtype,
            "general_path_rows": general, "kernels": kernels,
            "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
-    if name not in ("c4", "hist", "propose", "seed", "step"):
+    if name not in ("c4", "head", "hist", "propose", "seed", "step"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
+    if name == "head":
+        cfg.update(head_extra)
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LIB_NAME = "libdsr_sampling.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -47,8 +47,11 @@ EXPORTS = (
     "dsr_abi_version", "dsr_status_message", "dsr_sample_workspace_bytes", "dsr_verify_workspace_bytes",
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
     "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append", "dsr_sample_rows_noalloc",
+    "dsr_vocab_head", "dsr_verify_drafts_head",
 )
 NOALLOC_SCRATCH_BYTES = 268435456
+HEAD_TILE = 128
+HEAD_MAX_ROWS = 256
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -86,6 +89,18 @@ class VerifyArgs(ctypes.Structure):
         ("out_used_accept", _p), ("out_used_target", _p), ("out_status", _p), ("out_flags", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_accept", _p), ("rng_target", _p),
         ("hints", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+    ]
+
+
+class HeadPart(ctypes.Structure):
+    """``dsr_head_part_t``: one (row, 128-column tile) record of a vocabulary projection."""
+    _fields_ = [("sum", _f64), ("max", ctypes.c_float), ("info", _i32)]
+
+
+class HeadArgs(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _p), ("weight", _p), ("rows", _i64), ("dim", _i64), ("vocab", _i64), ("policy", _p),
+        ("rows_per_policy", _i32), ("reserved", _i32), ("logits", _p), ("parts", _p),
     ]
 
 
@@ -132,6 +147,10 @@ def load(path: str = LIB_PATH):
     lib.dsr_history_from_dense.argtypes = [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p]
     lib.dsr_history_append.restype = _i32
     lib.dsr_history_append.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p]
+    lib.dsr_vocab_head.restype = _i32
+    lib.dsr_vocab_head.argtypes = [ctypes.POINTER(HeadArgs), _p]
+    lib.dsr_verify_drafts_head.restype = _i32
+    lib.dsr_verify_drafts_head.argtypes = [ctypes.POINTER(VerifyArgs), _p, _p, _p]
     _lib = lib
     return lib
 

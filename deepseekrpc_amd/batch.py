@@ -701,6 +701,7 @@ class VerifyResult:
     flags: torch.Tensor
     args: object = None  # the marshalled dsr_verify_args_t
     keep: tuple = ()     # every tensor ``args`` points into, kept alive with it
+    head: tuple | None = None  # (target records, draft records) of dsr_verify_drafts_head
 
 
 def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Tensor, policies, u_accept: torch.Tensor,
@@ -708,7 +709,8 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
                   bias: BiasTable | None = None, allow_bits: torch.Tensor | None = None,
                   eos_offsets: torch.Tensor | None = None, eos_ids: torch.Tensor | None = None,
                   rng_accept: torch.Tensor | None = None, rng_target: torch.Tensor | None = None,
-                  workspace: Workspace | None = None, hints: int | None = None) -> VerifyResult:
+                  workspace: Workspace | None = None, hints: int | None = None,
+                  head: tuple | None = None) -> VerifyResult:
     """Exact sampled verification of ``rows`` requests with ``K`` drafts each.
 
     ``target [rows, K+1, V]`` and ``draft [rows, K, V]`` are logits; row ``j``
@@ -717,9 +719,13 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     (int64 ``[rows, 4]``, see ``pcg64_states``) instead draw them on the
     device from each request's accept / target PCG64 state, which is advanced
     by exactly the draws the decision uses.  ``hints`` overrides the
-    DSR_HINT_VERIFY_FAST bit derived from the policies.
+    DSR_HINT_VERIFY_FAST bit derived from the policies.  ``head`` =
+    ``(target, draft)`` ``HeadResult`` s of the ``vocab_head`` calls that
+    wrote ``target`` and ``draft``: the per-row statistics then come from
+    their records (``dsr_verify_drafts_head``).
     """
     lib = N.load()
+    given_policies = policies
     _require_cuda(target, "target")
     rows, K1, V = target.shape
     K = K1 - 1
@@ -783,7 +789,25 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     res.args = a
     res.keep = (target, draft, draft_ids, policies, u_accept, u_target, output_limit, history, bias, allow_bits,
                 eos_offsets, eos_ids, rng_accept, rng_target, ws)
-    N.check(lib.dsr_verify_drafts(ctypes.byref(a), _stream()), "dsr_verify_drafts")
+    if head is None:
+        N.check(lib.dsr_verify_drafts(ctypes.byref(a), _stream()), "dsr_verify_drafts")
+        return res
+    th, dh = head
+    def wrote(h, t):
+        return h is not None and h.parts is not None and h.logits.data_ptr() == t.data_ptr() \
+            and h.logits.numel() == t.numel() and t.dtype == torch.float32
+
+    if not wrote(th, target) or (K > 0 and not wrote(dh, draft)):
+        raise ValueError("head must hold the records of the vocab_head calls that wrote target and draft")
+    if th.rows_per_policy != K + 1 or (K > 0 and dh.rows_per_policy != K) or \
+            not _same_policies(th.policies, given_policies) or \
+            (K > 0 and not _same_policies(dh.policies, given_policies)):
+        raise ValueError("head records must be computed over the verifier's policies, K + 1 (target) and K "
+                         "(draft) rows per request")
+    res.head = (th.parts, dh.parts if K > 0 else None)
+    res.keep = res.keep + res.head
+    N.check(lib.dsr_verify_drafts_head(ctypes.byref(a), _ptr(res.head[0]), _ptr(res.head[1]), _stream()),
+            "dsr_verify_drafts_head")
     return res
 
 
@@ -799,10 +823,115 @@ class PreparedVerify:
         self._lib = N.load()
 
     def launch(self):
-        rc = self._lib.dsr_verify_drafts(ctypes.byref(self.args), _stream())
+        head = self.result.head
+        if head is None:
+            rc = self._lib.dsr_verify_drafts(ctypes.byref(self.args), _stream())
+        else:
+            rc = self._lib.dsr_verify_drafts_head(ctypes.byref(self.args), _ptr(head[0]), _ptr(head[1]), _stream())
         if rc != 0:
             N.check(rc, "dsr_verify_drafts")
         return self.result
+
+
+# ---------------------------------------------------------------------------
+# Vocabulary projection (the terminal stage's lm_head) with the verifier's
+# per-row statistics in its epilogue.
+
+HEAD_TILE = N.HEAD_TILE
+
+
+def _same_policies(x, y) -> bool:
+    """The same policies: one object, one device tensor, or equal lists."""
+    if x is y:
+        return True
+    if isinstance(x, torch.Tensor) or isinstance(y, torch.Tensor):
+        return isinstance(x, torch.Tensor) and isinstance(y, torch.Tensor) and x.data_ptr() == y.data_ptr() \
+            and x.numel() == y.numel()
+    return x is not None and y is not None and np.array_equal(policy_array(x), policy_array(y))
+
+
+@dataclass
+class HeadResult:
+    """FP32 logits ``[rows, vocab]`` and, with records, ``parts`` ``[rows,
+    vocab / 128, 4]`` int32: one ``dsr_head_part_t`` per (row, 128-column
+    tile), viewed by ``part_sum`` / ``part_max`` / ``part_info``."""
+    logits: torch.Tensor
+    parts: torch.Tensor | None
+    policies: object = None
+    rows_per_policy: int = 1
+    args: object = None
+    keep: tuple = ()
+
+    @property
+    def part_sum(self):
+        return self.parts[..., 0:2].contiguous().view(torch.float64)[..., 0]
+
+    @property
+    def part_max(self):
+        return self.parts[..., 2:3].contiguous().view(torch.float32)[..., 0]
+
+    @property
+    def part_info(self):
+        return self.parts[..., 3]
+
+    def finite_rows(self) -> torch.Tensor:
+        """Device bool per row: every logit is finite (the terminal stage's
+        torch.isfinite(logits).all() per row, stage_graph.py:361), read from
+        the records' flags instead of the logits."""
+        return ((self.part_info & 5) == 0).all(dim=1)
+
+
+def vocab_head(hidden: torch.Tensor, weight: torch.Tensor, *, policies=None, rows_per_policy: int = 1,
+               records: bool = True, out: HeadResult | None = None) -> HeadResult:
+    """``logits = hidden . weight^T`` (bf16 in, FP32 accumulation and out) for
+    ``hidden [rows, dim]`` and ``weight [vocab, dim]``, and with ``records``
+    one ``dsr_head_part_t`` per (row, 128-column tile).  Row r samples at the
+    temperature of ``policies[r // rows_per_policy]`` (a policy list or a
+    ``policy_tensor``); without policies the records carry no exp sums.
+    ``out`` reuses the tensors of an earlier result of the same shape."""
+    lib = N.load()
+    for t, name in ((hidden, "hidden"), (weight, "weight")):
+        _require_cuda(t, name)
+        if t.dtype != torch.bfloat16 or t.dim() != 2:
+            raise ValueError(f"{name} must be a 2-D bfloat16 tensor")
+    rows, dim = hidden.shape
+    vocab = weight.shape[0]
+    if weight.shape[1] != dim or weight.device != hidden.device:
+        raise ValueError("hidden and weight must share dim and device")
+    if not (0 <= rows <= N.HEAD_MAX_ROWS and dim >= 256 and dim % 256 == 0 and vocab % HEAD_TILE == 0
+            and HEAD_TILE <= vocab <= VOCAB):
+        raise ValueError("vocab_head needs rows <= 256, dim a multiple of 256 and vocab a multiple of 128")
+    dev = hidden.device
+    pol = None
+    if policies is not None:
+        if rows_per_policy < 1:
+            raise ValueError("rows_per_policy must be >= 1")
+        pol = policies if isinstance(policies, torch.Tensor) else policy_tensor(policies, dev)
+        if pol.numel() * pol.element_size() < -(-rows // rows_per_policy) * ctypes.sizeof(N.Policy):
+            raise ValueError("policies must cover every row")
+    if out is None:
+        logits = torch.empty(rows, vocab, dtype=torch.float32, device=dev)
+        parts = torch.empty(rows, vocab // HEAD_TILE, 4, dtype=torch.int32, device=dev) if records else None
+    else:
+        logits, parts = out.logits, out.parts
+        if tuple(logits.shape) != (rows, vocab) or (records and parts is None):
+            raise ValueError("out does not match this call")
+        parts = parts if records else None
+    a = N.HeadArgs()
+    a.hidden, a.weight, a.logits = hidden.data_ptr(), weight.data_ptr(), logits.data_ptr()
+    a.rows, a.dim, a.vocab = rows, dim, vocab
+    a.policy = pol.data_ptr() if pol is not None else None
+    a.rows_per_policy = rows_per_policy if pol is not None else 0
+    a.parts = parts.data_ptr() if parts is not None else None
+    res = HeadResult(logits, parts, policies, rows_per_policy, a, (hidden, weight, pol))
+    N.check(lib.dsr_vocab_head(ctypes.byref(a), _stream()), "dsr_vocab_head")
+    return res
+
+
+def vocab_head_launch(res: HeadResult) -> HeadResult:
+    """Re-issue a marshalled ``vocab_head`` call on the current stream."""
+    N.check(N.load().dsr_vocab_head(ctypes.byref(res.args), _stream()), "dsr_vocab_head")
+    return res
 
 
 # ---------------------------------------------------------------------------

@@ -10,6 +10,10 @@
 //                         one per request for the sequential accept chain.
 //   dsr_prob_*         -> categorical / correction_distribution / the accept
 //                         test on float64 probability vectors.
+//   dsr_vocab_head     -> the terminal stage's vocabulary projection and its
+//                         finiteness check (stage_graph.py:356-362), with the
+//                         verifier's per-row statistics in the epilogue
+//                         (dsr_head.h); dsr_verify_drafts_head reads them.
 #include <hip/hip_runtime.h>
 #include <limits.h>
 #include <mutex>
@@ -19,6 +23,7 @@
 #include "dsr_fast.h"
 #include "dsr_full.h"
 #include "dsr_general.h"
+#include "dsr_head.h"
 #include "dsr_history.h"
 #include "dsr_numpy.h"
 #include "dsr_split.h"
@@ -510,9 +515,12 @@ int32_t dsr_sample_rows_noalloc(const dsr_sample_args_t* args, void* stream) {
   return dsr_sample_rows(&a, stream);
 }
 
-int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
-  if (!args) return DSR_ERR_ARG;
-  const dsr_verify_args_t& a = *args;
+}  // extern "C"
+
+// dsr_verify_drafts and dsr_verify_drafts_head: with head records (tp) the
+// fast path's statistics come from k_head_shares instead of k_verify_stats.
+static int32_t verify_launch(const dsr_verify_args_t& a, const dsr_head_part_t* tp, const dsr_head_part_t* dp,
+                             void* stream) {
   if (!a.target || (a.K > 0 && (!a.draft || !a.draft_ids || (!a.u_accept && !a.rng_accept))) || !a.policy ||
       (!a.u_target && !a.rng_target) ||
       !a.output_limit || !a.out_accepted || !a.out_ids || !a.out_count || !a.out_pending || !a.out_stop ||
@@ -543,7 +551,10 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
   const size_t elt = a.dtype == DSR_BF16 ? 2 : (a.dtype == DSR_F32 ? 4 : 8);
   const bool vec = ((uintptr_t)a.target & 15u) == 0 && (a.K == 0 || ((uintptr_t)a.draft & 15u) == 0) &&
                    ((size_t)a.ld * elt) % 16 == 0;
-  if (L.fast_inputs) {
+  if (L.fast_inputs && tp) {
+    hipLaunchKernelGGL(k_head_shares, dim3((unsigned)(a.rows * slots)), dim3(64), 0, s, a, L, tp, dp);
+    if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  } else if (L.fast_inputs) {
     const dim3 grid((unsigned)(a.rows * slots * kVerifySplit));
     if (a.dtype == DSR_BF16) {
       if (vec) hipLaunchKernelGGL((k_verify_stats<DSR_BF16, true>), grid, dim3(kStatThreads), 0, s, a, L);
@@ -573,6 +584,70 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
     }
     if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
     hipLaunchKernelGGL(k_verify_finish, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
+  }
+  return launched();
+}
+
+// From three 32-row blocks (65 rows) on, a workgroup takes 256 columns: each
+// staged hidden chunk then serves twice the weight (at 160 rows x dim 5,120 x
+// vocab 129,280: 331 us against 378 us with 128-column workgroups).
+#ifndef DSR_HEAD_CB2_MIN_BLOCKS
+#define DSR_HEAD_CB2_MIN_BLOCKS 3
+#endif
+#ifndef DSR_HEAD_CB2_MIN_BLOCKS_RECORDS
+#define DSR_HEAD_CB2_MIN_BLOCKS_RECORDS DSR_HEAD_CB2_MIN_BLOCKS
+#endif
+
+template <int NB>
+static void head_launch(const dsr_head_args_t& a, hipStream_t s) {
+  const dim3 block(kHeadThreads);
+  if (NB >= (a.parts ? DSR_HEAD_CB2_MIN_BLOCKS_RECORDS : DSR_HEAD_CB2_MIN_BLOCKS) && a.vocab % (2 * kHeadTile) == 0) {
+    const dim3 grid((unsigned)(a.vocab / (2 * kHeadTile)));
+    if (a.parts) hipLaunchKernelGGL((k_vocab_head<NB, 2, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_vocab_head<NB, 2, false>), grid, block, 0, s, a);
+    return;
+  }
+  const dim3 grid((unsigned)(a.vocab / kHeadTile));
+  if (a.parts) hipLaunchKernelGGL((k_vocab_head<NB, 1, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((k_vocab_head<NB, 1, false>), grid, block, 0, s, a);
+}
+
+extern "C" {
+
+int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  return verify_launch(*args, nullptr, nullptr, stream);
+}
+
+int32_t dsr_verify_drafts_head(const dsr_verify_args_t* args, const dsr_head_part_t* target_parts,
+                               const dsr_head_part_t* draft_parts, void* stream) {
+  if (!args || !target_parts || (args->K > 0 && !draft_parts)) return DSR_ERR_ARG;
+  const dsr_verify_args_t& a = *args;
+  if (a.dtype != DSR_F32 || a.vocab % kHeadTile != 0 || a.ld != a.vocab || ((uintptr_t)target_parts & 7u) ||
+      ((uintptr_t)draft_parts & 7u))
+    return DSR_ERR_ARG;
+  return verify_launch(a, target_parts, draft_parts, stream);
+}
+
+int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  const dsr_head_args_t& a = *args;
+  if (!a.hidden || !a.weight || !a.logits || a.rows < 0 || a.rows > DSR_HEAD_MAX_ROWS || a.dim < kHeadDimStep ||
+      a.dim % kHeadDimStep != 0 || a.vocab < kHeadTile || a.vocab % kHeadTile != 0 || a.vocab > DSR_MAX_VOCAB ||
+      a.reserved != 0 || (a.policy && a.rows_per_policy < 1) || ((uintptr_t)a.hidden & 15u) ||
+      ((uintptr_t)a.weight & 15u) || ((uintptr_t)a.logits & 15u) || ((uintptr_t)a.parts & 7u))
+    return DSR_ERR_ARG;
+  if (a.rows == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  switch ((a.rows + 31) / 32) {
+    case 1: head_launch<1>(a, s); break;
+    case 2: head_launch<2>(a, s); break;
+    case 3: head_launch<3>(a, s); break;
+    case 4: head_launch<4>(a, s); break;
+    case 5: head_launch<5>(a, s); break;
+    case 6: head_launch<6>(a, s); break;
+    case 7: head_launch<7>(a, s); break;
+    default: head_launch<8>(a, s); break;
   }
   return launched();
 }

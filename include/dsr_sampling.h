@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSR_ABI_VERSION 3
+#define DSR_ABI_VERSION 4
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
@@ -228,6 +228,37 @@ typedef struct dsr_verify_args {
   uint32_t reserved;           /* must be 0 */
 } dsr_verify_args_t;
 
+/* Vocabulary projection (the terminal stage's lm_head, stage_graph.py:356-362
+ * and :396).  One record per (row, DSR_HEAD_TILE-column tile) of its FP32
+ * logits, written by the projection's epilogue: what the verifier's fast
+ * path and the finiteness check (stage_graph.py:361) need from the row. */
+#define DSR_HEAD_TILE 128           /* columns per record */
+#define DSR_HEAD_MAX_ROWS 256       /* hidden rows per dsr_vocab_head call */
+
+typedef struct dsr_head_part {
+  double sum;        /* sum of exp((v - max) / T) over the tile at the row's temperature T;
+                        0 for greedy rows (T == 0), T outside (0, 100], or a non-finite max */
+  float max;         /* the tile's largest logit (NaN ignored; -inf if none) */
+  int32_t info;      /* bit 0: a NaN or +inf logit; bit 1: a finite logit; bit 2: a -inf
+                        logit; bits 8-31: the first column of the tile holding max
+                        (0xFFFFFF: none) */
+} dsr_head_part_t;
+
+typedef struct dsr_head_args {
+  const void* hidden;            /* [rows, dim] bf16, row-major, 16-byte aligned */
+  const void* weight;            /* [vocab, dim] bf16, row-major, 16-byte aligned */
+  int64_t rows;                  /* 0 .. DSR_HEAD_MAX_ROWS */
+  int64_t dim;                   /* a positive multiple of 256 */
+  int64_t vocab;                 /* a positive multiple of DSR_HEAD_TILE, <= DSR_MAX_VOCAB */
+  const dsr_policy_t* policy;    /* or NULL: row r's temperature is
+                                    policy[r / rows_per_policy].temperature */
+  int32_t rows_per_policy;       /* >= 1 when policy is set */
+  int32_t reserved;              /* must be 0 */
+  float* logits;                 /* [rows, vocab] out, 16-byte aligned */
+  dsr_head_part_t* parts;        /* [rows, vocab / DSR_HEAD_TILE] out, 8-byte aligned,
+                                    or NULL: logits only */
+} dsr_head_args_t;
+
 /* ABI gate, after the reference's abi_version() (native/bindings.cpp:25). */
 int32_t dsr_abi_version(void);
 
@@ -265,6 +296,25 @@ int32_t dsr_sample_rows_noalloc(const dsr_sample_args_t* args, void* stream);
  * :170-183) with verify_drafts (sampling.py:247-294) and the lazy
  * conditional targets (terminal_sampling.py:234-244). */
 int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream);
+
+/* Vocabulary projection: logits = hidden . weight^T with FP32 accumulation,
+ * and with `parts` the per-tile records above.  Replaces the terminal
+ * stage's logits_processor(lm_head, norm(hidden)) and its
+ * torch.isfinite(logits).all() (stage_graph.py:356-362, and :396 for the
+ * draft rows); a row's logits are finite exactly when none of its records
+ * has info bit 0 or 2. */
+int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream);
+
+/* dsr_verify_drafts for FP32 logits written by dsr_vocab_head together with
+ * their records: the verifier's per-row statistics come from the records
+ * instead of a pass over the logits.  target_parts holds the records of the
+ * args->rows * (K + 1) target rows, draft_parts those of the rows * K draft
+ * rows (NULL when K == 0), each computed with rows_per_policy = K + 1 (resp.
+ * K) over args->policy.  Requires dtype DSR_F32, ld == vocab and vocab a
+ * multiple of DSR_HEAD_TILE.  Same results and workspace as
+ * dsr_verify_drafts. */
+int32_t dsr_verify_drafts_head(const dsr_verify_args_t* args, const dsr_head_part_t* target_parts,
+                               const dsr_head_part_t* draft_parts, void* stream);
 
 /* Probability-vector kernels behind the drop-in categorical /
  * correction_distribution / verify_drafts on float64 distributions.

@@ -1,0 +1,244 @@
+"""Vocabulary projection with the verifier's row statistics in its epilogue
+(dsr_vocab_head, dsr_verify_drafts_head).
+
+The terminal stage computes logits = lm_head(norm(hidden)) in FP32, checks
+torch.isfinite(logits).all() and verifies the drafts against those rows
+(stage_graph.py:356-362 and :396, terminal_sampling.py:170-183).  Here:
+
+- the logits equal a float64 product of the same bf16 inputs, and torch's
+  FP32 matmul on the GPU, within the FP32 accumulation bound
+  (dim / 16 + 16) * 2^-24 * sum_k |x_k w_k|: the kernel adds dim / 16 matrix
+  core partial sums of 16 exact bf16 products into one FP32 accumulator;
+- every (row, 128-column tile) record equals the same quantities computed in
+  float64 from the kernel's own logits: the maximum and the first column
+  holding it bit for bit, the NaN / +inf / finite / -inf flags exactly, the
+  exp sum within 1e-12 relative;
+- verifier decisions read from the records equal, field for field, those of
+  the verifier that reads the logits, and the oracle's on the same FP32 rows
+  (a decision may differ only where the oracle's own margin is below 1e-11).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from deepseekrpc_amd import _native as N
+from deepseekrpc_amd import batch
+from oracle import sampling_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TILE = 128
+
+
+def bf16(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+
+
+def head_inputs(seed, rows, dim, vocab, scale=2.0):
+    rng = np.random.default_rng(seed)
+    x = bf16(rng.normal(0, 1, (rows, dim)))
+    w = bf16(rng.normal(0, scale / np.sqrt(dim), (vocab, dim)))
+    return x, w
+
+
+def check_logits(x, w, got, cols=None):
+    """``got`` [rows, vocab] (host float32) against the float64 product, on
+    the columns ``cols`` (all when None)."""
+    xd = x.double().numpy()
+    wd = w.double().numpy() if cols is None else w[cols].double().numpy()
+    want = xd @ wd.T
+    scale = np.abs(xd) @ np.abs(wd).T
+    g = got.astype(np.float64) if cols is None else got[:, cols].astype(np.float64)
+    tol = (x.shape[1] // 16 + 16) * 2.0 ** -24 * scale + 1e-30
+    err = np.abs(g - want)
+    assert np.all(err <= tol), float(np.max(err / tol))
+
+
+@pytest.mark.parametrize("rows,dim,vocab", [(1, 256, 128), (5, 256, 512), (32, 512, 2560), (33, 768, 1024),
+                                            (100, 256, 896), (160, 1024, 1280), (200, 256, 4096), (256, 256, 2048)])
+def test_logits_match_the_float64_product(rows, dim, vocab):
+    x, w = head_inputs(rows * 7 + dim, rows, dim, vocab)
+    for records in (False, True):
+        res = batch.vocab_head(x.to(DEV), w.to(DEV), records=records)
+        check_logits(x, w, res.logits.cpu().numpy())
+    # torch's FP32 product of the same inputs on the GPU, within the same bound.
+    ref = (x.to(DEV).float() @ w.to(DEV).float().T).cpu().double().numpy()
+    scale = np.abs(x.double().numpy()) @ np.abs(w.double().numpy()).T
+    assert np.all(np.abs(res.logits.cpu().double().numpy() - ref) <= 2 * (dim // 16 + 16) * 2.0 ** -24 * scale + 1e-30)
+
+
+def device_weight(seed, vocab, dim):
+    """bf16 weight q * 2^-10 with q uniform on [-64, 63], drawn on the device."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    q = torch.randint(-64, 64, (vocab, dim), generator=g, device=DEV, dtype=torch.int32)
+    return (q.to(torch.bfloat16) * 2.0 ** -10).contiguous()
+
+
+def test_full_vocabulary_logits_at_the_terminal_stage_width():
+    """160 rows x dim 5,120 x vocab 129,280 (the terminal stage's lm_head,
+    stage_graph.py:180-182), compared on 4,096 columns spread over the row."""
+    x = bf16(np.random.default_rng(5).normal(0, 1, (160, 5120)))
+    xd, wd = x.to(DEV), device_weight(5, 129280, 5120)
+    res = batch.vocab_head(xd, wd, policies=[dict(temperature=1.0)] * 32, rows_per_policy=5)
+    got = res.logits.cpu().numpy()
+    cols = np.sort(np.random.default_rng(6).choice(129280, 4096, replace=False))
+    check_logits(x, wd[torch.from_numpy(cols).to(DEV)].cpu(), got[:, cols])
+    assert bool(res.finite_rows().all())
+    plain = batch.vocab_head(xd, wd, records=False)
+    assert torch.equal(plain.logits, res.logits)  # the epilogue changes no logit
+
+
+def record_reference(logits, temps):
+    """Float64 records from FP32 logits [rows, vocab]: (sum, max, info)."""
+    rows, vocab = logits.shape
+    tiles = vocab // TILE
+    v = logits.reshape(rows, tiles, TILE)
+    nan = np.isnan(v)
+    mx = np.where(nan, -np.inf, v).max(axis=2).astype(np.float32)
+    flags = (np.any(nan | (v == np.inf), axis=2) * 1 | np.any(np.isfinite(v), axis=2) * 2
+             | np.any(v == -np.inf, axis=2) * 4)
+    hit = v == mx[..., None]
+    first = np.where(hit.any(axis=2), hit.argmax(axis=2), 0xFFFFFF)
+    info = (flags | (first << 8)).astype(np.uint32).view(np.int32)  # the record's int32 bits
+    sums = np.zeros((rows, tiles))
+    for r in range(rows):
+        T = temps[r]
+        if not (0 < T <= 100):
+            continue
+        for t in range(tiles):
+            m = float(mx[r, t])
+            if np.isfinite(m):
+                with np.errstate(invalid="ignore"):
+                    e = np.exp((v[r, t].astype(np.float64) - m) / T)
+                sums[r, t] = np.sum(np.where(np.isnan(e), 0.0, e))
+    return sums, mx, info
+
+
+@pytest.mark.parametrize("rows,dim,vocab", [(7, 256, 1024), (40, 512, 2048), (200, 256, 1024)])
+def test_records_equal_the_float64_statistics_of_the_logits(rows, dim, vocab):
+    x, w = head_inputs(rows + 3 * dim, rows, dim, vocab)
+    xn, wn = x.float().numpy(), w.float().numpy()
+    xn[1, 0] = np.inf                 # row 1: +inf and -inf logits (the sign of w[:, 0])
+    xn[2, 3] = np.nan                 # row 2: every logit NaN
+    xn[3] = 0.0                       # row 3: every logit 0: maximum at each tile's column 0, sum 128
+    wn[5] = wn[7] = 8.0 * np.sign(xn[4])  # row 4: the same maximum at columns 5 and 7
+    wn[5, 0] = wn[7, 0] = 0.0         # (row 1's columns 5 and 7: inf * 0, NaN)
+    x, w = bf16(xn), bf16(wn)
+    temps = [1.0, 0.7, 0.0, 2.5, 1e-3, 100.0]
+    pols = [dict(temperature=temps[i % len(temps)]) for i in range(-(-rows // 2))]
+    res = batch.vocab_head(x.to(DEV), w.to(DEV), policies=pols, rows_per_policy=2)
+    logits = res.logits.cpu().numpy()
+    row_t = [pols[r // 2]["temperature"] for r in range(rows)]
+    sums, mx, info = record_reference(logits, row_t)
+    assert np.array_equal(res.part_max.cpu().numpy().view(np.uint32), mx.view(np.uint32))
+    assert np.array_equal(res.part_info.cpu().numpy(), info)
+    got = res.part_sum.cpu().numpy()
+    np.testing.assert_allclose(got, sums, rtol=1e-12, atol=0)
+    assert (info[3, 0] >> 8) & 0xFFFFFF == 0 and got[3, 0] == float(TILE) * (row_t[3] > 0)
+    assert (info[4, 0] >> 8) & 0xFFFFFF == 5 and (info[2, 0] >> 8) & 0xFFFFFF == 0xFFFFFF
+    finite = res.finite_rows().cpu().numpy()
+    assert np.array_equal(finite, np.isfinite(logits).all(axis=1))
+    assert not finite[1] and not finite[2]
+
+
+def verify_case(seed, dim=256, R=32, K=4, V=129280, poison=None):
+    """C4-shaped requests whose target and draft rows come from one head."""
+    rng = np.random.default_rng(seed)
+    w = device_weight(seed, V, dim) * (2.0 / np.sqrt(dim) / 0.036)
+    xt_np = rng.normal(0, 1, (R * (K + 1), dim)).astype(np.float32)
+    xd_np = xt_np.reshape(R, K + 1, dim)[:, :K].reshape(R * K, dim) + rng.normal(0, 0.35, (R * K, dim))
+    if poison is not None:
+        xt_np[poison] = np.nan
+    xt, xd = bf16(xt_np).to(DEV), bf16(xd_np).to(DEV)
+    temps = [1.0, 0.7, 1.3, 0.0]
+    pols = [dict(temperature=temps[r % 4]) for r in range(R)]
+    pols[5] = dict(temperature=0.8, top_k=50)   # a filtered request: the full-distribution path
+    pt = batch.policy_tensor(pols, DEV)
+    th = batch.vocab_head(xt, w, policies=pt, rows_per_policy=K + 1)
+    dh = batch.vocab_head(xd, w, policies=pt, rows_per_policy=K)
+    tgt, drf = th.logits.view(R, K + 1, V), dh.logits.view(R, K, V)
+    draw = batch.sample_rows(dh.logits, [pols[r // K] for r in range(R * K)],
+                             uniforms=torch.from_numpy(rng.random(R * K)).to(DEV))
+    ids = draw.tokens.reshape(R, K).contiguous()
+    greedy = torch.tensor([p["temperature"] == 0 for p in pols], device=DEV)
+    ids[greedy] = drf.argmax(dim=-1).to(torch.int32)[greedy]
+    ua_np, ut_np = rng.random((R, K)), rng.random(R)
+    ua, ut = torch.from_numpy(ua_np).to(DEV), torch.from_numpy(ut_np).to(DEV)
+    lim = torch.from_numpy(np.array([10, 2, 3, 10] * (R // 4), np.int32)).to(DEV)
+    eos_ids = ids[:, 1].contiguous()
+    eos_off = torch.arange(0, R + 1, dtype=torch.int64, device=DEV)
+    kw = dict(eos_offsets=eos_off, eos_ids=eos_ids)
+    by_logits = batch.verify_drafts(tgt, drf, ids, pt, ua, ut, lim, **kw)
+    by_head = batch.verify_drafts(tgt, drf, ids, pt, ua, ut, lim, head=(th, dh), **kw)
+    return dict(pols=pols, tgt=tgt, drf=drf, ids=ids, ua=ua_np, ut=ut_np, lim=lim, eos=eos_ids,
+                a=by_logits, b=by_head, th=th)
+
+
+FIELDS = ("accepted", "ids", "count", "pending", "stop", "used_accept", "used_target", "status", "flags")
+
+
+def test_verify_from_head_records_equals_the_logits_path_and_the_oracle():
+    c = verify_case(21)
+    a, b = c["a"], c["b"]
+    for f in FIELDS:
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    tgt, drf = c["tgt"].cpu().numpy(), c["drf"].cpu().numpy()
+    ids, lim, eos = c["ids"].cpu().numpy(), c["lim"].cpu().numpy(), c["eos"].cpu().numpy()
+    R = tgt.shape[0]
+    waived = 0
+    for r in range(R):
+        p = c["pols"][r]
+        ref = O.verify(tgt[r], drf[r], list(ids[r]), O.Policy(**p), c["ua"][r], float(c["ut"][r]),
+                       output_limit=int(lim[r]), eos_ids=(int(eos[r]),))
+        got = (int(b.status[r]), int(b.accepted[r]), tuple(int(t) for t in b.ids[r, :int(b.count[r])].tolist()),
+               None if int(b.pending[r]) < 0 else int(b.pending[r]), int(b.used_accept[r]), int(b.used_target[r]))
+        want = (ref.status, ref.accepted, ref.output_ids, ref.pending, ref.used_accept, ref.used_target)
+        if got != want:
+            assert ref.margin < 1e-11, (r, got, want, ref.margin)
+            waived += 1
+    assert waived == 0
+
+
+def test_a_non_finite_head_row_is_reported_the_same_way():
+    """Request 3's target row 1 is NaN: both verifiers report it (or not, when
+    the chain ends first) exactly as the oracle does."""
+    K = 4
+    c = verify_case(22, R=8, poison=3 * (K + 1) + 1)
+    a, b = c["a"], c["b"]
+    for f in FIELDS:
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    tgt, drf = c["tgt"].cpu().numpy(), c["drf"].cpu().numpy()
+    ids, lim, eos = c["ids"].cpu().numpy(), c["lim"].cpu().numpy(), c["eos"].cpu().numpy()
+    ref = O.verify(tgt[3], drf[3], list(ids[3]), O.Policy(**c["pols"][3]), c["ua"][3], float(c["ut"][3]),
+                   output_limit=int(lim[3]), eos_ids=(int(eos[3]),))
+    assert int(b.status[3]) == ref.status
+    finite = c["th"].finite_rows().cpu().numpy()
+    assert not finite[3 * (K + 1) + 1] and finite.sum() == finite.size - 1
+
+
+def test_head_arguments_are_checked_before_any_launch():
+    x, w = head_inputs(1, 4, 256, 512)
+    xd, wd = x.to(DEV), w.to(DEV)
+    with pytest.raises(ValueError):
+        batch.vocab_head(torch.zeros(257, 256, dtype=torch.bfloat16, device=DEV), wd)
+    with pytest.raises(ValueError):
+        batch.vocab_head(xd[:, :192].contiguous(), wd[:, :192].contiguous())
+    with pytest.raises(ValueError):
+        batch.vocab_head(xd, wd[:500].contiguous())
+    lib = N.load()
+    out = torch.empty(4, 512, dtype=torch.float32, device=DEV)
+    a = N.HeadArgs()
+    a.hidden, a.weight, a.logits = xd.data_ptr() + 2, wd.data_ptr(), out.data_ptr()  # misaligned hidden
+    a.rows, a.dim, a.vocab = 4, 256, 512
+    assert lib.dsr_vocab_head(ctypes.byref(a), None) == -1
+    a.hidden, a.dim = xd.data_ptr(), 320
+    assert lib.dsr_vocab_head(ctypes.byref(a), None) == -1
+    a.dim, a.reserved = 256, 1
+    assert lib.dsr_vocab_head(ctypes.byref(a), None) == -1
+    a.reserved = 0
+    assert lib.dsr_vocab_head(ctypes.byref(a), None) == 0   # the same call, valid
+    torch.cuda.synchronize()
+    check_logits(x, w, out.cpu().numpy())

@@ -45,7 +45,7 @@ def test_flag_and_status_constants_match_header():
     for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
                  "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
                  "E_GENERATED", "E_HISTORY", "E_APPEND", "E_HINT", "MAX_APPEND", "HINT_WHOLE_SOME", "HINT_WHOLE_ALL",
-                 "HINT_VERIFY_FAST"):
+                 "HINT_VERIFY_FAST", "HEAD_TILE", "HEAD_MAX_ROWS"):
         assert getattr(N, name) == defs["DSR_" + name], name
     assert N.ABI_VERSION == defs["DSR_ABI_VERSION"]
 
@@ -69,6 +69,21 @@ def test_argument_errors_return_before_any_launch():
     assert lib.dsr_sample_rows(None, None) == -1
     v = N.VerifyArgs()
     assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1
+    assert lib.dsr_verify_drafts_head(ctypes.byref(v), None, None, None) == -1
+    assert lib.dsr_vocab_head(None, None) == -1
+    h = N.HeadArgs()  # null pointers
+    assert lib.dsr_vocab_head(ctypes.byref(h), None) == -1
+    fake16 = 4096
+    h.hidden = h.weight = h.logits = fake16
+    h.rows, h.dim, h.vocab = 8, 256, 512
+    for field, bad in (("rows", 257), ("rows", -1), ("dim", 320), ("dim", 0), ("vocab", 300), ("vocab", 129536),
+                       ("reserved", 1), ("hidden", fake16 + 2), ("parts", fake16 + 4)):
+        good = getattr(h, field)
+        setattr(h, field, bad)
+        assert lib.dsr_vocab_head(ctypes.byref(h), None) == -1, field
+        setattr(h, field, good)
+    h.policy, h.rows_per_policy = fake16, 0
+    assert lib.dsr_vocab_head(ctypes.byref(h), None) == -1
     assert lib.dsr_prob_stats(None, 3, None, None, None) == -1
     assert lib.dsr_prob_categorical(None, 3, 0.5, None, None) == -1
     # History builders: null inputs, vocabularies out of range, ld below the
@@ -96,16 +111,21 @@ int main(void) {
   printf("dsr_policy_t size %zu\n", sizeof(dsr_policy_t));
   printf("dsr_sample_args_t size %zu\n", sizeof(dsr_sample_args_t));
   printf("dsr_verify_args_t size %zu\n", sizeof(dsr_verify_args_t));
+  printf("dsr_head_part_t size %zu\n", sizeof(dsr_head_part_t));
+  printf("dsr_head_args_t size %zu\n", sizeof(dsr_head_args_t));
   %FIELDS%
   return 0;
 }
 """
 
 
+STRUCTS = (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs), ("dsr_verify_args_t", N.VerifyArgs),
+           ("dsr_head_part_t", N.HeadPart), ("dsr_head_args_t", N.HeadArgs))
+
+
 def test_struct_layouts_match_header(tmp_path):
     fields = []
-    for cname, cls in (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs),
-                       ("dsr_verify_args_t", N.VerifyArgs)):
+    for cname, cls in STRUCTS:
         fields += [f"F({cname}, {f})" for f, _ in cls._fields_]
     src = tmp_path / "layout.c"
     src.write_text(LAYOUT_C.replace("%FIELDS%", "\n  ".join(fields)))
@@ -117,10 +137,7 @@ def test_struct_layouts_match_header(tmp_path):
         if line:
             t, f, off = line.split()
             got[(t, f)] = int(off)
-    assert got[("dsr_policy_t", "size")] == ctypes.sizeof(N.Policy)
-    assert got[("dsr_sample_args_t", "size")] == ctypes.sizeof(N.SampleArgs)
-    assert got[("dsr_verify_args_t", "size")] == ctypes.sizeof(N.VerifyArgs)
-    for cname, cls in (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs),
-                       ("dsr_verify_args_t", N.VerifyArgs)):
+    for cname, cls in STRUCTS:
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
         for f, _ in cls._fields_:
             assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
