@@ -306,6 +306,9 @@ def cpu_baseline(name, w, passes):
     unit = WORKLOADS[name][1]
     what = {"c4": "requests", "head": "requests", "propose": "chains", "seed": "calls", "step": "steps"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
+    if name == "head":
+        oracle += (" (verification only: the reference projects on its GPU; the rows' logits were computed "
+                   "beforehand by NumPy's float32 product, untimed)")
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
             "sample": f"{n} {what} ({passes} pass(es) over the {_units(name, w)} of the same workload, "

@@ -43,16 +43,16 @@ static_assert(kHeadTile == 4 * 32, "four waves of 32 columns");
 
 template <int N> using HeadSlot = std::integral_constant<int, N>;
 
-template <int NB>
+template <int NB, int CB>
 union alignas(16) HeadShared {  // 16-byte aligned: the staged rows are read as b128
   __bf16 x[2][NB * 32][kHeadStride];  // hidden chunk, double-buffered
-  struct {                            // epilogue, after the last chunk
-    float m[4][NB * 32];              // per wave and row: maximum of its 32 columns
-    uint32_t f[4][NB * 32];           // flags
-    int32_t i[4][NB * 32];            // first column holding the tile maximum
-    double s[4][NB * 32];             // sum of exp((v - max) / T)
-    float tm[NB * 32];                // tile maximum
-    uint32_t tf[NB * 32];             // tile flags
+  struct {                            // epilogue, after the last chunk: [tile][wave][row]
+    double s[CB][4][NB * 32];         // sum of exp((v - max) / T) over the wave's 32 columns
+    float m[CB][4][NB * 32];          // maximum of the wave's 32 columns
+    uint32_t f[CB][4][NB * 32];       // flags
+    int32_t i[CB][4][NB * 32];        // first column holding the tile maximum
+    float tm[CB][NB * 32];            // tile maximum
+    uint32_t tf[CB][NB * 32];         // tile flags
   } r;
 };
 
@@ -66,7 +66,7 @@ __device__ __forceinline__ double head_temperature(const dsr_head_args_t& a, int
 // workgroup's span, so block b of the four waves is record tile b.
 template <int NB, int CB, bool STATS>
 __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vocab_head(dsr_head_args_t a) {
-  __shared__ HeadShared<NB> sh;
+  __shared__ HeadShared<NB, CB> sh;
   __shared__ double etab[64];
   const int t = threadIdx.x, l = t & 63, w = t >> 6, j = l & 31, h = l >> 5;
   const int64_t dim = a.dim, rows = a.rows;
@@ -79,7 +79,13 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
   const int64_t wstep = (int64_t)kHeadTile * dim;
 
   bf16x8_t wr[4][CB][4];  // weight ring: chunk c in slot c % 4, [column block][16-wide dim step]
-  bf16x8_t xr[2][NB];     // hidden chunks c + 1 and c + 2 on their way to LDS (slot chunk % 2)
+  // Hidden chunks in flight to LDS: chunk c in slot c % XL.  Four for the
+  // 256-column workgroups with up to five row blocks (then the weight loads
+  // of the last four steps stay in flight through each step's wait: 160 rows
+  // x dim 5,120 x vocab 129,280 in 309-325 us against 331-368 us with two);
+  // two otherwise, where more workgroups per CU share the latency.
+  constexpr int XL = CB == 2 && NB <= 5 ? 4 : 2;
+  bf16x8_t xr[XL][NB];
   f32x16_t acc[CB][NB];
 #pragma unroll
   for (int b = 0; b < CB; ++b)
@@ -143,33 +149,44 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
     }
     __builtin_amdgcn_sched_group_barrier(0x008, CB * NB, 0);
   };
-  // Chunk c: fetch hidden chunk c + 2, multiply chunk c, refill this weight
-  // slot four chunks ahead, stage hidden chunk c + 1 (fetched one step
-  // earlier, so that waiting for it leaves the last two steps' weight loads
-  // in flight).  The barrier ends every reader of buffer c & 1 before the
-  // next step overwrites it.  nc is a multiple of 4 (dim of 256).
+  // Chunk c: fetch hidden chunk c + XL, multiply chunk c, refill this
+  // weight slot four chunks ahead, stage hidden chunk c + 1 (fetched XL - 1
+  // steps earlier, so that waiting for it leaves the weight loads of the
+  // last XL steps in flight).  The barrier ends every reader of buffer c & 1
+  // before the next step overwrites it.  nc is a multiple of 4 (dim of 256).
   // The scheduling barriers keep this order of issue: the wait counts depend
   // on it.
   auto step = [&](auto S, int c) __attribute__((always_inline)) {
     constexpr int s = decltype(S)::value;
-    load_x(HeadSlot<s & 1>{}, c + 2);
+    load_x(HeadSlot<s % XL>{}, c + XL);
     __builtin_amdgcn_sched_barrier(0);
     compute(S, c & 1);
     __builtin_amdgcn_sched_barrier(0);
     load_w(S, c + 4);
     __builtin_amdgcn_sched_barrier(0);
-    store_x(HeadSlot<(s + 1) & 1>{}, (c + 1) & 1);
+    store_x(HeadSlot<(s + 1) % XL>{}, (c + 1) & 1);
     __syncthreads();
   };
 
-  // The same order as the loop's steady state (hidden chunk 1, then a
-  // weight chunk), so that the first step's waits are the steady ones.
-  load_w(HeadSlot<0>{}, 0);
-  load_w(HeadSlot<1>{}, 1);
-  load_x(HeadSlot<0>{}, 0);
-  load_w(HeadSlot<2>{}, 2);
-  load_x(HeadSlot<1>{}, 1);
-  load_w(HeadSlot<3>{}, 3);
+  // The steady state's order of issue (each hidden chunk before the weight
+  // chunk of its step), so that the first steps' waits are the steady ones.
+  if constexpr (XL == 4) {
+    load_x(HeadSlot<0>{}, 0);
+    load_w(HeadSlot<0>{}, 0);
+    load_x(HeadSlot<1>{}, 1);
+    load_w(HeadSlot<1>{}, 1);
+    load_x(HeadSlot<2>{}, 2);
+    load_w(HeadSlot<2>{}, 2);
+    load_x(HeadSlot<3>{}, 3);
+    load_w(HeadSlot<3>{}, 3);
+  } else {
+    load_w(HeadSlot<0>{}, 0);
+    load_w(HeadSlot<1>{}, 1);
+    load_x(HeadSlot<0>{}, 0);
+    load_w(HeadSlot<2>{}, 2);
+    load_x(HeadSlot<1>{}, 1);
+    load_w(HeadSlot<3>{}, 3);
+  }
   __builtin_amdgcn_sched_barrier(0);
   store_x(HeadSlot<0>{}, 0);
   if (STATS) exp_table_init(etab);
@@ -182,14 +199,14 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
   }
 
   // acc[b][n] element e holds column v0 + 128 b + 32 w + 8 (e >> 2) + 4 h +
-  // (e & 3) of hidden row 32 n + j.  One tile and row block at a time: its 16
-  // values per lane go to VGPRs, to the logits, and (with records) through the
-  // tile's maximum, first maximum column and exp sum, so that only one block's
-  // values are live outside the accumulators.
+  // (e & 3) of hidden row 32 n + j.  Each (tile, row block) is copied from
+  // the accumulators when it is used, so that only one block's values are
+  // live outside them.  With records, three workgroup barriers in all: the
+  // lanes' maxima and flags, the tile maxima, the lanes' first maximum column
+  // and exp sum, then one thread per (tile, row) writes the record.
   float* out = a.logits;
 #pragma unroll
-  for (int b = 0; b < CB; ++b) {
-    const int64_t vb = v0 + kHeadTile * b;
+  for (int b = 0; b < CB; ++b)
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       const int r = 32 * n + j;
@@ -200,7 +217,7 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f32x4_t x4 = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-          *(f32x4_t*)(out + (int64_t)r * a.vocab + vb + 32 * w + 8 * q + 4 * h) = x4;
+          *(f32x4_t*)(out + (int64_t)r * a.vocab + v0 + kHeadTile * b + 32 * w + 8 * q + 4 * h) = x4;
         }
       }
       if constexpr (STATS) {
@@ -219,49 +236,59 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
         m = fmaxf(m, __shfl_xor(m, 32));
         fl |= __shfl_xor(fl, 32);
         if (h == 0) {
-          sh.r.m[w][r] = m;
-          sh.r.f[w][r] = fl;
+          sh.r.m[b][w][r] = m;
+          sh.r.f[b][w][r] = fl;
         }
-        __syncthreads();
-        if (t < 32) {
-          const int rr = 32 * n + t;
-          sh.r.tm[rr] = fmaxf(fmaxf(sh.r.m[0][rr], sh.r.m[1][rr]), fmaxf(sh.r.m[2][rr], sh.r.m[3][rr]));
-          sh.r.tf[rr] = sh.r.f[0][rr] | sh.r.f[1][rr] | sh.r.f[2][rr] | sh.r.f[3][rr];
-        }
-        __syncthreads();
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keeps the next block's copies after this one
+    }
+  if constexpr (STATS) {
+    __syncthreads();
+    for (int x = t; x < CB * NB * 32; x += kHeadThreads) {
+      const int b = x / (NB * 32), rr = x % (NB * 32);
+      sh.r.tm[b][rr] = fmaxf(fmaxf(sh.r.m[b][0][rr], sh.r.m[b][1][rr]), fmaxf(sh.r.m[b][2][rr], sh.r.m[b][3][rr]));
+      sh.r.tf[b][rr] = sh.r.f[b][0][rr] | sh.r.f[b][1][rr] | sh.r.f[b][2][rr] | sh.r.f[b][3][rr];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const int r = 32 * n + j;
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = acc[b][n][e];
         // First column holding the maximum, and sum exp((v - max) / T).
-        const float M = sh.r.tm[r];
+        const float M = sh.r.tm[b][r];
         int first = INT_MAX;
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           if (v[e] == M) first = min(first, 32 * w + 8 * (e >> 2) + 4 * h + (e & 3));
         first = min(first, __shfl_xor(first, 32));
-        double s = 0.0;
+        double sum = 0.0;
         const double T = r < rows ? head_temperature(a, r) : 0.0;
         if (T > 0.0 && T <= 100.0 && fabsf(M) != INFINITY) {  // sampled rows with a finite maximum
           const ExpTerm term{(double)M, exp_scale(T), etab};
 #pragma unroll
-          for (int e = 0; e < 16; ++e) s += term((double)v[e]);
+          for (int e = 0; e < 16; ++e) sum += term((double)v[e]);
         }
-        s += __shfl_xor(s, 32);  // both lanes add the same two values
+        sum += __shfl_xor(sum, 32);  // both lanes add the same two values
         if (h == 0) {
-          sh.r.i[w][r] = first;
-          sh.r.s[w][r] = s;
+          sh.r.i[b][w][r] = first;
+          sh.r.s[b][w][r] = sum;
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);  // keeps the next block's copies after this one
-    }
-    if constexpr (STATS) {
-      __syncthreads();
-      if (t < rows) {
-        const int first = min(min(sh.r.i[0][t], sh.r.i[1][t]), min(sh.r.i[2][t], sh.r.i[3][t]));
-        dsr_head_part_t p;
-        p.sum = ((sh.r.s[0][t] + sh.r.s[1][t]) + sh.r.s[2][t]) + sh.r.s[3][t];
-        p.max = sh.r.tm[t];
-        p.info = (int32_t)((sh.r.tf[t] & 7u) | ((uint32_t)(first == INT_MAX ? 0xFFFFFF : first) << 8));
-        a.parts[(int64_t)t * (a.vocab / kHeadTile) + (int64_t)blockIdx.x * CB + b] = p;
-      }
-      __syncthreads();  // the next tile reuses the reduction arrays
+    __syncthreads();
+    const int64_t tiles = a.vocab / kHeadTile;
+    for (int x = t; x < CB * rows; x += kHeadThreads) {
+      const int b = x / (int)rows, rr = x % (int)rows;
+      const int first = min(min(sh.r.i[b][0][rr], sh.r.i[b][1][rr]), min(sh.r.i[b][2][rr], sh.r.i[b][3][rr]));
+      dsr_head_part_t p;
+      p.sum = ((sh.r.s[b][0][rr] + sh.r.s[b][1][rr]) + sh.r.s[b][2][rr]) + sh.r.s[b][3][rr];
+      p.max = sh.r.tm[b][rr];
+      p.info = (int32_t)((sh.r.tf[b][rr] & 7u) | ((uint32_t)(first == INT_MAX ? 0xFFFFFF : first) << 8));
+      a.parts[(int64_t)rr * tiles + (int64_t)blockIdx.x * CB + b] = p;
     }
   }
 }
