@@ -68,6 +68,7 @@ template <int NB, int CB, bool STATS>
 __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vocab_head(dsr_head_args_t a) {
   __shared__ HeadShared<NB, CB> sh;
   __shared__ double etab[64];
+  __shared__ double temp[STATS ? NB * 32 : 1];  // each row's temperature
   const int t = threadIdx.x, l = t & 63, w = t >> 6, j = l & 31, h = l >> 5;
   const int64_t dim = a.dim, rows = a.rows;
   const int nc = (int)(dim / kHeadChunk);
@@ -168,8 +169,11 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
     __syncthreads();
   };
 
-  // The steady state's order of issue (each hidden chunk before the weight
+  // The rows' temperatures first (the epilogue reads them from LDS), then
+  // the steady state's order of issue (each hidden chunk before the weight
   // chunk of its step), so that the first steps' waits are the steady ones.
+  double tr = 0.0;
+  if (STATS && t < NB * 32 && t < rows) tr = head_temperature(a, t);
   if constexpr (XL == 4) {
     load_x(HeadSlot<0>{}, 0);
     load_w(HeadSlot<0>{}, 0);
@@ -189,7 +193,10 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
   }
   __builtin_amdgcn_sched_barrier(0);
   store_x(HeadSlot<0>{}, 0);
-  if (STATS) exp_table_init(etab);
+  if (STATS) {
+    exp_table_init(etab);
+    if (t < NB * 32) temp[t] = tr;
+  }
   __syncthreads();
   for (int c = 0; c < nc; c += 4) {
     step(HeadSlot<0>{}, c);
@@ -266,7 +273,7 @@ __global__ __launch_bounds__(kHeadThreads, CB == 1 && NB <= 5 ? 2 : 1) void k_vo
           if (v[e] == M) first = min(first, 32 * w + 8 * (e >> 2) + 4 * h + (e & 3));
         first = min(first, __shfl_xor(first, 32));
         double sum = 0.0;
-        const double T = r < rows ? head_temperature(a, r) : 0.0;
+        const double T = temp[r];  // 0 for rows past `rows`
         if (T > 0.0 && T <= 100.0 && fabsf(M) != INFINITY) {  // sampled rows with a finite maximum
           const ExpTerm term{(double)M, exp_scale(T), etab};
 #pragma unroll
