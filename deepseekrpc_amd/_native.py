@@ -47,10 +47,11 @@ EXPORTS = (
     "dsr_abi_version", "dsr_status_message", "dsr_sample_workspace_bytes", "dsr_verify_workspace_bytes",
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
     "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append", "dsr_sample_rows_noalloc",
-    "dsr_vocab_head", "dsr_verify_drafts_head",
+    "dsr_vocab_head", "dsr_verify_drafts_head", "dsr_prob_stats_rows",
 )
 NOALLOC_SCRATCH_BYTES = 268435456
 HEAD_TILE = 128
+STATS_MAX_ROWS = 16
 HEAD_MAX_ROWS = 256
 
 _p = ctypes.c_void_p
@@ -137,6 +138,8 @@ def load(path: str = LIB_PATH):
     lib.dsr_verify_drafts.argtypes = [ctypes.POINTER(VerifyArgs), _p]
     lib.dsr_prob_stats.restype = _i32
     lib.dsr_prob_stats.argtypes = [_p, _i64, _p, _p, _p]
+    lib.dsr_prob_stats_rows.restype = _i32
+    lib.dsr_prob_stats_rows.argtypes = [ctypes.POINTER(_p), _i32, _i64, _p, _p]
     lib.dsr_prob_categorical.restype = _i32
     lib.dsr_prob_categorical.argtypes = [_p, _i64, _f64, _p, _p]
     lib.dsr_prob_correction.restype = _i32

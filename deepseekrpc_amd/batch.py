@@ -946,6 +946,22 @@ def prob_stats_launch(p: torch.Tensor, slot: torch.Tensor):
     N.check(lib.dsr_prob_stats(_ptr(p), p.numel(), _ptr(slot[0:1]), _ptr(slot[1:3]), _stream()), "dsr_prob_stats")
 
 
+def prob_stats_rows_launch(rows, out: torch.Tensor):
+    """``dsr_prob_stats`` of every row (contiguous float64 device vectors of
+    one length) into ``out``, a contiguous float64 ``[len(rows), 3]`` device
+    tensor of slots, one launch per 16 rows.  Nothing is synchronised."""
+    lib = N.load()
+    n = rows[0].numel()
+    if out.shape != (len(rows), 3) or out.dtype != torch.float64 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float64 [rows, 3] tensor")
+    for r in rows:
+        _require(r, "row", torch.float64, n)
+    for start in range(0, len(rows), N.STATS_MAX_ROWS):
+        chunk = rows[start:start + N.STATS_MAX_ROWS]
+        ptrs = (ctypes.c_void_p * len(chunk))(*[t.data_ptr() for t in chunk])
+        N.check(lib.dsr_prob_stats_rows(ptrs, len(chunk), n, _ptr(out[start]), _stream()), "dsr_prob_stats_rows")
+
+
 def prob_stats_read(slot: torch.Tensor):
     """(sum, valid, n_positive, first_positive, argmax) from a host copy of a slot."""
     o = slot[1:3].view(torch.int32).tolist()

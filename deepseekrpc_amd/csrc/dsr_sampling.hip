@@ -203,10 +203,8 @@ __global__ __launch_bounds__(kThreads) void k_sample_bf16_full(dsr_sample_args_t
 // ---------------------------------------------------------------------------
 // Probability-vector kernels (single workgroup).
 
-__global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_t n, double* out_sum,
-                                                         int32_t* out) {
-  __shared__ GenShared sh;
-  __shared__ NpSumShared np;
+__device__ __forceinline__ void prob_stats_row(const double* p, int64_t n, double* out_sum, int32_t* out,
+                                               GenShared& sh, NpSumShared& np) {
   int bad = 0;
   long long npos = 0, first = LLONG_MAX;
   RowMax mx;  // every thread visits its elements in increasing index order
@@ -232,6 +230,27 @@ __global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_
     out[2] = first == LLONG_MAX ? -1 : (int32_t)first;
     out[3] = am == LLONG_MAX ? -1 : (int32_t)am;
   }
+}
+
+__global__ __launch_bounds__(kThreads) void k_prob_stats(const double* p, int64_t n, double* out_sum,
+                                                         int32_t* out) {
+  __shared__ GenShared sh;
+  __shared__ NpSumShared np;
+  prob_stats_row(p, n, out_sum, out, sh, np);
+}
+
+// Up to DSR_STATS_MAX_ROWS vectors at once, one workgroup each: row r's
+// statistics go to out[3 r] (the sum) and out[3 r + 1 .. 3 r + 2] (the four
+// int32 results).
+struct StatsRows {
+  const double* p[DSR_STATS_MAX_ROWS];
+};
+
+__global__ __launch_bounds__(kThreads) void k_prob_stats_rows(StatsRows r, int64_t n, double* out) {
+  __shared__ GenShared sh;
+  __shared__ NpSumShared np;
+  const int row = blockIdx.x;
+  prob_stats_row(r.p[row], n, out + 3 * row, (int32_t*)(out + 3 * row + 1), sh, np);
 }
 
 // First i with c_i / c_last > u for the sequential running sum c of p
@@ -655,6 +674,18 @@ int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream) {
 int32_t dsr_prob_stats(const double* p, int64_t n, double* out_sum, int32_t* out_i32, void* stream) {
   if (!p || !out_sum || !out_i32 || n < 1 || n > DSR_MAX_VOCAB) return DSR_ERR_ARG;
   hipLaunchKernelGGL(k_prob_stats, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, p, n, out_sum, out_i32);
+  return launched();
+}
+
+int32_t dsr_prob_stats_rows(const double* const* rows, int32_t count, int64_t n, double* out, void* stream) {
+  if (!rows || !out || count < 0 || count > DSR_STATS_MAX_ROWS || n < 1 || n > DSR_MAX_VOCAB) return DSR_ERR_ARG;
+  if (count == 0) return 0;
+  StatsRows r{};
+  for (int i = 0; i < count; ++i) {
+    if (!rows[i]) return DSR_ERR_ARG;
+    r.p[i] = rows[i];
+  }
+  hipLaunchKernelGGL(k_prob_stats_rows, dim3((unsigned)count), dim3(kThreads), 0, (hipStream_t)stream, r, n, out);
   return launched();
 }
 

@@ -19,7 +19,7 @@ arithmetic path: without the HIP library every computing call raises.
 """
 from __future__ import annotations
 
-from dataclasses import asdict, dataclass
+from dataclasses import asdict, dataclass, field
 import hashlib
 import math
 
@@ -94,16 +94,17 @@ class SamplingPolicy:
     def as_dict(self):
         return asdict(self)
 
-    def _device_tensor(self, device):
-        """The policy packed for the kernels on ``device``, made once per
-        device: the policy is immutable.  Copies and pickles leave it out."""
+    def _device_tensor(self, device, rows=1):
+        """The policy packed for the kernels on ``device`` (``rows`` copies,
+        one per row of a launch), made once per device and row count: the
+        policy is immutable.  Copies and pickles leave it out."""
         cache = self.__dict__.get("_packed")
         if cache is None:
             cache = {}
             object.__setattr__(self, "_packed", cache)
-        packed = cache.get(device.index)
+        packed = cache.get((device.index, rows))
         if packed is None:
-            packed = cache[device.index] = batch.policy_tensor([self], device)
+            packed = cache[(device.index, rows)] = batch.policy_tensor([self] * rows, device)
         return packed
 
     def __getstate__(self):
@@ -134,8 +135,9 @@ class SamplingPolicy:
                                  allow_bits=allow, uniforms=uniform, probs="f64")
 
 
-def _bias_table(logit_bias, n):
-    """A validated logit-bias mapping as a one-row device table (sampling.py:69-74)."""
+def _bias_table(logit_bias, n, rows=1):
+    """A validated logit-bias mapping as a device table, the same for each of
+    ``rows`` rows (sampling.py:69-74)."""
     if logit_bias is None:
         return None
     if not isinstance(logit_bias, dict) or len(logit_bias) > n:
@@ -144,7 +146,7 @@ def _bias_table(logit_bias, n):
     for token, value in logit_bias.items():
         integer(token, "biased token", 0, n - 1)
         checked[token] = _real(value, "logit bias", -100, 100)
-    return batch.BiasTable.from_dicts([checked], device=_device())
+    return batch.BiasTable.from_dicts([checked] * rows, device=_device())
 
 
 def _allow_row(allowed, n):
@@ -229,7 +231,7 @@ def _dist_input(values):
         ok = values.ndim == 1 and 1 <= len(values) <= VOCAB and values.dtype == np.float64
     if not ok:
         raise ValidationError(_DIST_MSG)
-    return _on_device(values)[0]
+    return _on_device(values)[0].contiguous()
 
 
 def _dist_checked(t, stats):
@@ -246,20 +248,39 @@ def _distribution(values):
     return _dist_checked(t, batch.prob_stats(t))
 
 
-def _distributions(rows):
+def _token_index(token, n):
+    """``token`` as an index into a vector of ``n``, or None where it is not one
+    (the verifier's own range check reports such tokens later)."""
+    return token if type(token) is int and 0 <= token < n else None
+
+
+def _distributions(rows, tokens=None):
     """``_as_dist`` of every row, with one synchronisation for all the rows
-    that still need their statistics.  Every rejection carries the same
-    message, so checking the shapes first and the values after reports what
-    checking row by row would."""
+    that still need their statistics; with ``tokens`` (one per row), each
+    such row's probability at its token comes back in the same copy.  Every
+    rejection carries the same message, so checking the shapes first and the
+    values after reports what checking row by row would."""
     items = [row if isinstance(row, _Dist) else _dist_input(row) for row in rows]
     pending = [i for i, item in enumerate(items) if not isinstance(item, _Dist)]
     if pending:
-        slots = torch.empty(len(pending), 3, dtype=torch.float64, device=items[pending[0]].device)
+        m = len(pending)
+        buf = torch.empty(4 * m, dtype=torch.float64, device=items[pending[0]].device)  # [m, 3] stats, m values
+        stats = buf[:3 * m].view(m, 3)
+        index = {i: None if tokens is None else _token_index(tokens[i], items[i].numel()) for i in pending}
+        if len({items[i].numel() for i in pending}) == 1:
+            batch.prob_stats_rows_launch([items[i] for i in pending], stats)
+        else:
+            for n, i in enumerate(pending):
+                batch.prob_stats_launch(items[i], stats[n])
         for n, i in enumerate(pending):
-            batch.prob_stats_launch(items[i], slots[n])
-        host = slots.cpu()
+            if index[i] is not None:
+                buf[3 * m + n:3 * m + n + 1].copy_(items[i][index[i]:index[i] + 1])
+        host = buf.cpu()
         for n, i in enumerate(pending):
-            items[i] = _dist_checked(items[i], batch.prob_stats_read(host[n]))
+            d = _dist_checked(items[i], batch.prob_stats_read(host[3 * n:3 * n + 3]))
+            if index[i] is not None:
+                d.at[index[i]] = float(host[3 * m + n])
+            items[i] = d
     return tuple(items)
 
 
@@ -284,6 +305,7 @@ class _Dist:
     positive: int
     first: int
     argmax: int
+    at: dict = field(default_factory=dict)  # {token: probability} read back with the statistics
 
     def __len__(self):
         return self.tensor.numel()
@@ -447,7 +469,7 @@ def verify_drafts(target_rows, proposal_rows, proposal_ids, transaction, *, gree
     integer(output_limit, "remaining output limit", 1, MAX_COUNT)
     if type(greedy) is not bool or len(proposal_rows) != len(proposal_ids) or len(target_rows) != len(proposal_ids) + 1:
         raise ValidationError("target/proposal verification row counts differ")
-    proposals = _distributions(proposal_rows)
+    proposals = _distributions(proposal_rows, proposal_ids)
     first_target = _as_dist(target_rows[0])
     vocabulary = len(first_target)
     if any(len(row) != vocabulary for row in proposals):
@@ -465,7 +487,17 @@ def verify_drafts(target_rows, proposal_rows, proposal_ids, transaction, *, gree
     output = []
     for index, token in enumerate(proposal_ids):
         target, proposal = target_at(index), proposals[index]
-        if greedy:
+        p, q = target.at.get(token), proposal.at.get(token)
+        if p is not None and q is not None:
+            # Both probabilities came back with the rows' statistics: the
+            # reference's own host arithmetic (sampling.py:276-281).
+            if not q > 0.0:
+                raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")
+            if greedy:
+                accepted = token == target.argmax
+            else:
+                accepted = transaction.random("accept") < min(1.0, p / q)
+        elif greedy:
             positive, _ = batch.prob_accept(target.tensor, proposal.tensor, token, 0.0)
             if not positive:
                 raise ValidationError("a proposed token has zero probability under its claimed conditional proposal")

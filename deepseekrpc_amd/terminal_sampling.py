@@ -29,6 +29,7 @@ How it is built here:
 """
 from __future__ import annotations
 
+from concurrent.futures import ThreadPoolExecutor
 from contextlib import contextmanager
 from dataclasses import asdict, dataclass, replace
 import enum
@@ -41,7 +42,7 @@ from . import _native as N
 from . import batch
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
 from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _device,
-                       _dist_checked, _logit_vector, _on_device, _raise_status, verify_drafts)
+                       _dist_checked, _logit_vector, _on_device, _raise_status, _token_index, verify_drafts)
 
 _HISTORY_LIMIT = 1048576
 _MAX_PROPOSALS = 5
@@ -123,6 +124,19 @@ class _Controls:
 def _sha256_i8(values):
     """SHA-256 hex digest of a count vector's little-endian int64 bytes."""
     return hashlib.sha256(np.ascontiguousarray(values, dtype="<i8")).hexdigest()
+
+
+def _count_hashes(counts, generated):
+    """The digest's two count hashes; equal vectors (no separate generated
+    counts) share one."""
+    sha = _sha256_i8(counts)
+    return sha, sha if np.array_equal(counts, generated) else _sha256_i8(generated)
+
+
+# The count hashes (about 0.4 ms per megabyte vector) run on a worker thread
+# from the moment a transaction opens (hashlib and NumPy release the GIL), so
+# that prepared() finds them done.
+_HASHER = ThreadPoolExecutor(max_workers=1, thread_name_prefix="dsr-count-sha")
 
 
 def _valid_count_vector(values, vocabulary):
@@ -231,6 +245,91 @@ class _LazyRows:
         return item
 
 
+class _TargetRows:
+    """The verifier's target rows, all launched at once: row j conditioned on
+    the proposals ``ids[:j]`` (terminal_sampling.py:234-244), then every
+    row's statistics in one launch, with each row's status and its
+    probability at proposal j, read back with one synchronisation when the
+    verifier first asks for a row.  A row's failure, at launch or on the
+    device, is raised when the verifier reaches that row, as the lazily
+    built rows of the reference raise it."""
+
+    def __init__(self, work, rows, ids):
+        n = len(rows)
+        self._rows, self._ids, self._host = [], ids, None
+        # [n, 3] statistics, then n statuses (int32 in a double each), then n probabilities.
+        self._buf = torch.empty(5 * n, dtype=torch.float64, device=rows.device)
+        if not work._needs_history(len(ids)):
+            self._launch_together(work, rows, ids)
+        else:
+            self._launch_each(work, rows, ids)
+
+    def _launch_together(self, work, rows, ids):
+        """No row reads a history table, so the rows are independent: one
+        launch over all of them (a launch-time failure is the same for every
+        row, and the first row reports it)."""
+        n = len(rows)
+        try:
+            result = work._rows_launch(rows)
+        except Exception as exc:
+            self._rows = [exc] * n
+            return
+        self._buf[3 * n:4 * n].view(torch.int32)[0::2].copy_(result.status)
+        for j in range(n):
+            row = result.probs[j]
+            x = _token_index(ids[j], row.numel()) if j < len(ids) else None
+            if x is not None:
+                self._buf[4 * n + j:4 * n + j + 1].copy_(row[x:x + 1])
+            self._rows.append(row)
+        self._stats = self._buf[:3 * n].view(n, 3)
+        batch.prob_stats_rows_launch(self._rows, self._stats)
+
+    def _launch_each(self, work, rows, ids):
+        n = len(rows)
+        launched = []
+        for j in range(n):
+            try:
+                result, _ = work._row_launch(rows[j], ids[:j])
+            except Exception as exc:
+                self._rows.append(exc)
+                continue
+            row = result.probs[0]
+            self._buf[3 * n + j:3 * n + j + 1].view(torch.int32)[0:1].copy_(result.status)
+            x = _token_index(ids[j], row.numel()) if j < len(ids) else None
+            if x is not None:
+                self._buf[4 * n + j:4 * n + j + 1].copy_(row[x:x + 1])
+            self._rows.append(row)
+            launched.append(j)
+        self._stats = self._buf[:3 * n].view(n, 3)
+        if launched:
+            # The rows that launched fill their own slots (a failed row's slot stays unread).
+            lo = launched[0]
+            if launched == list(range(lo, lo + len(launched))):
+                batch.prob_stats_rows_launch([self._rows[j] for j in launched], self._stats[lo:lo + len(launched)])
+            else:
+                for j in launched:
+                    batch.prob_stats_launch(self._rows[j], self._stats[j])
+
+    def __len__(self):
+        return len(self._rows)
+
+    def __getitem__(self, j):
+        if self._host is None:
+            self._host = self._buf.cpu()
+        n = len(self._rows)
+        row = self._rows[j]
+        if isinstance(row, Exception):
+            raise row
+        code = int(self._host[3 * n + j:3 * n + j + 1].view(torch.int32)[0])
+        if code != N.OK:
+            _raise_status(code)
+        dist = _dist_checked(row, batch.prob_stats_read(self._host[3 * j:3 * j + 3]))
+        x = _token_index(self._ids[j], row.numel()) if j < len(self._ids) else None
+        if x is not None:
+            dist.at[x] = float(self._host[4 * n + j])
+        return dist
+
+
 class SamplingWork:
     """One open sampling transaction of a ``TerminalSampler``."""
 
@@ -243,7 +342,8 @@ class SamplingWork:
         self.decision = None
         self.proposal_ids, self.proposal_rows = [], []
         self._device_history = None   # the counts as a device table, built for the first row
-        self._counts_sha = None       # SHA-256 of the frozen count vectors, for the digest
+        # SHA-256 of the frozen count vectors, for the digest: a future until prepared() reads it.
+        self._counts_sha = _HASHER.submit(_count_hashes, controls.counts, controls.generated)
 
     # -- the frozen controls, under the reference's attribute names --------
     policy = property(lambda self: self._controls.policy)
@@ -323,6 +423,17 @@ class SamplingWork:
         p, total = self.policy, self._controls.total
         return (p.repetition_penalty != 1 or p.presence_penalty != 0 or p.frequency_penalty != 0
                 or total is None or total + grown > _HISTORY_LIMIT)
+
+    def _rows_launch(self, rows):
+        """All the verifier's target rows in one launch, for rows that read no
+        history table and no grammar mask (``_row_launch``'s checks, which
+        are the same for every row)."""
+        size, _ = _logit_vector(rows[0])
+        if size != len(self.counts):
+            raise ValidationError(_COUNTS_MSG)
+        n = len(rows)
+        bias = _bias_table(self.logit_bias, size, rows=n)
+        return batch.sample_rows(rows, self.policy._device_tensor(rows.device, rows=n), bias=bias, probs="f64")
 
     def _row_launch(self, logits, prefix, uniform=None):
         """Validate one row and launch its distribution (and draw, given a
@@ -468,7 +579,11 @@ class SamplingWork:
         with self._aborting_on_error():
             rows = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
             ids = list(self.proposal_ids)
-            targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
+            if self.allowed is None:
+                targets = _TargetRows(self, rows, ids)
+            else:
+                # A grammar is asked for the masks of the prefixes the verifier reaches only.
+                targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
             self._decide(verify_drafts(targets, self.proposal_rows, ids, self.transaction,
                                        greedy=self.policy.temperature == 0, output_limit=self.remaining,
                                        eos_ids=self.eos_ids))
@@ -477,13 +592,10 @@ class SamplingWork:
     def _digest_record(self):
         """The fields the decision digest covers (terminal_sampling.py:189-196).
         The two count hashes cover the transaction's frozen copies, so they
-        are computed once per transaction (prepared() runs at prepare and
-        again at commit)."""
-        if self._counts_sha is None:
-            counts, generated = self.counts, self.generated_counts
-            sha = _sha256_i8(counts)
-            # Equal vectors (no separate generated counts) share one hash.
-            self._counts_sha = (sha, sha if np.array_equal(counts, generated) else _sha256_i8(generated))
+        are computed once per transaction, from its opening on (prepared()
+        runs at prepare and again at commit)."""
+        if not isinstance(self._counts_sha, tuple):
+            self._counts_sha = self._counts_sha.result()
         decision = asdict(self.decision)
         return {
             "decision": decision, "accepted_target_rows": self.decision.accepted_target_rows,

@@ -39,6 +39,7 @@ extern "C" {
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
 #define DSR_MAX_APPEND 16384        /* new tokens per row in one dsr_history_append call */
+#define DSR_STATS_MAX_ROWS 16       /* vectors per dsr_prob_stats_rows call */
 
 /* Logit element types. */
 #define DSR_BF16 1
@@ -325,6 +326,14 @@ int32_t dsr_verify_drafts_head(const dsr_verify_args_t* args, const dsr_head_par
  *   positive entries, out_i32[2] = first positive index, out_i32[3] = first
  *   index of the maximum (np.argmax). */
 int32_t dsr_prob_stats(const double* p, int64_t n, double* out_sum, int32_t* out_i32, void* stream);
+
+/* dsr_prob_stats of `count` <= DSR_STATS_MAX_ROWS float64 vectors of length n
+ * in one launch (one workgroup each), for the verifier's rows
+ * (sampling.py:109-115 applied to every target and proposal row).  `rows`
+ * is a host array of `count` device pointers; `out` is a device float64
+ * array [count, 3]: row r's sum at out[3 r], then its four int32 results
+ * (as dsr_prob_stats's out_i32) in the next 16 bytes. */
+int32_t dsr_prob_stats_rows(const double* const* rows, int32_t count, int64_t n, double* out, void* stream);
 
 /* dsr_prob_categorical (sampling.py:126-128): first i with
  * cumsum(p)[i] / sum(p) > u.  out_i32[0] = token, out_i32[1] = flags. */

@@ -50,6 +50,35 @@ def test_stats_sum_is_numpy_sum_bit_for_bit(n):
         assert first == (int(pos[0]) if len(pos) else -1) and argmax == int(np.argmax(p))
 
 
+def test_batched_stats_equal_the_one_row_kernel():
+    """dsr_prob_stats_rows (one launch for the verifier's rows) gives every
+    row what dsr_prob_stats gives it: 20 rows (two launches) with valid,
+    off-sum, negative, NaN, sparse and single-positive rows."""
+    rng = np.random.default_rng(21)
+    rows = []
+    for k in range(20):
+        p = softmax_row(rng, zeros=0.3 if k % 3 == 0 else 0.0)
+        if k == 4:
+            p *= 1.0 + 2e-10
+        if k == 7:
+            p[99] = -1e-3
+        if k == 11:
+            p[5] = np.nan
+        if k == 13:
+            p[:] = 0.0
+            p[1234] = 1.0
+        rows.append(dev(p))
+    out = torch.empty(len(rows), 3, dtype=torch.float64, device=DEV)
+    batch.prob_stats_rows_launch(rows, out)
+    host = out.cpu()
+    for k, r in enumerate(rows):
+        got = batch.prob_stats_read(host[k])
+        want = batch.prob_stats(r)
+        assert (got[0] == want[0] or (math.isnan(got[0]) and math.isnan(want[0]))) and got[1:] == want[1:], k
+    assert not batch.prob_stats_read(host[7])[1] and not batch.prob_stats_read(host[11])[1]
+    assert batch.prob_stats_read(host[13])[2:4] == (1, 1234)
+
+
 @pytest.mark.parametrize("offset", [0.9e-10, -0.9e-10, 1.1e-10, -1.1e-10, 0.0])
 def test_sum_tolerance_decides_as_the_oracle(offset):
     rng = np.random.default_rng(abs(hash(offset)) % 1000)

@@ -45,7 +45,7 @@ def test_flag_and_status_constants_match_header():
     for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
                  "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
                  "E_GENERATED", "E_HISTORY", "E_APPEND", "E_HINT", "MAX_APPEND", "HINT_WHOLE_SOME", "HINT_WHOLE_ALL",
-                 "HINT_VERIFY_FAST", "HEAD_TILE", "HEAD_MAX_ROWS"):
+                 "HINT_VERIFY_FAST", "HEAD_TILE", "HEAD_MAX_ROWS", "STATS_MAX_ROWS"):
         assert getattr(N, name) == defs["DSR_" + name], name
     assert N.ABI_VERSION == defs["DSR_ABI_VERSION"]
 
@@ -85,6 +85,12 @@ def test_argument_errors_return_before_any_launch():
     h.policy, h.rows_per_policy = fake16, 0
     assert lib.dsr_vocab_head(ctypes.byref(h), None) == -1
     assert lib.dsr_prob_stats(None, 3, None, None, None) == -1
+    ptrs = (ctypes.c_void_p * 17)(*([4096] * 17))
+    assert lib.dsr_prob_stats_rows(ptrs, 17, 8, ctypes.c_void_p(4096), None) == -1   # more rows than one launch takes
+    assert lib.dsr_prob_stats_rows(None, 2, 8, ctypes.c_void_p(4096), None) == -1
+    assert lib.dsr_prob_stats_rows(ptrs, 2, 0, ctypes.c_void_p(4096), None) == -1
+    ptrs[1] = None
+    assert lib.dsr_prob_stats_rows(ptrs, 2, 8, ctypes.c_void_p(4096), None) == -1
     assert lib.dsr_prob_categorical(None, 3, 0.5, None, None) == -1
     # History builders: null inputs, vocabularies out of range, ld below the
     # vocabulary, a capacity without output arrays, a table without its ids.
