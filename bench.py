@@ -62,8 +62,8 @@ WORKLOADS = {
     "whole": ("sampled rows/sec at B=256×V=129,280 bf16 with no top-k (default / top-p / min-p policies)", "rows/s",
               5, "k_sample_bf16_full"),
     "step": ("drop-in speculative steps/sec: propose 5 rows on the device, verify against 6 fp32 rows, digest",
-             "steps/s", 30, "k_split_select + k_split_finish (proposals and targets) + k_prob_stats / "
-             "k_prob_accept / k_prob_correction / k_prob_categorical"),
+             "steps/s", 30, "k_split_select + k_split_finish (proposals; the six targets in one launch) + "
+             "k_prob_stats_rows + k_prob_correction / k_prob_stats / k_prob_categorical (a rejection's draw)"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
              300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
     "head": ("verify-rows/sec with the vocabulary projection: B=32 requests × K=4 drafts, 160 target rows × "
