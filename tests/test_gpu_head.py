@@ -5,14 +5,15 @@ The terminal stage computes logits = lm_head(norm(hidden)) in FP32, checks
 torch.isfinite(logits).all() and verifies the drafts against those rows
 (stage_graph.py:356-362 and :396, terminal_sampling.py:170-183).  Here:
 
-- the logits equal a float64 product of the same bf16 inputs, and torch's
-  FP32 matmul on the GPU, within the FP32 accumulation bound
-  (dim / 16 + 16) * 2^-24 * sum_k |x_k w_k|: the kernel adds dim / 16 matrix
-  core partial sums of 16 exact bf16 products into one FP32 accumulator;
-- every (row, 128-column tile) record equals the same quantities computed in
-  float64 from the kernel's own logits: the maximum and the first column
-  holding it bit for bit, the NaN / +inf / finite / -inf flags exactly, the
-  exp sum within 1e-12 relative;
+- the logits equal the oracle's float64 product of the same bf16 inputs
+  (oracle/head_oracle.py ``project``), and torch's FP32 matmul on the GPU,
+  within the FP32 accumulation bound (dim / 16 + 16) * 2^-24 * sum_k |x_k w_k|:
+  the kernel adds dim / 16 matrix core partial sums of 16 exact bf16 products
+  into one FP32 accumulator;
+- every (row, 128-column tile) record equals the oracle's ``records`` of the
+  kernel's own logits: the maximum and the first column holding it bit for
+  bit, the NaN / +inf / finite / -inf flags exactly, the exp sum within 1e-12
+  relative;
 - verifier decisions read from the records equal, field for field, those of
   the verifier that reads the logits, and the oracle's on the same FP32 rows
   (a decision may differ only where the oracle's own margin is below 1e-11).
@@ -25,6 +26,7 @@ import torch
 
 from deepseekrpc_amd import _native as N
 from deepseekrpc_amd import batch
+from oracle import head_oracle as H
 from oracle import sampling_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -44,12 +46,9 @@ def head_inputs(seed, rows, dim, vocab, scale=2.0):
 
 
 def check_logits(x, w, got, cols=None):
-    """``got`` [rows, vocab] (host float32) against the float64 product, on
-    the columns ``cols`` (all when None)."""
-    xd = x.double().numpy()
-    wd = w.double().numpy() if cols is None else w[cols].double().numpy()
-    want = xd @ wd.T
-    scale = np.abs(xd) @ np.abs(wd).T
+    """``got`` [rows, vocab] (host float32) against the oracle's float64
+    product, on the columns ``cols`` (all when None)."""
+    want, scale = H.project(x.float().numpy(), (w if cols is None else w[cols]).float().numpy())
     g = got.astype(np.float64) if cols is None else got[:, cols].astype(np.float64)
     tol = (x.shape[1] // 16 + 16) * 2.0 ** -24 * scale + 1e-30
     err = np.abs(g - want)
@@ -92,28 +91,9 @@ def test_full_vocabulary_logits_at_the_terminal_stage_width():
 
 
 def record_reference(logits, temps):
-    """Float64 records from FP32 logits [rows, vocab]: (sum, max, info)."""
-    rows, vocab = logits.shape
-    tiles = vocab // TILE
-    v = logits.reshape(rows, tiles, TILE)
-    nan = np.isnan(v)
-    mx = np.where(nan, -np.inf, v).max(axis=2).astype(np.float32)
-    flags = (np.any(nan | (v == np.inf), axis=2) * 1 | np.any(np.isfinite(v), axis=2) * 2
-             | np.any(v == -np.inf, axis=2) * 4)
-    hit = v == mx[..., None]
-    first = np.where(hit.any(axis=2), hit.argmax(axis=2), 0xFFFFFF)
-    info = (flags | (first << 8)).astype(np.uint32).view(np.int32)  # the record's int32 bits
-    sums = np.zeros((rows, tiles))
-    for r in range(rows):
-        T = temps[r]
-        if not (0 < T <= 100):
-            continue
-        for t in range(tiles):
-            m = float(mx[r, t])
-            if np.isfinite(m):
-                with np.errstate(invalid="ignore"):
-                    e = np.exp((v[r, t].astype(np.float64) - m) / T)
-                sums[r, t] = np.sum(np.where(np.isnan(e), 0.0, e))
+    """The oracle's records as the kernel stores them: (sum, max, info)."""
+    sums, mx, first, flags = H.records(logits, temps, tile=TILE)
+    info = (flags | (np.where(first >= 0, first, 0xFFFFFF) << 8)).astype(np.uint32).view(np.int32)
     return sums, mx, info
 
 
