@@ -133,9 +133,10 @@ def _count_hashes(counts, generated):
     return sha, sha if np.array_equal(counts, generated) else _sha256_i8(generated)
 
 
-# The count hashes (about 0.4 ms per megabyte vector) run on a worker thread
-# from the moment a transaction opens (hashlib and NumPy release the GIL), so
-# that prepared() finds them done.
+# The count hashes (about 0.4 ms per megabyte vector) of a verification run on
+# a worker thread while its target rows are on the device (hashlib and NumPy
+# release the GIL), so that prepared() finds them done; other transactions
+# hash at prepared().
 _HASHER = ThreadPoolExecutor(max_workers=1, thread_name_prefix="dsr-count-sha")
 
 
@@ -342,8 +343,9 @@ class SamplingWork:
         self.decision = None
         self.proposal_ids, self.proposal_rows = [], []
         self._device_history = None   # the counts as a device table, built for the first row
-        # SHA-256 of the frozen count vectors, for the digest: a future until prepared() reads it.
-        self._counts_sha = _HASHER.submit(_count_hashes, controls.counts, controls.generated)
+        # SHA-256 of the frozen count vectors, for the digest (a future while a
+        # worker thread computes it).
+        self._counts_sha = None
 
     # -- the frozen controls, under the reference's attribute names --------
     policy = property(lambda self: self._controls.policy)
@@ -581,6 +583,8 @@ class SamplingWork:
             ids = list(self.proposal_ids)
             if self.allowed is None:
                 targets = _TargetRows(self, rows, ids)
+                if self._counts_sha is None:   # the digest's hashes, while the rows are on the device
+                    self._counts_sha = _HASHER.submit(_count_hashes, self.counts, self.generated_counts)
             else:
                 # A grammar is asked for the masks of the prefixes the verifier reaches only.
                 targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
@@ -592,9 +596,11 @@ class SamplingWork:
     def _digest_record(self):
         """The fields the decision digest covers (terminal_sampling.py:189-196).
         The two count hashes cover the transaction's frozen copies, so they
-        are computed once per transaction, from its opening on (prepared()
-        runs at prepare and again at commit)."""
-        if not isinstance(self._counts_sha, tuple):
+        are computed once per transaction (prepared() runs at prepare and
+        again at commit)."""
+        if self._counts_sha is None:
+            self._counts_sha = _count_hashes(self.counts, self.generated_counts)
+        elif not isinstance(self._counts_sha, tuple):
             self._counts_sha = self._counts_sha.result()
         decision = asdict(self.decision)
         return {
