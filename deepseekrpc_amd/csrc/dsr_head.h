@@ -38,7 +38,7 @@ constexpr int kHeadTile = DSR_HEAD_TILE;        // vocabulary columns per workgr
 constexpr int kHeadChunk = 64;                  // dim per LDS stage
 constexpr int kHeadDimStep = 4 * kHeadChunk;    // dim is a multiple of this (the main loop's unrolling)
 constexpr int kHeadStride = 72;                 // bf16 per staged hidden row: 144 B, rows 36 banks apart
-constexpr int kHeadMaxBlocks = DSR_HEAD_MAX_ROWS / 32;
+static_assert(DSR_HEAD_MAX_ROWS == 8 * 32, "the dispatch instantiates one to eight 32-row blocks");
 static_assert(kHeadTile == 4 * 32, "four waves of 32 columns");
 
 template <int N> using HeadSlot = std::integral_constant<int, N>;
