@@ -54,10 +54,10 @@ def test_workspace_queries():
     lib = N.load()
     assert lib.dsr_sample_workspace_bytes(256, 129280) == 256 * 129280 * 8
     assert lib.dsr_sample_workspace_bytes(1, 3) == 32 * 8
-    # float64 rows + per-distribution info, statistics and 32 share partials,
+    # float64 rows + per-distribution info, statistics and 16 share partials,
     # 32 draw partials, 2,048 draw block sums and one 64-byte decision per request.
     rows, slots = 32, 9
-    expect = (rows * slots * 129280 * 8 + rows * slots * 16 + rows * slots * 32 + rows * slots * 32 * 32
+    expect = (rows * slots * 129280 * 8 + rows * slots * 16 + rows * slots * 32 + rows * slots * 16 * 32
               + rows * 32 * 32 + rows * 2048 * 8 + rows * 64)
     assert lib.dsr_verify_workspace_bytes(rows, 4, 129280) == expect
 
