@@ -903,21 +903,32 @@ struct DrawWeights {
   }
 };
 
-__device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row,
-                                                    const Decision& d, const double* etab) {
+// From the statistics (M, s1) of the target row at the draw (p) and of the
+// matching proposal row (q, read only for a replacement).
+__device__ __forceinline__ DrawWeights draw_weights_of(const dsr_verify_args_t& a, int64_t row, const Decision& d,
+                                                       double T, double Mp, double sp, double Mq, double sq,
+                                                       const double* etab) {
   const int K = a.K;
-  const VerifyStat* st = L.stat + row * L.slots;
-  const double c1 = exp_scale(a.policy[row].temperature);
+  const double c1 = exp_scale(T);
   DrawWeights w;
   w.resid = d.next == 1;
   w.P = verify_logits(a, row, d.draw_j);
   w.Q = w.resid ? verify_logits(a, row, K + 1 + d.draw_j) : nullptr;
   w.dt = a.dtype;
-  w.isp = 1.0 / st[d.draw_j].s1;
-  w.isq = w.resid ? 1.0 / st[K + 1 + d.draw_j].s1 : 0.0;
-  w.ep = ExpTerm{st[d.draw_j].M, c1, etab};
-  w.eq = ExpTerm{w.resid ? st[K + 1 + d.draw_j].M : 0.0, c1, etab};
+  w.isp = 1.0 / sp;
+  w.isq = w.resid ? 1.0 / sq : 0.0;
+  w.ep = ExpTerm{Mp, c1, etab};
+  w.eq = ExpTerm{w.resid ? Mq : 0.0, c1, etab};
   return w;
+}
+
+__device__ __forceinline__ DrawWeights draw_weights(const dsr_verify_args_t& a, const VerifyLayout& L, int64_t row,
+                                                    const Decision& d, const double* etab) {
+  const VerifyStat* st = L.stat + row * L.slots;
+  const bool resid = d.next == 1;
+  const int jq = a.K + 1 + d.draw_j;
+  return draw_weights_of(a, row, d, a.policy[row].temperature, st[d.draw_j].M, st[d.draw_j].s1,
+                         resid ? st[jq].M : 0.0, resid ? st[jq].s1 : 1.0, etab);
 }
 
 // The 64-token block of share `owner` that holds the crossing of thr: one
@@ -1036,7 +1047,6 @@ __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t 
   __shared__ double etab[64];
   __shared__ double sf[kStatWaves];
   __shared__ long long si[2][kStatWaves];
-  __shared__ Decision sd;
   using X = typename LogitT<DT>::T;
   constexpr int kElt = DT == DSR_BF16 ? 2 : (int)sizeof(X);
   constexpr int W = 16 / kElt;       // tokens per 16-byte group
@@ -1045,15 +1055,24 @@ __global__ __launch_bounds__(kStatThreads) void k_verify_draw(dsr_verify_args_t 
   static_assert(NQ * W == kDrawPer && LB * W == 64, "groups tile the lane's tokens and the blocks");
   const int64_t row = blockIdx.x / kDrawSplit;
   const int g = (int)(blockIdx.x % kDrawSplit);
-  if (!verify_fast_row(a, L, row)) return;
-  const int status = L.dec[row].status, next = L.dec[row].next;
-  if (status != DSR_OK || next == 0) return;
-  exp_table_init(etab);
-  if (threadIdx.x == 0) sd = L.dec[row];
-  __syncthreads();
-  const DrawWeights wf = draw_weights(a, L, row, sd, etab);
-  const int64_t V = a.vocab;
   const int l = lane_id(), w = wave_id();
+  // The decision and the statistics of every distribution of the request
+  // (lane s: distribution s) in one round trip; the draw's rows are picked
+  // from them once the decision has arrived.
+  const bool fast = verify_fast_row(a, L, row);
+  const Decision d0 = L.dec[row];
+  VerifyStat vs;
+  vs.M = 0.0;
+  vs.s1 = 1.0;
+  if (l < (int)L.slots) vs = L.stat[row * L.slots + l];
+  exp_table_init(etab);
+  if (!fast || d0.status != DSR_OK || d0.next == 0) return;  // uniform over the workgroup
+  __syncthreads();
+  const int jq = a.K + 1 + d0.draw_j;
+  const DrawWeights wf =
+      draw_weights_of(a, row, d0, policy_of(a, row).temperature, __shfl(vs.M, d0.draw_j), __shfl(vs.s1, d0.draw_j),
+                      __shfl(vs.M, jq), d0.next == 1 ? __shfl(vs.s1, jq) : 1.0, etab);
+  const int64_t V = a.vocab;
   const int64_t wbase = (int64_t)g * (kDrawBlocks * 64) + (int64_t)w * 1024;  // this wave's first token
   auto token = [&](int q, int e) { return wbase + (int64_t)(64 * q + l) * W + e; };
   X pv[kDrawPer], qv[kDrawPer];
