@@ -34,6 +34,7 @@ from contextlib import contextmanager
 from dataclasses import asdict, dataclass, replace
 import enum
 import hashlib
+import os
 
 import numpy as np
 import torch
@@ -136,8 +137,18 @@ def _count_hashes(counts, generated):
 # The count hashes (about 0.4 ms per megabyte vector) of a verification run on
 # a worker thread while its target rows are on the device (hashlib and NumPy
 # release the GIL), so that prepared() finds them done; other transactions
-# hash at prepared().
-_HASHER = ThreadPoolExecutor(max_workers=1, thread_name_prefix="dsr-count-sha")
+# hash at prepared().  One worker per process: a forked child makes its own
+# (an executor inherited over fork has no thread to run its work).
+_hasher = None
+_hasher_pid = None
+
+
+def _hash_worker():
+    global _hasher, _hasher_pid
+    if _hasher is None or _hasher_pid != os.getpid():
+        _hasher = ThreadPoolExecutor(max_workers=1, thread_name_prefix="dsr-count-sha")
+        _hasher_pid = os.getpid()
+    return _hasher
 
 
 def _valid_count_vector(values, vocabulary):
@@ -584,7 +595,7 @@ class SamplingWork:
             if self.allowed is None:
                 targets = _TargetRows(self, rows, ids)
                 if self._counts_sha is None:   # the digest's hashes, while the rows are on the device
-                    self._counts_sha = _HASHER.submit(_count_hashes, self.counts, self.generated_counts)
+                    self._counts_sha = _hash_worker().submit(_count_hashes, self.counts, self.generated_counts)
             else:
                 # A grammar is asked for the masks of the prefixes the verifier reaches only.
                 targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))

@@ -150,3 +150,25 @@ def test_verify_hint_needs_filter_free_policies_and_plain_inputs():
     assert batch.verify_hints(arr, 129280, False) == 0
     for bad in (dict(top_k=50), dict(top_p=0.9), dict(min_p=0.1)):
         assert batch.verify_hints(batch.policy_array([dict(), bad]), 129280, True) == 0
+
+
+def _hash_in_child(q):
+    from deepseekrpc_amd import terminal_sampling as T
+    c = np.arange(5, dtype=np.int64)
+    q.put(T._hash_worker().submit(T._count_hashes, c, c).result(timeout=20)[0])
+
+
+def test_count_hash_worker_runs_in_a_forked_child():
+    """The digest's hash worker is per process: a child forked after the
+    parent used it still gets its hashes."""
+    import multiprocessing as mp
+    from deepseekrpc_amd import terminal_sampling as T
+    c = np.arange(5, dtype=np.int64)
+    want = T._hash_worker().submit(T._count_hashes, c, c).result(timeout=20)[0]
+    ctx = mp.get_context("fork")
+    q = ctx.Queue()
+    p = ctx.Process(target=_hash_in_child, args=(q,))
+    p.start()
+    got = q.get(timeout=30)
+    p.join(timeout=30)
+    assert p.exitcode == 0 and got == want == T._sha256_i8(c)
