@@ -67,6 +67,16 @@ def policy_array(policies) -> np.ndarray:
     return out
 
 
+def _policy_arg(policies, dev) -> torch.Tensor:
+    """Packed policies on ``dev``: a list or array is packed here; a tensor
+    must be a contiguous uint8 tensor on ``dev``, as ``policy_tensor`` makes
+    (the kernels read it through a device pointer)."""
+    t = policies if isinstance(policies, torch.Tensor) else policy_tensor(policies, dev)
+    if not t.is_cuda or t.device != dev or t.dtype != torch.uint8 or not t.is_contiguous():
+        raise ValueError("a policy tensor must be a contiguous uint8 tensor on the call's device (policy_tensor)")
+    return t
+
+
 def policy_tensor(policies, device) -> torch.Tensor:
     """The packed policies on ``device``; the tensor keeps its host copy as
     ``dsr_policies``, from which ``sample_rows`` and ``verify_drafts`` derive
@@ -393,8 +403,7 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         raise ValueError("logits must be a [rows, V] bf16/f32/f64 tensor")
     rows, V = logits.shape
     dev = logits.device
-    if not isinstance(policies, torch.Tensor):
-        policies = policy_tensor(policies, dev)
+    policies = _policy_arg(policies, dev)
     if policies.numel() != rows * POLICY_DTYPE.itemsize:
         raise ValueError("one policy per row is required")
     out = dict(out or {})
@@ -617,7 +626,9 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
     _require(rng_state, "rng_state", torch.int64, 4)
     _require(seed_token, "seed_token", torch.int32, 1)
     dev = rng_state.device
-    pol = policy if isinstance(policy, torch.Tensor) else policy_tensor([policy], dev)
+    pol = _policy_arg(policy if isinstance(policy, torch.Tensor) else [policy], dev)
+    if pol.numel() != POLICY_DTYPE.itemsize:
+        raise ValueError("one policy is required")
     tokens = torch.empty(steps, dtype=torch.int32, device=dev)
     rows = torch.empty(steps, vocab, dtype=torch.float64, device=dev)
     consumed = torch.empty(steps, dtype=torch.uint8, device=dev)
@@ -746,8 +757,9 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     _require(output_limit, "output_limit", torch.int32, rows)
     if target.dtype not in _DTYPES:
         raise ValueError("target must be bf16/f32/f64")
-    if not isinstance(policies, torch.Tensor):
-        policies = policy_tensor(policies, dev)
+    policies = _policy_arg(policies, dev)
+    if policies.numel() != rows * POLICY_DTYPE.itemsize:
+        raise ValueError("one policy per request is required")
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     res = VerifyResult(i32(rows), i32(rows, K + 1), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows),
                        torch.empty(rows, dtype=torch.uint8, device=dev))
@@ -906,7 +918,7 @@ def vocab_head(hidden: torch.Tensor, weight: torch.Tensor, *, policies=None, row
     if policies is not None:
         if rows_per_policy < 1:
             raise ValueError("rows_per_policy must be >= 1")
-        pol = policies if isinstance(policies, torch.Tensor) else policy_tensor(policies, dev)
+        pol = _policy_arg(policies, dev)
         if pol.numel() * pol.element_size() < -(-rows // rows_per_policy) * ctypes.sizeof(N.Policy):
             raise ValueError("policies must cover every row")
     if out is None:

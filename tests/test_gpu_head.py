@@ -222,3 +222,23 @@ def test_head_arguments_are_checked_before_any_launch():
     assert lib.dsr_vocab_head(ctypes.byref(a), None) == 0   # the same call, valid
     torch.cuda.synchronize()
     check_logits(x, w, out.cpu().numpy())
+
+
+def test_policy_tensors_off_the_device_are_refused():
+    """A policy tensor the kernels cannot read (host memory, another dtype,
+    a strided view) is refused before any launch, by every entry that takes one."""
+    x, w = head_inputs(1, 4, 256, 512)
+    xd, wd = x.to(DEV), w.to(DEV)
+    pols = [dict(temperature=1.0)] * 4
+    host = batch.policy_tensor(pols, "cpu")
+    dev = batch.policy_tensor(pols, DEV)
+    for bad in (host, dev.to(torch.int32), dev.view(4, -1)[:, ::2]):
+        with pytest.raises(ValueError):
+            batch.vocab_head(xd, wd, policies=bad)
+        with pytest.raises(ValueError):
+            batch.sample_rows(torch.zeros(4, 512, dtype=torch.float32, device=DEV), bad,
+                              uniforms=torch.full((4,), 0.5, dtype=torch.float64, device=DEV))
+    one = batch.policy_tensor([dict(temperature=1.0)] * 2, DEV)
+    with pytest.raises(ValueError):   # two policies for four rows
+        batch.sample_rows(torch.zeros(4, 512, dtype=torch.float32, device=DEV), one,
+                          uniforms=torch.full((4,), 0.5, dtype=torch.float64, device=DEV))
