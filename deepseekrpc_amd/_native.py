@@ -33,6 +33,7 @@ E_HISTORY = 13
 E_APPEND = 14
 E_HINT = 15
 MAX_APPEND = 16384
+MAX_VOCAB = 129280
 
 FLAG_MARGIN = 1
 FLAG_GENERAL = 2

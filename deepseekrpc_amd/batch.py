@@ -12,8 +12,9 @@ streams advance exactly as the reference's would.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+import collections
 import ctypes
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -113,13 +114,26 @@ def _policy_hints(policies, vocab: int) -> int:
     return hints
 
 
+def policies_in_bounds(arr: np.ndarray) -> np.ndarray:
+    """Per packed policy: the bounds of SamplingPolicy (sampling.py:38-43) as
+    the kernels test them (NaN fails every comparison)."""
+    return ((arr["temperature"] >= 0.0) & (arr["temperature"] <= 100.0) & (arr["top_p"] >= 0.0) & (arr["top_p"] <= 1.0)
+            & (arr["min_p"] >= 0.0) & (arr["min_p"] <= 1.0) & (arr["repetition_penalty"] >= 0.01)
+            & (arr["repetition_penalty"] <= 100.0) & (arr["presence_penalty"] >= -2.0)
+            & (arr["presence_penalty"] <= 2.0) & (arr["frequency_penalty"] >= -2.0)
+            & (arr["frequency_penalty"] <= 2.0) & (arr["top_k"] >= 0) & (arr["top_k"] <= N.MAX_VOCAB)
+            & (arr["reserved"] == 0))
+
+
 def verify_hints(arr: np.ndarray | None, vocab: int, plain: bool) -> int:
-    """DSR_HINT_VERIFY_FAST when every request's policy has no filter and the
-    call carries no history, bias or allow mask (``plain``)."""
+    """DSR_HINT_VERIFY_FAST when every request's policy is in bounds and has
+    no filter, and the call carries no history, bias or allow mask
+    (``plain``).  A request whose policy is out of bounds leaves the bit
+    off, so its distributions are built and it reports its policy error."""
     if arr is None or len(arr) == 0 or not plain:
         return 0
     k = arr["top_k"]
-    ok = ((k == 0) | (k >= vocab)) & (arr["top_p"] >= 1.0) & (arr["min_p"] == 0.0)
+    ok = ((k == 0) | (k >= vocab)) & (arr["top_p"] >= 1.0) & (arr["min_p"] == 0.0) & policies_in_bounds(arr)
     return N.HINT_VERIFY_FAST if ok.all() else 0
 
 
@@ -354,10 +368,13 @@ class Workspace:
     One buffer per (device, stream): calls on different streams never share
     scratch memory.  A buffer is allocated while its stream is current, so
     torch's caching allocator orders its reuse after that stream's work when
-    it is replaced by a larger one."""
+    it is replaced by a larger one or dropped.  At most ``streams`` buffers
+    are kept, the least recently used dropped first, so a caller that makes
+    a stream per request does not hold scratch for every stream it used."""
 
-    def __init__(self):
-        self._bufs = {}
+    def __init__(self, streams: int = 4):
+        self._bufs = collections.OrderedDict()
+        self._limit = max(1, int(streams))
 
     def get(self, nbytes: int, device, stream=None) -> torch.Tensor:
         device = torch.device(device)
@@ -368,7 +385,12 @@ class Workspace:
         key = (device.index, stream.cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = self._bufs[key] = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        self._bufs.move_to_end(key)
+        while len(self._bufs) > self._limit:
+            self._bufs.popitem(last=False)
         return buf
 
 
@@ -599,6 +621,10 @@ class Proposals:
     logits: torch.Tensor      # float32 [steps, V]: each row's logits as sampled, checked for finiteness at the end
     states: torch.Tensor      # int64 [steps + 1, 4]: PCG64 state before row 0 and after each row
     keep: tuple = ()
+    # (position, exception) when row_logits failed for a row after the
+    # first: the chain stops there, and the error counts only if no stop
+    # token comes before that row.
+    deferred: tuple | None = None
 
 
 def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_state: torch.Tensor, *,
@@ -640,11 +666,21 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
     seen = torch.empty(steps, vocab, dtype=torch.float32, device=dev)
     keep, appended = [pol, bounds, flags], []
     table, previous = history, seed_token
+    made, deferred = steps, None
     for j in range(steps):
-        logits = row_logits(j, previous)
-        if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
-                and logits.numel() == vocab):
-            raise ValueError("row_logits must return FP32 device logits of the vocabulary")
+        try:
+            logits = row_logits(j, previous)
+            if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
+                    and logits.numel() == vocab):
+                raise ValueError("row_logits must return FP32 device logits of the vocabulary")
+        except Exception as exc:
+            # Row 0 is always kept.  A later row may lie past a stop token,
+            # where the reference never asks for it: its error waits for the
+            # synchronisation that knows.
+            if j == 0:
+                raise
+            made, deferred = j, (j, exc)
+            break
         logits = logits.reshape(1, vocab).contiguous()
         seen[j].copy_(logits[0])
         if j > 0 and grow:
@@ -662,8 +698,9 @@ def propose_rows(row_logits, seed_token: torch.Tensor, steps: int, policy, rng_s
         # A failed row writes token -1; the chain is rejected at its end, but
         # the caller's bias step and the history only ever see a valid id.
         previous = torch.clamp(tokens[j:j + 1], min=0)
-    states[steps].copy_(rng_state.reshape(4))
-    return Proposals(tokens, rows, consumed, status, tuple(appended), seen, states, tuple(keep))
+    states[made].copy_(rng_state.reshape(4))
+    return Proposals(tokens[:made], rows[:made], consumed[:made], status[:made], tuple(appended), seen[:made],
+                     states[:made + 1], tuple(keep), deferred)
 
 
 def finish_proposals(p: Proposals, eos_ids=()):
@@ -672,20 +709,22 @@ def finish_proposals(p: Proposals, eos_ids=()):
     of ``draft`` draws they consumed, the PCG64 state after the last kept row
     (int64 ``[1, 4]`` on the device, for ``pcg64_restore``), and the first row
     whose logits, sampling or history append failed
-    (``(position, status)`` with status -1 for non-finite logits, or None)."""
+    (``(position, status)`` with status -1 for non-finite logits, or None;
+    ``(position, exception)`` when the caller's ``row_logits`` failed for a
+    kept row)."""
     steps = p.tokens.numel()
     if steps == 0:
-        return (), p.rows[:0], 0, p.states[0:1], None
+        return (), p.rows[:0], 0, p.states[0:1], p.deferred
     dev = p.tokens.device
     finite = torch.isfinite(p.logits).all(dim=1).to(torch.int32)
     # Row j > 0 carries the status of the append before it; a chain without appends has none.
     app = torch.cat([torch.zeros(1 if p.appended else steps, dtype=torch.int32, device=dev), *p.appended])
     info = torch.stack([p.tokens, p.consumed.to(torch.int32), p.status, app, finite]).cpu().numpy()
     toks, used, st, ap, fin = info
-    count = steps
+    count, cut = steps, False
     for j, t in enumerate(toks):
         if int(t) in eos_ids:
-            count = j + 1
+            count, cut = j + 1, True
             break
     failed = None
     for j in range(count):
@@ -695,6 +734,8 @@ def finish_proposals(p: Proposals, eos_ids=()):
             failed = (j, int(st[j] if st[j] != 0 else ap[j]))
         if failed:
             break
+    if failed is None and not cut:
+        failed = p.deferred
     return tuple(int(t) for t in toks[:count]), p.rows[:count], int(used[:count].sum()), p.states[count:count + 1], \
         failed
 

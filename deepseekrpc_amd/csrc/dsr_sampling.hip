@@ -433,6 +433,10 @@ size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab) {
   return verify_ws_bytes(rows, K, vocab);
 }
 
+// The DSR_HINT_* bits a caller may set; any other bit is rejected, so the
+// field can take new meanings later without an ABI change.
+static constexpr uint32_t kHintBits = DSR_HINT_WHOLE_SOME | DSR_HINT_WHOLE_ALL | DSR_HINT_VERIFY_FAST;
+
 static bool dtype_ok(int32_t d) { return d == DSR_BF16 || d == DSR_F32 || d == DSR_F64; }
 
 int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
@@ -440,7 +444,8 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
   const dsr_sample_args_t& a = *args;
   const int64_t words = (a.vocab + 31) / 32;
   if (!a.logits || !a.policy || !a.out_token || !a.out_consumed || !a.out_status || !dtype_ok(a.dtype) ||
-      a.rows < 0 || a.rows > INT_MAX || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab)
+      a.rows < 0 || a.rows > INT_MAX || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab ||
+      (a.hints & ~kHintBits))
     return DSR_ERR_ARG;
   if (a.pen_off && (!a.pen_ids || !a.pen_count || !a.pen_gen)) return DSR_ERR_ARG;
   if (a.bias_off && (!a.bias_ids || !a.bias_val)) return DSR_ERR_ARG;
@@ -544,7 +549,8 @@ static int32_t verify_launch(const dsr_verify_args_t& a, const dsr_head_part_t* 
       (!a.u_target && !a.rng_target) ||
       !a.output_limit || !a.out_accepted || !a.out_ids || !a.out_count || !a.out_pending || !a.out_stop ||
       !a.out_used_accept || !a.out_used_target || !a.out_status || !dtype_ok(a.dtype) || a.K < 0 ||
-      a.K > DSR_MAX_DRAFTS || a.rows < 0 || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab)
+      a.K > DSR_MAX_DRAFTS || a.rows < 0 || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.ld < a.vocab ||
+      a.reserved != 0 || (a.hints & ~kHintBits))
     return DSR_ERR_ARG;
   if (a.pen_off && (!a.pen_ids || !a.pen_count || !a.pen_gen)) return DSR_ERR_ARG;
   if (a.bias_off && (!a.bias_ids || !a.bias_val)) return DSR_ERR_ARG;

@@ -456,7 +456,7 @@ class VerificationDecision:
 
     @property
     def accepted_target_rows(self):
-        # The first verification input was the already sampled seed token.
+        # Rows checked: the seed's own target row, then one per draft kept.
         return 1 + self.accepted_drafts
 
 

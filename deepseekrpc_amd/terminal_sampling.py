@@ -550,7 +550,10 @@ class SamplingWork:
         device.  Rows after a stop token are computed speculatively and
         dropped at the one synchronisation, where the domain takes the state
         saved after the last kept row and the draws it consumed are counted
-        in the transaction's window, exactly as the host loop draws them."""
+        in the transaction's window, exactly as the host loop draws them.
+        The device method may therefore be called for rows past a stop
+        token: an error it raises there (or a row of the wrong type or
+        shape) stops the chain and is raised only if the row is kept."""
         vocab = self.owner.vocabulary
         device = torch.device("cuda", torch.cuda.current_device())
         generator = self.transaction.owner._streams["draft"]
@@ -571,6 +574,8 @@ class SamplingWork:
                                    bias=_bias_table(self.logit_bias, vocab), vocab=vocab)
         ids, rows, draws, final, failed = batch.finish_proposals(chain, self.eos_ids)
         if failed is not None:
+            if isinstance(failed[1], BaseException):
+                raise failed[1]
             if failed[1] == -1:
                 raise ValidationError(_MSG_WINDOW)
             _raise_status(failed[1])

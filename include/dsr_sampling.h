@@ -145,7 +145,7 @@ typedef struct dsr_policy {
 typedef struct dsr_sample_args {
   const void* logits;          /* [rows, ld] of dtype */
   int32_t dtype;               /* DSR_BF16 | DSR_F32 | DSR_F64 */
-  uint32_t hints;              /* DSR_HINT_* bits, or 0 */
+  uint32_t hints;              /* DSR_HINT_* bits, or 0; other bits: DSR_ERR_ARG */
   int64_t rows;
   int64_t vocab;               /* 1 .. 129280 */
   int64_t ld;                  /* elements between rows, >= vocab */
@@ -225,8 +225,8 @@ typedef struct dsr_verify_args {
   size_t workspace_bytes;
   uint64_t* rng_accept;        /* [rows, 4] PCG64 states of the accept domain, or NULL */
   uint64_t* rng_target;        /* [rows, 4] PCG64 states of the target domain, or NULL */
-  uint32_t hints;              /* DSR_HINT_* bits, or 0 */
-  uint32_t reserved;           /* must be 0 */
+  uint32_t hints;              /* DSR_HINT_* bits, or 0; other bits: DSR_ERR_ARG */
+  uint32_t reserved;           /* must be 0 (else DSR_ERR_ARG) */
 } dsr_verify_args_t;
 
 /* Vocabulary projection (the terminal stage's lm_head, stage_graph.py:356-362
@@ -281,8 +281,10 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream);
  * capture, tight serving loops, harnesses that forbid allocation).
  * Arguments as dsr_sample_rows, except that workspace and workspace_bytes
  * must be 0: the workspace is a device array of DSR_NOALLOC_SCRATCH_BYTES
- * inside the library, one per device, allocated when the library is loaded
- * on that device and held until the process ends.  The call uses the current
+ * inside the library, one per device, allocated when the library's code is
+ * loaded on that device and held until the process ends.  Every process
+ * that uses the library on a device holds that 256 MiB there, whether or not
+ * it calls this entry point.  The call uses the current
  * device's array (the stream must belong to the current device) and calls
  * no allocating routine.  A call needing more than the array, that is
  * dsr_sample_workspace_bytes(rows, vocab) > DSR_NOALLOC_SCRATCH_BYTES (more

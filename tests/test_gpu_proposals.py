@@ -217,3 +217,46 @@ def test_rows_below_the_limit_match_the_oracle_without_a_table():
         previous = ref.token
     assert proposals == tuple(want) and state == txn.prepared_state()
     txn.abort()
+
+
+class FailingPastRows(DeviceMarkovRows):
+    """Raises for every row from ``fail_from`` on, as a graph that cannot
+    make rows past a stop token might."""
+
+    def __init__(self, seed, fail_from, poison=None):
+        super().__init__(seed, poison=poison)
+        self.fail_from = fail_from
+
+    def draft_conditional_logits_device(self, result, row, previous):
+        if row >= self.fail_from:
+            self.device_calls.append(row)
+            raise RuntimeError(f"no draft row {row}")
+        return super().draft_conditional_logits_device(result, row, previous)
+
+
+def test_a_row_the_graph_cannot_make_past_an_eos_is_not_needed():
+    """The reference never asks the graph for a row after an EOS proposal
+    (terminal_sampling.py:146-158): the device chain asks speculatively, so
+    an error there is dropped when an earlier row is a stop token, and
+    raised (aborting the transaction) when that row is kept."""
+    policy = POLICIES[0]
+    full, _, _, _, _ = run(DeviceMarkovRows, 11, policy)
+    eos = frozenset({full[1]}) if full[1] not in full[:1] else frozenset({full[2]})
+    cut = len(run(DeviceMarkovRows, 11, policy, eos)[0])
+    sampler = TerminalSampler(900 + 11)
+    work = sampler.begin_verification(seed_token=77, policy=SamplingPolicy(**policy), counts=history(),
+                                      remaining=9, eos_ids=eos)
+    graph = FailingPastRows(11, fail_from=cut)
+    proposals = work.propose(graph, None)
+    state = work.transaction.prepared_state()
+    work.abort()
+    assert graph.device_calls == list(range(cut + 1))   # the chain stopped at the failing row
+    assert (proposals, state) == oracle_chain(11, policy, eos)[:2]
+    # The same failure on a row the chain keeps: raised, and the domains restored.
+    sampler = TerminalSampler(900 + 11)
+    initial = sampler.random.snapshot()
+    work = sampler.begin_verification(seed_token=77, policy=SamplingPolicy(**policy), counts=history(),
+                                      remaining=9)
+    with pytest.raises(RuntimeError, match=f"no draft row {cut}"):
+        work.propose(FailingPastRows(11, fail_from=cut), None)
+    assert sampler.active is None and sampler.random.snapshot() == initial

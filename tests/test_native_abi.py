@@ -45,7 +45,7 @@ def test_flag_and_status_constants_match_header():
     for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
                  "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
                  "E_GENERATED", "E_HISTORY", "E_APPEND", "E_HINT", "MAX_APPEND", "HINT_WHOLE_SOME", "HINT_WHOLE_ALL",
-                 "HINT_VERIFY_FAST", "HEAD_TILE", "HEAD_MAX_ROWS", "STATS_MAX_ROWS"):
+                 "HINT_VERIFY_FAST", "MAX_VOCAB", "HEAD_TILE", "HEAD_MAX_ROWS", "STATS_MAX_ROWS"):
         assert getattr(N, name) == defs["DSR_" + name], name
     assert N.ABI_VERSION == defs["DSR_ABI_VERSION"]
 
@@ -71,6 +71,27 @@ def test_argument_errors_return_before_any_launch():
     assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1
     assert lib.dsr_verify_drafts_head(ctypes.byref(v), None, None, None) == -1
     assert lib.dsr_vocab_head(None, None) == -1
+    # A verifier call over zero requests returns before any launch; the
+    # reserved word and unknown hint bits are rejected ahead of that.
+    v.target = v.draft = v.policy = v.u_target = v.output_limit = 4096
+    v.out_accepted = v.out_ids = v.out_count = v.out_pending = v.out_stop = 4096
+    v.out_used_accept = v.out_used_target = v.out_status = 4096
+    v.dtype, v.K, v.rows, v.vocab, v.ld = N.F32, 0, 0, 8, 8
+    v.workspace, v.workspace_bytes = 4096, 1 << 20
+    assert lib.dsr_verify_drafts(ctypes.byref(v), None) == 0
+    for field, bad in (("reserved", 1), ("hints", 8), ("hints", 1 << 31)):
+        setattr(v, field, bad)
+        assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1, (field, bad)
+        setattr(v, field, 0)
+    v.hints = N.HINT_VERIFY_FAST
+    assert lib.dsr_verify_drafts(ctypes.byref(v), None) == 0
+    s = N.SampleArgs()
+    s.logits = s.policy = s.out_token = s.out_consumed = s.out_status = 4096
+    s.dtype, s.rows, s.vocab, s.ld = N.F32, 0, 8, 8
+    s.workspace, s.workspace_bytes = 4096, 1 << 20
+    assert lib.dsr_sample_rows(ctypes.byref(s), None) == 0
+    s.hints = 1 << 8
+    assert lib.dsr_sample_rows(ctypes.byref(s), None) == -1
     h = N.HeadArgs()  # null pointers
     assert lib.dsr_vocab_head(ctypes.byref(h), None) == -1
     fake16 = 4096
