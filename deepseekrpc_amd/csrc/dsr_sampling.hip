@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "dsr_fast.h"
+#include "dsr_topk.h"
 #include "dsr_full.h"
 #include "dsr_general.h"
 #include "dsr_head.h"
@@ -158,9 +159,9 @@ __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, 
 // path inside the same workgroup.
 template <bool RNG>
 __global__ __launch_bounds__(kThreads) void k_sample_bf16_fast(dsr_sample_args_t a) {
-  __shared__ FastShared sh;
+  __shared__ TopkShared sh;
   const int64_t row = blockIdx.x;
-  const int why = fast_sample_row<RNG>(a, row, sh);
+  const int why = topk_sample_row<RNG>(a, row, sh);
   // A whole row under kModeDeferWhole is the next launch's (k_sample_bf16_full).
   if (why == 0 || (why == kHandTopK && (a.hints & kModeDeferWhole))) return;
   __syncthreads();

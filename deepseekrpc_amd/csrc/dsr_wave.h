@@ -230,6 +230,29 @@ class BlockSync {
     return lane_value(wa - ya, wave_id()) + ai - a;
   }
 
+  // scan2 with an unsigned 64-bit first operand (sums up to 2^64 - 1).
+  __device__ unsigned long long scan2u(unsigned long long a, uint32_t b, unsigned long long& atotal, uint32_t& bex,
+                                       uint32_t& btotal) {
+    const int p = next();
+    long long* si = s_.i[p];
+    uint32_t* su = s_.u[p];
+    const unsigned long long ai = wave_scan_dpp(a);
+    const uint32_t bi = wave_scan_dpp(b);
+    if (lane_id() == 63) {
+      si[wave_id()] = (long long)ai;
+      su[wave_id()] = bi;
+    }
+    lds_barrier();
+    const unsigned long long ya = lane_id() < kWaves ? (unsigned long long)si[lane_id()] : 0ull;
+    const uint32_t yb = lane_id() < kWaves ? su[lane_id()] : 0u;
+    const unsigned long long wa = row_scan_dpp(ya);
+    const uint32_t wb = row_scan_dpp(yb);
+    atotal = lane_value(wa, kWaves - 1);
+    btotal = lane_value(wb, kWaves - 1);
+    bex = lane_value(wb - yb, wave_id()) + bi - b;
+    return lane_value(wa - ya, wave_id()) + ai - a;
+  }
+
   // Index-order CDF of non-negative x behind one barrier.  Returns this
   // thread's inclusive value; `ex` is exactly the previous thread's inclusive
   // value (0 for thread 0), so the intervals [ex, inc) tile [0, total)
