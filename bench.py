@@ -596,6 +596,7 @@ def main():
             raise SystemExit("kernel reported row errors in the timed region")
         general = max(general, int(((res.flags.cpu().numpy() & N.FLAG_GENERAL) != 0).sum()))
     prep = preps[0]
+    calibration_bytes = None
     if args.copy_calibration:
         # A plain read-N/write-N kernel over the batch's logit bytes, for
         # scaling the FETCH_SIZE / WRITE_SIZE counters.
@@ -605,6 +606,7 @@ def main():
         for _ in range(args.steps):
             torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
+        calibration_bytes = src.numel() * 4
 
     if name == "head":
         # The same step without the projection's records: the projection
@@ -643,6 +645,8 @@ def main():
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
     if name == "head":
         cfg.update(head_extra)
+    if calibration_bytes is not None:
+        cfg["calibration_bytes"] = calibration_bytes  # bytes the copy kernel reads, and writes, per launch
     line = {
         "metric": metric, "value": units / (ms_per_step * 1e-3), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
