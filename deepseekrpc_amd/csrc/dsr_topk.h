@@ -9,13 +9,14 @@
 // dependent workgroup steps, so the chain is started while the row is still
 // arriving:
 //
-//   * once slots 0..7 (the first half of each wave's range) have landed, tau_lb
-//     is the k-th largest maximum over pairs of chunks of that half, taken from a
-//     histogram of 4-level bins.  A subset's k-th largest value never exceeds
-//     the row's (k tokens of the half reach it), so every top-k token, boundary
-//     ties included, lies in a chunk whose maximum reaches tau_lb;
+//   * once slots 0..7 (the first half of each wave's range) have landed,
+//     tau_lb is the k-th largest maximum over pairs of chunks of those slots,
+//     taken from a histogram of 4-level bins.  A subset's k-th largest value
+//     never exceeds the row's (k tokens of the subset reach it), so every
+//     top-k token, boundary ties included, lies in a chunk whose maximum
+//     reaches tau_lb;
 //   * such chunks are listed whole, in index order, in their wave's LDS list, the
-//     first half at once and the second half slot by slot as it lands; batches of
+//     slots already landed at once and the rest slot by slot as they land; batches of
 //     listed chunks feed an exact histogram of the keys at or above tau_lb (4,096
 //     keys) and keep an 8-bit mask of their tokens that reach it;
 //   * after the last slot: the row maximum, one scan of the histogram bins (count,
@@ -42,7 +43,7 @@
 
 namespace dsr {
 
-constexpr int kTkHalf = 8;             // slots whose pair maxima give the lower bound
+constexpr int kTkBound = 8;            // slots whose pair maxima give the lower bound (even, 6 to 12; 8 measured best)
 constexpr uint32_t kTkRing = 128;      // candidate chunks waiting for a histogram round, per wave
 constexpr uint32_t kTkTokCap = 512;    // candidate tokens per wave
 constexpr int kTkWin = 4096;           // exact keys tracked from the lower bound up
@@ -54,7 +55,7 @@ struct TopkLists {
   uint32_t lut[256][4];                  // allow byte -> four 2 x 16-bit "disallowed" masks (every slot)
   uint32_t cnt[kTkWin];                  // candidate tokens by level - tau_lb
   union {
-    uint32_t coarse[kTkCoarseWords];     // pair maxima of the first half by level / 4
+    uint32_t coarse[kTkCoarseWords];     // pair maxima of slots 0 .. kTkBound-1 by level / 4
     unsigned long long ftab[kTkWin];     // fixed-point mass by distance below the maximum
   };
   uint4 ring[kWaves][kTkRing];           // candidate chunks (masked bf16 bits) waiting for a histogram round
@@ -67,6 +68,9 @@ struct TopkLists {
   unsigned long long wm[kWaves];         // per wave: fixed-point mass, then kept mass off the boundary
   int lb;                                // tau_lb as a level
   uint32_t close_min;                    // smallest distance of a key inside the min-p rounding band
+  unsigned long long ea[kWaves];         // per wave: kept mass off the boundary (CDF)
+  uint32_t et[kWaves];                   // per wave: boundary ties | top-k boundary ties << 16 (CDF)
+  int p_late;                            // top-p boundary checks: hand-over reason | margin << 8
   int p_dk, p_need, p_dl, p_keep, p_info;
   uint32_t p_close, p_npos;              // p_close: DSR_FLAG_MARGIN when a top-k mass sits in the min-p band
   unsigned long long p_C, p_fl;
@@ -183,8 +187,8 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
   // the last ones were taken.  Instead the slots are issued in rounds, one
   // slot per wave and a barrier per round, so they land slot by slot for the
   // whole workgroup, and each round does the work of a slot issued four
-  // rounds before (landed by then).  The lower bound tau_lb is taken from the
-  // first half (slots 0..7) in the barriers of rounds 11-13.
+  // rounds before (landed by then).  The lower bound tau_lb is taken from
+  // slots 0 .. kTkBound-1 in the barriers of the three rounds after theirs.
 #pragma unroll
   for (int j = 0; j < 4; ++j) issue(j);
   __builtin_amdgcn_sched_barrier(0);
@@ -194,19 +198,27 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
     sh.lut[m][q] = (((m >> (2 * q)) & 1u) ? 0u : 0x0000FFFFu) | (((m >> (2 * q + 1)) & 1u) ? 0u : 0xFFFF0000u);
     ((uint4*)sh.cnt)[tid] = make_uint4(0u, 0u, 0u, 0u);     // 4,096 words
     ((uint4*)sh.coarse)[tid] = make_uint4(0u, 0u, 0u, 0u);  // 4,096 words
-    if (tid == 0) sh.close_min = 0xFFFFFFFFu;
+    if (tid == 0) {
+      sh.close_min = 0xFFFFFFFFu;
+      sh.p_late = 0;
+    }
+    if (tid < kWaves) {
+      sh.ea[tid] = 0ull;
+      sh.et[tid] = 0u;
+    }
   }
   lds_barrier();
   if (wave == 0) {  // ordered by the next barrier
     if (tid < kPolWords + (RNG ? 8 : 2)) sh.polw[tid] = pw;
     sh.etab[lane] = etv;
   }
-  auto round = [&](int r) {
-    issue(r);
+  // Round r issues slot r (r < 16) and runs pass 1 of slot r - 4.
+  auto step = [&](int r) {
+    if (r < kFastChunks) issue(r);
     __builtin_amdgcn_sched_barrier(0);
     pass1(r - 4);
   };
-  round(4);
+  step(4);
   lds_barrier();
 
   dsr_policy_t pol;
@@ -232,17 +244,17 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
   const uint32_t k = greedy ? 1u : (uint32_t)top_k;
 
 #pragma unroll
-  for (int r = 5; r < 11; ++r) {
-    round(r);
+  for (int r = 5; r < kTkBound + 3; ++r) {
+    step(r);
     lds_barrier();
   }
-  round(11);
+  step(kTkBound + 3);
 
-  // ---- tau_lb: the k-th largest positive pair maximum of the first half, to
-  // 4 levels (its bin's lower edge).  Fewer than k positive pair maxima hand
-  // the row over (a top-k reaching zero or below).
+  // ---- tau_lb: the k-th largest positive pair maximum of slots
+  // 0 .. kTkBound-1, to 4 levels (its bin's lower edge).  Fewer than k
+  // positive pair maxima hand the row over (a top-k reaching zero or below).
 #pragma unroll
-  for (int q = 0; q < kTkHalf / 2; ++q) {
+  for (int q = 0; q < kTkBound / 2; ++q) {
     const int gq = max((int)(short)(cmx[q] & 0xFFFFu), (int)(short)(cmx[q] >> 16));
     if (gq > 0) {
       const uint32_t b = (uint32_t)gq >> 2;  // < 8,192
@@ -250,7 +262,7 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
     }
   }
   lds_barrier();
-  round(12);
+  step(kTkBound + 4);
   uint32_t cc[8];
   {
     const uint4 w4 = ((const uint4*)sh.coarse)[1023 - tid];  // words 4092-4t .. 4095-4t: bins 8191-8t down to 8184-8t
@@ -271,11 +283,11 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
       rr += cc[i];
     }
   }
-  round(13);
+  step(kTkBound + 5);
   lds_barrier();
   const int lb = __builtin_amdgcn_readfirstlane(sh.lb);
-  issue(14);
-  issue(15);
+#pragma unroll
+  for (int r = kTkBound + 6; r < kFastChunks; ++r) issue(r);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- candidate chunks (maximum >= tau_lb) pass, in index order, through a
@@ -283,7 +295,6 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
   // the candidate keys and append the candidate tokens (level, index in the
   // wave's range) to the wave's token list, in index order.
   uint32_t wn = 0, hdone = 0, ntok = 0;  // wave-uniform
-  bool lovf = false;                      // a candidate above the 4,096-key window
   auto hist = [&](uint32_t hend) {        // wave-uniform; hend - hdone <= kTkRing
     wave_lds_sync();
     for (uint32_t base = hdone; base < hend; base += 64u) {
@@ -293,17 +304,17 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
       if (e < hend) {
         r4 = sh.ring[wave][e & (kTkRing - 1u)];
         tb = 8u * (uint32_t)sh.rid[wave][e & (kTkRing - 1u)];
+        // A candidate more than 4,095 keys above tau_lb is counted in the top
+        // key's bin; the row maximum then lies above the window too, and the
+        // row is handed over once that is known.
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int off = chunk_elem_level(r4.x, r4.y, r4.z, r4.w, i) - lb;
-          if (off >= 0) {
-            if (off < kTkWin) {
-              atomicAdd(&sh.cnt[off], 1u);
-              m |= 1u << i;
-            } else {
-              lovf = true;
-            }
-          }
+          m |= (off >= 0 ? 1u : 0u) << i;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if ((m >> i) & 1u) atomicAdd(&sh.cnt[min(chunk_elem_level(r4.x, r4.y, r4.z, r4.w, i) - lb, kTkWin - 1)], 1u);
         }
       }
       const uint32_t n = (uint32_t)__popc(m);
@@ -334,9 +345,9 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
     if (wn - hdone >= 64u) hist(hdone + 64u);
   };
 #pragma unroll
-  for (int j = 0; j < 10; ++j) compact(j);
+  for (int j = 0; j < kTkBound + 2; ++j) compact(j);
 #pragma unroll
-  for (int j = 10; j < kFastChunks; ++j) {
+  for (int j = kTkBound + 2; j < kFastChunks; ++j) {
     pass1(j);
     compact(j);
   }
@@ -352,7 +363,7 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
                        max(vmax_u & 0xFFFFu, vmax_u >> 16) >= 0xFF81u;
   {
     const uint32_t wk = wave_reduce_dpp((uint32_t)(tmax + 0x8000), OpMax());
-    const uint32_t wf = wave_reduce_dpp(bad | (lovf ? 2u : 0u), OpOr());
+    const uint32_t wf = wave_reduce_dpp(bad, OpOr());
     if (lane == 0) sh.wred[wave] = wk | ((wf | (ntok > kTkTokCap ? 2u : 0u)) << 16);
   }
   lds_barrier();
@@ -363,10 +374,10 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
     F = lane_value(row_reduce(y >> 16, OpOr()), 0);
   }
   if (F & 1u) return kHandInvalid;   // NaN / +inf: the general path reports it in the reference's order
-  if (F & 2u) return kHandCapacity;  // a token list or the key window overflowed
   const int Mlev = (int)Mkey - 0x8000;  // at least k tokens reach tau_lb, so the maximum does
   const double M = bf16_key_value(Mkey);
-  const int dM = Mlev - lb;             // < 4,096: the maximum passed the window check
+  const int dM = Mlev - lb;
+  if ((F & 2u) || dM >= kTkWin) return kHandCapacity;  // a token list or the key window overflowed
 
   // ---- this lane's candidate tokens: lane l of wave w holds tokens
   // G*l .. G*l+G-1 of its wave's list (G = ceil(count / 64) <= 8, the same in
@@ -536,13 +547,19 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
       const unsigned long long cwm = lane < wk ? wml : (lane == wk ? S - lane_value(wmi - wml, wk) : 0ull);
       const unsigned long long cwi = row_scan_dpp(cwm);
       const int wl = __builtin_ctzll(__ballot(lane < kWaves && cwi >= tgt));
+      // The boundary lane's values, kept for its checks after the barrier.
+      bool mine = false;
+      unsigned long long A = 0, rt = 0;
+      uint32_t dlq = 0, n_above = 0, n_tie = 0;
+      long long keep = 0;
       if (wave == wl) {  // the wave holding the top-p boundary
         uint32_t kc[4], cex, pex, csum;
         unsigned long long mex, msum;
         lane_prefix(dk, need, lane_value(wci - wcl, wl), lane_value(cwi - cwm, wl), kc, mex, cex, pex, msum, csum);
-        if (mex < tgt && tgt <= mex + msum) {
-          unsigned long long run = mex, A = 0, rt = 0;
-          uint32_t ce = cex, dlq = 0, n_above = 0, n_tie = 0;
+        mine = mex < tgt && tgt <= mex + msum;
+        if (mine) {
+          unsigned long long run = mex;
+          uint32_t ce = cex;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const unsigned long long km = (unsigned long long)kc[q] * fx[q];
@@ -557,7 +574,6 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
             ce += kc[q];
           }
           // Tie member i (index order) keeps iff A + i * rt < P (:98-101).
-          long long keep;
           if (n_tie == 1) {
             keep = (double)A < P ? 1 : 0;
           } else {
@@ -567,37 +583,38 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
             while (keep < (long long)n_tie && (double)(A + (unsigned long long)keep * rt) < P) ++keep;
           }
           if (n_above == 0 && keep == 0) keep = 1;  // the first token is never removed
-          const unsigned long long uk = (unsigned long long)keep;
-          const double tol = ((double)(n_above + uk) + 16.0) * 0x1p-51 * (double)S + (double)(n_above + n_tie + 2);
-          bool near = fabs((double)(A + uk * rt) - P) <= tol;
-          if (uk >= 1 && n_above + uk > 1) near = near || fabs((double)(A + (uk - 1) * rt) - P) <= tol;
-          if (uk == 0 && n_above > 0) near = true;
-          if (uk == n_tie && (double)(A + (unsigned long long)n_tie * rt) < P) near = true;
-          // Key order must equal mass order next to the boundary: its bf16
-          // neighbours keep (v - max) / T at least 2^-40 apart (always so when
-          // the lower neighbour is at least 2^-24: its bf16 spacing is then at
-          // least 2^-32 and T <= 100); ties with +-0 never pass.
-          const uint32_t lkey = Mkey - dlq;
-          int hand = zero_key(lkey) ? kHandZero : 0;
-          if (!hand && !(bf16_key_value(lkey - 1u) >= 0x1p-24)) {
-            for (int side = -1; side <= 1 && !hand; side += 2) {
-              const uint32_t nb = lkey + side;
-              if (nb <= kKeyNegInf || nb >= kKeyPosInf || zero_key(nb)) continue;
-              if (!(fabs(bf16_key_value(nb) - bf16_key_value(lkey)) / T >= 0x1p-40)) hand = kHandOrder;
-            }
-          }
           sh.p_dl = (int)dlq;
           sh.p_keep = (int)keep;
-          sh.p_C = A + uk * rt;
+          sh.p_C = A + (unsigned long long)keep * rt;
           sh.p_fl = rt;
           sh.p_npos = n_above + (uint32_t)keep;  // the boundary key holds mass, so every kept token has r > 0
-          sh.p_info = hand | (near ? 0x100 : 0);
         }
       }
       lds_barrier();
-      const int info = __builtin_amdgcn_readfirstlane(sh.p_info);
-      if (info & 0xFF) return info & 0xFF;
-      if (info & 0x100) flags |= DSR_FLAG_MARGIN;
+      if (mine) {
+        // Checked while the other waves go on; read after the next barrier,
+        // before anything is written.  The rounding band of the boundary
+        // decision, and key order equal to mass order next to the boundary:
+        // its bf16 neighbours keep (v - max) / T at least 2^-40 apart (always
+        // so when the lower neighbour is at least 2^-24: its bf16 spacing is
+        // then at least 2^-32 and T <= 100); ties with +-0 never pass.
+        const unsigned long long uk = (unsigned long long)keep;
+        const double tol = ((double)(n_above + uk) + 16.0) * 0x1p-51 * (double)S + (double)(n_above + n_tie + 2);
+        bool near = fabs((double)(A + uk * rt) - P) <= tol;
+        if (uk >= 1 && n_above + uk > 1) near = near || fabs((double)(A + (uk - 1) * rt) - P) <= tol;
+        if (uk == 0 && n_above > 0) near = true;
+        if (uk == n_tie && (double)(A + (unsigned long long)n_tie * rt) < P) near = true;
+        const uint32_t lkey = Mkey - dlq;
+        int hand = zero_key(lkey) ? kHandZero : 0;
+        if (!hand && !(bf16_key_value(lkey - 1u) >= 0x1p-24)) {
+          for (int side = -1; side <= 1 && !hand; side += 2) {
+            const uint32_t nb = lkey + side;
+            if (nb <= kKeyNegInf || nb >= kKeyPosInf || zero_key(nb)) continue;
+            if (!(fabs(bf16_key_value(nb) - bf16_key_value(lkey)) / T >= 0x1p-40)) hand = kHandOrder;
+          }
+        }
+        sh.p_late = hand | (near ? 0x100 : 0);
+      }
       dl = (uint32_t)__builtin_amdgcn_readfirstlane(sh.p_dl);
       K = (uint32_t)__builtin_amdgcn_readfirstlane(sh.p_keep);
       Ct = sh.p_C;
@@ -631,14 +648,8 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
       Tk += ddv[t] == dk;
     }
   }
-  {
-    const unsigned long long wa = wave_reduce_dpp(At, OpSum());
-    const uint32_t wt = wave_reduce_dpp(Tt | (Tk << 16), OpSum());
-    if (lane == 0) {
-      sh.wm[wave] = wa;
-      sh.wc[wave] = wt;
-    }
-  }
+  if (At) atomicAdd(&sh.ea[wave], At);
+  if (Tt | Tk) atomicAdd(&sh.et[wave], Tt | (Tk << 16));
   // The draw's threshold, ahead of the barrier.
   const bool draws = has_draws<RNG>(a);
   unsigned long long thr = 0;
@@ -671,9 +682,14 @@ __device__ __forceinline__ int topk_sample_row(const dsr_sample_args_t& a, int64
   }
   const double tol = ((double)npos + 16.0) * 0x1p-51 * (double)Ct + (double)npos + 2.0;
   lds_barrier();
+  {
+    const int late = __builtin_amdgcn_readfirstlane(sh.p_late);
+    if (late & 0xFF) return late & 0xFF;
+    if (late & 0x100) flags |= DSR_FLAG_MARGIN;
+  }
   // Wave bases (strict mass, boundary ties, top-k boundary ties) on lanes 0..15.
-  const unsigned long long wal = lane < kWaves ? sh.wm[lane] : 0ull;
-  const uint32_t wtl = lane < kWaves ? sh.wc[lane] : 0u;
+  const unsigned long long wal = lane < kWaves ? sh.ea[lane] : 0ull;
+  const uint32_t wtl = lane < kWaves ? sh.et[lane] : 0u;
   const unsigned long long wai = row_scan_dpp(wal);
   const uint32_t wti = row_scan_dpp(wtl);
   const int64_t tok0 = 8 * (int64_t)wave * (int64_t)CW;  // row index of the wave's first token

@@ -91,11 +91,11 @@ def test_rows_handed_to_the_general_path_still_match():
     R, V = 6, workloads.VOCAB
     x = rng.normal(0, 1, (R, V))
     x[0] = -np.abs(x[0]) - 1.0                                 # every value negative
-    # Slots 8..15 of every wave far above slots 0..7: the lower bound taken from
-    # the first half admits most of the second half as candidates.  Wave w
+    # Slots 12..15 of every wave far above slots 0..11: the lower bound taken
+    # from the earlier slots admits most of the last ones as candidates.  Wave w
     # holds chunks [1010 w, 1010 (w + 1)), slot j its chunks 64 j .. 64 j + 63.
     for wv in range(16):
-        x[1, 8 * (1010 * wv + 512):8 * 1010 * (wv + 1)] += 6.0
+        x[1, 8 * (1010 * wv + 768):8 * 1010 * (wv + 1)] += 6.0
     x[2] = np.sort(x[2])                                       # increasing
     x[3, 17] = np.nan
     x[4, 99] = np.inf
