@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIB_NAME = "libdsr_sampling.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
@@ -48,7 +48,8 @@ EXPORTS = (
     "dsr_abi_version", "dsr_status_message", "dsr_sample_workspace_bytes", "dsr_verify_workspace_bytes",
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
     "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append", "dsr_sample_rows_noalloc",
-    "dsr_vocab_head", "dsr_verify_drafts_head", "dsr_prob_stats_rows",
+    "dsr_vocab_head", "dsr_verify_drafts_head", "dsr_prob_stats_rows", "dsr_verify_probs_workspace_bytes",
+    "dsr_verify_probs",
 )
 NOALLOC_SCRATCH_BYTES = 268435456
 HEAD_TILE = 128
@@ -91,6 +92,17 @@ class VerifyArgs(ctypes.Structure):
         ("out_used_accept", _p), ("out_used_target", _p), ("out_status", _p), ("out_flags", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_accept", _p), ("rng_target", _p),
         ("hints", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+    ]
+
+
+class VerifyProbsArgs(ctypes.Structure):
+    _fields_ = [
+        ("target", _p), ("draft", _p), ("target_status", _p), ("K", _i32), ("reserved", ctypes.c_uint32),
+        ("rows", _i64), ("vocab", _i64), ("draft_ids", _p), ("greedy", _p), ("u_accept", _p), ("u_target", _p),
+        ("eos_off", _p), ("eos_ids", _p), ("output_limit", _p),
+        ("out_accepted", _p), ("out_ids", _p), ("out_count", _p), ("out_pending", _p), ("out_stop", _p),
+        ("out_used_accept", _p), ("out_used_target", _p), ("out_status", _p), ("out_flags", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t), ("rng_accept", _p), ("rng_target", _p),
     ]
 
 
@@ -155,6 +167,10 @@ def load(path: str = LIB_PATH):
     lib.dsr_vocab_head.argtypes = [ctypes.POINTER(HeadArgs), _p]
     lib.dsr_verify_drafts_head.restype = _i32
     lib.dsr_verify_drafts_head.argtypes = [ctypes.POINTER(VerifyArgs), _p, _p, _p]
+    lib.dsr_verify_probs_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsr_verify_probs_workspace_bytes.argtypes = [_i64, _i32]
+    lib.dsr_verify_probs.restype = _i32
+    lib.dsr_verify_probs.argtypes = [ctypes.POINTER(VerifyProbsArgs), _p]
     _lib = lib
     return lib
 

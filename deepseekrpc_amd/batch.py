@@ -864,6 +864,104 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     return res
 
 
+def _row_pointers(rows, count, V, dev, what, optional=False):
+    """Device pointers of ``count`` float64 rows of ``V``: a ``[..., V]`` tensor
+    split into its rows, or a sequence of ``[V]`` tensors (``None`` allowed
+    where ``optional``)."""
+    if isinstance(rows, torch.Tensor):
+        rows = list(rows.reshape(-1, rows.shape[-1])) if rows.numel() else []
+    rows = list(rows)
+    if len(rows) != count:
+        raise ValueError(f"{what}: {count} rows are required")
+    out = []
+    for r in rows:
+        if r is None and optional:
+            out.append(0)
+            continue
+        _require_cuda(r, what)
+        if r.dtype != torch.float64 or r.numel() != V or r.device != dev or not r.is_contiguous():
+            raise ValueError(f"{what} rows must be contiguous float64 [{V}] on {dev}")
+        out.append(r.data_ptr())
+    return out, rows
+
+
+def verify_probs(target_rows, draft_rows, draft_ids: torch.Tensor, output_limit: torch.Tensor, *, vocab: int,
+                 requests: int = 1, greedy: torch.Tensor | None = None, u_accept: torch.Tensor | None = None,
+                 u_target: torch.Tensor | None = None, rng_accept: torch.Tensor | None = None,
+                 rng_target: torch.Tensor | None = None, target_status: torch.Tensor | None = None,
+                 eos_offsets: torch.Tensor | None = None, eos_ids: torch.Tensor | None = None,
+                 workspace: Workspace | None = None) -> VerifyResult:
+    """``verify_drafts`` (sampling.py:247-294) over float64 rows already on the
+    device (``dsr_verify_probs``), for ``requests`` requests of ``K`` drafts.
+
+    ``target_rows`` holds ``requests * (K + 1)`` rows and ``draft_rows``
+    ``requests * K`` (a ``[..., V]`` tensor or a sequence of ``[V]``
+    tensors), request-major.  ``target_status`` (int32, one per target row)
+    is the status of whatever built each target row: a failed row is
+    reported when the chain reaches it, and may be ``None`` in
+    ``target_rows``.  ``greedy`` is a uint8 flag per request.  Draws come
+    from ``u_accept`` / ``u_target`` or, on the device, from the PCG64 states
+    ``rng_accept`` / ``rng_target`` (int64 ``[requests, 4]``), advanced by
+    exactly the draws the decision uses.  The row pointers go to the device
+    in one pinned upload; nothing here synchronises.
+    """
+    lib = N.load()
+    R, V = int(requests), int(vocab)
+    K = draft_ids.numel() // R if R else 0
+    dev = draft_ids.device if K else output_limit.device
+    tp, trows = _row_pointers(target_rows, R * (K + 1), V, dev, "target", optional=target_status is not None)
+    dp, drows = _row_pointers(draft_rows if K else [], R * K, V, dev, "draft")
+    if K:
+        _require(draft_ids, "draft_ids", torch.int32, R * K)
+        if rng_accept is None:
+            _require(u_accept, "u_accept", torch.float64, R * K)
+    if rng_accept is not None:
+        _require(rng_accept, "rng_accept", torch.int64, R * 4)
+    if rng_target is None:
+        _require(u_target, "u_target", torch.float64, R)
+    else:
+        _require(rng_target, "rng_target", torch.int64, R * 4)
+    _require(output_limit, "output_limit", torch.int32, R)
+    if greedy is not None:
+        _require(greedy, "greedy", torch.uint8, R)
+    if target_status is not None:
+        _require(target_status, "target_status", torch.int32, R * (K + 1))
+    host = torch.tensor(tp + dp, dtype=torch.int64).pin_memory()
+    ptrs = host.to(dev, non_blocking=True)
+    i32 = lambda *sh: torch.empty(*sh, dtype=torch.int32, device=dev)
+    res = VerifyResult(i32(R), i32(R, K + 1), i32(R), i32(R), i32(R), i32(R), i32(R), i32(R),
+                       torch.empty(R, dtype=torch.uint8, device=dev))
+    ws = (workspace or _default_ws).get(max(lib.dsr_verify_probs_workspace_bytes(R, K), 8), dev)
+    a = N.VerifyProbsArgs()
+    a.target = ptrs.data_ptr()
+    a.draft = ptrs.data_ptr() + 8 * R * (K + 1) if K else None
+    a.target_status = target_status.data_ptr() if target_status is not None else None
+    a.K, a.rows, a.vocab = K, R, V
+    a.draft_ids = draft_ids.data_ptr() if K else None
+    a.greedy = greedy.data_ptr() if greedy is not None else None
+    a.u_accept = u_accept.data_ptr() if K and u_accept is not None else None
+    a.u_target = u_target.data_ptr() if u_target is not None else None
+    if rng_accept is not None and R:
+        a.rng_accept = rng_accept.data_ptr()
+    if rng_target is not None and R:
+        a.rng_target = rng_target.data_ptr()
+    if eos_offsets is not None and eos_ids is not None and eos_ids.numel() > 0:
+        _require(eos_offsets, "eos_offsets", torch.int64, R + 1)
+        _require_cuda(eos_ids, "eos_ids")
+        a.eos_off, a.eos_ids = eos_offsets.data_ptr(), eos_ids.data_ptr()
+    a.output_limit = output_limit.data_ptr()
+    a.out_accepted, a.out_ids, a.out_count = res.accepted.data_ptr(), res.ids.data_ptr(), res.count.data_ptr()
+    a.out_pending, a.out_stop = res.pending.data_ptr(), res.stop.data_ptr()
+    a.out_used_accept, a.out_used_target = res.used_accept.data_ptr(), res.used_target.data_ptr()
+    a.out_status, a.out_flags = res.status.data_ptr(), res.flags.data_ptr()
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    res.args = a
+    res.keep = (trows, drows, ptrs, host, draft_ids, output_limit, greedy, u_accept, u_target, rng_accept, rng_target,
+                target_status, eos_offsets, eos_ids, ws)
+    N.check(lib.dsr_verify_probs(ctypes.byref(a), _stream()), "dsr_verify_probs")
+    return res
+
+
 class PreparedVerify:
     """A ``dsr_verify_drafts`` call whose arguments are marshalled once;
     ``launch()`` re-issues it on the current stream, overwriting the outputs."""

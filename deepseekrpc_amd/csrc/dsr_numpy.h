@@ -193,4 +193,154 @@ __device__ __forceinline__ double np_sum(Load load, int64_t n, NpSumShared& sh) 
   return np_sum(load, n, sh, [](int64_t, double) {});
 }
 
+// One buffer, load(lo .. lo + len - 1) with 0 < len <= 8,192, summed in
+// NumPy's order by a workgroup of kNpBufWaves waves, so that the buffers of
+// a vector go to separate workgroups (their results are then added in
+// order: sum = b0, then sum + b1, ...).  Wave v of a full buffer takes
+// leaves 8v .. 8v + 7 (elements 1,024 v .. 1,024 v + 1,023) as np_sum's
+// wave takes them and the tree's top three levels add the eight results; a
+// shorter buffer's tree is listed by wave 0 and its leaves shared out eight
+// per wave.  Every thread of the workgroup calls it and gets the result;
+// visit(i, x) sees every element once, within a thread in increasing i.
+constexpr int kNpBufWaves = 8;
+constexpr int kNpBufThreads = 64 * kNpBufWaves;
+
+struct NpBufShared {
+  int32_t node_lo[kNpLevels][kNpMaxLeaves];
+  int32_t node_len[kNpLevels][kNpMaxLeaves];
+  int32_t node_pos[kNpLevels][kNpMaxLeaves];
+  int32_t nodes[kNpLevels];
+  double val[kNpLevels][kNpMaxLeaves];
+  double gsum[kNpBufWaves];
+  double result;
+};
+
+template <class Load, class Visit>
+__device__ __forceinline__ double np_buffer_sum(Load load, int64_t lo, int len, NpBufShared& sh, Visit visit) {
+  const int w = wave_id(), lane = lane_id();
+  const int g = lane >> 3, k = lane & 7;
+  if (len == kNpBuffer) {
+    const int64_t base = lo + 128 * (8 * w + g) + k;  // leaf 8w + g, running sum k
+    double v[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v[t] = load(base + 8 * t);
+    double r = v[0];
+    visit(base, v[0]);
+#pragma unroll
+    for (int t = 1; t < 16; ++t) {
+      r += v[t];
+      visit(base + 8 * t, v[t]);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) r += __shfl_xor(r, m);
+    if (lane == 0) sh.gsum[w] = r;
+    __syncthreads();
+    const double* q = sh.gsum;
+    const double total = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    __syncthreads();  // the shared arrays may be used again on return
+    return total;
+  }
+  if (len < 8) {  // a running sum from 0.0
+    if (threadIdx.x == 0) {
+      double r = 0.0;
+      for (int i = 0; i < len; ++i) {
+        const double x = load(lo + i);
+        r += x;
+        visit(lo + i, x);
+      }
+      sh.result = r;
+    }
+    __syncthreads();
+    const double total = sh.result;
+    __syncthreads();
+    return total;
+  }
+  // The tree, breadth first, by wave 0 (np_sum's listing); every thread
+  // takes part in the barriers.
+  if (w == 0 && lane == 0) {
+    sh.nodes[0] = 1;
+    sh.node_lo[0][0] = 0;
+    sh.node_len[0][0] = len;
+  }
+  __syncthreads();
+  for (int l = 0; l + 1 < kNpLevels; ++l) {
+    if (w == 0) {
+      const int cnt = sh.nodes[l];
+      const int i0 = lane, i1 = lane + 64;
+      const int m0 = i0 < cnt ? sh.node_len[l][i0] : 0, m1 = i1 < cnt ? sh.node_len[l][i1] : 0;
+      const uint32_t c0 = i0 < cnt ? (m0 > kNpLeaf ? 2u : 1u) : 0u;
+      const uint32_t c1 = i1 < cnt ? (m1 > kNpLeaf ? 2u : 1u) : 0u;
+      const uint32_t s0 = wave_scan_dpp(c0), s1 = wave_scan_dpp(c1);
+      const uint32_t t0 = lane_value(s0, 63), t1 = lane_value(s1, 63);
+      auto emit = [&](int i, int m, uint32_t c, uint32_t e) {
+        if (c == 0 || e + c > (uint32_t)kNpMaxLeaves) return;  // the bound never binds: leaves hold >= 64
+        const int a = sh.node_lo[l][i];
+        sh.node_pos[l][i] = (int)e;
+        if (c == 2) {
+          int h = m / 2;
+          h -= h % 8;
+          sh.node_lo[l + 1][e] = a;
+          sh.node_len[l + 1][e] = h;
+          sh.node_lo[l + 1][e + 1] = a + h;
+          sh.node_len[l + 1][e + 1] = m - h;
+        } else {
+          sh.node_lo[l + 1][e] = a;
+          sh.node_len[l + 1][e] = m;
+        }
+      };
+      emit(i0, m0, c0, s0 - c0);
+      emit(i1, m1, c1, t0 + s1 - c1);
+      if (lane == 0) sh.nodes[l + 1] = (int)(t0 + t1 < (uint32_t)kNpMaxLeaves ? t0 + t1 : kNpMaxLeaves);
+    }
+    __syncthreads();
+  }
+  constexpr int L = kNpLevels - 1;
+  const int leaves = sh.nodes[L];
+  for (int q0 = 8 * w; q0 < leaves; q0 += 8 * kNpBufWaves) {  // uniform over the wave
+    const int j = q0 + g;
+    const bool has = j < leaves;
+    const int llo = has ? sh.node_lo[L][j] : 0, llen = has ? sh.node_len[L][j] : 0;
+    const int nb = llen >> 3;  // full 8-element rows of the leaf (every leaf here holds >= 8)
+    const int64_t base = lo + llo + k;
+    double v[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v[t] = t < nb ? load(base + 8 * t) : 0.0;
+    double r = v[0];
+    if (nb > 0) visit(base, v[0]);
+#pragma unroll
+    for (int t = 1; t < 16; ++t) {
+      if (t < nb) {
+        r += v[t];
+        visit(base + 8 * t, v[t]);
+      }
+    }
+    r += __shfl_xor(r, 1);
+    r += __shfl_xor(r, 2);
+    r += __shfl_xor(r, 4);
+    if (has && k == 0) {
+      for (int i = 8 * nb; i < llen; ++i) {  // the leftovers, in order
+        const double x = load(lo + llo + i);
+        r += x;
+        visit(lo + llo + i, x);
+      }
+      sh.val[L][j] = r;
+    }
+  }
+  __syncthreads();
+  for (int l = kNpLevels - 2; l >= 0; --l) {  // from the leaves up
+    if (w == 0) {
+      const int cnt = sh.nodes[l];
+      for (int i = lane; i < cnt; i += 64) {
+        const int p = sh.node_pos[l][i];
+        const double a = sh.val[l + 1][p];
+        sh.val[l][i] = sh.node_len[l][i] > kNpLeaf ? a + sh.val[l + 1][p + 1] : a;
+      }
+    }
+    __syncthreads();
+  }
+  const double total = sh.val[0][0];
+  __syncthreads();
+  return total;
+}
+
 }  // namespace dsr

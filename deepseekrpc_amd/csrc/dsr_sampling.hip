@@ -254,35 +254,42 @@ __global__ __launch_bounds__(kThreads) void k_prob_stats_rows(StatsRows r, int64
   prob_stats_row(r.p[row], n, out + 3 * row, (int32_t*)(out + 3 * row + 1), sh, np);
 }
 
-// First i with c_i / c_last > u for the sequential running sum c of p
-// (np.cumsum, then searchsorted "right"; sampling.py:126-128), by one lane.
-__device__ int64_t sequential_cdf_search(const double* p, int64_t n, double u) {
+// First i with c_i / c_last > u for the sequential running sum c of the
+// vector p(0 .. n-1) (np.cumsum, then searchsorted "right";
+// sampling.py:126-128), by one lane.
+template <class F>
+__device__ int64_t sequential_cdf_search(F p, int64_t n, double u) {
   double last = 0.0;
-  for (int64_t i = 0; i < n; ++i) last += p[i];
+  for (int64_t i = 0; i < n; ++i) last += p(i);
   double c = 0.0;
   for (int64_t i = 0; i < n; ++i) {
-    c += p[i];
+    c += p(i);
     if (c / last > u) return i;
   }
   return n - 1;  // not reached: c_last / c_last = 1 > u
 }
 
-// categorical (sampling.py:118-128) over one float64 vector, one workgroup.
-// Wave w owns elements [8192 w, 8192 (w + 1)) as 16 chunks of 512.  One
-// coalesced pass gives every chunk's sum (8 strided loads per lane, then a
-// wave sum) and the positive count; the crossing of u * total is then found
-// by wave, by chunk, and inside the chunk by its wave's running scan.  These
-// sums take another order than np.cumsum: where u sits within that rounding
-// band of a cell edge (or no crossing shows), the sequential sum decides.
+// categorical (sampling.py:118-128) over one float64 vector p(0 .. n-1), one
+// workgroup.  Wave w owns elements [8192 w, 8192 (w + 1)) as 16 chunks of
+// 512.  One coalesced pass gives every chunk's sum (8 strided loads per lane,
+// then a wave sum) and the positive count; the crossing of u * total is then
+// found by wave, by chunk, and inside the chunk by its wave's running scan.
+// These sums take another order than np.cumsum: where u sits within that
+// rounding band of a cell edge (or no crossing shows), the sequential sum
+// decides.  Every thread gets the token and the flags.
 constexpr int kCatChunk = 512;
 constexpr int kCatChunks = 16;
 static_assert((int64_t)kWaves * kCatChunks * kCatChunk >= DSR_MAX_VOCAB, "one workgroup covers the vocabulary");
 
-__global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, int64_t n, double u, int32_t* out) {
-  __shared__ double csum[kWaves][kCatChunks];
-  __shared__ double wsum[kWaves];
-  __shared__ long long wpos[kWaves];
-  __shared__ long long found[2];
+struct CatShared {
+  double csum[kWaves][kCatChunks];
+  double wsum[kWaves];
+  long long wpos[kWaves];
+  long long found[2];
+};
+
+template <class F>
+__device__ void prob_categorical_row(F p, int64_t n, double u, CatShared& cs, int64_t& token, unsigned& flags) {
   const int w = wave_id(), lane = lane_id();
   const int64_t lo = (int64_t)w * kCatChunks * kCatChunk;
   long long np = 0;
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, 
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int64_t i = lo + (int64_t)c * kCatChunk + 64 * q + lane;
-      x[q] = i < n ? p[i] : 0.0;
+      x[q] = i < n ? p(i) : 0.0;
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -303,65 +310,70 @@ __global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, 
         part += x[q];
         np += x[q] > 0.0 ? 1 : 0;
       }
-      const double cs = wave_reduce_dpp(part, OpSum());  // the same value in every lane
-      if (lane == 0) csum[w][c + h] = cs;
-      wtot += cs;
+      const double s = wave_reduce_dpp(part, OpSum());  // the same value in every lane
+      if (lane == 0) cs.csum[w][c + h] = s;
+      wtot += s;
     }
   }
   const long long wnp = wave_reduce_dpp(np, OpSum());
   if (lane == 0) {
-    wsum[w] = wtot;
-    wpos[w] = wnp;
+    cs.wsum[w] = wtot;
+    cs.wpos[w] = wnp;
   }
-  if (threadIdx.x == 0) found[1] = 1;
+  if (threadIdx.x == 0) cs.found[1] = 1;
   __syncthreads();
   double total = 0.0;
   long long npos = 0;
   for (int v = 0; v < kWaves; ++v) {
-    total += wsum[v];
-    npos += wpos[v];
+    total += cs.wsum[v];
+    npos += cs.wpos[v];
   }
   const double thr = u * total;
   int ow = -1;  // the last wave with mass whose running sum before it is at most thr
   double obase = 0.0, base = 0.0;
   for (int v = 0; v < kWaves; ++v) {
-    if (wsum[v] > 0.0 && base <= thr) {
+    if (cs.wsum[v] > 0.0 && base <= thr) {
       ow = v;
       obase = base;
     }
-    base += wsum[v];
+    base += cs.wsum[v];
   }
   if (w == ow) {  // uniform over the wave
     int oc = -1;  // the same over its chunks
     double ocb = 0.0, cb = obase;
     for (int c = 0; c < kCatChunks; ++c) {
-      const double cs = csum[w][c];
-      if (cs > 0.0 && cb <= thr) {
+      const double s = cs.csum[w][c];
+      if (s > 0.0 && cb <= thr) {
         oc = c;
         ocb = cb;
       }
-      cb += cs;
+      cb += s;
     }
     int64_t tok = -1;
     int margin = 1;
     if (oc >= 0) {
       const int64_t clo = lo + (int64_t)oc * kCatChunk, chi = clo + kCatChunk < n ? clo + kCatChunk : n;
       const double tol = ((double)npos + 16.0) * 0x1p-51 * total;
-      wave_slice_cdf([&](int64_t i) { return p[i]; }, clo, chi, ocb, thr, tol, tok, margin);
+      wave_slice_cdf(p, clo, chi, ocb, thr, tol, tok, margin);
     }
     if (lane == 0) {
-      found[0] = tok;
-      found[1] = margin;
+      cs.found[0] = tok;
+      cs.found[1] = margin;
     }
   }
   __syncthreads();
+  if (threadIdx.x == 0 && cs.found[1]) cs.found[0] = sequential_cdf_search(p, n, u);
+  __syncthreads();
+  token = cs.found[0];
+  flags = cs.found[1] ? DSR_FLAG_MARGIN : 0u;
+}
+
+__global__ __launch_bounds__(kThreads) void k_prob_categorical(const double* p, int64_t n, double u, int32_t* out) {
+  __shared__ CatShared cs;
+  int64_t tok;
+  unsigned flags;
+  prob_categorical_row([&](int64_t i) { return p[i]; }, n, u, cs, tok, flags);
   if (threadIdx.x == 0) {
-    int64_t tok = found[0];
-    unsigned flags = 0;
-    if (found[1]) {
-      flags |= DSR_FLAG_MARGIN;
-      tok = sequential_cdf_search(p, n, u);
-    }
     out[0] = (int32_t)tok;
     out[1] = (int32_t)flags;
   }
@@ -386,6 +398,335 @@ __global__ void k_prob_accept(const double* p, const double* q, int32_t x, doubl
     double ratio = p[x] / qx;
     ratio = ratio < 1.0 ? ratio : 1.0;
     out[1] = (qx > 0.0 && u < ratio) ? 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dsr_verify_probs: verify_drafts (sampling.py:247-294) on float64 rows the
+// caller has built, in four launches:
+//  1. k_vprobs_stats, one workgroup per 8,192-element buffer of every row:
+//     the buffer's NumPy-ordered sum, whether every entry is finite and
+//     >= 0, its positive count, first positive index, maximum and first
+//     index of the maximum;
+//  2. k_vprobs_chain, one wave per request: each row's statistics (buffer
+//     sums added in order, as np.add.reduce adds them), the checks in the
+//     reference's order and the accept chain; greedy requests end here;
+//  3. k_vprobs_draw, one workgroup per buffer of a pending replacement or
+//     bonus draw: the NumPy-ordered buffer sum of max(p - q, 0) (or of p),
+//     its support and the sums of its 512-element chunks;
+//  4. k_vprobs_finish, one wave per request: the correction total, the
+//     single-support case, the target draw and the CDF search over
+//     max(p - q, 0) / total formed on the fly.
+// The correction vector's own _distribution check is not repeated: its
+// entries r_i / total are each within half an ulp of exact and sum to 1
+// within 2^-47, far inside 1e-10, and r_i / total > 0 exactly when r_i > 0
+// (total <= 1 + 1e-10 cannot round a positive quotient to zero).
+
+constexpr int kVpBuffers = 16;  // 8,192-element buffers per row
+static_assert((int64_t)kVpBuffers * kNpBuffer >= DSR_MAX_VOCAB, "the buffers cover a row");
+constexpr int kVpChunks = kNpBuffer / kCatChunk;  // 512-element CDF chunks per buffer
+static_assert(kVpChunks == 2 * kNpBufWaves, "two chunks per wave of a draw workgroup");
+
+struct VpStat {  // one buffer of one row
+  double sum, max;
+  int32_t ok, npos, first, amax;
+};
+struct VpDraw {  // one buffer of a pending draw
+  double sum;
+  int32_t npos, first;
+  double csum[kVpChunks];
+};
+
+struct VpLayout {
+  VpStat* stat;   // [rows, 2K+1, kVpBuffers]
+  Decision* dec;  // [rows]
+  VpDraw* draw;   // [rows, kVpBuffers]
+};
+
+__host__ __device__ inline size_t vprobs_ws_bytes(int64_t rows, int32_t K) {
+  return (size_t)rows * ((size_t)(2 * K + 1) * kVpBuffers * sizeof(VpStat) + kDecisionBytes +
+                         kVpBuffers * sizeof(VpDraw));
+}
+
+__host__ __device__ inline VpLayout vprobs_layout(void* ws, int64_t rows, int32_t K) {
+  VpLayout L;
+  char* p = (char*)ws;
+  L.stat = (VpStat*)p;
+  p += (size_t)rows * (2 * K + 1) * kVpBuffers * sizeof(VpStat);
+  L.dec = (Decision*)p;
+  p += (size_t)rows * kDecisionBytes;
+  L.draw = (VpDraw*)p;
+  return L;
+}
+
+// Row `slot` of request `row`: targets 0..K, drafts K+1..2K.
+__device__ __forceinline__ const double* probs_row(const dsr_verify_probs_args_t& a, int64_t row, int slot) {
+  return slot <= a.K ? a.target[row * (a.K + 1) + slot] : a.draft[row * a.K + (slot - a.K - 1)];
+}
+
+// A reduction over the kNpBufWaves waves of a workgroup; every call needs its
+// own slot array.
+template <class T, class Op>
+__device__ __forceinline__ T buf_reduce(T x, T* slot, T id, Op op) {
+  x = wave_reduce_dpp(x, op);
+  if (lane_id() == 0) slot[wave_id()] = x;
+  __syncthreads();
+  T y = id;
+#pragma unroll
+  for (int w = 0; w < kNpBufWaves; ++w) y = op(y, slot[w]);
+  return y;
+}
+
+// Step 1.  A target row whose builder failed is not read (its records stay
+// unread too); a NULL row reads as an invalid distribution.
+__global__ __launch_bounds__(kNpBufThreads) void k_vprobs_stats(dsr_verify_probs_args_t a, VpLayout L) {
+  __shared__ NpBufShared nb;
+  __shared__ double rmax[kNpBufWaves];
+  __shared__ long long rbad[kNpBufWaves], rnpos[kNpBufWaves], rfirst[kNpBufWaves], ramax[kNpBufWaves];
+  const int slots = 2 * a.K + 1;
+  const uint32_t item = blockIdx.x;
+  const int b = (int)(item % kVpBuffers);
+  const uint32_t rs = item / kVpBuffers;
+  const int64_t row = rs / slots;
+  const int slot = (int)(rs % slots);
+  const int64_t lo = (int64_t)b * kNpBuffer;
+  if (lo >= a.vocab) return;
+  if (slot <= a.K && a.target_status && a.target_status[row * (a.K + 1) + slot] != DSR_OK) return;
+  VpStat* out = L.stat + item;
+  const double* p = probs_row(a, row, slot);
+  if (!p) {
+    if (threadIdx.x == 0) out->ok = 0;
+    return;
+  }
+  // 32-bit: hipcc (ROCm 7.2) built the 64-bit form of this minimum as an
+  // s_cselect on a stale SCC, giving 8,192 for the short last buffer.
+  const int len = min((int)(a.vocab - lo), kNpBuffer);
+  long long bad = 0, npos = 0, first = LLONG_MAX, am = LLONG_MAX;
+  double m = -INFINITY;
+  const double sum = np_buffer_sum([&](int64_t i) { return p[i]; }, lo, len, nb, [&](int64_t i, double x) {
+    if (!(isfinite(x) && x >= 0.0)) bad = 1;
+    if (x > 0.0) {
+      ++npos;
+      if (i < first) first = i;
+    }
+    if (x > m) {
+      m = x;
+      am = i;
+    }
+  });
+  bad = buf_reduce(bad, rbad, 0ll, OpMax());
+  npos = buf_reduce(npos, rnpos, 0ll, OpSum());
+  first = buf_reduce(first, rfirst, LLONG_MAX, OpMin());
+  const double M = buf_reduce(m, rmax, -(double)INFINITY, OpMax());
+  am = buf_reduce(m == M ? am : LLONG_MAX, ramax, LLONG_MAX, OpMin());
+  if (threadIdx.x == 0) {
+    out->sum = sum;
+    out->max = M;
+    out->ok = bad ? 0 : 1;
+    out->npos = (int32_t)npos;
+    out->first = first == LLONG_MAX ? -1 : (int32_t)first;
+    out->amax = am == LLONG_MAX ? -1 : (int32_t)am;
+  }
+}
+
+// Step 2.  Lane b holds buffer b of the row being combined.
+__global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, VpLayout L) {
+  __shared__ Decision d;
+  __shared__ double gua[DSR_MAX_DRAFTS];
+  __shared__ int32_t sst[2 * DSR_MAX_DRAFTS + 1], samax[2 * DSR_MAX_DRAFTS + 1];
+  const int64_t row = blockIdx.x;
+  const int K = a.K, slots = 2 * K + 1, l = lane_id();
+  const int nbuf = (int)((a.vocab + kNpBuffer - 1) / kNpBuffer);
+  for (int slot = 0; slot < slots; ++slot) {  // uniform
+    int st = DSR_OK;
+    if (slot <= K && a.target_status) st = a.target_status[row * (K + 1) + slot];
+    int32_t amax = -1;
+    if (st == DSR_OK) {
+      const VpStat* r = L.stat + (row * slots + slot) * kVpBuffers;
+      VpStat x;
+      x.sum = 0.0;
+      x.max = -INFINITY;
+      x.ok = 1;
+      x.npos = 0;
+      x.first = -1;
+      x.amax = -1;
+      if (l < nbuf) x = r[l];
+      double total = 0.0;  // np.add.reduce adds the buffers' sums in order
+      for (int b = 0; b < nbuf; ++b) {
+        const double v = __shfl(x.sum, b);
+        total = b == 0 ? v : total + v;
+      }
+      const bool ok = wave_reduce_dpp(x.ok ? 0ll : 1ll, OpMax()) == 0;
+      const double M = wave_reduce_dpp(x.max, OpMax());
+      const long long am = wave_reduce_dpp(l < nbuf && x.max == M ? (long long)x.amax : LLONG_MAX, OpMin());
+      amax = am == LLONG_MAX ? -1 : (int32_t)am;
+      // _distribution (sampling.py:109-115): finite, >= 0, sum within 1e-10 of 1.
+      st = ok && fabs(total - 1.0) <= 1e-10 ? DSR_OK : DSR_E_DISTRIBUTION;
+    }
+    if (l == 0) {
+      sst[slot] = st;
+      samax[slot] = amax;
+    }
+  }
+  __syncthreads();
+  if (l != 0) return;
+  auto status_of = [&](int slot) { return (int)sst[slot]; };
+  const bool greedy = a.greedy && a.greedy[row] != 0;
+  Request rq = request_of(a, row);
+  if (a.rng_accept) {  // the accept domain's next K draws, consumed in order
+    pcg64_draws(a.rng_accept + 4 * row, K, gua);
+    rq.ua = gua;
+  }
+  verify_precheck(a, rq, status_of, d);
+  if (d.status == DSR_OK)
+    verify_chain(
+        a, rq, greedy, 0.0, status_of, [&](int slot, int j) { return probs_row(a, row, slot)[rq.ids[j]]; },
+        [&](int j) { return (int64_t)samax[j]; }, [](int) {}, d);
+  if (d.status == DSR_OK && d.next != 0 && greedy) {  // the target's argmax (sampling.py:286,290)
+    verify_append(a, rq, d, samax[d.draw_j], 0);
+    d.next = 0;
+  }
+  L.dec[row] = d;
+  if (d.status != DSR_OK || d.next == 0) write_decision(a, row, d);
+}
+
+// Step 3.  Wave w also sums chunks 2w and 2w + 1 of the buffer (any order:
+// the search in step 4 allows for it).
+__global__ __launch_bounds__(kNpBufThreads) void k_vprobs_draw(dsr_verify_probs_args_t a, VpLayout L) {
+  __shared__ NpBufShared nb;
+  __shared__ long long rnpos[kNpBufWaves], rfirst[kNpBufWaves];
+  const int64_t row = blockIdx.x / kVpBuffers;
+  const int b = (int)(blockIdx.x % kVpBuffers);
+  const Decision* dp = L.dec + row;
+  if (dp->status != DSR_OK || dp->next == 0) return;
+  const int64_t lo = (int64_t)b * kNpBuffer;
+  if (lo >= a.vocab) return;
+  // 32-bit: hipcc (ROCm 7.2) built the 64-bit form of this minimum as an
+  // s_cselect on a stale SCC, giving 8,192 for the short last buffer.
+  const int len = min((int)(a.vocab - lo), kNpBuffer);
+  const int j = dp->draw_j;
+  const double* P = probs_row(a, row, j);
+  const double* Q = dp->next == 1 ? probs_row(a, row, a.K + 1 + j) : nullptr;
+  auto r = [&](int64_t i) { return Q ? fmax(P[i] - Q[i], 0.0) : P[i]; };
+  long long npos = 0, first = LLONG_MAX;
+  const double sum = np_buffer_sum(r, lo, len, nb, [&](int64_t i, double x) {
+    if (x > 0.0) {
+      ++npos;
+      if (i < first) first = i;
+    }
+  });
+  npos = buf_reduce(npos, rnpos, 0ll, OpSum());
+  first = buf_reduce(first, rfirst, LLONG_MAX, OpMin());
+  VpDraw* out = L.draw + blockIdx.x;
+  const int w = wave_id(), l = lane_id();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = 2 * w + h;
+    const int64_t clo = lo + (int64_t)c * kCatChunk;
+    double part = 0.0;
+#pragma unroll
+    for (int t = 0; t < kCatChunk / 64; ++t) {
+      const int64_t i = clo + 64 * t + l;
+      part += i < lo + len ? r(i) : 0.0;
+    }
+    part = wave_reduce_dpp(part, OpSum());
+    if (l == 0) out->csum[c] = part;
+  }
+  if (threadIdx.x == 0) {
+    out->sum = sum;
+    out->npos = (int32_t)npos;
+    out->first = first == LLONG_MAX ? -1 : (int32_t)first;
+  }
+}
+
+// Step 4.  Lane l holds chunks 4l .. 4l + 3 of the row (chunk c covers
+// elements 512 c .. 512 c + 511), scaled by 1 / total for a correction; the
+// chunk holding the crossing of u times their sum is walked with the exact
+// entries max(p - q, 0) / total, and a decision within the rounding band of
+// a cell edge is settled by the sequential cumulative sum (np.cumsum).
+__global__ __launch_bounds__(64) void k_vprobs_finish(dsr_verify_probs_args_t a, VpLayout L) {
+  const int64_t row = blockIdx.x;
+  Decision d = L.dec[row];
+  if (d.status != DSR_OK || d.next == 0) return;
+  const int K = a.K, l = lane_id(), j = d.draw_j;
+  const int nbuf = (int)((a.vocab + kNpBuffer - 1) / kNpBuffer);
+  const VpDraw* parts = L.draw + row * kVpBuffers;
+  const bool resid = d.next == 1;
+  const double* P = probs_row(a, row, j);
+  const double* Q = resid ? probs_row(a, row, K + 1 + j) : nullptr;
+  double bs = 0.0;
+  long long np_ = 0, f = LLONG_MAX;
+  if (l < nbuf) {
+    bs = parts[l].sum;
+    np_ = parts[l].npos;
+    f = parts[l].npos > 0 ? (long long)parts[l].first : LLONG_MAX;
+  }
+  double total = 0.0;  // np.add.reduce's order over the buffers
+  for (int b = 0; b < nbuf; ++b) {
+    const double v = __shfl(bs, b);
+    total = b == 0 ? v : total + v;
+  }
+  const long long npos = wave_reduce_dpp(np_, OpSum());
+  const long long first = wave_reduce_dpp(f, OpMin());
+  int64_t rep = -1;
+  int used = 0, status = DSR_OK, margin = 0;
+  if (resid && !(total > 0.0 && isfinite(total))) {
+    status = DSR_E_CORRECTION;  // correction_distribution (sampling.py:137-138)
+  } else if (npos == 1) {
+    rep = first;  // a single positive entry: no uniform is drawn (sampling.py:120-122)
+  } else {
+    double u = 0.0;
+    if (a.rng_target) pcg64_draws(a.rng_target + 4 * row, 1, &u);
+    else u = a.u_target[row];
+    if (!(u >= 0.0 && u < 1.0)) {
+      status = DSR_E_UNIFORM;
+    } else {
+      used = 1;
+      const double scale = resid ? total : 1.0;
+      auto q = [&](int64_t i) { return resid ? fmax(P[i] - Q[i], 0.0) / scale : P[i]; };
+      double cs[4], lane_sum = 0.0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int c = 4 * l + t, b = c / kVpChunks;
+        cs[t] = b < nbuf ? parts[b].csum[c % kVpChunks] / scale : 0.0;
+        lane_sum += cs[t];
+      }
+      const double incl = wave_scan_dpp(lane_sum);
+      const double tq = lane_value(incl, 63);
+      const double thr = u * tq;
+      // The last chunk with mass starting at or below thr.
+      double st = incl - lane_sum, cbase = 0.0;
+      int cand = -1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (cs[t] > 0.0 && st <= thr) {
+          cand = 4 * l + t;
+          cbase = st;
+        }
+        st += cs[t];
+      }
+      const unsigned long long cb = __ballot(cand >= 0);
+      if (cb) {
+        const int owner = 63 - __clzll((long long)cb);
+        const int c = __shfl(cand, owner);
+        const double base = __shfl(cbase, owner);
+        const int64_t clo = (int64_t)c * kCatChunk;
+        const int64_t chi = clo + kCatChunk < a.vocab ? clo + kCatChunk : a.vocab;
+        const double tol = ((double)npos + 16.0) * 0x1p-51 * tq;
+        wave_slice_cdf(q, clo, chi, base, thr, tol, rep, margin);
+      } else {
+        margin = 1;
+      }
+      if (margin && l == 0) rep = sequential_cdf_search(q, a.vocab, u);
+      rep = (int64_t)__shfl((long long)rep, 0);
+    }
+  }
+  if (l == 0) {
+    if (margin) d.flags |= DSR_FLAG_MARGIN;
+    Request rq = request_of(a, row);
+    if (status != DSR_OK) d.status = status;
+    else verify_append(a, rq, d, rep, used);
+    write_decision(a, row, d);
   }
 }
 
@@ -675,6 +1016,38 @@ int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream) {
     case 7: head_launch<7>(a, s); break;
     default: head_launch<8>(a, s); break;
   }
+  return launched();
+}
+
+size_t dsr_verify_probs_workspace_bytes(int64_t rows, int32_t K) {
+  if (rows < 0 || K < 0 || K > DSR_MAX_DRAFTS) return 0;
+  return vprobs_ws_bytes(rows, K);
+}
+
+int32_t dsr_verify_probs(const dsr_verify_probs_args_t* args, void* stream) {
+  if (!args) return DSR_ERR_ARG;
+  const dsr_verify_probs_args_t& a = *args;
+  if (!a.target || (a.K > 0 && (!a.draft || !a.draft_ids || (!a.u_accept && !a.rng_accept))) ||
+      (!a.u_target && !a.rng_target) || !a.output_limit || !a.out_accepted || !a.out_ids || !a.out_count ||
+      !a.out_pending || !a.out_stop || !a.out_used_accept || !a.out_used_target || !a.out_status || a.K < 0 ||
+      a.K > DSR_MAX_DRAFTS || a.rows < 0 || a.vocab < 1 || a.vocab > DSR_MAX_VOCAB || a.reserved != 0 ||
+      (a.eos_off && !a.eos_ids))
+    return DSR_ERR_ARG;
+  const int64_t slots = 2 * (int64_t)a.K + 1;
+  if (a.rows * slots * kVpBuffers > INT_MAX) return DSR_ERR_ARG;
+  if (!a.workspace || a.workspace_bytes < dsr_verify_probs_workspace_bytes(a.rows, a.K) ||
+      ((uintptr_t)a.workspace & 7u))
+    return DSR_ERR_WORKSPACE;
+  if (a.rows == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const VpLayout L = vprobs_layout(a.workspace, a.rows, a.K);
+  hipLaunchKernelGGL(k_vprobs_stats, dim3((unsigned)(a.rows * slots * kVpBuffers)), dim3(kNpBufThreads), 0, s, a, L);
+  if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  hipLaunchKernelGGL(k_vprobs_chain, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
+  if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  hipLaunchKernelGGL(k_vprobs_draw, dim3((unsigned)(a.rows * kVpBuffers)), dim3(kNpBufThreads), 0, s, a, L);
+  if (hipGetLastError() != hipSuccess) return DSR_ERR_LAUNCH;
+  hipLaunchKernelGGL(k_vprobs_finish, dim3((unsigned)a.rows), dim3(64), 0, s, a, L);
   return launched();
 }
 

@@ -177,7 +177,8 @@ struct Request {
   }
 };
 
-__device__ __forceinline__ Request request_of(const dsr_verify_args_t& a, int64_t row) {
+template <class A>
+__device__ __forceinline__ Request request_of(const A& a, int64_t row) {
   Request q;
   q.ids = a.draft_ids + row * a.K;
   q.ua = a.u_accept + row * a.K;
@@ -296,7 +297,8 @@ struct Decision {
 };
 static_assert(sizeof(Decision) == kDecisionBytes, "workspace slot of a decision");
 
-__device__ void write_decision(const dsr_verify_args_t& a, int64_t row, const Decision& d) {
+template <class A>
+__device__ void write_decision(const A& a, int64_t row, const Decision& d) {
   const int K = a.K;
   int32_t* out_ids = a.out_ids + row * (K + 1);
   const bool ok = d.status == DSR_OK;
@@ -320,8 +322,8 @@ __device__ void write_decision(const dsr_verify_args_t& a, int64_t row, const De
 // Checks made before the chain, in the reference's order (sampling.py:255-272):
 // the output limit, every proposal, the first target, then token ids.
 // status_of(slot) gives a distribution's status.
-template <class StatusOf>
-__device__ void verify_precheck(const dsr_verify_args_t& a, const Request& rq, StatusOf status_of, Decision& d) {
+template <class A, class StatusOf>
+__device__ void verify_precheck(const A& a, const Request& rq, StatusOf status_of, Decision& d) {
   const int K = a.K;
   const int64_t V = a.vocab;
   d.status = DSR_OK;
@@ -352,8 +354,8 @@ __device__ void verify_precheck(const dsr_verify_args_t& a, const Request& rq, S
 // onehot(slot) its greedy argmax, and reach(j) is called as target j is
 // reached.  On return d.next is 0 (decided), 1 (replacement draw at
 // d.draw_j) or 2 (bonus draw at d.draw_j = K).
-template <class StatusOf, class Prob, class Onehot, class Reach>
-__device__ void verify_chain(const dsr_verify_args_t& a, const Request& rq, bool greedy, double margin_rel,
+template <class A, class StatusOf, class Prob, class Onehot, class Reach>
+__device__ void verify_chain(const A& a, const Request& rq, bool greedy, double margin_rel,
                              StatusOf status_of, Prob prob, Onehot onehot, Reach reach, Decision& d) {
   const int K = a.K;
   for (int j = 0; j < K && d.status == DSR_OK; ++j) {
@@ -407,7 +409,8 @@ __device__ void verify_chain(const dsr_verify_args_t& a, const Request& rq, bool
 }
 
 // Appends the replacement / bonus token `rep` and its stop reason.
-__device__ __forceinline__ void verify_append(const dsr_verify_args_t& a, const Request& rq, Decision& d, int64_t rep,
+template <class A>
+__device__ __forceinline__ void verify_append(const A& a, const Request& rq, Decision& d, int64_t rep,
                                               int used) {
   d.ut += used;
   if (d.next == 2) d.accepted = a.K;

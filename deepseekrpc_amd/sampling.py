@@ -125,14 +125,16 @@ class SamplingPolicy:
         out = res.probs[0]
         return out if device_input else out.cpu().numpy()
 
-    def _launch_row(self, logits, n, table, bias, allow, uniform=None):
+    def _launch_row(self, logits, n, table, bias, allow, uniform=None, rng_state=None):
         """One ``dsr_sample_rows`` launch over a single validated row: its
         float64 probabilities, and with a pre-drawn ``uniform`` (a float64
-        device tensor of one element) also its categorical draw and whether
-        the draw consumed the uniform.  Nothing is synchronised."""
+        device tensor of one element) or a PCG64 ``rng_state`` (int64 ``[1,
+        4]``, advanced on the device only if the draw is needed) also its
+        categorical draw and whether the draw consumed a uniform.  Nothing is
+        synchronised."""
         x, _ = _on_device(logits)
         return batch.sample_rows(x.reshape(1, n), self._device_tensor(x.device), history=table, bias=bias,
-                                 allow_bits=allow, uniforms=uniform, probs="f64")
+                                 allow_bits=allow, uniforms=uniform, rng_state=rng_state, probs="f64")
 
 
 def _bias_table(logit_bias, n, rows=1):

@@ -42,14 +42,41 @@ import torch
 from . import _native as N
 from . import batch
 from .jsonutil import ValidationError, fingerprint, hex_id, integer
-from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, _allow_row, _bias_table, _device,
-                       _dist_checked, _logit_vector, _on_device, _raise_status, _token_index, verify_drafts)
+from .sampling import (_COUNTS_MSG, RandomStreams, SamplingPolicy, VerificationDecision, _allow_row, _bias_table,
+                       _device, _dist_checked, _logit_vector, _on_device, _raise_status, _token_index, verify_drafts)
 
 _HISTORY_LIMIT = 1048576
 _MAX_PROPOSALS = 5
 
 _MSG_WINDOW = "terminal logits do not match the complete bounded vocabulary window"
 _MSG_HEAD = "terminal logits must come from the actual FP32 CUDA vocabulary head"
+
+
+_M64 = (1 << 64) - 1
+
+
+def _state_words(generators):
+    """uint64 ``[n, 4]``: each PCG64 generator's state lo, hi, increment lo, hi."""
+    out = np.zeros((len(generators), 4), np.uint64)
+    for i, g in enumerate(generators):
+        st = g.bit_generator.state["state"]
+        out[i] = (st["state"] & _M64, st["state"] >> 64, st["inc"] & _M64, st["inc"] >> 64)
+    return out
+
+
+def _states_on_device(generators, device):
+    """The generators' PCG64 states as an int64 ``[n, 4]`` device tensor,
+    uploaded from pinned memory without a synchronisation."""
+    host = torch.from_numpy(_state_words(generators).view(np.int64)).pin_memory()
+    return host.to(device, non_blocking=True)
+
+
+def _set_state(generator, lo, hi):
+    """Give a PCG64 generator the state a kernel advanced (two int64 words)."""
+    bg = generator.bit_generator
+    st = bg.state
+    st["state"]["state"] = (lo & _M64) | ((hi & _M64) << 64)
+    bg.state = st
 
 
 def _logits_device(logits, rows, vocabulary):
@@ -131,14 +158,14 @@ def _count_hashes(counts, generated):
     """The digest's two count hashes; equal vectors (no separate generated
     counts) share one."""
     sha = _sha256_i8(counts)
-    return sha, sha if np.array_equal(counts, generated) else _sha256_i8(generated)
+    return sha, sha if generated is counts or np.array_equal(counts, generated) else _sha256_i8(generated)
 
 
-# The count hashes (about 0.4 ms per megabyte vector) of a verification run on
-# a worker thread while its target rows are on the device (hashlib and NumPy
-# release the GIL), so that prepared() finds them done; other transactions
-# hash at prepared().  One worker per process: a forked child makes its own
-# (an executor inherited over fork has no thread to run its work).
+# The count hashes (about 0.4 ms per megabyte vector) run on a worker thread
+# from the moment a transaction opens, while its rows are on the device
+# (hashlib and NumPy release the GIL), so that prepared() finds them done.
+# One worker per process: a forked child makes its own (an executor
+# inherited over fork has no thread to run its work).
 _hasher = None
 _hasher_pid = None
 
@@ -183,7 +210,15 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
     if generated is not counts and (generated.shape != counts.shape or not _valid_count_vector(
             generated, sampler.vocabulary) or (generated > counts).any()):
         raise ValidationError("generated sampling counts must be a subset of the complete history")
-    return _Controls(policy, counts.copy(), generated.copy(), remaining, frozenset(eos_ids),
+    # Frozen copies; without separate generated counts both names hold one copy.
+    frozen = counts.copy()
+    frozen.setflags(write=False)
+    if generated is counts:
+        generated = frozen
+    else:
+        generated = generated.copy()
+        generated.setflags(write=False)
+    return _Controls(policy, frozen, generated, remaining, frozenset(eos_ids),
                      None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity,
                      support, total)
 
@@ -200,6 +235,8 @@ class TerminalSampler:
         checked = _check_controls(self, *controls)   # nothing starts unless every control is valid
         work = SamplingWork(self, self.random.begin(), checked, stage)
         self.active = work
+        # The digest's count hashes, on the worker thread from here on.
+        work._counts_sha = _hash_worker().submit(_count_hashes, work.counts, work.generated_counts)
         return work
 
     def begin_seed(self, logits, *, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
@@ -259,24 +296,27 @@ class _LazyRows:
 
 class _TargetRows:
     """The verifier's target rows, all launched at once: row j conditioned on
-    the proposals ``ids[:j]`` (terminal_sampling.py:234-244), then every
-    row's statistics in one launch, with each row's status and its
-    probability at proposal j, read back with one synchronisation when the
-    verifier first asks for a row.  A row's failure, at launch or on the
-    device, is raised when the verifier reaches that row, as the lazily
-    built rows of the reference raise it."""
+    the proposals ``ids[:j]`` (terminal_sampling.py:234-244).  A row's
+    failure, at launch or on the device, is raised when the verifier reaches
+    that row, as the lazily built rows of the reference raise it.
 
-    def __init__(self, work, rows, ids):
+    ``device()`` hands the rows and their statuses to ``dsr_verify_probs``
+    when every row launched.  Otherwise (or with ``host=True``) the rows'
+    statistics are launched together, and each row's status and its
+    probability at proposal j come back with one synchronisation when the
+    host verifier first asks for a row."""
+
+    def __init__(self, work, rows, ids, host=True):
         n = len(rows)
-        self._rows, self._ids, self._host = [], ids, None
-        # [n, 3] statistics, then n statuses (int32 in a double each), then n probabilities.
-        self._buf = torch.empty(5 * n, dtype=torch.float64, device=rows.device)
+        self._rows, self._ids, self._host, self._status, self._stats = [], ids, None, [], None
         if not work._needs_history(len(ids)):
-            self._launch_together(work, rows, ids)
+            self._launch_together(work, rows)
         else:
             self._launch_each(work, rows, ids)
+        if host:
+            self._host_inputs()
 
-    def _launch_together(self, work, rows, ids):
+    def _launch_together(self, work, rows):
         """No row reads a history table, so the rows are independent: one
         launch over all of them (a launch-time failure is the same for every
         row, and the first row reports it)."""
@@ -286,52 +326,63 @@ class _TargetRows:
         except Exception as exc:
             self._rows = [exc] * n
             return
-        self._buf[3 * n:4 * n].view(torch.int32)[0::2].copy_(result.status)
-        for j in range(n):
-            row = result.probs[j]
-            x = _token_index(ids[j], row.numel()) if j < len(ids) else None
-            if x is not None:
-                self._buf[4 * n + j:4 * n + j + 1].copy_(row[x:x + 1])
-            self._rows.append(row)
-        self._stats = self._buf[:3 * n].view(n, 3)
-        batch.prob_stats_rows_launch(self._rows, self._stats)
+        self._rows = [result.probs[j] for j in range(n)]
+        self._status = [result.status]
 
     def _launch_each(self, work, rows, ids):
-        n = len(rows)
-        launched = []
-        for j in range(n):
+        for j in range(len(rows)):
             try:
                 result, _ = work._row_launch(rows[j], ids[:j])
             except Exception as exc:
                 self._rows.append(exc)
                 continue
-            row = result.probs[0]
-            self._buf[3 * n + j:3 * n + j + 1].view(torch.int32)[0:1].copy_(result.status)
-            x = _token_index(ids[j], row.numel()) if j < len(ids) else None
+            self._rows.append(result.probs[0])
+            self._status.append(result.status)
+
+    def device(self):
+        """(rows, int32 statuses) for ``dsr_verify_probs``, or None if a row
+        failed at launch."""
+        if any(isinstance(r, Exception) for r in self._rows):
+            return None
+        return self._rows, self._status[0] if len(self._status) == 1 else torch.cat(self._status)
+
+    def _host_inputs(self):
+        """The host verifier's inputs: [n, 3] statistics, then n statuses
+        (int32 in a double each), then n probabilities at the proposals, in
+        one buffer read back when the first row is asked for."""
+        n = len(self._rows)
+        launched = [j for j in range(n) if not isinstance(self._rows[j], Exception)]
+        if not launched:
+            return
+        self._buf = torch.empty(5 * n, dtype=torch.float64, device=self._rows[launched[0]].device)
+        if len(launched) == n and len(self._status) == 1 and self._status[0].numel() == n:
+            self._buf[3 * n:4 * n].view(torch.int32)[0::2].copy_(self._status[0])
+        else:  # one status per launched row
+            for status, j in zip(self._status, launched):
+                self._buf[3 * n + j:3 * n + j + 1].view(torch.int32)[0:1].copy_(status)
+        for j in launched:
+            x = _token_index(self._ids[j], self._rows[j].numel()) if j < len(self._ids) else None
             if x is not None:
-                self._buf[4 * n + j:4 * n + j + 1].copy_(row[x:x + 1])
-            self._rows.append(row)
-            launched.append(j)
+                self._buf[4 * n + j:4 * n + j + 1].copy_(self._rows[j][x:x + 1])
         self._stats = self._buf[:3 * n].view(n, 3)
-        if launched:
-            # The rows that launched fill their own slots (a failed row's slot stays unread).
-            lo = launched[0]
-            if launched == list(range(lo, lo + len(launched))):
-                batch.prob_stats_rows_launch([self._rows[j] for j in launched], self._stats[lo:lo + len(launched)])
-            else:
-                for j in launched:
-                    batch.prob_stats_launch(self._rows[j], self._stats[j])
+        # The rows that launched fill their own slots (a failed row's slot stays unread).
+        lo = launched[0]
+        if launched == list(range(lo, lo + len(launched))):
+            batch.prob_stats_rows_launch([self._rows[j] for j in launched], self._stats[lo:lo + len(launched)])
+        else:
+            for j in launched:
+                batch.prob_stats_launch(self._rows[j], self._stats[j])
 
     def __len__(self):
         return len(self._rows)
 
     def __getitem__(self, j):
-        if self._host is None:
-            self._host = self._buf.cpu()
         n = len(self._rows)
         row = self._rows[j]
         if isinstance(row, Exception):
             raise row
+        if self._host is None:
+            self._host = self._buf.cpu()
         code = int(self._host[3 * n + j:3 * n + j + 1].view(torch.int32)[0])
         if code != N.OK:
             _raise_status(code)
@@ -353,6 +404,9 @@ class SamplingWork:
         self.seed_token = None
         self.decision = None
         self.proposal_ids, self.proposal_rows = [], []
+        # Each proposal row's FP32 logits (None once a row came without them):
+        # with them the verifier runs as one batched launch that draws on the device.
+        self._draft_logits = []
         self._device_history = None   # the counts as a device table, built for the first row
         # SHA-256 of the frozen count vectors, for the digest (a future while a
         # worker thread computes it).
@@ -448,7 +502,7 @@ class SamplingWork:
         bias = _bias_table(self.logit_bias, size, rows=n)
         return batch.sample_rows(rows, self.policy._device_tensor(rows.device, rows=n), bias=bias, probs="f64")
 
-    def _row_launch(self, logits, prefix, uniform=None):
+    def _row_launch(self, logits, prefix, uniform=None, rng_state=None):
         """Validate one row and launch its distribution (and draw, given a
         uniform).  The grammar is asked for its mask first, then the row and
         controls are checked in the order of sampling.py:50-79."""
@@ -459,7 +513,7 @@ class SamplingWork:
         table = self._history(prefix) if self._needs_history(len(prefix)) else None
         bias = _bias_table(self.logit_bias, size)
         allow = _allow_row(mask, size)
-        return self.policy._launch_row(logits, size, table, bias, allow, uniform), device_input
+        return self.policy._launch_row(logits, size, table, bias, allow, uniform, rng_state), device_input
 
     def distribution(self, logits, prefix):
         """Float64 distribution of one row given a tentative accepted prefix
@@ -490,10 +544,43 @@ class SamplingWork:
 
     def _draw(self, logits, prefix, domain, finite=None):
         """(token, distribution): one fused launch draws from the row's
-        distribution with the domain's next uniform; the domain advances
-        only if the kernel consumed it.  ``finite`` is a deferred window
-        check (a device bool), read with the result and reported first."""
+        distribution with the domain's next ``Generator.random()``, taken on
+        the device from the domain's PCG64 state; the domain takes the state
+        the kernel wrote back (advanced only when the draw was needed) and the
+        draw counts in the transaction's window.  The result and the state
+        come back with one synchronisation.  ``finite`` is a deferred window
+        check (a device bool), read with the result and reported first.  A
+        window already full takes the uniform from a preview of the generator
+        instead, so that ``RandomTransaction.random`` raises exactly when the
+        draw is needed."""
         self._require_open()
+        tr = self.transaction
+        if tr.draws[domain] >= 64:
+            return self._draw_previewed(logits, prefix, domain, finite)
+        generator = tr.owner._streams[domain]
+        state = _states_on_device([generator], logits.device)
+        try:
+            result, _ = self._row_launch(logits, prefix, rng_state=state)
+        except Exception:
+            _require_finite(finite)
+            raise
+        parts = [result.tokens.long(), result.consumed.long(), result.status.long()]
+        if finite is not None:
+            parts.append(finite.long().view(1))
+        parts.append(state.view(-1)[:2])
+        token, consumed, code, *rest = torch.cat(parts).tolist()
+        if finite is not None and not rest[0]:
+            raise ValidationError(_MSG_WINDOW)
+        if code != N.OK:
+            _raise_status(code)
+        if consumed:
+            _set_state(generator, rest[-2], rest[-1])
+            tr.draws[domain] += 1
+        return token, result.probs[0]
+
+    def _draw_previewed(self, logits, prefix, domain, finite=None):
+        """``_draw`` with the uniform read from a copy of the generator; the
+        domain advances (and may raise) only if the kernel consumed it."""
         upcoming = self.transaction._preview(domain)
         # A fill kernel, not a host-to-device copy: nothing waits for it.
         uniform = torch.full((1,), upcoming, dtype=torch.float64, device=logits.device)
@@ -536,6 +623,7 @@ class SamplingWork:
                     previous, dist = self._draw(row, tuple(self.proposal_ids), "draft")
                     self.proposal_ids.append(previous)
                     self.proposal_rows.append(dist)
+                    self._draft_logits.append(row.clone())  # the caller may reuse its buffer
                     if previous in self.eos_ids:
                         break
             self._stage = _Stage.PROPOSED
@@ -585,6 +673,7 @@ class SamplingWork:
         self.transaction.draws["draft"] += draws
         self.proposal_ids.extend(ids)
         self.proposal_rows.extend(rows[j] for j in range(len(ids)))
+        self._draft_logits.extend(chain.logits[j] for j in range(len(ids)))
 
     def use_normal_decode(self):
         """Verify with no proposals: the target row's draw is the bonus token."""
@@ -597,17 +686,119 @@ class SamplingWork:
         with self._aborting_on_error():
             rows = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
             ids = list(self.proposal_ids)
-            if self.allowed is None:
-                targets = _TargetRows(self, rows, ids)
-                if self._counts_sha is None:   # the digest's hashes, while the rows are on the device
-                    self._counts_sha = _hash_worker().submit(_count_hashes, self.counts, self.generated_counts)
-            else:
+            K = len(ids)
+            if self.allowed is not None:
                 # A grammar is asked for the masks of the prefixes the verifier reaches only.
                 targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
+            elif self._draws_fit(K) and self._unfiltered(K):
+                self._decide(self._verify_logits(rows, ids))
+                return self.decision
+            else:
+                device = self._draws_fit(K) and self._rows_at_hand(K, rows.device)
+                targets = _TargetRows(self, rows, ids, host=not device)
+                ready = targets.device() if device else None
+                if ready is not None:
+                    self._decide(self._verify_rows(*ready, ids))
+                    return self.decision
+                if device:
+                    targets._host_inputs()
             self._decide(verify_drafts(targets, self.proposal_rows, ids, self.transaction,
                                        greedy=self.policy.temperature == 0, output_limit=self.remaining,
                                        eos_ids=self.eos_ids))
         return self.decision
+
+    def _draws_fit(self, K):
+        """Whether the accept and target windows hold every draw the verifier
+        may take (else the host verifier draws, and the window raises at the
+        draw that overflows it)."""
+        tr = self.transaction
+        return self.policy.temperature == 0 or (tr.draws["accept"] + K <= 64 and tr.draws["target"] + 1 <= 64)
+
+    def _rows_at_hand(self, K, device):
+        """Whether the K proposal rows are contiguous float64 vocabulary rows
+        on ``device`` (the proposal steps leave them there; rows a caller
+        supplies in another form go to the host verifier)."""
+        V = self.owner.vocabulary
+        return len(self.proposal_rows) == K and all(
+            isinstance(r, torch.Tensor) and r.device == device and r.dtype == torch.float64 and r.numel() == V
+            and r.is_contiguous() for r in self.proposal_rows)
+
+    def _unfiltered(self, K):
+        """Whether ``dsr_verify_drafts`` takes the request on its fast path:
+        the proposal logits at hand, no history table, no bias and a policy
+        with no top-k, top-p or min-p."""
+        return (len(self._draft_logits) == K == len(self.proposal_rows)
+                and all(t is not None for t in self._draft_logits)
+                and not self._needs_history(K) and not self.logit_bias
+                and batch.verify_hints(batch.policy_array([self.policy]), self.owner.vocabulary, True) != 0)
+
+    def _upload(self, ids, dev):
+        """One pinned upload: the accept and target PCG64 states, then (int32)
+        the proposal ids, the output limit and the EOS ids."""
+        tr, K, eos = self.transaction, len(ids), sorted(self.eos_ids)
+        gens = [tr.owner._streams["accept"], tr.owner._streams["target"]]
+        host = torch.empty(8 + (K + 1 + len(eos) + 1) // 2 + 1, dtype=torch.int64, pin_memory=True)
+        host[:8] = torch.from_numpy(_state_words(gens).view(np.int64).reshape(-1))
+        small = host[8:].view(torch.int32)
+        small[:K] = torch.tensor(ids, dtype=torch.int32)
+        small[K] = self.remaining
+        small[K + 1:K + 1 + len(eos)] = torch.tensor(eos, dtype=torch.int32)
+        up = host.to(dev, non_blocking=True)
+        states, small_d = up[:8].view(2, 4), up[8:].view(torch.int32)
+        eos_kw = {}
+        if eos:
+            eos_kw = dict(eos_offsets=torch.tensor([0, len(eos)], dtype=torch.int64).pin_memory().to(dev, non_blocking=True),
+                          eos_ids=small_d[K + 1:K + 1 + len(eos)])
+        return gens, states, small_d[:K], small_d[K:K + 1], eos_kw
+
+    def _decision_of(self, res, gens, states, K):
+        """The decision, the status, the draws used and the advanced states
+        read back with one synchronisation; each domain takes its state and
+        counts its draws."""
+        out = torch.cat([res.status.long(), res.accepted.long(), res.count.long(), res.pending.long(),
+                         res.stop.long(), res.used_accept.long(), res.used_target.long(), res.ids.long().view(-1),
+                         states.view(-1)]).tolist()
+        code, accepted, count, pending, stop, used_a, used_t = out[:7]
+        out_ids, words = out[7:7 + K + 1], out[8 + K:]
+        if code != N.OK:
+            _raise_status(code)
+        tr = self.transaction
+        for g, used, domain, w in ((gens[0], used_a, "accept", words[0:2]), (gens[1], used_t, "target", words[4:6])):
+            if used:
+                _set_state(g, w[0], w[1])
+                tr.draws[domain] += used
+        return VerificationDecision(accepted, tuple(out_ids[:count]), None if pending < 0 else pending,
+                                    {N.STOP_NONE: None, N.STOP_EOS: "eos", N.STOP_LENGTH: "length"}[stop])
+
+    def _verify_logits(self, rows, ids):
+        """verify_drafts (sampling.py:247-294) as one ``dsr_verify_drafts``
+        call on the target and proposal logits (its fast path: no filter,
+        history or bias), the accept test with the accept domain's next draws
+        and the replacement or bonus draw with the target domain's, all taken
+        on the device from the domains' PCG64 states."""
+        K, V = len(ids), self.owner.vocabulary
+        dev = rows.device
+        gens, states, ids_d, limit, eos_kw = self._upload(ids, dev)
+        draft = torch.stack(self._draft_logits).reshape(1, K, V) if K else None
+        res = batch.verify_drafts(rows.contiguous().reshape(1, K + 1, V), draft, ids_d,
+                                  self.policy._device_tensor(dev), None, None, limit,
+                                  rng_accept=states[0:1], rng_target=states[1:2], **eos_kw)
+        return self._decision_of(res, gens, states, K)
+
+    def _verify_rows(self, targets, status, ids):
+        """verify_drafts (sampling.py:247-294) as one ``dsr_verify_probs`` call
+        on the float64 target rows (row j conditioned on ``ids[:j]``,
+        terminal_sampling.py:127-136) and the proposal rows the proposals
+        were drawn from, with the accept and target draws taken on the device
+        from the domains' PCG64 states; a target row whose launch failed on
+        the device fails when the chain reaches it."""
+        K, dev = len(ids), targets[0].device
+        gens, states, ids_d, limit, eos_kw = self._upload(ids, dev)
+        greedy = torch.ones(1, dtype=torch.uint8, device=dev) if self.policy.temperature == 0 else None
+        res = batch.verify_probs(targets, self.proposal_rows, ids_d, limit, vocab=self.owner.vocabulary,
+                                 greedy=greedy, rng_accept=states[0:1], rng_target=states[1:2],
+                                 target_status=status, **eos_kw)
+        return self._decision_of(res, gens, states, K)
 
     def _digest_record(self):
         """The fields the decision digest covers (terminal_sampling.py:189-196).
@@ -663,6 +854,8 @@ class SamplingWork:
     def _close(self):
         self.closed = True
         self.owner.active = None
+        if self._counts_sha is not None and not isinstance(self._counts_sha, tuple):
+            self._counts_sha.cancel()   # a hash not yet started is dropped
 
 
 def _cut_at_stop(decision, kept):

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSR_ABI_VERSION 4
+#define DSR_ABI_VERSION 5
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
@@ -229,6 +229,50 @@ typedef struct dsr_verify_args {
   uint32_t reserved;           /* must be 0 (else DSR_ERR_ARG) */
 } dsr_verify_args_t;
 
+/* Arguments of dsr_verify_probs: verify_drafts (sampling.py:247-294) on
+ * float64 probability rows the caller has already built, one request per
+ * `rows`, K drafts each.  Row pointers are read on the device: `target` and
+ * `draft` are device arrays of device pointers, each to `vocab` float64
+ * probabilities (target row j of request r at target[r * (K + 1) + j],
+ * draft row j at draft[r * K + j]).  Every row is checked as
+ * _distribution checks it (finite, >= 0, NumPy-ordered sum within 1e-10 of
+ * 1; sampling.py:109-115), the drafts and target 0 before the chain, target
+ * j > 0 when the chain reaches it.  target_status, when set, holds the
+ * status of whatever built each target row: a row whose status is not
+ * DSR_OK fails with that status when the chain reaches it (its pointer is
+ * then never read and may be NULL), as the reference's lazily built targets
+ * fail.  Draws and the write-back of rng_accept / rng_target are those of
+ * dsr_verify_args_t. */
+typedef struct dsr_verify_probs_args {
+  const double* const* target; /* device [rows * (K+1)] device row pointers */
+  const double* const* draft;  /* device [rows * K] device row pointers (unread when K == 0) */
+  const int32_t* target_status;/* [rows, K+1] or NULL (every target row DSR_OK) */
+  int32_t K;                   /* 0 .. 5 */
+  uint32_t reserved;           /* must be 0 (else DSR_ERR_ARG) */
+  int64_t rows;
+  int64_t vocab;               /* 1 .. 129280 */
+  const int32_t* draft_ids;    /* [rows, K] */
+  const uint8_t* greedy;       /* [rows]: nonzero = verify_drafts(greedy=True), or NULL: none */
+  const double* u_accept;      /* [rows, K], or NULL with rng_accept */
+  const double* u_target;      /* [rows], or NULL with rng_target */
+  const int64_t* eos_off;      /* [rows + 1] CSR of EOS ids, or NULL */
+  const int32_t* eos_ids;
+  const int32_t* output_limit; /* [rows], 1 .. 1048576 */
+  int32_t* out_accepted;       /* outputs as dsr_verify_args_t */
+  int32_t* out_ids;            /* [rows, K+1] */
+  int32_t* out_count;
+  int32_t* out_pending;
+  int32_t* out_stop;
+  int32_t* out_used_accept;
+  int32_t* out_used_target;
+  int32_t* out_status;
+  uint8_t* out_flags;          /* [rows] or NULL */
+  void* workspace;             /* >= dsr_verify_probs_workspace_bytes(rows, K), 8-byte aligned */
+  size_t workspace_bytes;
+  uint64_t* rng_accept;        /* [rows, 4] PCG64 states of the accept domain, or NULL */
+  uint64_t* rng_target;        /* [rows, 4] PCG64 states of the target domain, or NULL */
+} dsr_verify_probs_args_t;
+
 /* Vocabulary projection (the terminal stage's lm_head, stage_graph.py:356-362
  * and :396).  One record per (row, DSR_HEAD_TILE-column tile) of its FP32
  * logits, written by the projection's epilogue: what the verifier's fast
@@ -269,6 +313,7 @@ const char* dsr_status_message(int32_t code);
 /* Workspace queries. */
 size_t dsr_sample_workspace_bytes(int64_t rows, int64_t vocab);
 size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab);
+size_t dsr_verify_probs_workspace_bytes(int64_t rows, int32_t K);
 
 /* Fused penalties -> temperature -> top-k -> softmax -> min-p -> top-p ->
  * categorical draw for `rows` independent rows.
@@ -318,6 +363,14 @@ int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream);
  * dsr_verify_drafts. */
 int32_t dsr_verify_drafts_head(const dsr_verify_args_t* args, const dsr_head_part_t* target_parts,
                                const dsr_head_part_t* draft_parts, void* stream);
+
+/* Exact sampled verifier over float64 rows already on the device; replaces
+ * verify_drafts (sampling.py:247-294) as SamplingWork.verify calls it
+ * (terminal_sampling.py:170-183) with target rows it has built.  Four
+ * launches: every row's statistics (one workgroup per 8,192 entries), the
+ * chain (one wave per request), the sums of a pending replacement or bonus
+ * draw (one workgroup per 8,192 entries) and the draw itself. */
+int32_t dsr_verify_probs(const dsr_verify_probs_args_t* args, void* stream);
 
 /* Probability-vector kernels behind the drop-in categorical /
  * correction_distribution / verify_drafts on float64 distributions.

@@ -60,6 +60,10 @@ def test_workspace_queries():
     expect = (rows * slots * 129280 * 8 + rows * slots * 16 + rows * slots * 32 + rows * slots * 16 * 32
               + rows * 32 * 32 + rows * 2048 * 8 + rows * 64)
     assert lib.dsr_verify_workspace_bytes(rows, 4, 129280) == expect
+    # Per request: a 32-byte record per 8,192-entry buffer (16) of each of
+    # the 2K+1 rows, a 64-byte decision, and 16 draw records of 144 bytes.
+    assert lib.dsr_verify_probs_workspace_bytes(rows, 4) == rows * (9 * 16 * 32 + 64 + 16 * 144)
+    assert lib.dsr_verify_probs_workspace_bytes(rows, 6) == 0
 
 
 def test_argument_errors_return_before_any_launch():
@@ -85,6 +89,30 @@ def test_argument_errors_return_before_any_launch():
         setattr(v, field, 0)
     v.hints = N.HINT_VERIFY_FAST
     assert lib.dsr_verify_drafts(ctypes.byref(v), None) == 0
+    p = N.VerifyProbsArgs()  # all null
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == -1
+    assert lib.dsr_verify_probs(None, None) == -1
+    p.target = p.u_target = p.output_limit = 4096
+    p.out_accepted = p.out_ids = p.out_count = p.out_pending = p.out_stop = 4096
+    p.out_used_accept = p.out_used_target = p.out_status = 4096
+    p.K, p.rows, p.vocab = 0, 0, 8
+    p.workspace, p.workspace_bytes = 4096, 0
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == 0       # no requests: nothing to launch
+    for field, bad in (("reserved", 1), ("K", 6), ("K", -1), ("vocab", 0), ("vocab", 129281), ("rows", -1),
+                       ("eos_off", 4096)):
+        good = getattr(p, field)
+        setattr(p, field, bad)
+        assert lib.dsr_verify_probs(ctypes.byref(p), None) == -1, (field, bad)
+        setattr(p, field, good)
+    p.K = 2                                                        # drafts without their rows, ids or uniforms
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == -1
+    p.draft = p.draft_ids = p.u_accept = 4096
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == 0
+    p.rows = 1                                                     # workspace one byte short
+    p.workspace_bytes = lib.dsr_verify_probs_workspace_bytes(1, 2) - 1
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == -3
+    p.workspace, p.workspace_bytes = 4100, p.workspace_bytes + 1   # misaligned
+    assert lib.dsr_verify_probs(ctypes.byref(p), None) == -3
     s = N.SampleArgs()
     s.logits = s.policy = s.out_token = s.out_consumed = s.out_status = 4096
     s.dtype, s.rows, s.vocab, s.ld = N.F32, 0, 8, 8
@@ -140,6 +168,7 @@ int main(void) {
   printf("dsr_verify_args_t size %zu\n", sizeof(dsr_verify_args_t));
   printf("dsr_head_part_t size %zu\n", sizeof(dsr_head_part_t));
   printf("dsr_head_args_t size %zu\n", sizeof(dsr_head_args_t));
+  printf("dsr_verify_probs_args_t size %zu\n", sizeof(dsr_verify_probs_args_t));
   %FIELDS%
   return 0;
 }
@@ -147,7 +176,8 @@ int main(void) {
 
 
 STRUCTS = (("dsr_policy_t", N.Policy), ("dsr_sample_args_t", N.SampleArgs), ("dsr_verify_args_t", N.VerifyArgs),
-           ("dsr_head_part_t", N.HeadPart), ("dsr_head_args_t", N.HeadArgs))
+           ("dsr_head_part_t", N.HeadPart), ("dsr_head_args_t", N.HeadArgs),
+           ("dsr_verify_probs_args_t", N.VerifyProbsArgs))
 
 
 def test_struct_layouts_match_header(tmp_path):

@@ -459,3 +459,83 @@ def test_digests_match_the_reference_recording():
     assert work.prepared()["digest"] == gold["verify"]["digest"]
     work.commit(work.prepared()["digest"])
     assert sampler.random.snapshot() == gold["final_rng"]["snapshot"]
+
+
+class _DeviceMarkov(MarkovGraph):
+    """A graph that also makes its rows on the device (the proposal chain's
+    device route); the previous token arrives as a device int32 tensor."""
+
+    def draft_conditional_logits_device(self, result, row, previous):
+        base = torch.as_tensor(self.rows(row, 0), device="cuda").reshape(1, -1).clone()
+        base[0].index_add_(0, previous.long(), torch.full((1,), 2.5, device="cuda"))
+        return base, None
+
+
+@pytest.mark.parametrize("device_graph", [False, True])
+def test_batched_device_draws_decide_as_the_host_verifier(device_graph, monkeypatch):
+    """The speculative step with every draw on the device (the seed, the
+    proposals, the accept tests and the replacement or bonus draw: one
+    ``dsr_verify_drafts`` call on the logits for unfiltered requests, one
+    ``dsr_verify_probs`` call on the float64 rows for the others) against
+    the same steps through the host verifier loop: equal decisions, digests
+    and RNG snapshots, over penalties, bias, filters, EOS ids and output
+    limits."""
+    import deepseekrpc_amd.terminal_sampling as TS
+    rng = np.random.default_rng(4242 + device_graph)
+    base = rng.normal(0, 2, (6, V)).astype(np.float32)
+    batched = []
+    real_logits, real_rows = TS.SamplingWork._verify_logits, TS.SamplingWork._verify_rows
+
+    def spy_logits(self, rows, ids):
+        batched.append("logits")
+        return real_logits(self, rows, ids)
+
+    def spy_rows(self, targets, status, ids):
+        batched.append("rows")
+        return real_rows(self, targets, status, ids)
+
+    def run(force_host, seed, policy, remaining, eos, bias):
+        if force_host:
+            monkeypatch.setattr(TS.SamplingWork, "_draws_fit", lambda self, K: False)
+        else:
+            monkeypatch.setattr(TS.SamplingWork, "_verify_logits", spy_logits)
+            monkeypatch.setattr(TS.SamplingWork, "_verify_rows", spy_rows)
+        sampler = TerminalSampler(seed)
+        counts = np.zeros(V, np.int32)
+        counts[rng_hist] = 1
+        work = sampler.begin_seed(base[:1], policy=policy, counts=counts, remaining=remaining, eos_ids=eos,
+                                  logit_bias=bias)
+        out = [work.prepared()]
+        work.commit(work.prepared()["digest"])
+        counts[work.decision.token] += 1
+        draft = (lambda row, prev: base[1 + row % 4] * 0.9) if device_graph else \
+            (lambda row, prev: base[1 + row % 4] * 0.9 + (prev % 7) * 0.01)
+        graph = _DeviceMarkov(draft) if device_graph else MarkovGraph(draft)
+        work = sampler.begin_verification(seed_token=work.decision.token, policy=policy, counts=counts,
+                                          remaining=remaining, eos_ids=eos, logit_bias=bias)
+        ids = work.propose(graph, None)
+        targets = base[:len(ids) + 1] + rng_noise[:len(ids) + 1]
+        work.verify(targets)
+        out.append(work.prepared())
+        work.commit(work.prepared()["digest"])
+        out.append(sampler.random.snapshot())
+        monkeypatch.undo()
+        return out
+
+    cases = [
+        (SamplingPolicy(), 20, frozenset(), None),
+        (SamplingPolicy(temperature=0.8, top_k=40, top_p=0.9), 20, frozenset(), {3: 2.0, 11: -1.5}),
+        (SamplingPolicy(temperature=1.1, repetition_penalty=1.3, presence_penalty=0.4, frequency_penalty=0.2),
+         3, frozenset(), None),
+        (SamplingPolicy(temperature=0.0), 20, frozenset(), None),
+        (SamplingPolicy(temperature=0.6, min_p=0.02), 20, frozenset(range(0, V, 3)), None),
+    ]
+    for i, (policy, remaining, eos, bias) in enumerate(cases):
+        rng_hist = rng.choice(V, 200, replace=False)
+        rng_noise = rng.normal(0, 0.3, (6, V)).astype(np.float32)
+        n_before = len(batched)
+        dev = run(False, 700 + i, policy, remaining, eos, bias)
+        host = run(True, 700 + i, policy, remaining, eos, bias)
+        assert len(batched) == n_before + 1, "the device route was not taken"
+        assert dev == host, (i, dev[1]["decision"], host[1]["decision"])
+    assert batched == ["logits", "rows", "rows", "logits", "rows"], batched
