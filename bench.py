@@ -49,6 +49,8 @@ PEAK_HBM_GBS = 8000.0
 WORKLOADS = {
     "c3": ("sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline", "rows/s", 5,
            "k_sample_bf16_fast"),
+    "c3f32": ("sampled rows/sec at B=256×V=129,280 fp32; % of HBM roofline", "rows/s", 5,
+              "k_split_select + k_split_finish"),
     "c1": ("sampled rows/sec at B=1×V=129,280 fp32 with fp32 probabilities out", "rows/s", 1000,
            "k_split_select + k_split_finish"),
     "c2": ("sampled rows/sec at B=64×V=129,280 bf16 with 4,096-token histories", "rows/s", 20,
@@ -63,9 +65,10 @@ WORKLOADS = {
               5, "k_sample_bf16_full"),
     "step": ("drop-in speculative steps/sec: propose 5 rows on the device, verify against 6 fp32 rows, digest",
              "steps/s", 30, "k_split_select + k_split_finish (proposals; the six targets in one launch) + "
-             "k_prob_stats_rows + k_prob_correction / k_prob_stats / k_prob_categorical (a rejection's draw)"),
+             "k_rows_finite + k_vprobs_stats + k_vprobs_chain + k_vprobs_draw + k_vprobs_finish"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
-             300, "k_split_select + k_split_finish (a policy without penalties carries no history table)"),
+             300, "k_rows_finite + k_split_select + k_split_finish (a policy without penalties carries no history "
+             "table)"),
     "head": ("verify-rows/sec with the vocabulary projection: B=32 requests × K=4 drafts, 160 target rows × "
              "dim 5,120 → V=129,280 fp32 logits", "verify-rows/s", 30,
              "k_vocab_head + k_head_shares + k_verify_chain + k_verify_draw + k_verify_finish"),
@@ -75,7 +78,8 @@ WORKLOADS = {
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
-PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "propose": "k_split", "seed": "k_split", "step": "k_split",
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "c3f32": "k_split", "propose": "k_split", "seed": "k_split",
+                  "step": "k_split",
                   "head": "k_vocab_head"}
 
 DESCRIPTIONS = {
@@ -83,6 +87,7 @@ DESCRIPTIONS = {
     "c2": "c2: 64 rows x 129280 bf16 N(0,3^2), 4096-token generated histories, rep 1.1 / pres 0.5 / freq 0.3, "
           "T 1, top-p 0.95",
     "c3": "c3: 256 rows x 129280 bf16 heavy-tail logits, per-row T/top-k/top-p, 10% allow mask",
+    "c3f32": "c3f32: c3's rows as fp32 logits (before bf16 rounding), per-row T/top-k/top-p, 10% allow mask",
     "c4": "c4: 32 requests x 4 drafts, fp32 target [32,5,129280] and draft [32,4,129280], default policy, limit 10",
     "c5": "c5: 1024 rows x 129280 bf16 (N(0,1) / near-flat with 8-way max ties), even rows greedy, odd rows T 1 "
           "top-p 0.9, rep 1.1 / pres 0.5 / freq 0.3 over 16384-token histories",
@@ -325,6 +330,18 @@ class _HistResult:
         self.flags = torch.zeros_like(status)
 
 
+_DONE = []
+
+
+def _done_result():
+    """A status-OK result for the drop-in legs (which raise on any error),
+    made once so that the timed calls allocate nothing for it."""
+    if not _DONE:
+        import torch
+        _DONE.append(_HistResult(torch.zeros(1, dtype=torch.int32, device="cuda")))
+    return _DONE[0]
+
+
 # Inputs rotated through the timed region exceed this many bytes together.
 ROTATION_BYTES = 300 * 2**20
 
@@ -389,7 +406,7 @@ class _Chain:
         if len(ids) != self.w.extra["steps"]:
             raise SystemExit(f"the proposal chain stopped after {len(ids)} rows")
         work.abort()
-        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        self.result = _done_result()
         return self
 
 
@@ -411,7 +428,7 @@ class _Step(_Chain):
         work.verify(self.target[: len(ids) + 1])
         work.prepared()
         work.abort()
-        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        self.result = _done_result()
         return self
 
 
@@ -436,7 +453,7 @@ class _Seed:
         import torch
         work = self.sampler.begin_seed(self.logits, policy=self.policy, counts=self.counts, remaining=9)
         work.abort()
-        self.result = _HistResult(torch.zeros(1, dtype=torch.int32, device="cuda"))
+        self.result = _done_result()
         return self
 
 

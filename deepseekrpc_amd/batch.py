@@ -1089,6 +1089,23 @@ def vocab_head_launch(res: HeadResult) -> HeadResult:
 # Probability-vector kernels used by the drop-in API.
 
 
+def rows_finite(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 ``[rows]``: 1 where every value of the FP32 row of ``x [rows, n]``
+    is finite (``dsr_rows_finite``); nothing synchronises.  ``out`` may be an
+    int32 device tensor of ``rows`` elements that already holds 1s (the
+    kernel only clears the flags of rows with a non-finite value)."""
+    lib = N.load()
+    _require_cuda(x, "x", rows_strided=True)
+    if x.dim() != 2 or x.dtype != torch.float32:
+        raise ValueError("x must be a [rows, n] float32 tensor")
+    rows, n = x.shape
+    if out is None:
+        out = torch.ones(rows, dtype=torch.int32, device=x.device)
+    _require(out, "out", torch.int32, rows)
+    N.check(lib.dsr_rows_finite(_ptr(x), rows, n, x.stride(0), _ptr(out), _stream()), "dsr_rows_finite")
+    return out
+
+
 def prob_stats_launch(p: torch.Tensor, slot: torch.Tensor):
     """``dsr_prob_stats`` of a float64 device vector into ``slot``, a float64
     ``[3]`` device view: the sum, then the four int32 results.  Nothing is

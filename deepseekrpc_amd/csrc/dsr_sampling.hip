@@ -402,6 +402,45 @@ __global__ void k_prob_accept(const double* p, const double* q, int32_t x, doubl
 }
 
 // ---------------------------------------------------------------------------
+// dsr_rows_finite: np.isfinite(row).all() of FP32 rows (the terminal window
+// check, terminal_sampling.py:25).  A row is spread over workgroups of 4,096
+// values (one CU pulls a 517 KB row at about 28 GB/s: 18.5 us for one
+// workgroup per row), and a thread that finds a value whose exponent field
+// is all ones stores 0 to the row's flag, which the caller set to 1: no
+// reduction and no second launch.  16-byte loads when the row starts on a
+// 16-byte boundary.
+constexpr int kFiniteChunk = 4096;
+constexpr int kFiniteThreads = 256;
+
+__device__ __forceinline__ uint32_t nonfinite_bits(uint32_t u) { return (u & 0x7F800000u) == 0x7F800000u; }
+
+__global__ __launch_bounds__(kFiniteThreads) void k_rows_finite(const float* x, int64_t n, int64_t ld, int chunks,
+                                                                int32_t* out) {
+  const int64_t r = blockIdx.x / chunks;
+  const int64_t lo = (int64_t)(blockIdx.x % chunks) * kFiniteChunk;
+  const int64_t hi = lo + kFiniteChunk < n ? lo + kFiniteChunk : n;
+  const float* row = x + r * ld;
+  uint32_t bad = 0;
+  if (((uintptr_t)row & 15u) == 0) {
+    const uint4* v = (const uint4*)(row + lo);
+    const int64_t nv = (hi - lo) / 4;
+    uint4 q[kFiniteChunk / 4 / kFiniteThreads];
+#pragma unroll
+    for (int u = 0; u < kFiniteChunk / 4 / kFiniteThreads; ++u) {
+      const int64_t i = threadIdx.x + (int64_t)u * kFiniteThreads;
+      q[u] = i < nv ? v[i] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kFiniteChunk / 4 / kFiniteThreads; ++u)
+      bad |= nonfinite_bits(q[u].x) | nonfinite_bits(q[u].y) | nonfinite_bits(q[u].z) | nonfinite_bits(q[u].w);
+    for (int64_t i = lo + 4 * nv + threadIdx.x; i < hi; i += kFiniteThreads) bad |= nonfinite_bits(__float_as_uint(row[i]));
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kFiniteThreads) bad |= nonfinite_bits(__float_as_uint(row[i]));
+  }
+  if (bad) out[r] = 0;
+}
+
+// ---------------------------------------------------------------------------
 // dsr_verify_probs: verify_drafts (sampling.py:247-294) on float64 rows the
 // caller has built, in four launches:
 //  1. k_vprobs_stats, one workgroup per 8,192-element buffer of every row:
@@ -1086,6 +1125,16 @@ int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, 
                         void* stream) {
   if (!p || !q || !out_i32 || n < 1 || n > DSR_MAX_VOCAB || x < 0 || x >= n) return DSR_ERR_ARG;
   hipLaunchKernelGGL(k_prob_accept, dim3(1), dim3(64), 0, (hipStream_t)stream, p, q, x, u, out_i32);
+  return launched();
+}
+
+int32_t dsr_rows_finite(const float* x, int64_t rows, int64_t n, int64_t ld, int32_t* out, void* stream) {
+  if (!x || !out || rows < 0 || n < 1 || ld < n) return DSR_ERR_ARG;
+  if (rows == 0) return 0;
+  const int64_t chunks = (n + kFiniteChunk - 1) / kFiniteChunk;
+  if (chunks > INT_MAX || rows * chunks > INT_MAX) return DSR_ERR_ARG;
+  hipLaunchKernelGGL(k_rows_finite, dim3((unsigned)(rows * chunks)), dim3(kFiniteThreads), 0, (hipStream_t)stream, x,
+                     n, ld, (int)chunks, out);
   return launched();
 }
 

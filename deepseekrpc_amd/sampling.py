@@ -125,16 +125,18 @@ class SamplingPolicy:
         out = res.probs[0]
         return out if device_input else out.cpu().numpy()
 
-    def _launch_row(self, logits, n, table, bias, allow, uniform=None, rng_state=None):
+    def _launch_row(self, logits, n, table, bias, allow, uniform=None, rng_state=None, out=None, probs="f64"):
         """One ``dsr_sample_rows`` launch over a single validated row: its
-        float64 probabilities, and with a pre-drawn ``uniform`` (a float64
-        device tensor of one element) or a PCG64 ``rng_state`` (int64 ``[1,
-        4]``, advanced on the device only if the draw is needed) also its
+        float64 probabilities (unless ``probs`` is None; ``out`` may hold the
+        per-row outputs, as ``sample_rows`` takes them), and with a pre-drawn
+        ``uniform`` (a float64 device tensor of one element) or a PCG64
+        ``rng_state`` (int64 ``[1, 4]``, advanced on the device only if the
+        draw is needed) also its
         categorical draw and whether the draw consumed a uniform.  Nothing is
         synchronised."""
         x, _ = _on_device(logits)
         return batch.sample_rows(x.reshape(1, n), self._device_tensor(x.device), history=table, bias=bias,
-                                 allow_bits=allow, uniforms=uniform, rng_state=rng_state, probs="f64")
+                                 allow_bits=allow, uniforms=uniform, rng_state=rng_state, probs=probs, out=out)
 
 
 def _bias_table(logit_bias, n, rows=1):
@@ -346,7 +348,10 @@ def correction_distribution(target, proposal):
 
 
 def _export(generator):
-    state = generator.bit_generator.state
+    return _export_state(generator.bit_generator.state)
+
+
+def _export_state(state):
     return {"state": f"{state['state']['state']:032x}", "increment": f"{state['state']['inc']:032x}",
             "has_uint32": state["has_uint32"], "uinteger": state["uinteger"]}
 
@@ -403,7 +408,9 @@ class RandomStreams:
     def begin(self):
         if self.active:
             raise ValidationError("terminal RNG transaction is already active")
-        before = self.snapshot()
+        # The domains' raw bit-generator states: an abort puts them back in
+        # place, with no snapshot text to format or parse.
+        before = {name: g.bit_generator.state for name, g in self._streams.items()}
         self.active = True
         return RandomTransaction(self, before)
 
@@ -412,8 +419,13 @@ class RandomTransaction:
     """One bounded window of draws, committed or fully rolled back (sampling.py:205-231)."""
 
     def __init__(self, owner, before):
-        self.owner, self.before, self.closed = owner, before, False
+        self.owner, self._before, self.closed = owner, before, False
         self.draws = dict.fromkeys(DOMAINS, 0)
+
+    @property
+    def before(self):
+        """The snapshot taken when the transaction began."""
+        return {"algorithm": "PCG64-domains-v1", "domains": {name: _export_state(st) for name, st in self._before.items()}}
 
     def random(self, domain):
         if self.closed or domain not in DOMAINS or self.draws[domain] >= 64:
@@ -445,7 +457,8 @@ class RandomTransaction:
     def abort(self):
         if self.closed:
             raise ValidationError("terminal RNG transaction is already closed")
-        self.owner._restore(self.before)
+        for name, state in self._before.items():
+            self.owner._streams[name].bit_generator.state = state
         self.closed, self.owner.active = True, False
 
 

@@ -91,27 +91,60 @@ def _logits_device(logits, rows, vocabulary):
         return _on_device(logits)[0]
     if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32):
         raise ValidationError(_MSG_HEAD)
-    if tuple(logits.shape) != (rows, vocabulary) or not bool(torch.isfinite(logits).all()):
+    if tuple(logits.shape) != (rows, vocabulary):
         raise ValidationError(_MSG_WINDOW)
-    return logits.detach().contiguous()
+    window = logits.detach().contiguous()
+    _require_finite(batch.rows_finite(window))
+    return window
 
 
 def _logits_deferred(logits, rows, vocabulary):
-    """``_logits_device`` with the finiteness test of a CUDA window left on
-    the device: ``(window, finite)``, ``finite`` a device bool the caller
-    reads with its next synchronisation (None when the window was checked
-    here).  Every other check runs at once, as in ``_logits_device``."""
+    """``_logits_device`` with the finiteness test of a CUDA window left to
+    the caller: ``(window, deferred)``, ``deferred`` True when the caller
+    must still run ``dsr_rows_finite`` on the window (into flags it has set
+    to 1) and read the flags with its next synchronisation.  Every other
+    check runs at once, as in ``_logits_device``."""
     if (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
             and tuple(logits.shape) == (rows, vocabulary)):
-        window = logits.detach().contiguous()
-        return window, torch.isfinite(window).all()
-    return _logits_device(logits, rows, vocabulary), None
+        return logits.detach().contiguous(), True
+    return _logits_device(logits, rows, vocabulary), False
 
 
 def _require_finite(finite):
     """Reports a deferred non-finite window, ahead of any later error."""
-    if finite is not None and not bool(finite):
+    if finite is not None and int(finite.min()) == 0:
         raise ValidationError(_MSG_WINDOW)
+
+
+class _DrawIO:
+    """A sampler's device buffer for single-row draws on one device: the
+    domain's PCG64 state (advanced in place by the kernel), the row's token,
+    status, consumed and flags outputs and the window's finite flag, all in
+    64 bytes read back with one copy."""
+
+    def __init__(self, device):
+        self.dev = torch.zeros(8, dtype=torch.int64, device=device)
+        b32, b8 = self.dev.view(torch.int32), self.dev.view(torch.uint8)
+        self.state = self.dev[0:4].view(1, 4)
+        self.out = {"tokens": b32[8:9], "status": b32[9:10], "consumed": b8[40:41], "flags": b8[41:42]}
+        self.finite = b32[12:13]
+
+    def upload(self, generator, finite=False):
+        """The generator's state into the buffer (and with ``finite`` the
+        window's flag set to 1 for ``dsr_rows_finite``), from pinned memory,
+        without a synchronisation (the caching host allocator keeps the
+        pinned block until the copy has run)."""
+        host = torch.zeros(8 if finite else 4, dtype=torch.int64, pin_memory=True)
+        words = host.numpy()
+        words[:4] = _state_words([generator]).view(np.int64)[0]
+        if finite:
+            words.view(np.int32)[12] = 1
+        self.dev[:host.numel()].copy_(host, non_blocking=True)
+
+    def read(self):
+        w = self.dev.cpu().numpy()
+        i32, u8 = w.view(np.int32), w.view(np.uint8)
+        return int(w[0]), int(w[1]), int(i32[8]), int(i32[9]), int(u8[40]), int(i32[12])
 
 
 @dataclass(frozen=True)
@@ -161,9 +194,10 @@ def _count_hashes(counts, generated):
     return sha, sha if generated is counts or np.array_equal(counts, generated) else _sha256_i8(generated)
 
 
-# The count hashes (about 0.4 ms per megabyte vector) run on a worker thread
-# from the moment a transaction opens, while its rows are on the device
-# (hashlib and NumPy release the GIL), so that prepared() finds them done.
+# The count hashes (about 0.4 ms per megabyte vector) of a verification run on
+# a worker thread from the moment its transaction opens, while its rows are on
+# the device (hashlib and NumPy release the GIL), so that prepared() finds
+# them done.
 # One worker per process: a forked child makes its own (an executor
 # inherited over fork has no thread to run its work).
 _hasher = None
@@ -231,12 +265,23 @@ class TerminalSampler:
         self.vocabulary = integer(vocabulary, "sampling vocabulary", 1, 129280)
         self.active = None
 
+    def _io(self, device):
+        """The ``_DrawIO`` of ``device`` (made on first use)."""
+        ios = self.__dict__.setdefault("_ios", {})
+        io = ios.get(device.index)
+        if io is None:
+            io = ios[device.index] = _DrawIO(device)
+        return io
+
     def _open_work(self, stage, *controls):
         checked = _check_controls(self, *controls)   # nothing starts unless every control is valid
         work = SamplingWork(self, self.random.begin(), checked, stage)
         self.active = work
-        # The digest's count hashes, on the worker thread from here on.
-        work._counts_sha = _hash_worker().submit(_count_hashes, work.counts, work.generated_counts)
+        if stage is _Stage.AWAITING_PROPOSALS:
+            # The digest's count hashes, on the worker thread while the
+            # proposals and the verification run (a seed's digest follows its
+            # one launch at once, so its hashes wait for prepared()).
+            work._counts_sha = _hash_worker().submit(_count_hashes, work.counts, work.generated_counts)
         return work
 
     def begin_seed(self, logits, *, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
@@ -249,10 +294,11 @@ class TerminalSampler:
             # between the window check and the draw, so the window's
             # finiteness is read with the draw's result.
             if work.allowed is None:
-                window, finite = _logits_deferred(logits, 1, self.vocabulary)
+                window, deferred = _logits_deferred(logits, 1, self.vocabulary)
             else:
-                window, finite = _logits_device(logits, 1, self.vocabulary), None
-            token, _ = work._draw(window[0], (), "target", finite)
+                window, deferred = _logits_device(logits, 1, self.vocabulary), False
+            # The seed's row is not kept.
+            token, _ = work._draw(window[0], (), "target", window if deferred else None, probs=None)
             stop = "eos" if token in work.eos_ids else "length" if remaining == 1 else None
             work._decide(SeedDecision(token, stop))
         return work
@@ -502,7 +548,7 @@ class SamplingWork:
         bias = _bias_table(self.logit_bias, size, rows=n)
         return batch.sample_rows(rows, self.policy._device_tensor(rows.device, rows=n), bias=bias, probs="f64")
 
-    def _row_launch(self, logits, prefix, uniform=None, rng_state=None):
+    def _row_launch(self, logits, prefix, uniform=None, rng_state=None, out=None, probs="f64"):
         """Validate one row and launch its distribution (and draw, given a
         uniform).  The grammar is asked for its mask first, then the row and
         controls are checked in the order of sampling.py:50-79."""
@@ -513,7 +559,7 @@ class SamplingWork:
         table = self._history(prefix) if self._needs_history(len(prefix)) else None
         bias = _bias_table(self.logit_bias, size)
         allow = _allow_row(mask, size)
-        return self.policy._launch_row(logits, size, table, bias, allow, uniform, rng_state), device_input
+        return self.policy._launch_row(logits, size, table, bias, allow, uniform, rng_state, out, probs), device_input
 
     def distribution(self, logits, prefix):
         """Float64 distribution of one row given a tentative accepted prefix
@@ -542,59 +588,55 @@ class SamplingWork:
             _raise_status(code)
         return _dist_checked(row, batch.prob_stats_read(host[0:3]))
 
-    def _draw(self, logits, prefix, domain, finite=None):
+    def _draw(self, logits, prefix, domain, window=None, probs="f64"):
         """(token, distribution): one fused launch draws from the row's
         distribution with the domain's next ``Generator.random()``, taken on
         the device from the domain's PCG64 state; the domain takes the state
         the kernel wrote back (advanced only when the draw was needed) and the
-        draw counts in the transaction's window.  The result and the state
-        come back with one synchronisation.  ``finite`` is a deferred window
-        check (a device bool), read with the result and reported first.  A
-        window already full takes the uniform from a preview of the generator
-        instead, so that ``RandomTransaction.random`` raises exactly when the
-        draw is needed."""
+        draw counts in the transaction's window.  ``window`` is a CUDA window
+        whose finiteness is still to be checked: ``dsr_rows_finite`` runs on
+        it into the sampler's ``_DrawIO``, and a non-finite window is reported
+        ahead of any later error.  The token, status, state and window flag
+        come back with one copy.  With ``probs=None`` the distribution is not
+        kept.  A window already full takes the uniform from a preview of the
+        generator instead, so that ``RandomTransaction.random`` raises
+        exactly when the draw is needed."""
         self._require_open()
         tr = self.transaction
         if tr.draws[domain] >= 64:
-            return self._draw_previewed(logits, prefix, domain, finite)
+            if window is not None:
+                _require_finite(batch.rows_finite(window))
+            return self._draw_previewed(logits, prefix, domain)
         generator = tr.owner._streams[domain]
-        state = _states_on_device([generator], logits.device)
+        io = self.owner._io(logits.device)
+        io.upload(generator, window is not None)
+        if window is not None:
+            batch.rows_finite(window, io.finite)
         try:
-            result, _ = self._row_launch(logits, prefix, rng_state=state)
+            result, _ = self._row_launch(logits, prefix, rng_state=io.state, out=io.out, probs=probs)
         except Exception:
-            _require_finite(finite)
+            if window is not None:
+                _require_finite(io.finite)
             raise
-        parts = [result.tokens.long(), result.consumed.long(), result.status.long()]
-        if finite is not None:
-            parts.append(finite.long().view(1))
-        parts.append(state.view(-1)[:2])
-        token, consumed, code, *rest = torch.cat(parts).tolist()
-        if finite is not None and not rest[0]:
+        lo, hi, token, code, consumed, ok = io.read()
+        if window is not None and not ok:
             raise ValidationError(_MSG_WINDOW)
         if code != N.OK:
             _raise_status(code)
         if consumed:
-            _set_state(generator, rest[-2], rest[-1])
+            _set_state(generator, lo, hi)
             tr.draws[domain] += 1
-        return token, result.probs[0]
+        return token, None if result.probs is None else result.probs[0]
 
-    def _draw_previewed(self, logits, prefix, domain, finite=None):
+    def _draw_previewed(self, logits, prefix, domain):
         """``_draw`` with the uniform read from a copy of the generator; the
         domain advances (and may raise) only if the kernel consumed it."""
         upcoming = self.transaction._preview(domain)
         # A fill kernel, not a host-to-device copy: nothing waits for it.
         uniform = torch.full((1,), upcoming, dtype=torch.float64, device=logits.device)
-        try:
-            result, _ = self._row_launch(logits, prefix, uniform)
-        except Exception:
-            _require_finite(finite)
-            raise
+        result, _ = self._row_launch(logits, prefix, uniform)
         parts = [result.tokens.long(), result.consumed.long(), result.status.long()]
-        if finite is not None:
-            parts.append(finite.long().view(1))
-        token, consumed, code, *window_ok = torch.stack(parts).view(-1).tolist()
-        if window_ok and not window_ok[0]:
-            raise ValidationError(_MSG_WINDOW)
+        token, consumed, code = torch.stack(parts).view(-1).tolist()
         if code != N.OK:
             _raise_status(code)
         if consumed and self.transaction.random(domain) != upcoming:
@@ -684,22 +726,27 @@ class SamplingWork:
         """Exact sampled verification of the proposals against ``K + 1`` target rows."""
         self._require_stage(_Stage.PROPOSED, "target verification is duplicate or proposals are not complete")
         with self._aborting_on_error():
-            rows = _logits_device(target_logits, len(self.proposal_ids) + 1, self.owner.vocabulary)
             ids = list(self.proposal_ids)
             K = len(ids)
             if self.allowed is not None:
+                rows = _logits_device(target_logits, K + 1, self.owner.vocabulary)
                 # A grammar is asked for the masks of the prefixes the verifier reaches only.
                 targets = _LazyRows(len(rows), lambda j: self._target(rows[j], ids[:j]))
-            elif self._draws_fit(K) and self._unfiltered(K):
-                self._decide(self._verify_logits(rows, ids))
-                return self.decision
             else:
+                # Without a grammar nothing the caller sees happens before the
+                # decision is read back, so the window's finiteness is read with it.
+                rows, deferred = _logits_deferred(target_logits, K + 1, self.owner.vocabulary)
+                if self._draws_fit(K) and self._unfiltered(K):
+                    self._decide(self._device_decision(lambda: self._verify_logits(rows, ids, deferred), K))
+                    return self.decision
                 device = self._draws_fit(K) and self._rows_at_hand(K, rows.device)
                 targets = _TargetRows(self, rows, ids, host=not device)
                 ready = targets.device() if device else None
                 if ready is not None:
-                    self._decide(self._verify_rows(*ready, ids))
+                    self._decide(self._device_decision(lambda: self._verify_rows(rows, *ready, ids, deferred), K))
                     return self.decision
+                if deferred:
+                    _require_finite(batch.rows_finite(rows))
                 if device:
                     targets._host_inputs()
             self._decide(verify_drafts(targets, self.proposal_rows, ids, self.transaction,
@@ -732,34 +779,53 @@ class SamplingWork:
                 and not self._needs_history(K) and not self.logit_bias
                 and batch.verify_hints(batch.policy_array([self.policy]), self.owner.vocabulary, True) != 0)
 
-    def _upload(self, ids, dev):
+    def _upload(self, ids, dev, rows, deferred):
         """One pinned upload: the accept and target PCG64 states, then (int32)
-        the proposal ids, the output limit and the EOS ids."""
+        the proposal ids, the output limit, the EOS ids and, for a window
+        whose finiteness is ``deferred``, one flag per target row set to 1,
+        on which ``dsr_rows_finite`` then runs.  Returns the generators, the
+        device states, ids, limit, EOS arguments and flags (or None)."""
         tr, K, eos = self.transaction, len(ids), sorted(self.eos_ids)
         gens = [tr.owner._streams["accept"], tr.owner._streams["target"]]
-        host = torch.empty(8 + (K + 1 + len(eos) + 1) // 2 + 1, dtype=torch.int64, pin_memory=True)
-        host[:8] = torch.from_numpy(_state_words(gens).view(np.int64).reshape(-1))
-        small = host[8:].view(torch.int32)
-        small[:K] = torch.tensor(ids, dtype=torch.int32)
+        nflag = K + 1 if deferred else 0
+        n32 = K + 1 + len(eos) + nflag
+        host = torch.zeros(8 + (n32 + 1) // 2, dtype=torch.int64, pin_memory=True)
+        words = host.numpy()
+        words[:8] = _state_words(gens).view(np.int64).reshape(-1)
+        small = words[8:].view(np.int32)
+        small[:K] = ids
         small[K] = self.remaining
-        small[K + 1:K + 1 + len(eos)] = torch.tensor(eos, dtype=torch.int32)
+        small[K + 1:K + 1 + len(eos)] = eos
+        small[K + 1 + len(eos):n32] = 1
         up = host.to(dev, non_blocking=True)
         states, small_d = up[:8].view(2, 4), up[8:].view(torch.int32)
         eos_kw = {}
         if eos:
             eos_kw = dict(eos_offsets=torch.tensor([0, len(eos)], dtype=torch.int64).pin_memory().to(dev, non_blocking=True),
                           eos_ids=small_d[K + 1:K + 1 + len(eos)])
-        return gens, states, small_d[:K], small_d[K:K + 1], eos_kw
+        finite = None
+        if deferred:
+            finite = small_d[K + 1 + len(eos):n32]
+            batch.rows_finite(rows, finite)
+        return gens, states, small_d[:K], small_d[K:K + 1], eos_kw, finite
 
-    def _decision_of(self, res, gens, states, K):
-        """The decision, the status, the draws used and the advanced states
-        read back with one synchronisation; each domain takes its state and
-        counts its draws."""
-        out = torch.cat([res.status.long(), res.accepted.long(), res.count.long(), res.pending.long(),
-                         res.stop.long(), res.used_accept.long(), res.used_target.long(), res.ids.long().view(-1),
-                         states.view(-1)]).tolist()
+    def _device_decision(self, launch, K):
+        """The decision of a device verifier ``launch()`` (returning its result,
+        the two generators, their device states and the window's deferred
+        finite flags or None), read back with the status, the draws used, the
+        advanced states and the flags in one synchronisation; a non-finite
+        window is reported first.  Each domain then takes its state and counts
+        its draws."""
+        res, gens, states, finite = launch()
+        parts = [res.status.long(), res.accepted.long(), res.count.long(), res.pending.long(), res.stop.long(),
+                 res.used_accept.long(), res.used_target.long(), res.ids.long().view(-1), states.view(-1)]
+        if finite is not None:
+            parts.append(finite.long().view(-1))
+        out = torch.cat(parts).tolist()
+        if finite is not None and not all(out[len(out) - finite.numel():]):
+            raise ValidationError(_MSG_WINDOW)
         code, accepted, count, pending, stop, used_a, used_t = out[:7]
-        out_ids, words = out[7:7 + K + 1], out[8 + K:]
+        out_ids, words = out[7:7 + K + 1], out[8 + K:16 + K]
         if code != N.OK:
             _raise_status(code)
         tr = self.transaction
@@ -770,35 +836,45 @@ class SamplingWork:
         return VerificationDecision(accepted, tuple(out_ids[:count]), None if pending < 0 else pending,
                                     {N.STOP_NONE: None, N.STOP_EOS: "eos", N.STOP_LENGTH: "length"}[stop])
 
-    def _verify_logits(self, rows, ids):
+    def _verify_logits(self, rows, ids, deferred):
         """verify_drafts (sampling.py:247-294) as one ``dsr_verify_drafts``
         call on the target and proposal logits (its fast path: no filter,
         history or bias), the accept test with the accept domain's next draws
         and the replacement or bonus draw with the target domain's, all taken
-        on the device from the domains' PCG64 states."""
+        on the device from the domains' PCG64 states.  Returns the launch's
+        result, the two generators and their device states."""
         K, V = len(ids), self.owner.vocabulary
         dev = rows.device
-        gens, states, ids_d, limit, eos_kw = self._upload(ids, dev)
+        gens, states, ids_d, limit, eos_kw, finite = self._upload(ids, dev, rows, deferred)
         draft = torch.stack(self._draft_logits).reshape(1, K, V) if K else None
-        res = batch.verify_drafts(rows.contiguous().reshape(1, K + 1, V), draft, ids_d,
-                                  self.policy._device_tensor(dev), None, None, limit,
-                                  rng_accept=states[0:1], rng_target=states[1:2], **eos_kw)
-        return self._decision_of(res, gens, states, K)
+        try:
+            res = batch.verify_drafts(rows.contiguous().reshape(1, K + 1, V), draft, ids_d,
+                                      self.policy._device_tensor(dev), None, None, limit,
+                                      rng_accept=states[0:1], rng_target=states[1:2], **eos_kw)
+        except Exception:
+            _require_finite(finite)
+            raise
+        return res, gens, states, finite
 
-    def _verify_rows(self, targets, status, ids):
+    def _verify_rows(self, rows, targets, status, ids, deferred):
         """verify_drafts (sampling.py:247-294) as one ``dsr_verify_probs`` call
         on the float64 target rows (row j conditioned on ``ids[:j]``,
         terminal_sampling.py:127-136) and the proposal rows the proposals
         were drawn from, with the accept and target draws taken on the device
         from the domains' PCG64 states; a target row whose launch failed on
-        the device fails when the chain reaches it."""
+        the device fails when the chain reaches it.  Returns what
+        ``_verify_logits`` returns."""
         K, dev = len(ids), targets[0].device
-        gens, states, ids_d, limit, eos_kw = self._upload(ids, dev)
+        gens, states, ids_d, limit, eos_kw, finite = self._upload(ids, dev, rows, deferred)
         greedy = torch.ones(1, dtype=torch.uint8, device=dev) if self.policy.temperature == 0 else None
-        res = batch.verify_probs(targets, self.proposal_rows, ids_d, limit, vocab=self.owner.vocabulary,
-                                 greedy=greedy, rng_accept=states[0:1], rng_target=states[1:2],
-                                 target_status=status, **eos_kw)
-        return self._decision_of(res, gens, states, K)
+        try:
+            res = batch.verify_probs(targets, self.proposal_rows, ids_d, limit, vocab=self.owner.vocabulary,
+                                     greedy=greedy, rng_accept=states[0:1], rng_target=states[1:2],
+                                     target_status=status, **eos_kw)
+        except Exception:
+            _require_finite(finite)
+            raise
+        return res, gens, states, finite
 
     def _digest_record(self):
         """The fields the decision digest covers (terminal_sampling.py:189-196).

@@ -404,6 +404,14 @@ int32_t dsr_prob_correction(const double* p, const double* q, int64_t n, double*
 int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, double u, int32_t* out_i32,
                         void* stream);
 
+/* The terminal window check np.isfinite(logits).all() (terminal_sampling.py
+ * :25) on the device: out[r] is set to 0 when one of the n FP32 values of
+ * row r (x + r * ld) is NaN or +-inf, and left as it is otherwise, so the
+ * caller sets out[0 .. rows-1] to 1 first (in the same stream order).  Each
+ * row is spread over workgroups of 4,096 values; nothing is read back, so
+ * a caller can read the flags with its next synchronisation. */
+int32_t dsr_rows_finite(const float* x, int64_t rows, int64_t n, int64_t ld, int32_t* out, void* stream);
+
 /* Device history tables: the reference's dense per-request counts and
  * generated counts (history.py:46-47,92,136-137; terminal_sampling.py
  * :127-136) kept on the device as the sparse CSR table of

@@ -178,3 +178,26 @@ def test_accept_test_on_the_ratio_edge():
     q[123] = 0.0
     positive, accepted = batch.prob_accept(tp, dev(q), 123, 0.5)
     assert not positive and not accepted
+
+
+@pytest.mark.parametrize("n,offset", [(129280, 0), (129281, 1), (7, 0), (1, 3), (4096, 2)])
+def test_rows_finite_is_numpy_isfinite_all(n, offset):
+    """dsr_rows_finite against np.isfinite(row).all() (terminal_sampling.py:25):
+    NaN, +inf and -inf anywhere (first, last, middle), FLT_MAX and
+    subnormals (finite), rows that start off a 16-byte boundary and lengths
+    that are not a multiple of 4."""
+    rng = np.random.default_rng(n + offset)
+    R = 9
+    x = rng.normal(0, 3, (R, n + offset + 5)).astype(np.float32)
+    x[1, offset + n - 1] = np.nan
+    x[2, offset] = np.inf
+    x[3, offset + n // 2] = -np.inf
+    x[4, offset:offset + n] = np.finfo(np.float32).max
+    x[5, offset:offset + n:2] = np.float32(1e-45)
+    x[6, offset + n:] = np.nan                              # past the row: not read
+    x[7, offset:offset + n] = -np.finfo(np.float32).max
+    x[8, offset + (n - 1) // 3] = np.nan
+    t = torch.from_numpy(x).cuda()[:, offset:offset + n]
+    got = batch.rows_finite(t).cpu().numpy()
+    want = np.isfinite(x[:, offset:offset + n]).all(axis=1).astype(np.int32)
+    np.testing.assert_array_equal(got, want)

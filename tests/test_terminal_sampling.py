@@ -114,6 +114,25 @@ def test_invalid_target_window_aborts_and_restores_the_proposal_draws():
     assert sampler.random.snapshot() == initial
 
 
+@pytest.mark.parametrize("policy", [SamplingPolicy(), SamplingPolicy(temperature=0.8, top_k=3)])
+def test_a_non_finite_cuda_target_window_aborts_the_device_verifier(policy):
+    """A NaN, +inf or -inf in CUDA target rows gives the window message on
+    both device verifier routes (the window check is read back with the
+    decision), and the transaction ends with the RNG as it began."""
+    for bad in (float("nan"), float("inf"), -float("inf")):
+        sampler = TerminalSampler(17)
+        initial = sampler.random.snapshot()
+        counts = np.zeros(V, np.int32)
+        counts[4] = 1
+        work = sampler.begin_verification(seed_token=4, policy=policy, counts=counts, remaining=10)
+        ids = work.propose(_DeviceMarkov(lambda row, prev: np.linspace(0, 1, V, dtype=np.float32)), None)
+        target = torch.zeros((len(ids) + 1, V), dtype=torch.float32, device="cuda")
+        target[len(ids), 5] = bad
+        with pytest.raises(ValidationError, match="vocabulary window"):
+            work.verify(target)
+        assert sampler.active is None and sampler.random.snapshot() == initial
+
+
 def test_an_accepted_eos_draft_ends_the_grammar_queries():
     def mask(prefix):
         assert prefix == (), "no distribution exists after the grammar's EOS"
@@ -486,13 +505,13 @@ def test_batched_device_draws_decide_as_the_host_verifier(device_graph, monkeypa
     batched = []
     real_logits, real_rows = TS.SamplingWork._verify_logits, TS.SamplingWork._verify_rows
 
-    def spy_logits(self, rows, ids):
+    def spy_logits(self, rows, ids, deferred):
         batched.append("logits")
-        return real_logits(self, rows, ids)
+        return real_logits(self, rows, ids, deferred)
 
-    def spy_rows(self, targets, status, ids):
+    def spy_rows(self, rows, targets, status, ids, deferred):
         batched.append("rows")
-        return real_rows(self, targets, status, ids)
+        return real_rows(self, rows, targets, status, ids, deferred)
 
     def run(force_host, seed, policy, remaining, eos, bias):
         if force_host:
