@@ -50,9 +50,9 @@ WORKLOADS = {
     "c3": ("sampled rows/sec at B=256×V=129,280 bf16; % of HBM roofline", "rows/s", 5,
            "k_sample_bf16_fast"),
     "c3f32": ("sampled rows/sec at B=256×V=129,280 fp32; % of HBM roofline", "rows/s", 5,
-              "k_split_select + k_split_finish"),
+              "k_sample_f32"),
     "c1": ("sampled rows/sec at B=1×V=129,280 fp32 with fp32 probabilities out", "rows/s", 1000,
-           "k_split_select + k_split_finish"),
+           "k_zero_probs + k_sample_f32"),
     "c2": ("sampled rows/sec at B=64×V=129,280 bf16 with 4,096-token histories", "rows/s", 20,
            "k_sample_bf16_full"),
     "c4": ("verify-rows/sec at B=32 requests × K=4 drafts × V=129,280 fp32", "verify-rows/s", 60,
@@ -64,22 +64,22 @@ WORKLOADS = {
     "whole": ("sampled rows/sec at B=256×V=129,280 bf16 with no top-k (default / top-p / min-p policies)", "rows/s",
               5, "k_sample_bf16_full"),
     "step": ("drop-in speculative steps/sec: propose 5 rows on the device, verify against 6 fp32 rows, digest",
-             "steps/s", 30, "k_split_select + k_split_finish (proposals; the six targets in one launch) + "
+             "steps/s", 30, "k_zero_probs + k_sample_f32 (each proposal; the six targets in one launch) + "
              "k_rows_finite + k_vprobs_stats + k_vprobs_chain + k_vprobs_draw + k_vprobs_finish"),
     "seed": ("drop-in TerminalSampler.begin_seed calls/sec (1 fp32 row, V=129,280, dense counts)", "calls/s",
-             300, "k_rows_finite + k_split_select + k_split_finish (a policy without penalties carries no history "
+             300, "k_rows_finite + k_zero_probs + k_sample_f32 (a policy without penalties carries no history "
              "table)"),
     "head": ("verify-rows/sec with the vocabulary projection: B=32 requests × K=4 drafts, 160 target rows × "
              "dim 5,120 → V=129,280 fp32 logits", "verify-rows/s", 30,
              "k_vocab_head + k_head_shares + k_verify_chain + k_verify_draw + k_verify_finish"),
     "propose": ("drop-in 5-row draft proposal steps/sec at V=129,280 fp32, one host synchronisation per step",
-                "chains/s", 100, "k_split_select + k_split_finish (5x; a policy without penalties carries no "
+                "chains/s", 100, "k_zero_probs + k_sample_f32 (5x; a policy without penalties carries no "
                 "history table)"),
 }
 
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
-PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_split", "c3f32": "k_split", "propose": "k_split", "seed": "k_split",
-                  "step": "k_split",
+PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_sample_f32", "propose": "k_sample_f32", "seed": "k_sample_f32",
+                  "step": "k_sample_f32",
                   "head": "k_vocab_head"}
 
 DESCRIPTIONS = {

@@ -38,10 +38,12 @@ MAX_VOCAB = 129280
 FLAG_MARGIN = 1
 FLAG_GENERAL = 2
 FLAG_SPLIT = 4
+FLAG_F32_TOPK = 8
 # Kernel-choice hints (statements about a batch's policies; results never depend on them).
 HINT_WHOLE_SOME = 1
 HINT_WHOLE_ALL = 2
 HINT_VERIFY_FAST = 4
+HINT_TOPK_ALL = 8
 STOP_NONE, STOP_EOS, STOP_LENGTH = 0, 1, 2
 
 EXPORTS = (

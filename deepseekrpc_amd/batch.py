@@ -92,14 +92,18 @@ FAST_MAX_K = 1024   # the largest top-k the bf16 register kernel cuts to
 
 
 def sample_hints(arr: np.ndarray | None, vocab: int) -> int:
-    """DSR_HINT_WHOLE_* bits for packed policies: whole rows are sampled
+    """DSR_HINT_* bits for packed policies: WHOLE_* when whole rows are sampled
     (0 < T <= 100) with no top-k or one above ``FAST_MAX_K`` (the kernels'
-    ``whole_row``).  The bits only choose launches; results never depend on them."""
+    ``whole_row``), TOPK_ALL when every row is in bounds and greedy or has
+    1 <= top_k <= ``FAST_MAX_K`` below the vocabulary.  The bits only choose
+    launches; results never depend on them."""
     if arr is None or len(arr) == 0:
         return 0
     T, k = arr["temperature"], arr["top_k"]
     whole = (T > 0) & (T <= 100) & ~((k >= 1) & (k <= FAST_MAX_K) & (k < vocab))
-    return (N.HINT_WHOLE_SOME if whole.any() else 0) | (N.HINT_WHOLE_ALL if whole.all() else 0)
+    topk = ((T == 0) | ((k >= 1) & (k <= FAST_MAX_K) & (k < vocab))) & policies_in_bounds(arr)
+    return ((N.HINT_WHOLE_SOME if whole.any() else 0) | (N.HINT_WHOLE_ALL if whole.all() else 0)
+            | (N.HINT_TOPK_ALL if topk.all() else 0))
 
 
 def _policy_hints(policies, vocab: int) -> int:
@@ -716,7 +720,7 @@ def finish_proposals(p: Proposals, eos_ids=()):
     if steps == 0:
         return (), p.rows[:0], 0, p.states[0:1], p.deferred
     dev = p.tokens.device
-    finite = torch.isfinite(p.logits).all(dim=1).to(torch.int32)
+    finite = rows_finite(p.logits)
     # Row j > 0 carries the status of the append before it; a chain without appends has none.
     app = torch.cat([torch.zeros(1 if p.appended else steps, dtype=torch.int32, device=dev), *p.appended])
     info = torch.stack([p.tokens, p.consumed.to(torch.int32), p.status, app, finite]).cpu().numpy()

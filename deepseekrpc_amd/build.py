@@ -21,7 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libdsr_sampling.so")
 SOURCES = ["dsr_sampling.hip"]
-HEADERS = ["dsr_common.h", "dsr_wave.h", "dsr_general.h", "dsr_fast.h", "dsr_topk.h", "dsr_full.h", "dsr_verify.h", "dsr_history.h", "dsr_split.h", "dsr_numpy.h", "dsr_head.h"]
+HEADERS = ["dsr_common.h", "dsr_wave.h", "dsr_general.h", "dsr_fast.h", "dsr_topk.h", "dsr_full.h", "dsr_verify.h", "dsr_history.h", "dsr_split.h", "dsr_numpy.h", "dsr_head.h", "dsr_f32.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

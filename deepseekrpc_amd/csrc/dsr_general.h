@@ -596,6 +596,31 @@ struct IdentityMap {
   __device__ __forceinline__ int64_t operator()(int64_t i) const { return i; }
 };
 
+// The top-p tie group at the crossing value rt (sampling.py:97-102): A is the
+// mass of the n_above tokens above rt, n_tie tokens equal rt.  Tie member j
+// (index order) has exclusive prefix A + j*rt; it is kept while that prefix
+// is below top_p, and rank 0 always.  Returns the members kept; `close` is
+// set when a float64 prefix over this many terms could round across top_p.
+__device__ __forceinline__ long long top_p_tie_keep(double A, long long n_above, long long n_tie, double rt,
+                                                    double top_p, bool& close) {
+  long long keep = 0;
+  {
+    double q = ceil((top_p - A) / rt);
+    keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
+    while (keep > 0 && A + (double)(keep - 1) * rt >= top_p) --keep;
+    while (keep < n_tie && A + (double)keep * rt < top_p) ++keep;
+  }
+  if (n_above == 0 && keep == 0) keep = 1;
+  // Rounding band of a float64 prefix over this many terms.
+  const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51;
+  close = fabs(A + (double)keep * rt - top_p) <= tol;                 // first removed
+  if (keep >= 1 && n_above + keep > 1)
+    close = close || fabs(A + (double)(keep - 1) * rt - top_p) <= tol;  // last kept
+  if (keep == 0 && n_above > 0) close = true;                          // crossing above this group
+  if (keep == n_tie && A + (double)n_tie * rt < top_p) close = true;   // crossing below it
+  return keep;
+}
+
 // Steps 10-13 (sampling.py:92-106) over W[0, n), which holds s = (v - max) / T
 // and the top-k decision (`kth`, `cut` from radix_top_k).  Position j of W is
 // token map(j), positions in token order, so index-order ties and the CDF keep
@@ -669,23 +694,8 @@ __device__ __forceinline__ int filter_tail(const RowSpec& r, double* W, int64_t 
       const double A = block_sum(a, sh.b);
       n_above = block_sum_i64(n_above, sh.b);
       n_tie = block_sum_i64(n_tie, sh.b);
-      // Tie member j (index order) has exclusive prefix A + j*rt; it is kept
-      // while that prefix is below top_p, and rank 0 always (sampling.py:99-102).
-      long long keep = 0;
-      {
-        double q = ceil((p.top_p - A) / rt);
-        keep = q <= 0.0 ? 0 : (q >= (double)n_tie ? n_tie : (long long)q);
-        while (keep > 0 && A + (double)(keep - 1) * rt >= p.top_p) --keep;
-        while (keep < n_tie && A + (double)keep * rt < p.top_p) ++keep;
-      }
-      if (n_above == 0 && keep == 0) keep = 1;
-      // Rounding band of a float64 prefix over this many terms.
-      const double tol = ((double)(n_above + keep) + 16.0) * 0x1p-51;
-      bool close = fabs(A + (double)keep * rt - p.top_p) <= tol;           // first removed
-      if (keep >= 1 && n_above + keep > 1)
-        close = close || fabs(A + (double)(keep - 1) * rt - p.top_p) <= tol;  // last kept
-      if (keep == 0 && n_above > 0) close = true;                          // crossing above this group
-      if (keep == n_tie && A + (double)n_tie * rt < p.top_p) close = true;  // crossing below it
+      bool close;
+      const long long keep = top_p_tie_keep(A, n_above, n_tie, rt, p.top_p, close);
       if (close) flags |= DSR_FLAG_MARGIN;
       const int64_t cutp = nth_equal_index(W, n, lbits, keep, [](double x) { return raw_bits(x); }, sh);
       cur = 0.0;

@@ -20,6 +20,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "dsr_f32.h"
 #include "dsr_fast.h"
 #include "dsr_topk.h"
 #include "dsr_full.h"
@@ -153,6 +154,49 @@ __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, 
   DistOut d;
   int st = general_distribution(r, sh, flags, d);
   finish_row<RNG>(a, row, W, a.vocab, st, d, flags, sh);
+}
+
+// One-workgroup FP32 top-k path; rows it does not take are redone by the
+// general path inside the same workgroup.
+template <bool RNG>
+__global__ __launch_bounds__(kThreads) void k_sample_f32(dsr_sample_args_t a) {
+  __shared__ F32Shared sh;
+  const int64_t row = blockIdx.x;
+  double* W = (double*)a.workspace + row * ws_stride(a.vocab);
+  RowSpec r = sample_row_spec(a, row, W);
+  unsigned flags = DSR_FLAG_F32_TOPK;
+  DistOut d;
+  int64_t n = 0;
+  int why = 0;
+  const int st = f32_distribution(a, row, r, sh, flags, d, n, why);
+  if (st >= 0) {
+    const int32_t* kid = sh.t.kid;
+    finish_row<RNG>(a, row, sh.t.kz, n, st, d, flags, sh.gen, [kid](int64_t j) { return (int64_t)kid[j]; });
+    return;
+  }
+  __syncthreads();  // every thread is done with the list
+  flags = DSR_FLAG_GENERAL | ((unsigned)why << 4);
+  DistOut dg;
+  const int sg = general_distribution(r, sh.gen, flags, dg);
+  finish_row<RNG>(a, row, W, a.vocab, sg, dg, flags, sh.gen);
+}
+
+// Zeroes [0, V) of each probability row of a dsr_sample_rows call ahead of
+// k_sample_f32, which writes only the kept tokens' entries: the rows are
+// spread over the whole chip (a row of 129,280 float64 probabilities is a
+// megabyte, about 40 us for the one workgroup that samples it).
+constexpr int kZeroChunk = 4096;
+constexpr int kZeroThreads = 256;
+
+__global__ __launch_bounds__(kZeroThreads) void k_zero_probs(float* f32, double* f64, int64_t ld, int64_t V,
+                                                             int chunks) {
+  const int64_t r = blockIdx.x / chunks;
+  const int64_t lo = (int64_t)(blockIdx.x % chunks) * kZeroChunk;
+  const int64_t hi = lo + kZeroChunk < V ? lo + kZeroChunk : V;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kZeroThreads) {
+    if (f32) f32[r * ld + i] = 0.0f;
+    if (f64) f64[r * ld + i] = 0.0;
+  }
 }
 
 // Fast path for bf16 rows; rows it does not take are redone by the general
@@ -816,7 +860,7 @@ size_t dsr_verify_workspace_bytes(int64_t rows, int32_t K, int64_t vocab) {
 
 // The DSR_HINT_* bits a caller may set; any other bit is rejected, so the
 // field can take new meanings later without an ABI change.
-static constexpr uint32_t kHintBits = DSR_HINT_WHOLE_SOME | DSR_HINT_WHOLE_ALL | DSR_HINT_VERIFY_FAST;
+static constexpr uint32_t kHintBits = DSR_HINT_WHOLE_SOME | DSR_HINT_WHOLE_ALL | DSR_HINT_VERIFY_FAST | DSR_HINT_TOPK_ALL;
 
 static bool dtype_ok(int32_t d) { return d == DSR_BF16 || d == DSR_F32 || d == DSR_F64; }
 
@@ -864,6 +908,14 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
     }
   } else if (full_path_eligible(a)) {
     launch_full(0u);
+  } else if (f32_path_eligible(a)) {
+    if (a.out_probs_f32 || a.out_probs_f64) {
+      const int64_t chunks = (a.vocab + kZeroChunk - 1) / kZeroChunk;
+      hipLaunchKernelGGL(k_zero_probs, dim3((unsigned)(a.rows * chunks)), dim3(kZeroThreads), 0, s, a.out_probs_f32,
+                         a.out_probs_f64, a.probs_ld, a.vocab, (int)chunks);
+    }
+    if (a.rng_state) hipLaunchKernelGGL(k_sample_f32<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_sample_f32<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
   } else if (split_path_eligible(a)) {
     const int smax = split_max_slices(a.rows);
     hipLaunchKernelGGL(k_split_select, dim3((unsigned)(a.rows * smax)), dim3(kThreads), 0, s, a, smax);

@@ -81,6 +81,8 @@ extern "C" {
                                    workgroups: top-k <= 1024, greedy, top-p / min-p whose
                                    kept set lies among the row's 512 largest values, or no
                                    filter with no history or bias) */
+#define DSR_FLAG_F32_TOPK 8u    /* decided by the one-workgroup FP32 top-k path (greedy or
+                                   1 <= top-k <= 1024, no history or bias) */
 
 /* Kernel-choice hints (dsr_sample_args_t.hints, dsr_verify_args_t.hints):
  * statements about the batch's policies that let the library choose its
@@ -95,6 +97,11 @@ extern "C" {
  *   full-vocabulary kernel alone.
  *   The two WHOLE hints change no result: a row that contradicts them is
  *   still decided exactly, by a slower path.
+ * DSR_HINT_TOPK_ALL: every row's policy is in bounds and is greedy or has
+ *   1 <= top_k <= 1024 below the vocabulary; an FP32 batch with no history
+ *   or bias (rows 16-byte aligned, vocab a multiple of 4, at most 131,072)
+ *   then runs the one-workgroup FP32 top-k kernel.  Like the WHOLE hints it
+ *   changes no result.
  * DSR_HINT_VERIFY_FAST: a promise that every request has a policy with no
  *   filter (top_k 0 or >= vocab, top_p 1, min_p 0) and that the call passes
  *   no history, bias or allow mask, so the launch that builds general-path
@@ -103,6 +110,7 @@ extern "C" {
 #define DSR_HINT_WHOLE_SOME 1u
 #define DSR_HINT_WHOLE_ALL 2u
 #define DSR_HINT_VERIFY_FAST 4u
+#define DSR_HINT_TOPK_ALL 8u
 
 /* Verifier stop reasons (sampling.py:286,289,294). */
 #define DSR_STOP_NONE 0

@@ -13,10 +13,10 @@ from oracle import sampling_oracle as O
 MARGIN = 1e-11
 
 
-def run_gpu(w, probs="f32", kept=True):
+def run_gpu(w, probs="f32", kept=True, hints=None):
     d = workloads.to_device(w)
     res = batch.sample_rows(d.logits, d.policies, history=d.history, allow_bits=d.allow_bits, uniforms=d.uniforms,
-                            probs=probs, kept=kept)
+                            probs=probs, kept=kept, hints=hints)
     torch.cuda.synchronize()
     out = dict(tokens=res.tokens.cpu().numpy(), consumed=res.consumed.cpu().numpy(),
                status=res.status.cpu().numpy(), flags=res.flags.cpu().numpy())

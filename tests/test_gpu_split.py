@@ -25,6 +25,9 @@ DEV = "cuda"
 
 
 def run(logits, pols, u, allowed=None, dtype=torch.float32, probs="f64", **kw):
+    # No TOPK_ALL hint: fp32 top-k batches would otherwise take the one-workgroup
+    # FP32 kernel (tests/test_gpu_f32.py), and these tests are the split path's.
+    kw.setdefault("hints", 0)
     x = torch.from_numpy(np.ascontiguousarray(logits)).to(DEV).to(dtype)
     allow = None if allowed is None else torch.from_numpy(batch.pack_allow(allowed).view(np.int32)).to(DEV)
     res = batch.sample_rows(x, pols, allow_bits=allow, uniforms=torch.from_numpy(np.asarray(u, np.float64)).to(DEV),
@@ -68,7 +71,7 @@ def policies(rng, rows, ks=(1, 2, 7, 50, 333, 1024)):
 
 def test_c1_takes_the_split_path():
     w = workloads.c1()
-    gpu = run_gpu(w)
+    gpu = run_gpu(w, hints=0)
     rep = compare(w, gpu)
     assert not rep.mismatches, rep.mismatches
     assert gpu["flags"][0] & N.FLAG_SPLIT and not gpu["flags"][0] & N.FLAG_GENERAL
@@ -189,7 +192,7 @@ def test_strided_rows_and_f32_probabilities():
     x = torch.from_numpy(base).to(DEV)[:, :V]
     pols = [dict(top_k=k, top_p=0.8, temperature=0.9) for k in (1, 9, 64, 512, 1024)]
     u = rng.random(5)
-    res = batch.sample_rows(x, pols, uniforms=torch.from_numpy(u).to(DEV), probs="f32")
+    res = batch.sample_rows(x, pols, uniforms=torch.from_numpy(u).to(DEV), probs="f32", hints=0)
     torch.cuda.synchronize()
     for r in range(5):
         ref = O.sample_row(base[r, :V], O.Policy(**pols[r]), float(u[r]))
@@ -208,7 +211,7 @@ def test_device_draws_on_the_split_path():
     st0 = [g.bit_generator.state["state"] for g in gens]
     states = batch.pcg64_states(gens, DEV)
     x = torch.from_numpy(logits).to(DEV)
-    res = batch.sample_rows(x, pols, rng_state=states)
+    res = batch.sample_rows(x, pols, rng_state=states, hints=0)
     torch.cuda.synchronize()
     words = states.cpu().numpy().view(np.uint64)
     for r in range(B):

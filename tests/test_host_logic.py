@@ -136,12 +136,17 @@ def _mixed_policies(rows=96):
 def test_hints_follow_the_policies():
     arr = batch.policy_array(workloads.whole().policies)
     assert batch.sample_hints(arr, 129280) == N.HINT_WHOLE_SOME | N.HINT_WHOLE_ALL
-    assert batch.sample_hints(batch.policy_array(workloads.c3().policies), 129280) == 0
+    # Every C3 row has 1 <= top_k <= 1024: the FP32 top-k kernel's hint.
+    assert batch.sample_hints(batch.policy_array(workloads.c3().policies), 129280) == N.HINT_TOPK_ALL
     assert batch.sample_hints(batch.policy_array(_mixed_policies()), 129280) == N.HINT_WHOLE_SOME
     # Greedy rows and rows with a top-k the register kernel takes are not whole.
     arr = batch.policy_array([dict(temperature=0.0), dict(top_k=1024), dict(top_k=1025), dict(top_k=8, top_p=0.5)])
     assert batch.sample_hints(arr, 129280) == N.HINT_WHOLE_SOME
     assert batch.sample_hints(batch.policy_array([dict(top_k=8)]), 8) == N.HINT_WHOLE_ALL | N.HINT_WHOLE_SOME
+    # TOPK_ALL needs every row greedy or with 1 <= top_k <= 1024 below V, and in bounds.
+    assert batch.sample_hints(batch.policy_array([dict(temperature=0.0), dict(top_k=1024)]), 129280) == \
+        N.HINT_TOPK_ALL
+    assert batch.sample_hints(batch.policy_array([dict(top_k=50, temperature=101.0)]), 129280) & N.HINT_TOPK_ALL == 0
 
 
 def test_verify_hint_needs_filter_free_policies_and_plain_inputs():

@@ -42,7 +42,7 @@ def test_status_messages_match_reference_texts():
 def test_flag_and_status_constants_match_header():
     text = open(HEADER).read()
     defs = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (DSR_\w+) \(?(-?\d+)u?\)?", text)}
-    for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
+    for name in ("FLAG_MARGIN", "FLAG_GENERAL", "FLAG_SPLIT", "FLAG_F32_TOPK", "HINT_TOPK_ALL", "E_LOGITS", "E_MASKED", "E_NO_MASS", "E_UNIFORM",
                  "E_COUNTS", "E_BIAS", "E_PROPOSAL_ZERO", "E_CORRECTION", "E_TOKEN", "E_DISTRIBUTION", "E_POLICY",
                  "E_GENERATED", "E_HISTORY", "E_APPEND", "E_HINT", "MAX_APPEND", "HINT_WHOLE_SOME", "HINT_WHOLE_ALL",
                  "HINT_VERIFY_FAST", "MAX_VOCAB", "HEAD_TILE", "HEAD_MAX_ROWS", "STATS_MAX_ROWS"):
@@ -83,7 +83,7 @@ def test_argument_errors_return_before_any_launch():
     v.dtype, v.K, v.rows, v.vocab, v.ld = N.F32, 0, 0, 8, 8
     v.workspace, v.workspace_bytes = 4096, 1 << 20
     assert lib.dsr_verify_drafts(ctypes.byref(v), None) == 0
-    for field, bad in (("reserved", 1), ("hints", 8), ("hints", 1 << 31)):
+    for field, bad in (("reserved", 1), ("hints", 16), ("hints", 1 << 31)):
         setattr(v, field, bad)
         assert lib.dsr_verify_drafts(ctypes.byref(v), None) == -1, (field, bad)
         setattr(v, field, 0)

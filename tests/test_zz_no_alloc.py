@@ -55,7 +55,7 @@ def test_two_calls_match_the_workspace_entry_point(top_k, first, second):
         got = outputs(batch.sample_rows(x, pols, uniforms=u, probs="f64", kept=True, noalloc=True))
         same(got, want)
         assert (got["status"] == 0).all()
-        path = N.FLAG_GENERAL if top_k > 1024 else N.FLAG_SPLIT
+        path = N.FLAG_GENERAL if top_k > 1024 else N.FLAG_F32_TOPK
         assert (got["flags"] & path).all()
 
 
