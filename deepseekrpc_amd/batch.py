@@ -30,7 +30,16 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_current_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
 def _stream():
+    """The current stream's handle.  torch's raw accessor: the public
+    ``torch.cuda.current_stream()`` costs several microseconds a call, a
+    sizeable part of a one-row draw's host time."""
+    if _raw_stream is not None and _current_device is not None:
+        return ctypes.c_void_p(_raw_stream(_current_device()))
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
@@ -1108,6 +1117,25 @@ def rows_finite(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     _require(out, "out", torch.int32, rows)
     N.check(lib.dsr_rows_finite(_ptr(x), rows, n, x.stride(0), _ptr(out), _stream()), "dsr_rows_finite")
     return out
+
+
+def count_scan(counts: np.ndarray):
+    """``dsr_count_scan`` of a host int32 / int64 count vector: ``(support,
+    total, largest)`` (the increasing ids of the positive entries, their
+    int64 sum, wrapping as NumPy's does, and the largest entry), or None when
+    an entry is negative.  One read-only pass in native code."""
+    lib = N.load()
+    c = np.ascontiguousarray(counts)
+    if c.ndim != 1 or c.dtype not in (np.int32, np.int64):
+        raise ValueError("counts must be a 1-D int32 or int64 array")
+    support = np.empty(max(c.size, 1), np.int64)
+    out = np.zeros(3, np.int64)
+    rc = lib.dsr_count_scan(c.ctypes.data, c.itemsize, c.size, support.ctypes.data, out.ctypes.data)
+    if rc < 0:
+        N.check(rc, "dsr_count_scan")
+    if rc == 1:
+        return None
+    return support[:int(out[0])].copy(), int(out[1]), int(out[2])
 
 
 def prob_stats_launch(p: torch.Tensor, slot: torch.Tensor):

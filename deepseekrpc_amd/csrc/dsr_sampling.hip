@@ -19,6 +19,7 @@
 #include <mutex>
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "dsr_f32.h"
 #include "dsr_fast.h"
@@ -1188,6 +1189,43 @@ int32_t dsr_rows_finite(const float* x, int64_t rows, int64_t n, int64_t ld, int
   hipLaunchKernelGGL(k_rows_finite, dim3((unsigned)(rows * chunks)), dim3(kFiniteThreads), 0, (hipStream_t)stream, x,
                      n, ld, (int)chunks, out);
   return launched();
+}
+
+// Host scan of a count vector in one read-only pass, skipping blocks of 64
+// zeros (an OR the compiler vectorises).
+extern "C++" template <class T>
+static int32_t count_scan(const T* c, int64_t n, int64_t* support, int64_t* out3) {
+  int64_t k = 0, mx = 0;
+  uint64_t total = 0;  // wraps as NumPy's int64 sum does
+  int neg = 0;
+  auto visit = [&](int64_t i) {
+    const T v = c[i];
+    if (v < 0) {
+      neg = 1;
+    } else if (v > 0) {
+      support[k++] = i;
+      total += (uint64_t)v;
+      if ((int64_t)v > mx) mx = (int64_t)v;
+    }
+  };
+  int64_t i = 0;
+  for (; i + 64 <= n; i += 64) {
+    T o = 0;
+    for (int j = 0; j < 64; ++j) o |= c[i + j];
+    if (o == 0) continue;
+    for (int j = 0; j < 64; ++j) visit(i + j);
+  }
+  for (; i < n; ++i) visit(i);
+  out3[0] = k;
+  out3[1] = (int64_t)total;
+  out3[2] = mx;
+  return neg;
+}
+
+int32_t dsr_count_scan(const void* counts, int32_t width, int64_t n, int64_t* support, int64_t* out3) {
+  if ((!counts && n > 0) || !support || !out3 || n < 0 || (width != 4 && width != 8)) return DSR_ERR_ARG;
+  return width == 4 ? count_scan((const int32_t*)counts, n, support, out3)
+                    : count_scan((const int64_t*)counts, n, support, out3);
 }
 
 int32_t dsr_history_from_dense(const int32_t* counts, const int32_t* generated, int64_t rows, int64_t vocab,

@@ -166,12 +166,44 @@ class SeedDecision:
         return 0
 
 
+class _Counts:
+    """A frozen count vector kept as its positive entries: ``support`` (the
+    increasing token ids), their ``values``, and the vector's length and
+    dtype.  The dense read-only vector is built on first use only (a draw
+    that reads no history table and a transaction without a digest never
+    need it)."""
+
+    __slots__ = ("support", "values", "length", "dtype", "_dense")
+
+    def __init__(self, support, values, length, dtype):
+        self.support, self.values, self.length, self.dtype = support, values, length, dtype
+        self._dense = None
+
+    def dense(self):
+        if self._dense is None:
+            out = np.zeros(self.length, self.dtype)
+            out[self.support] = self.values
+            out.setflags(write=False)
+            self._dense = out
+        return self._dense
+
+    def at(self, token):
+        i = int(np.searchsorted(self.support, token))
+        return int(self.values[i]) if i < self.support.size and self.support[i] == token else 0
+
+    def int64(self):
+        """A fresh dense int64 copy (for the digest hashes, on any thread)."""
+        out = np.zeros(self.length, np.int64)
+        out[self.support] = self.values
+        return out
+
+
 @dataclass(frozen=True)
 class _Controls:
     """The frozen inputs of one transaction (copies: callers cannot mutate them)."""
     policy: SamplingPolicy
-    counts: np.ndarray
-    generated: np.ndarray
+    counts: _Counts
+    generated: _Counts              # the same object when no separate generated counts were given
     remaining: int
     eos_ids: frozenset
     logit_bias: dict | None
@@ -188,10 +220,11 @@ def _sha256_i8(values):
 
 
 def _count_hashes(counts, generated):
-    """The digest's two count hashes; equal vectors (no separate generated
-    counts) share one."""
-    sha = _sha256_i8(counts)
-    return sha, sha if generated is counts or np.array_equal(counts, generated) else _sha256_i8(generated)
+    """The digest's two count hashes of two ``_Counts``; equal vectors (no
+    separate generated counts) share one."""
+    sha = _sha256_i8(counts.int64())
+    same = generated is counts or np.array_equal(counts.values, generated.values)  # one support
+    return sha, sha if same else _sha256_i8(generated.int64())
 
 
 # The count hashes (about 0.4 ms per megabyte vector) of a verification run on
@@ -223,12 +256,14 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
     if sampler.active is not None or not isinstance(policy, SamplingPolicy):
         raise ValidationError("terminal sampling is active or its policy is invalid")
     counts = np.asarray(counts)
-    support = np.flatnonzero(counts > 0) if _valid_count_vector(counts, sampler.vocabulary) else None
-    # Zero entries add nothing, so the int64 total (wrapping as a plain sum would) is taken over the support.
-    total = None if support is None else int(counts[support].sum(dtype=np.int64))
+    # One native pass: no negative entry, the positive entries and their
+    # int64 total (zero entries add nothing; the sum wraps as NumPy's does).
+    scan = (batch.count_scan(counts) if counts.shape == (sampler.vocabulary,)
+            and counts.dtype in (np.int32, np.int64) else None)
+    support, total, largest = (None, None, None) if scan is None else scan
     if total is None or total > _HISTORY_LIMIT:
         raise ValidationError("terminal counts differ from the exact published token history")
-    if support.size and int(counts[support].max()) > _HISTORY_LIMIT:
+    if support.size and largest > _HISTORY_LIMIT:
         total = None   # the int64 sum wrapped: every row's distribution rejects these counts
     for token in eos_ids:
         integer(token, "terminal EOS token", 0, sampler.vocabulary - 1)
@@ -244,14 +279,14 @@ def _check_controls(sampler, policy, counts, remaining, eos_ids, generated_count
     if generated is not counts and (generated.shape != counts.shape or not _valid_count_vector(
             generated, sampler.vocabulary) or (generated > counts).any()):
         raise ValidationError("generated sampling counts must be a subset of the complete history")
-    # Frozen copies; without separate generated counts both names hold one copy.
-    frozen = counts.copy()
-    frozen.setflags(write=False)
+    # Frozen copies of the positive entries; generated counts lie within the
+    # support (0 <= generated <= counts), and without separate generated
+    # counts both names hold one copy.
+    frozen = _Counts(support, counts[support], counts.size, counts.dtype)
     if generated is counts:
         generated = frozen
     else:
-        generated = generated.copy()
-        generated.setflags(write=False)
+        generated = _Counts(support, generated[support], generated.size, generated.dtype)
     return _Controls(policy, frozen, generated, remaining, frozenset(eos_ids),
                      None if logit_bias is None else dict(logit_bias), allowed, grammar_identity, stop_identity,
                      support, total)
@@ -281,15 +316,21 @@ class TerminalSampler:
             # The digest's count hashes, on the worker thread while the
             # proposals and the verification run (a seed's digest follows its
             # one launch at once, so its hashes wait for prepared()).
-            work._counts_sha = _hash_worker().submit(_count_hashes, work.counts, work.generated_counts)
+            work._counts_sha = _hash_worker().submit(_count_hashes, work._controls.counts, work._controls.generated)
         return work
 
     def begin_seed(self, logits, *, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
                    logit_bias=None, allowed=None, grammar_identity=None, stop_identity=None):
         """Sample the first token of a request from one row of target logits."""
+        early = self._seed_launch(logits, policy, logit_bias, allowed)
         work = self._open_work(_Stage.SEEDING, policy, counts, remaining, eos_ids, generated_counts, logit_bias,
                                allowed, grammar_identity, stop_identity)
         with work._aborting_on_error():
+            if early is not None and not work._needs_history(0):
+                token = work._take_draw(early, "target")
+                stop = "eos" if token in work.eos_ids else "length" if remaining == 1 else None
+                work._decide(SeedDecision(token, stop))
+                return work
             # Without a grammar provider nothing the caller sees happens
             # between the window check and the draw, so the window's
             # finiteness is read with the draw's result.
@@ -303,13 +344,40 @@ class TerminalSampler:
             work._decide(SeedDecision(token, stop))
         return work
 
+    def _seed_launch(self, logits, policy, logit_bias, allowed):
+        """The seed's draw, launched ahead of the control checks when the call
+        hands a CUDA FP32 window and has no grammar, bias or penalties: the
+        host checks then run while the row is sampled.  Nothing the caller
+        sees changes until the result is read, which happens only once every
+        check has passed and the row needs no history table; otherwise the
+        launch is dropped and the call takes the ordinary route (which
+        raises what it would have raised).  Returns the sampler's ``_DrawIO``
+        holding the launch, or None."""
+        if (self.active is not None or allowed is not None or logit_bias is not None
+                or not isinstance(policy, SamplingPolicy) or policy.repetition_penalty != 1
+                or policy.presence_penalty != 0 or policy.frequency_penalty != 0):
+            return None
+        if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32
+                and tuple(logits.shape) == (1, self.vocabulary)):
+            return None
+        window = logits.detach().contiguous()
+        io = self._io(window.device)
+        try:
+            io.upload(self.random._streams["target"], True)
+            batch.rows_finite(window, io.finite)
+            policy._launch_row(window[0], self.vocabulary, None, None, None, rng_state=io.state, out=io.out,
+                               probs=None)
+        except Exception:
+            return None
+        return io
+
     def begin_verification(self, *, seed_token, policy, counts, remaining, eos_ids=frozenset(), generated_counts=None,
                            logit_bias=None, allowed=None, grammar_identity=None, stop_identity=None):
         """Open a speculative step after ``seed_token``, which must already be in the history."""
         integer(seed_token, "pending verification seed", 0, self.vocabulary - 1)
         work = self._open_work(_Stage.AWAITING_PROPOSALS, policy, counts, remaining, eos_ids, generated_counts,
                                logit_bias, allowed, grammar_identity, stop_identity)
-        if min(work.counts[seed_token], work.generated_counts[seed_token]) < 1:
+        if min(work._controls.counts.at(seed_token), work._controls.generated.at(seed_token)) < 1:
             work.abort()
             raise ValidationError("pending seed must already belong to published sampling history")
         work.seed_token = seed_token
@@ -460,8 +528,8 @@ class SamplingWork:
 
     # -- the frozen controls, under the reference's attribute names --------
     policy = property(lambda self: self._controls.policy)
-    counts = property(lambda self: self._controls.counts)
-    generated_counts = property(lambda self: self._controls.generated)
+    counts = property(lambda self: self._controls.counts.dense())
+    generated_counts = property(lambda self: self._controls.generated.dense())
     remaining = property(lambda self: self._controls.remaining)
     eos_ids = property(lambda self: self._controls.eos_ids)
     logit_bias = property(lambda self: self._controls.logit_bias)
@@ -512,15 +580,15 @@ class SamplingWork:
             # The controls were checked on entry (no negative count, 2^20 in
             # total, generated <= counts), so nothing here can be rejected and
             # the table is built on the host from the positive entries.
-            ids = self._controls.support
+            c = self._controls
             self._device_history = batch.HistoryTable.from_support(
-                ids, self.counts[ids], self.generated_counts[ids], device=_device())
+                c.support, c.counts.values, c.generated.values, device=_device())
         if not prefix:
             return self._device_history
         dev = self._device_history.offsets.device
         tokens = torch.tensor(list(prefix), dtype=torch.int32, device=dev)
         bounds = torch.tensor([0, len(prefix)], dtype=torch.int64, device=dev)
-        table, status = self._device_history.append(tokens, bounds, vocab=len(self.counts))
+        table, status = self._device_history.append(tokens, bounds, vocab=self._controls.counts.length)
         code = int(status.item())
         if code != N.OK:
             _raise_status(code)
@@ -542,7 +610,7 @@ class SamplingWork:
         history table and no grammar mask (``_row_launch``'s checks, which
         are the same for every row)."""
         size, _ = _logit_vector(rows[0])
-        if size != len(self.counts):
+        if size != self._controls.counts.length:
             raise ValidationError(_COUNTS_MSG)
         n = len(rows)
         bias = _bias_table(self.logit_bias, size, rows=n)
@@ -554,7 +622,7 @@ class SamplingWork:
         controls are checked in the order of sampling.py:50-79."""
         mask = None if self.allowed is None else self.allowed(tuple(prefix))
         size, device_input = _logit_vector(logits)
-        if size != len(self.counts):
+        if size != self._controls.counts.length:
             raise ValidationError(_COUNTS_MSG)
         table = self._history(prefix) if self._needs_history(len(prefix)) else None
         bias = _bias_table(self.logit_bias, size)
@@ -618,15 +686,22 @@ class SamplingWork:
             if window is not None:
                 _require_finite(io.finite)
             raise
+        token = self._take_draw(io, domain, window is not None)
+        return token, None if result.probs is None else result.probs[0]
+
+    def _take_draw(self, io, domain, window=True):
+        """The token of a launched single-row draw, read back with its status,
+        the domain's advanced state and (with ``window``) the window's finite
+        flag; the domain takes the state when the draw consumed its uniform."""
         lo, hi, token, code, consumed, ok = io.read()
-        if window is not None and not ok:
+        if window and not ok:
             raise ValidationError(_MSG_WINDOW)
         if code != N.OK:
             _raise_status(code)
         if consumed:
-            _set_state(generator, lo, hi)
-            tr.draws[domain] += 1
-        return token, None if result.probs is None else result.probs[0]
+            _set_state(self.transaction.owner._streams[domain], lo, hi)
+            self.transaction.draws[domain] += 1
+        return token
 
     def _draw_previewed(self, logits, prefix, domain):
         """``_draw`` with the uniform read from a copy of the generator; the
@@ -882,7 +957,7 @@ class SamplingWork:
         are computed once per transaction (prepared() runs at prepare and
         again at commit)."""
         if self._counts_sha is None:
-            self._counts_sha = _count_hashes(self.counts, self.generated_counts)
+            self._counts_sha = _count_hashes(self._controls.counts, self._controls.generated)
         elif not isinstance(self._counts_sha, tuple):
             self._counts_sha = self._counts_sha.result()
         decision = asdict(self.decision)

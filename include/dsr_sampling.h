@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSR_ABI_VERSION 5
+#define DSR_ABI_VERSION 6
 #define DSR_MAX_VOCAB 129280        /* sampling.py:50 */
 #define DSR_MAX_COUNT 1048576       /* sampling.py:57 */
 #define DSR_MAX_DRAFTS 5            /* sampling.py:255 */
@@ -419,6 +419,16 @@ int32_t dsr_prob_accept(const double* p, const double* q, int64_t n, int32_t x, 
  * row is spread over workgroups of 4,096 values; nothing is read back, so
  * a caller can read the flags with its next synchronisation. */
 int32_t dsr_rows_finite(const float* x, int64_t rows, int64_t n, int64_t ld, int32_t* out, void* stream);
+
+/* Host-side scan of a terminal count vector (no device work), in one
+ * read-only pass: the checks of terminal_sampling.py:58-61 (no entry
+ * negative, the int64 sum).  `width` is the entry size (4 or 8);
+ * `support` (room for n) receives the indices of the positive entries,
+ * ascending; out3 = {positive entries, their int64 sum (wrapping as NumPy's
+ * does), the largest entry}.  The caller keeps the positive entries as its
+ * frozen copy of the vector (:77-79).  Returns 0, 1 when an entry is
+ * negative (the other outputs are then meaningless), or DSR_ERR_ARG. */
+int32_t dsr_count_scan(const void* counts, int32_t width, int64_t n, int64_t* support, int64_t* out3);
 
 /* Device history tables: the reference's dense per-request counts and
  * generated counts (history.py:46-47,92,136-137; terminal_sampling.py

@@ -157,9 +157,15 @@ def test_verify_hint_needs_filter_free_policies_and_plain_inputs():
         assert batch.verify_hints(batch.policy_array([dict(), bad]), 129280, True) == 0
 
 
+def _frozen(v):
+    from deepseekrpc_amd import terminal_sampling as T
+    support = np.flatnonzero(v > 0)
+    return T._Counts(support, v[support], v.size, v.dtype)
+
+
 def _hash_in_child(q):
     from deepseekrpc_amd import terminal_sampling as T
-    c = np.arange(5, dtype=np.int64)
+    c = _frozen(np.arange(5, dtype=np.int64))
     q.put(T._hash_worker().submit(T._count_hashes, c, c).result(timeout=20)[0])
 
 
@@ -168,7 +174,8 @@ def test_count_hash_worker_runs_in_a_forked_child():
     parent used it still gets its hashes."""
     import multiprocessing as mp
     from deepseekrpc_amd import terminal_sampling as T
-    c = np.arange(5, dtype=np.int64)
+    v = np.arange(5, dtype=np.int64)
+    c = _frozen(v)
     want = T._hash_worker().submit(T._count_hashes, c, c).result(timeout=20)[0]
     ctx = mp.get_context("fork")
     q = ctx.Queue()
@@ -176,4 +183,5 @@ def test_count_hash_worker_runs_in_a_forked_child():
     p.start()
     got = q.get(timeout=30)
     p.join(timeout=30)
-    assert p.exitcode == 0 and got == want == T._sha256_i8(c)
+    assert p.exitcode == 0 and got == want == T._sha256_i8(v)
+    assert np.array_equal(c.dense(), v) and not c.dense().flags.writeable and c.at(3) == 3 and c.at(0) == 0

@@ -198,3 +198,37 @@ def test_struct_layouts_match_header(tmp_path):
         assert got[(cname, "size")] == ctypes.sizeof(cls), cname
         for f, _ in cls._fields_:
             assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
+
+
+def test_count_scan_is_numpys_support_sum_and_max():
+    """dsr_count_scan (host code, no device) against NumPy on ragged
+    lengths, blocks of zeros, negative entries, int64 sums that wrap, both
+    widths and the empty vector."""
+    import numpy as np
+
+    from deepseekrpc_amd import batch
+    rng = np.random.default_rng(4242)
+    for dtype in (np.int32, np.int64):
+        for n in (0, 1, 7, 63, 64, 65, 129, 1000, 129280):
+            for case in range(4):
+                c = np.zeros(n, dtype)
+                if n:
+                    idx = rng.choice(n, min(n, int(rng.integers(1, 50))), replace=False)
+                    c[idx] = rng.integers(1, 9, idx.size)
+                    if case == 1:
+                        c[rng.integers(0, n)] = -1
+                    if case == 2:
+                        c[idx[:4]] = np.iinfo(dtype).max // 2 + 1  # the int64 sum may wrap
+                got = batch.count_scan(c)
+                if (c < 0).any():
+                    assert got is None
+                    continue
+                support = np.flatnonzero(c > 0)
+                want_total = int(c[support].sum(dtype=np.int64))
+                want_max = int(c[support].max()) if support.size else 0
+                assert got is not None and np.array_equal(got[0], support)
+                assert got[1] == want_total and got[2] == want_max
+    lib = N.load()
+    out = np.zeros(3, np.int64)
+    assert lib.dsr_count_scan(None, 4, 5, out.ctypes.data, out.ctypes.data) == -1  # DSR_ERR_ARG
+    assert lib.dsr_count_scan(out.ctypes.data, 2, 1, out.ctypes.data, out.ctypes.data) == -1

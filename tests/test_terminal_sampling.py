@@ -347,6 +347,43 @@ def test_a_non_finite_cuda_window_is_reported_before_later_errors():
     assert sampler.random.snapshot() == RandomStreams(3).snapshot()
 
 
+def test_a_seed_launched_ahead_of_its_checks_changes_nothing_when_they_fail():
+    """A CUDA seed window with no grammar, bias or penalties is sampled while
+    the host checks the controls; a failing check raises its own message and
+    leaves the RNG where it was, counts whose int64 sum wraps take the
+    ordinary route to the row's error, and the next valid seeds draw the
+    oracle's tokens in sequence."""
+    from oracle import sampling_oracle as O
+    rng = np.random.default_rng(31)
+    logits = rng.normal(0, 2, (1, V)).astype(np.float32)
+    device_logits = torch.from_numpy(logits).cuda()
+    sampler = TerminalSampler(404)
+    bad_counts = np.zeros(V, np.int32)
+    bad_counts[5] = -1
+    with pytest.raises(ValidationError, match="exact published token history"):
+        sampler.begin_seed(device_logits, policy=SamplingPolicy(), counts=bad_counts, remaining=3)
+    with pytest.raises(ValidationError, match="remaining output capacity"):
+        sampler.begin_seed(device_logits, policy=SamplingPolicy(), counts=np.zeros(V, np.int32), remaining=0)
+    wrap = np.zeros(V, np.int64)
+    wrap[:4] = 1 << 62
+    with pytest.raises(ValidationError, match="frequency counts"):
+        sampler.begin_seed(device_logits, policy=SamplingPolicy(), counts=wrap, remaining=3)
+    assert sampler.active is None and not sampler.random.active
+    assert sampler.random.snapshot() == RandomStreams(404).snapshot()
+    reference = RandomStreams(404).begin()
+    policy = dict(temperature=0.7, top_k=50, top_p=0.9)
+    for _ in range(2):
+        work = sampler.begin_seed(device_logits, policy=SamplingPolicy(**policy), counts=np.zeros(V, np.int32),
+                                  remaining=4)
+        with pytest.raises(ValidationError, match="active"):
+            sampler.begin_seed(device_logits, policy=SamplingPolicy(**policy), counts=np.zeros(V, np.int32),
+                               remaining=4)
+        ref = O.sample_row(logits[0], O.Policy(**policy), reference.random("target"))
+        assert work.decision.token == ref.token
+        work.commit(work.prepared()["digest"])
+    assert sampler.random.snapshot() == reference.commit()
+
+
 def test_proposal_rows_are_kept_on_the_device_for_verification():
     sampler = TerminalSampler(99)
     history = np.zeros(V, np.int32)
