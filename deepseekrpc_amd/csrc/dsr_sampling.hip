@@ -615,18 +615,37 @@ __global__ __launch_bounds__(kNpBufThreads) void k_vprobs_stats(dsr_verify_probs
 
 // Step 2.  Lane b holds buffer b of the row being combined.
 __global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, VpLayout L) {
+  constexpr int kSlots = 2 * DSR_MAX_DRAFTS + 1;
   __shared__ Decision d;
   __shared__ double gua[DSR_MAX_DRAFTS];
-  __shared__ int32_t sst[2 * DSR_MAX_DRAFTS + 1], samax[2 * DSR_MAX_DRAFTS + 1];
+  __shared__ int32_t sst[kSlots], samax[kSlots];
+  __shared__ VpStat stats[kSlots * kVpBuffers];
+  __shared__ double pv[2 * DSR_MAX_DRAFTS];  // target j, then draft j, at draft j's token
   const int64_t row = blockIdx.x;
   const int K = a.K, slots = 2 * K + 1, l = lane_id();
   const int nbuf = (int)((a.vocab + kNpBuffer - 1) / kNpBuffer);
+  auto status_in = [&](int slot) {
+    return slot <= K && a.target_status ? a.target_status[row * (K + 1) + slot] : (int32_t)DSR_OK;
+  };
+  // Every load the chain needs, issued at once: the buffers' statistics of
+  // each row, and the two probabilities of each draft's token (a row that
+  // failed to build, or a token outside the vocabulary, is not read).
+  for (int i = l; i < slots * kVpBuffers; i += 64) {
+    const int slot = i / kVpBuffers, b = i % kVpBuffers;
+    if (b < nbuf && status_in(slot) == DSR_OK) stats[i] = L.stat[(row * slots + slot) * kVpBuffers + b];
+  }
+  if (l < 2 * K) {
+    const int j = l < K ? l : l - K;
+    const int slot = l < K ? j : K + 1 + j;
+    const int32_t x = a.draft_ids[row * K + j];
+    const double* p = status_in(slot) == DSR_OK ? probs_row(a, row, slot) : nullptr;
+    pv[l] = p && x >= 0 && x < a.vocab ? p[x] : 0.0;
+  }
+  __syncthreads();
   for (int slot = 0; slot < slots; ++slot) {  // uniform
-    int st = DSR_OK;
-    if (slot <= K && a.target_status) st = a.target_status[row * (K + 1) + slot];
+    int st = status_in(slot);
     int32_t amax = -1;
     if (st == DSR_OK) {
-      const VpStat* r = L.stat + (row * slots + slot) * kVpBuffers;
       VpStat x;
       x.sum = 0.0;
       x.max = -INFINITY;
@@ -634,7 +653,7 @@ __global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, 
       x.npos = 0;
       x.first = -1;
       x.amax = -1;
-      if (l < nbuf) x = r[l];
+      if (l < nbuf) x = stats[slot * kVpBuffers + l];
       double total = 0.0;  // np.add.reduce adds the buffers' sums in order
       for (int b = 0; b < nbuf; ++b) {
         const double v = __shfl(x.sum, b);
@@ -664,7 +683,7 @@ __global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, 
   verify_precheck(a, rq, status_of, d);
   if (d.status == DSR_OK)
     verify_chain(
-        a, rq, greedy, 0.0, status_of, [&](int slot, int j) { return probs_row(a, row, slot)[rq.ids[j]]; },
+        a, rq, greedy, 0.0, status_of, [&](int slot, int j) { return slot <= K ? pv[j] : pv[K + j]; },
         [&](int j) { return (int64_t)samax[j]; }, [](int) {}, d);
   if (d.status == DSR_OK && d.next != 0 && greedy) {  // the target's argmax (sampling.py:286,290)
     verify_append(a, rq, d, samax[d.draw_j], 0);
