@@ -621,12 +621,32 @@ __global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, 
   __shared__ int32_t sst[kSlots], samax[kSlots];
   __shared__ VpStat stats[kSlots * kVpBuffers];
   __shared__ double pv[2 * DSR_MAX_DRAFTS];  // target j, then draft j, at draft j's token
+  __shared__ int32_t tst[DSR_MAX_DRAFTS + 1];  // the target rows' build statuses
+  // The request, staged: draft ids, pre-drawn accept uniforms, the output
+  // limit and greedy flag, the EOS range and its first kEosStage ids, and the
+  // accept domain's PCG64 state (the one thread that runs the chain then
+  // reads no global memory on its way).
+  constexpr int kEosStage = 64;
+  __shared__ int32_t sids[DSR_MAX_DRAFTS], seos[kEosStage], smeta[2];
+  __shared__ double sua[DSR_MAX_DRAFTS];
+  __shared__ int64_t seoff[2];
+  __shared__ uint64_t srng[4];
   const int64_t row = blockIdx.x;
   const int K = a.K, slots = 2 * K + 1, l = lane_id();
   const int nbuf = (int)((a.vocab + kNpBuffer - 1) / kNpBuffer);
-  auto status_in = [&](int slot) {
-    return slot <= K && a.target_status ? a.target_status[row * (K + 1) + slot] : (int32_t)DSR_OK;
-  };
+  if (l <= K) tst[l] = a.target_status ? a.target_status[row * (K + 1) + l] : (int32_t)DSR_OK;
+  if (l < K) {
+    sids[l] = a.draft_ids[row * K + l];
+    if (a.u_accept) sua[l] = a.u_accept[row * K + l];
+  }
+  if (l == 32) smeta[0] = a.output_limit[row];
+  if (l == 33) smeta[1] = a.greedy ? (int32_t)a.greedy[row] : 0;
+  if (l >= 34 && l < 36) seoff[l - 34] = a.eos_off ? a.eos_off[row + (l - 34)] : 0;
+  if (l >= 40 && l < 44 && a.rng_accept) srng[l - 40] = a.rng_accept[4 * row + (l - 40)];
+  __syncthreads();
+  auto status_in = [&](int slot) { return slot <= K ? tst[slot] : (int32_t)DSR_OK; };
+  const int64_t e0 = seoff[0], n_eos = seoff[1] - seoff[0];
+  if (l < n_eos && l < kEosStage) seos[l] = a.eos_ids[e0 + l];
   // Every load the chain needs, issued at once: the buffers' statistics of
   // each row, and the two probabilities of each draft's token (a row that
   // failed to build, or a token outside the vocabulary, is not read).
@@ -637,47 +657,49 @@ __global__ __launch_bounds__(64) void k_vprobs_chain(dsr_verify_probs_args_t a, 
   if (l < 2 * K) {
     const int j = l < K ? l : l - K;
     const int slot = l < K ? j : K + 1 + j;
-    const int32_t x = a.draft_ids[row * K + j];
+    const int32_t x = sids[j];
     const double* p = status_in(slot) == DSR_OK ? probs_row(a, row, slot) : nullptr;
     pv[l] = p && x >= 0 && x < a.vocab ? p[x] : 0.0;
   }
   __syncthreads();
-  for (int slot = 0; slot < slots; ++slot) {  // uniform
-    int st = status_in(slot);
+  // Lane s settles row s from its buffers' statistics, all rows at once.
+  if (l < slots) {
+    int st = status_in(l);
     int32_t amax = -1;
     if (st == DSR_OK) {
-      VpStat x;
-      x.sum = 0.0;
-      x.max = -INFINITY;
-      x.ok = 1;
-      x.npos = 0;
-      x.first = -1;
-      x.amax = -1;
-      if (l < nbuf) x = stats[slot * kVpBuffers + l];
-      double total = 0.0;  // np.add.reduce adds the buffers' sums in order
+      double total = 0.0, M = -INFINITY;  // np.add.reduce adds the buffers' sums in order
+      bool ok = true;
+      long long am = LLONG_MAX;
       for (int b = 0; b < nbuf; ++b) {
-        const double v = __shfl(x.sum, b);
-        total = b == 0 ? v : total + v;
+        const VpStat x = stats[l * kVpBuffers + b];
+        total = b == 0 ? x.sum : total + x.sum;
+        ok = ok && x.ok;
+        if (x.max > M) {
+          M = x.max;
+          am = x.amax;
+        } else if (x.max == M && (long long)x.amax < am) {
+          am = x.amax;
+        }
       }
-      const bool ok = wave_reduce_dpp(x.ok ? 0ll : 1ll, OpMax()) == 0;
-      const double M = wave_reduce_dpp(x.max, OpMax());
-      const long long am = wave_reduce_dpp(l < nbuf && x.max == M ? (long long)x.amax : LLONG_MAX, OpMin());
       amax = am == LLONG_MAX ? -1 : (int32_t)am;
       // _distribution (sampling.py:109-115): finite, >= 0, sum within 1e-10 of 1.
       st = ok && fabs(total - 1.0) <= 1e-10 ? DSR_OK : DSR_E_DISTRIBUTION;
     }
-    if (l == 0) {
-      sst[slot] = st;
-      samax[slot] = amax;
-    }
+    sst[l] = st;
+    samax[l] = amax;
   }
   __syncthreads();
   if (l != 0) return;
   auto status_of = [&](int slot) { return (int)sst[slot]; };
-  const bool greedy = a.greedy && a.greedy[row] != 0;
-  Request rq = request_of(a, row);
+  const bool greedy = smeta[1] != 0;
+  Request rq;  // request_of's fields, from the staged copies
+  rq.ids = sids;
+  rq.ua = sua;
+  rq.eos = n_eos <= kEosStage ? seos : a.eos_ids + e0;
+  rq.n_eos = (int)n_eos;
+  rq.limit = smeta[0];
   if (a.rng_accept) {  // the accept domain's next K draws, consumed in order
-    pcg64_draws(a.rng_accept + 4 * row, K, gua);
+    pcg64_draws(srng, K, gua);
     rq.ua = gua;
   }
   verify_precheck(a, rq, status_of, d);
@@ -764,11 +786,8 @@ __global__ __launch_bounds__(64) void k_vprobs_finish(dsr_verify_probs_args_t a,
     np_ = parts[l].npos;
     f = parts[l].npos > 0 ? (long long)parts[l].first : LLONG_MAX;
   }
-  double total = 0.0;  // np.add.reduce's order over the buffers
-  for (int b = 0; b < nbuf; ++b) {
-    const double v = __shfl(bs, b);
-    total = b == 0 ? v : total + v;
-  }
+  double total = lane_value(bs, 0);  // np.add.reduce's order over the buffers
+  for (int b = 1; b < nbuf; ++b) total += lane_value(bs, b);
   const long long npos = wave_reduce_dpp(np_, OpSum());
   const long long first = wave_reduce_dpp(f, OpMin());
   int64_t rep = -1;
