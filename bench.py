@@ -72,6 +72,9 @@ WORKLOADS = {
     "head": ("verify-rows/sec with the vocabulary projection: B=32 requests × K=4 drafts, 160 target rows × "
              "dim 5,120 → V=129,280 fp32 logits", "verify-rows/s", 30,
              "k_vocab_head + k_head_shares + k_verify_chain + k_verify_draw + k_verify_finish"),
+    "headk": ("sampled rows/sec with the vocabulary projection: 8 rows × dim 5,120 → V=129,280 fp32 logits, top-k "
+              "50 sampled from the projection's per-tile records", "rows/s", 32,
+              "k_vocab_head + k_sample_f32 (from the records)"),
     "propose": ("drop-in 5-row draft proposal steps/sec at V=129,280 fp32, one host synchronisation per step",
                 "chains/s", 100, "k_zero_probs + k_sample_f32 (5x; a policy without penalties carries no "
                 "history table)"),
@@ -80,7 +83,7 @@ WORKLOADS = {
 # Name prefix of a workload's committed profile summaries when it is not its first kernel's.
 PROFILE_PREFIX = {"c4": "k_verify", "c1": "k_sample_f32", "propose": "k_sample_f32", "seed": "k_sample_f32",
                   "step": "k_sample_f32",
-                  "head": "k_vocab_head"}
+                  "head": "k_vocab_head", "headk": "k_vocab_head"}
 
 DESCRIPTIONS = {
     "c1": "c1: 1 row x 129280 fp32 N(0,2^2), T 0.7, top-k 50, top-p 0.9, fp32 probabilities out",
@@ -104,6 +107,9 @@ DESCRIPTIONS = {
             "[160, 5120] x bf16 weight [129280, 5120] -> fp32 logits with per-tile verifier records), then "
             "verification of 4 drafts per request whose rows and records came from the same projection; default "
             "policy, limit 10",
+    "headk": "headk: the terminal stage's vocabulary projection of 8 rows (bf16 hidden [8, 5120] x bf16 weight "
+             "[129280, 5120] -> fp32 logits with per-tile records), then top-k sampling of every row from the "
+             "records (T 0.7, top-k 50, top-p 0.9, pre-drawn uniforms)",
     "propose": "propose: TerminalSampler.begin_verification, SamplingWork.propose over a device graph, then abort; "
                "5 fp32 rows x 129280 N(0,2^2), row j = base j with the previous token raised by 4 on the device, "
                "T 0.7 / top-k 50 / top-p 0.9, dense int32 counts of a 64-token history, draft PCG64 draws on the "
@@ -119,6 +125,8 @@ def _units(name, w):
         return w.extra["target"].shape[0]
     if name == "head":
         return w.extra["requests"]
+    if name == "headk":
+        return w.extra["rows"]
     if name in ("propose", "seed", "step"):
         return 1
     return w.extra["tokens"].shape[0] if name == "hist" else w.rows
@@ -151,6 +159,13 @@ def _cpu_rows(span):
         return hi - lo, _cpu_chains(w, hi - lo)
     if name == "step":
         return hi - lo, _cpu_steps(w, hi - lo)
+    if name == "headk":
+        e = w.extra
+        t0 = time.perf_counter()
+        for r in range(lo, hi):
+            r %= e["rows"]
+            O.sample_row(e["cpu_logits"][r], O.Policy(**w.policies[r]), float(w.uniforms[r]), keep_probs=False)
+        return hi - lo, time.perf_counter() - t0
     if name == "head":
         e = w.extra
         t0 = time.perf_counter()
@@ -271,6 +286,19 @@ def _head_cpu_rows(w):
                                   keep_probs=False).token for j in range(K)] for r in range(R)]
 
 
+def _headk_cpu_rows(w):
+    """The headk workload's logits for the CPU sample, by NumPy's float32
+    product of the same bf16 values (untimed: the reference projects on its
+    GPU and samples the copied rows on the host, so only the sampling is
+    timed)."""
+    from deepseekrpc_amd import workloads
+    e = w.extra
+    wt = e["weight_q"].astype(np.float32)
+    wt *= np.float32(workloads.head_weight_scale())
+    e["cpu_logits"] = e["hidden"] @ wt.T
+    del wt
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -292,6 +320,8 @@ def cpu_baseline(name, w, passes):
     (the single-core figure); run before the GPU is initialised."""
     if name == "head":
         _head_cpu_rows(w)
+    if name == "headk":
+        _headk_cpu_rows(w)
     _CPU.update(w=w, name=name)
     os.environ["OMP_NUM_THREADS"] = "1"
     cores = max(1, min(CPU_WORKERS, os.cpu_count() or 1))
@@ -311,9 +341,9 @@ def cpu_baseline(name, w, passes):
     unit = WORKLOADS[name][1]
     what = {"c4": "requests", "head": "requests", "propose": "chains", "seed": "calls", "step": "steps"}.get(name, "rows")
     oracle = "NumPy history oracle (np.add.at on dense counts)" if name == "hist" else "float64 NumPy oracle"
-    if name == "head":
-        oracle += (" (verification only: the reference projects on its GPU; the rows' logits were computed "
-                   "beforehand by NumPy's float32 product, untimed)")
+    if name in ("head", "headk"):
+        oracle += (f" ({'verification' if name == 'head' else 'sampling'} only: the reference projects on its "
+                   "GPU; the rows' logits were computed beforehand by NumPy's float32 product, untimed)")
     return {"value": n / wall, "unit": unit, "cores": cores, "kind": "port",
             "value_1core": one_n / one_wall, "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
             "sample": f"{n} {what} ({passes} pass(es) over the {_units(name, w)} of the same workload, "
@@ -347,7 +377,7 @@ ROTATION_BYTES = 300 * 2**20
 
 
 def _batch_bytes(name, w):
-    if name == "head":
+    if name in ("head", "headk"):
         return w.extra["weight_q"].nbytes * 2   # the bf16 weight
     if name == "hist":
         return w.extra["tokens"].nbytes
@@ -364,7 +394,7 @@ def variants(name, w):
     """Distinct input batches of the workload (vocabulary layouts rolled by
     different shifts), at least 4 and together above ROTATION_BYTES."""
     from deepseekrpc_amd import workloads
-    if name == "head":
+    if name in ("head", "headk"):
         return [w]   # its weight stream (1.3 GB per step) is read from HBM on every step
     count = max(4, -(-ROTATION_BYTES // max(1, _batch_bytes(name, w))))
     V = w.logits.shape[1]
@@ -496,6 +526,36 @@ class _Head:
         return self
 
 
+class _HeadK:
+    """The vocabulary projection of the workload's rows with its records, then
+    dsr_sample_rows_head over the logits and records.  ``records=False`` is
+    the same step without records: the projection alone, then
+    dsr_sample_rows over the logits."""
+
+    def __init__(self, w, records=True):
+        import torch
+
+        from deepseekrpc_amd import batch, workloads
+        e = w.extra
+        dev = "cuda"
+        self.weight = (torch.from_numpy(e["weight_q"]).to(dev).to(torch.bfloat16)
+                       * workloads.head_weight_scale()).contiguous()
+        x = torch.from_numpy(e["hidden"]).to(dev).to(torch.bfloat16)
+        self.policies = batch.policy_tensor(w.policies, dev)
+        self.uniforms = torch.from_numpy(np.asarray(w.uniforms, np.float64)).to(dev)
+        self.hr = batch.vocab_head(x, self.weight, records=records)
+        self.records = records
+        self.inputs = (self.weight,)
+        self.launch()
+
+    def launch(self):
+        from deepseekrpc_amd import batch
+        batch.vocab_head_launch(self.hr)
+        self.result = batch.sample_rows(self.hr.logits, self.policies, uniforms=self.uniforms,
+                                        head_parts=self.hr.parts if self.records else None)
+        return self
+
+
 def _prepare(name, w, device_rng=False):
     """Device inputs and a launch closure for one step of the workload."""
     import torch
@@ -510,6 +570,15 @@ def _prepare(name, w, device_rng=False):
         tiles = V // batch.HEAD_TILE
         alg = V * D * 2 + R * (K + 1) * (D * 2 + V * 4 + tiles * 16) + R * K * tiles * 16 + R * 120
         return _Head(w), alg, R
+    if name == "headk":
+        e = w.extra
+        R, V, D = e["rows"], e["weight_q"].shape[0], e["dim"]
+        # The weight stream, the hidden rows, the logits and records written,
+        # the records read again and each row's k = 50 kept tokens' logits,
+        # and the policy, uniform and outputs.
+        tiles = V // batch.HEAD_TILE
+        alg = V * D * 2 + R * (D * 2 + V * 4 + 2 * tiles * 16 + 50 * 4 + 68)
+        return _HeadK(w), alg, R
     if name == "propose":
         per_row = w.logits.shape[1] * (4 + 8) + 64 + 4   # logits in, float64 distribution out, controls, token
         return _Chain(w), w.extra["steps"] * per_row + 4 * len(w.histories[0]), 1
@@ -576,7 +645,7 @@ def main():
     from deepseekrpc_amd import _native as N
 
     N.load()
-    if args.device_rng and name in ("c4", "head", "hist", "propose", "seed", "step"):
+    if args.device_rng and name in ("c4", "head", "headk", "hist", "propose", "seed", "step"):
         raise SystemExit("--device-rng applies to the sampling workloads (c1, c2, c3, c5)")
     batches = variants(name, w)
     preps = []
@@ -625,6 +694,7 @@ def main():
         torch.cuda.synchronize()
         calibration_bytes = src.numel() * 4
 
+    head_extra = {}
     if name == "head":
         # The same step without the projection's records: the projection
         # alone, then the verifier's statistics pass over the logits.
@@ -645,6 +715,27 @@ def main():
                       "unfused_kernels": "k_vocab_head (no records) + k_verify_stats + k_verify_chain + "
                                          "k_verify_draw + k_verify_finish", "decisions_equal": same}
         del plain
+    if name == "headk" and not args.copy_calibration:
+        # The same step without records: the projection alone, then
+        # dsr_sample_rows over the logits (left out of the counter runs, whose
+        # per-kernel averages would mix the two steps).
+        plain = _HeadK(w, records=False)
+        for _ in range(args.warmup):
+            plain.launch()
+        ev2, ev3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev2.record(stream)
+        for _ in range(args.steps):
+            plain.launch()
+        ev3.record(stream)
+        torch.cuda.synchronize()
+        same = all(torch.equal(getattr(plain.result, f), getattr(prep.result, f))
+                   for f in ("tokens", "consumed", "status", "flags"))
+        if not same:
+            raise SystemExit("the steps with and without records decided differently")
+        head_extra = {"unrecorded_step_ms": ev2.elapsed_time(ev3) / args.steps,
+                      "unrecorded_kernels": "k_vocab_head (no records) + k_sample_f32 (a pass over each row)",
+                      "decisions_equal": same}
+        del plain
     ms_per_step = wall * 1e3 / args.steps
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     # HBM traffic per launch is not measurable from inside the run (counters
@@ -660,7 +751,7 @@ def main():
            "input_batches": len(batches), "input_bytes_rotated": sum(_batch_bytes(name, v) for v in batches)}
     if name not in ("c4", "head", "hist", "propose", "seed", "step"):
         cfg["draws"] = "device PCG64 state per row" if args.device_rng else "pre-drawn uniforms"
-    if name == "head":
+    if name in ("head", "headk"):
         cfg.update(head_extra)
     if calibration_bytes is not None:
         cfg["calibration_bytes"] = calibration_bytes  # bytes the copy kernel reads, and writes, per launch

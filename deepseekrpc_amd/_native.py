@@ -51,7 +51,7 @@ EXPORTS = (
     "dsr_sample_rows", "dsr_verify_drafts", "dsr_prob_stats", "dsr_prob_categorical", "dsr_prob_correction",
     "dsr_prob_accept", "dsr_history_from_dense", "dsr_history_append", "dsr_sample_rows_noalloc",
     "dsr_vocab_head", "dsr_verify_drafts_head", "dsr_prob_stats_rows", "dsr_verify_probs_workspace_bytes",
-    "dsr_verify_probs", "dsr_rows_finite", "dsr_count_scan",
+    "dsr_verify_probs", "dsr_rows_finite", "dsr_count_scan", "dsr_sample_rows_head",
 )
 NOALLOC_SCRATCH_BYTES = 268435456
 HEAD_TILE = 128
@@ -175,6 +175,8 @@ def load(path: str = LIB_PATH):
     lib.dsr_verify_probs.argtypes = [ctypes.POINTER(VerifyProbsArgs), _p]
     lib.dsr_rows_finite.restype = _i32
     lib.dsr_rows_finite.argtypes = [_p, _i64, _i64, _i64, _p, _p]
+    lib.dsr_sample_rows_head.restype = _i32
+    lib.dsr_sample_rows_head.argtypes = [ctypes.POINTER(SampleArgs), _p, _p]
     lib.dsr_count_scan.restype = _i32
     lib.dsr_count_scan.argtypes = [_p, _i32, _i64, _p, _p]
     _lib = lib

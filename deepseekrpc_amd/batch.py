@@ -34,13 +34,19 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 _current_device = getattr(torch._C, "_cuda_getDevice", None)
 
 
-def _stream():
-    """The current stream's handle.  torch's raw accessor: the public
-    ``torch.cuda.current_stream()`` costs several microseconds a call, a
-    sizeable part of a one-row draw's host time."""
+def _stream_handle(device=None) -> int:
+    """The current stream's handle on ``device`` (default: the current
+    device).  torch's raw accessor: the public ``torch.cuda.current_stream()``
+    costs several microseconds a call, a sizeable part of a one-row draw's
+    host time."""
+    index = device.index if device is not None and device.index is not None else None
     if _raw_stream is not None and _current_device is not None:
-        return ctypes.c_void_p(_raw_stream(_current_device()))
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        return _raw_stream(_current_device() if index is None else index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _stream():
+    return ctypes.c_void_p(_stream_handle())
 
 
 def _require_cuda(t, name, rows_strided=False):
@@ -389,15 +395,19 @@ class Workspace:
         self._bufs = collections.OrderedDict()
         self._limit = max(1, int(streams))
 
-    def get(self, nbytes: int, device, stream=None) -> torch.Tensor:
+    def get(self, nbytes: int, device, stream=None, handle: int | None = None) -> torch.Tensor:
         device = torch.device(device)
         if device.index is None:
             device = torch.device(device.type, torch.cuda.current_device())
-        if stream is None:
-            stream = torch.cuda.current_stream(device)
-        key = (device.index, stream.cuda_stream)
+        if handle is None:
+            if stream is None:
+                stream = torch.cuda.current_stream(device)
+            handle = stream.cuda_stream
+        key = (device.index, handle)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if stream is None:
+                stream = torch.cuda.current_stream(device)
             with torch.cuda.stream(stream):
                 buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
             self._bufs[key] = buf
@@ -414,7 +424,7 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
                 allow_bits: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
                 rng_state: torch.Tensor | None = None, probs: str | None = None, kept: bool = False,
                 workspace: Workspace | None = None, noalloc: bool = False, hints: int | None = None,
-                out: dict | None = None) -> SampleResult:
+                out: dict | None = None, head_parts: torch.Tensor | None = None) -> SampleResult:
     """Sample every row of ``logits [rows, V]`` on the current stream.
 
     ``policies`` is a device tensor made by ``policy_tensor`` or a list of
@@ -430,7 +440,11 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     DSR_HINT_* bits derived from the policies (they choose launches only).
     ``out`` may supply any of the result tensors (``tokens``, ``consumed``,
     ``status``, ``flags``, ``probs``), contiguous and of the result's dtype
-    and shape, for the kernels to write in place.
+    and shape, for the kernels to write in place.  ``head_parts`` (the
+    ``parts`` of a ``vocab_head`` call that wrote these logits) lets FP32 top-k
+    rows without a mask start from the projection's per-tile maxima instead
+    of a pass over the row (``dsr_sample_rows_head``); the results are the
+    same.
     """
     lib = N.load()
     _require_cuda(logits, "logits", rows_strided=True)
@@ -470,6 +484,10 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
             raise ValueError("uniforms must be float64 [rows]")
     if rng_state is not None:
         _require(rng_state, "rng_state", torch.int64, rows * 4)
+    if head_parts is not None:
+        if noalloc:
+            raise ValueError("head_parts are not taken by the allocation-free entry point")
+        _require(head_parts, "head_parts", torch.int32, rows * (V // HEAD_TILE) * 4)
     if allow_bits is not None:
         _require_cuda(allow_bits, "allow_bits")
         if allow_bits.dim() != 2 or allow_bits.shape[0] != rows or allow_bits.element_size() != 4:
@@ -478,8 +496,8 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
     if noalloc and need > N.NOALLOC_SCRATCH_BYTES:
         raise ValueError(f"{rows} rows of {V} tokens need {need} bytes of scratch; the allocation-free entry point "
                          f"holds {N.NOALLOC_SCRATCH_BYTES}")
-    stream = torch.cuda.current_stream(dev)
-    ws = None if noalloc else (workspace or _default_ws).get(need, dev, stream)
+    stream = _stream_handle(dev)
+    ws = None if noalloc else (workspace or _default_ws).get(need, dev, handle=stream)
     a = N.SampleArgs()
     a.logits = logits.data_ptr()
     a.dtype = _DTYPES[logits.dtype]
@@ -507,14 +525,17 @@ def sample_rows(logits: torch.Tensor, policies, *, history: HistoryTable | None 
         a.probs_ld = V
     if res.kept_bits is not None:
         a.out_kept_bits, a.kept_ld = res.kept_bits.data_ptr(), res.kept_bits.stride(0)
-    handle = ctypes.c_void_p(stream.cuda_stream)
+    handle = ctypes.c_void_p(stream)
     if noalloc:
         N.check(lib.dsr_sample_rows_noalloc(ctypes.byref(a), handle), "dsr_sample_rows_noalloc")
     else:
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        N.check(lib.dsr_sample_rows(ctypes.byref(a), handle), "dsr_sample_rows")
+        if head_parts is not None:
+            N.check(lib.dsr_sample_rows_head(ctypes.byref(a), _ptr(head_parts), handle), "dsr_sample_rows_head")
+        else:
+            N.check(lib.dsr_sample_rows(ctypes.byref(a), handle), "dsr_sample_rows")
     res.args = a
-    res.keep = (logits, policies, history, bias, allow_bits, uniforms, rng_state, ws)
+    res.keep = (logits, policies, history, bias, allow_bits, uniforms, rng_state, ws, head_parts)
     return res
 
 
@@ -817,7 +838,7 @@ def verify_drafts(target: torch.Tensor, draft: torch.Tensor, draft_ids: torch.Te
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     res = VerifyResult(i32(rows), i32(rows, K + 1), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows), i32(rows),
                        torch.empty(rows, dtype=torch.uint8, device=dev))
-    ws = (workspace or _default_ws).get(lib.dsr_verify_workspace_bytes(rows, K, V), dev)
+    ws = (workspace or _default_ws).get(lib.dsr_verify_workspace_bytes(rows, K, V), dev, handle=_stream_handle(dev))
     a = N.VerifyArgs()
     a.target = target.data_ptr()
     a.draft = draft.data_ptr() if K > 0 else None
@@ -944,7 +965,7 @@ def verify_probs(target_rows, draft_rows, draft_ids: torch.Tensor, output_limit:
     i32 = lambda *sh: torch.empty(*sh, dtype=torch.int32, device=dev)
     res = VerifyResult(i32(R), i32(R, K + 1), i32(R), i32(R), i32(R), i32(R), i32(R), i32(R),
                        torch.empty(R, dtype=torch.uint8, device=dev))
-    ws = (workspace or _default_ws).get(max(lib.dsr_verify_probs_workspace_bytes(R, K), 8), dev)
+    ws = (workspace or _default_ws).get(max(lib.dsr_verify_probs_workspace_bytes(R, K), 8), dev, handle=_stream_handle(dev))
     a = N.VerifyProbsArgs()
     a.target = ptrs.data_ptr()
     a.draft = ptrs.data_ptr() + 8 * R * (K + 1) if K else None

@@ -337,6 +337,144 @@ __device__ __forceinline__ int f32_sorted_tail(const RowSpec& r, F32Lists& t, Ge
   return DSR_OK;
 }
 
+// The 16-bit prefix of the k-th largest of the 16-bit key prefixes that the
+// workgroup's threads hold (NV each, val(0 .. NV-1); 0 is not counted), D
+// the largest of them; 0 when fewer than k are counted.  By distance d = D -
+// prefix: a coarse histogram of d / 8 over d < 2,048 (sixteen binades below a
+// positive maximum), then a fine one of d % 8 inside the selected coarse bin.
+// Few lanes of a wave share a bin either way, so the LDS atomics rarely
+// serialise; by top byte of the key instead, most prefixes of a row share a
+// handful of bins and a wave's atomics would hit one address.  Rows with
+// fewer than k prefixes inside that distance take two 8-bit radix passes
+// over the whole prefix instead.  Each wave counts into its own histogram,
+// cleared by itself.  Every thread calls it.
+template <int NV, class Val>
+__device__ __forceinline__ uint32_t f32_tau16(F32Lists& t, int wave, int lane, uint32_t D, long long k, Val val) {
+  auto clear_hist = [&]() {
+    *reinterpret_cast<uint4*>(&t.hist[wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+  };
+  uint32_t tau16 = 0u;
+  {
+    long long rem = k;
+    uint32_t cbin = 0u;  // selected coarse bin (d / 8)
+    for (int pass = 0; pass < 2; ++pass) {
+      clear_hist();
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const uint32_t x = val(i);
+        const uint32_t d = D - x;  // x <= D
+        if (pass == 0) {
+          if (x != 0u && d < 8u * kF32Bins) atomicAdd(&t.hist[wave][kF32Bins - 1 - (d >> 3)], 1u);
+        } else {
+          if (x != 0u && (d >> 3) == cbin) atomicAdd(&t.hist[wave][kF32Bins - 1 - (d & 7u)], 1u);
+        }
+      }
+      __syncthreads();
+      long long above;
+      const int b = f32_pick(t, rem, above);  // uniform
+      if (b < 0) break;  // fewer than k inside the distance (pass 0 only)
+      rem -= above;
+      if (pass == 0) cbin = (uint32_t)(kF32Bins - 1 - b);
+      else tau16 = D - (8u * cbin + (uint32_t)(kF32Bins - 1 - b));
+    }
+  }
+  if (tau16 == 0u) {
+    uint32_t prefix = 0u;
+    long long rem = k;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int shift = pass == 0 ? 24 : 16;
+      clear_hist();
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const uint32_t x = val(i) << 16;
+        const bool cnt = x != 0u && (pass == 0 || (x >> 24) == (prefix >> 24));
+        if (cnt) atomicAdd(&t.hist[wave][(x >> shift) & 0xFFu], 1u);
+      }
+      __syncthreads();
+      long long above;
+      const int b = f32_pick(t, rem, above);
+      if (b < 0) return 0u;  // fewer than k counted
+      rem -= above;
+      prefix |= (uint32_t)b << shift;
+    }
+    tau16 = prefix >> 16;
+  }
+  return tau16;
+}
+
+// From the per-wave token lists (t.lv / t.li, wn entries in this wave) to
+// the row's decision: the row-wide list as float64 z = (v - max) / T, then
+// f32_sorted_tail, or radix_top_k and filter_tail when a bucket is too full.
+__device__ __forceinline__ int f32_list_finish(const RowSpec& r, F32Shared& shu, int wave, int lane, int wn, double M,
+                                               long long k, int64_t V, unsigned& flags, DistOut& out, int64_t& n,
+                                               int& why) {
+  F32Lists& t = shu.t;
+  GenShared& sh = shu.gen;
+  const int tid = threadIdx.x;
+  const dsr_policy_t& p = r.pol;
+  if (lane == 0) t.wn[wave] = wn;
+  __syncthreads();
+  int base = 0, total = 0, over = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int c = t.wn[w];
+    over |= c > kF32WaveCap ? 1 : 0;
+    if (w < wave) base += c;
+    total += c;
+  }
+  if (over) {
+    why = kHandCapacity;
+    return -1;
+  }
+  // The row-wide list in index order, as float64 (v - max) / T
+  // (sampling.py:86-88, true division).
+  const double T = p.temperature;
+  for (int i = lane; i < wn; i += 64) {
+    t.cz[base + i] = ((double)t.lv[wave][i] - M) / T;
+    t.cid[base + i] = t.li[wave][i];
+  }
+  __syncthreads();
+  const int64_t nc = total;
+
+  const int st = f32_sorted_tail(r, t, sh, nc, k, V, flags, out, n);
+  if (st != kTailFallback) return st;
+
+  // ---- a bucket too full to rank: radix top-k over the list
+  // (sampling.py:89-91), the kept tokens in index order, and filter_tail.
+  uint64_t kth = 0;
+  int64_t cut = INT64_MAX;
+  if (k < nc) radix_top_k(t.cz, nc, k, sh, kth, cut);
+  auto kept = [&](int64_t j, double z) {
+    const uint64_t key = order_key(z);
+    return z > -(double)INFINITY && (key > kth || (key == kth && j <= cut));
+  };
+  int64_t lo, hi;
+  slice_of(tid, nc, lo, hi);
+  long long cnt = 0;
+  for (int64_t j = lo; j < hi; ++j) cnt += kept(j, t.cz[j]) ? 1 : 0;
+  long long nk;
+  long long pos = block_exclusive_scan_i64(cnt, sh.b, nk);
+  if (nk > kSplitMaxK || nk < 1) {  // not reached: top-k keeps k tokens, the maximum among them
+    why = kHandCapacity;
+    return -1;
+  }
+  for (int64_t j = lo; j < hi; ++j) {
+    const double z = t.cz[j];
+    if (kept(j, z)) {
+      const int32_t i = t.cid[j];
+      t.kz[pos] = z;
+      t.kid[pos] = i;
+      ++pos;
+      if (r.kept_bits) atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  n = nk;
+  const int32_t* kid = t.kid;
+  return filter_tail(r, t.kz, nk, V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; });
+}
+
 // Returns a status when the row is decided (kz / kid then hold the n final
 // probabilities and their tokens, in index order), or -1 with the reason in
 // `why` when the general path must decide it.
@@ -495,69 +633,12 @@ __device__ __forceinline__ int f32_distribution(const dsr_sample_args_t& a, int6
   // ---- tau: the 16-bit prefix of the k-th largest maximum over pairs of
   // quads (slots 2i and 2i + 1 of a lane; counted keys > 0).  The pairs
   // partition the row, so this is a lower bound for the k-th largest token
-  // too.  By distance d = D - prefix from the row maximum's prefix D: a
-  // coarse histogram of d / 8 over d < 2,048 (sixteen binades below a
-  // positive maximum), then a fine one of d % 8 inside the selected coarse
-  // bin.  Few lanes of a wave share a bin either way, so the LDS atomics
-  // rarely serialise; by top byte of the key instead, most pairs of a row
-  // share a handful of bins and a wave's atomics would hit one address.
-  // Rows with fewer than k pairs inside that distance take two 8-bit radix
-  // passes over the whole prefix instead.  Each wave counts into its own
-  // histogram, cleared by itself.
+  // too.
   auto pair16 = [&](int i) -> uint32_t { return max(qp[i] & 0xFFFFu, qp[i] >> 16); };
-  auto clear_hist = [&]() {
-    *reinterpret_cast<uint4*>(&t.hist[wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
-    wave_lds_sync();
-  };
-  const uint32_t D = K >> 16;
-  uint32_t tau16 = 0u;
-  {
-    long long rem = k;
-    uint32_t cbin = 0u;  // selected coarse bin (d / 8)
-    for (int pass = 0; pass < 2; ++pass) {
-      clear_hist();
-#pragma unroll
-      for (int i = 0; i < kF32Slots / 2; ++i) {
-        const uint32_t x = pair16(i);
-        const uint32_t d = D - x;  // x <= D
-        if (pass == 0) {
-          if (x != 0u && d < 8u * kF32Bins) atomicAdd(&t.hist[wave][kF32Bins - 1 - (d >> 3)], 1u);
-        } else {
-          if (x != 0u && (d >> 3) == cbin) atomicAdd(&t.hist[wave][kF32Bins - 1 - (d & 7u)], 1u);
-        }
-      }
-      __syncthreads();
-      long long above;
-      const int b = f32_pick(t, rem, above);  // uniform
-      if (b < 0) break;  // fewer than k pairs inside the distance (pass 0 only)
-      rem -= above;
-      if (pass == 0) cbin = (uint32_t)(kF32Bins - 1 - b);
-      else tau16 = D - (8u * cbin + (uint32_t)(kF32Bins - 1 - b));
-    }
-  }
-  if (tau16 == 0u) {
-    uint32_t prefix = 0u;
-    long long rem = k;
-    for (int pass = 0; pass < 2; ++pass) {
-      const int shift = pass == 0 ? 24 : 16;
-      clear_hist();
-#pragma unroll
-      for (int i = 0; i < kF32Slots / 2; ++i) {
-        const uint32_t x = pair16(i) << 16;
-        const bool cnt = x != 0u && (pass == 0 || (x >> 24) == (prefix >> 24));
-        if (cnt) atomicAdd(&t.hist[wave][(x >> shift) & 0xFFu], 1u);
-      }
-      __syncthreads();
-      long long above;
-      const int b = f32_pick(t, rem, above);
-      if (b < 0) {  // fewer allowed finite pairs than k
-        why = kHandCapacity;
-        return -1;
-      }
-      rem -= above;
-      prefix |= (uint32_t)b << shift;
-    }
-    tau16 = prefix >> 16;
+  const uint32_t tau16 = f32_tau16<kF32Slots / 2>(t, wave, lane, K >> 16, k, pair16);
+  if (tau16 == 0u) {  // fewer allowed finite pairs than k
+    why = kHandCapacity;
+    return -1;
   }
   const uint32_t tau = tau16 << 16;
 
@@ -626,66 +707,155 @@ __device__ __forceinline__ int f32_distribution(const dsr_sample_args_t& a, int6
       }
     }
   }
-  if (lane == 0) t.wn[wave] = wn;
-  __syncthreads();
-  int base = 0, total = 0, over = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int c = t.wn[w];
-    over |= c > kF32WaveCap ? 1 : 0;
-    if (w < wave) base += c;
-    total += c;
-  }
-  if (over) {
-    why = kHandCapacity;
-    return -1;
-  }
-  // The row-wide list in index order, as float64 (v - max) / T
-  // (sampling.py:86-88, true division).
-  const double T = p.temperature;
-  for (int i = lane; i < wn; i += 64) {
-    t.cz[base + i] = ((double)t.lv[wave][i] - M) / T;
-    t.cid[base + i] = t.li[wave][i];
-  }
-  __syncthreads();
-  const int64_t nc = total;
-
-  const int st = f32_sorted_tail(r, t, sh, nc, k, V, flags, out, n);
-  if (st != kTailFallback) return st;
-
-  // ---- a bucket too full to rank: radix top-k over the list
-  // (sampling.py:89-91), the kept tokens in index order, and filter_tail.
-  uint64_t kth = 0;
-  int64_t cut = INT64_MAX;
-  if (k < nc) radix_top_k(t.cz, nc, k, sh, kth, cut);
-  auto kept = [&](int64_t j, double z) {
-    const uint64_t key = order_key(z);
-    return z > -(double)INFINITY && (key > kth || (key == kth && j <= cut));
-  };
-  int64_t lo, hi;
-  slice_of(tid, nc, lo, hi);
-  long long cnt = 0;
-  for (int64_t j = lo; j < hi; ++j) cnt += kept(j, t.cz[j]) ? 1 : 0;
-  long long nk;
-  long long pos = block_exclusive_scan_i64(cnt, sh.b, nk);
-  if (nk > kSplitMaxK || nk < 1) {  // not reached: top-k keeps k tokens, the maximum among them
-    why = kHandCapacity;
-    return -1;
-  }
-  for (int64_t j = lo; j < hi; ++j) {
-    const double z = t.cz[j];
-    if (kept(j, z)) {
-      const int32_t i = t.cid[j];
-      t.kz[pos] = z;
-      t.kid[pos] = i;
-      ++pos;
-      if (r.kept_bits) atomicOr(&r.kept_bits[i >> 5], 1u << (i & 31));
-    }
-  }
-  __syncthreads();
-  n = nk;
-  const int32_t* kid = t.kid;
-  return filter_tail(r, t.kz, nk, V, false, 0, -1, sh, flags, out, [kid](int64_t j) { return (int64_t)kid[j]; });
+  return f32_list_finish(r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
 }
 
+
+// ---------------------------------------------------------------------------
+// Rows whose logits came from dsr_vocab_head, with its per-tile records
+// (the tile's maximum and first column holding it, and flags): the records
+// stand in for pass 1.  tau is the 16-bit prefix of the k-th largest tile
+// maximum (the tiles partition the row, so it bounds the k-th largest token
+// from below), and only the tiles whose maximum reaches it are read.  A row
+// with fewer than k finite tiles, or more than kF32HeadMaxTiles tiles to
+// read, returns kHeadFull: the full front end (pass 1 over the row) then
+// decides it in the same workgroup.  The allow mask is not in the records,
+// so masked batches never come here.
+
+constexpr int kF32HeadTile = 128;      // columns per record (DSR_HEAD_TILE)
+constexpr int kF32HeadMaxTiles = 256;  // tiles a row may read again: a fifth of a 129,280-token row
+constexpr int kHeadFull = -3;
+
+static inline bool f32_head_eligible(const dsr_sample_args_t& a) {
+  return f32_path_eligible(a) && !a.allow_bits && a.vocab % kF32HeadTile == 0 && a.vocab / kF32HeadTile <= kThreads;
+}
+
+__device__ __forceinline__ int f32_distribution_head(const dsr_sample_args_t& a, int64_t row,
+                                                     const dsr_head_part_t* parts, const RowSpec& r, F32Shared& shu,
+                                                     unsigned& flags, DistOut& out, int64_t& n, int& why) {
+  F32Lists& t = shu.t;
+  GenShared& sh = shu.gen;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int64_t V = a.vocab;
+  const int NT = (int)(V / kF32HeadTile);
+  const dsr_policy_t& p = r.pol;
+  out.onehot = -1;
+  out.npos = 0;
+  out.first = -1;
+  if (!policy_ok(p)) {
+    why = kHandPolicy;
+    return -1;
+  }
+  if (p.temperature != 0.0 && !(p.top_k >= 1 && p.top_k <= kSplitMaxK && p.top_k < V)) {
+    why = kHandTopK;
+    return -1;
+  }
+  const long long k = p.temperature == 0.0 ? 1 : p.top_k;
+
+  // Thread t holds tile t's record: its maximum's key (0 without a finite
+  // value), the maximum's first index, and NaN / +inf.
+  uint32_t key = 0u, fidx = 0xFFFFFFFFu, bad = 0u;
+  if (tid < NT) {
+    const dsr_head_part_t pt = parts[row * NT + tid];
+    const uint32_t info = (uint32_t)pt.info, col = info >> 8;
+    bad = info & 1u;
+    if ((info & 2u) && col < (uint32_t)kF32HeadTile) {
+      key = f32_key(__float_as_uint(pt.max), true);
+      fidx = (uint32_t)tid * kF32HeadTile + col;
+    }
+  }
+  if (r.kept_bits)
+    for (int64_t w = tid; w < r.kept_words; w += kThreads) r.kept_bits[w] = 0u;
+  const uint64_t mine = bad ? ~0ull : (((uint64_t)key << 32) | (uint64_t)(~fidx));
+  const uint64_t top = (uint64_t)block_max_i64((long long)(mine ^ 0x8000000000000000ull), sh.b) ^ 0x8000000000000000ull;
+  if (top == ~0ull) {
+    why = kHandInvalid;
+    return -1;
+  }
+  const uint32_t K = (uint32_t)(top >> 32);
+  if (K == 0u) {  // no finite value
+    why = kHandInvalid;
+    return -1;
+  }
+  const int64_t first = (int64_t)(~(uint32_t)top);
+  const uint32_t kb = (K & 0x80000000u) ? (K & 0x7FFFFFFFu) : ~K;
+  const double M = (double)__uint_as_float(kb);
+  if (p.temperature == 0.0) {  // sampling.py:82-85: the first index of the maximum
+    out.onehot = first;
+    out.npos = 1;
+    out.first = first;
+    if (tid == 0) {
+      if (r.probs_f32) r.probs_f32[first] = 1.0f;
+      if (r.probs_f64) r.probs_f64[first] = 1.0;
+    }
+    __syncthreads();  // the zeroing above is ordered before the kept bit
+    if (tid == 0 && r.kept_bits) r.kept_bits[first >> 5] = 1u << (first & 31);
+    n = 0;
+    return DSR_OK;
+  }
+
+  const uint32_t tau16 = f32_tau16<1>(t, wave, lane, K >> 16, k, [&](int) { return key >> 16; });
+  if (tau16 == 0u) return kHeadFull;  // fewer finite tiles than k
+  const uint32_t tau = tau16 << 16;
+
+  // The tiles to read, per wave in index order (wave w holds tiles 64w ..).
+  const bool need = key != 0u && (key >> 16) >= tau16;
+  const uint64_t bal = __ballot(need);
+  const int nt = __popcll(bal);  // uniform
+  uint32_t* ql = t.hist[wave];  // the histograms are no longer read (f32_pick ends on a barrier)
+  if (need) ql[__popcll(bal & ((1ull << lane) - 1ull))] = (uint32_t)tid;
+  if (lane == 0) ql[kF32Bins - 1] = (uint32_t)nt;  // past the wave's (at most 64) tiles
+  __syncthreads();
+  int tiles = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) tiles += (int)t.hist[w][kF32Bins - 1];
+  if (tiles > kF32HeadMaxTiles) return kHeadFull;  // uniform
+
+  // Two tiles per round (lanes 0-31 and 32-63, a quad each), eight rounds in
+  // flight; tokens at or above tau listed per wave in index order.
+  const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const float*)a.logits + row * a.ld), (short)0, (int)(V * 4), 0x00020000);
+  constexpr int kBatch = 8;
+  int wn = 0;  // this wave's listed tokens (uniform)
+  const int rounds = (nt + 1) >> 1;
+  for (int r0 = 0; r0 < rounds; r0 += kBatch) {
+    uint4 v[kBatch];
+    uint32_t qv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int slot = 2 * (r0 + u) + (lane >> 5);
+      qv[u] = slot < nt ? ql[slot] * (kF32HeadTile / 4) + (uint32_t)(lane & 31) : 0x0FFFFFFFu;
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(
+          rrs, (int)(qv[u] < (uint32_t)(V >> 2) ? qv[u] * 16u : 0x7FFFFFF0u), 0, 0);
+      v[u] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (r0 + u < rounds) {  // uniform
+        const uint32_t q = qv[u];
+        const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        uint32_t sel = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (q < (uint32_t)(V >> 2) && f32_key(w4[e], true) >= tau) sel |= 1u << e;
+        const uint32_t c = (uint32_t)__popc(sel);
+        const uint32_t incl = wave_scan_dpp(c);
+        int pos = wn + (int)(incl - c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if ((sel >> e) & 1u) {
+            if (pos < kF32WaveCap) {
+              t.lv[wave][pos] = __uint_as_float(w4[e]);
+              t.li[wave][pos] = (int32_t)(4 * q + (uint32_t)e);
+            }
+            ++pos;
+          }
+        }
+        wn += (int)lane_value(incl, 63);
+      }
+    }
+  }
+  return f32_list_finish(r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
+}
 }  // namespace dsr

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void k_split_finish(dsr_sample_args_t a, 
 // One-workgroup FP32 top-k path; rows it does not take are redone by the
 // general path inside the same workgroup.
 template <bool RNG>
-__global__ __launch_bounds__(kThreads) void k_sample_f32(dsr_sample_args_t a) {
+__global__ __launch_bounds__(kThreads) void k_sample_f32(dsr_sample_args_t a, const dsr_head_part_t* parts) {
   __shared__ F32Shared sh;
   const int64_t row = blockIdx.x;
   double* W = (double*)a.workspace + row * ws_stride(a.vocab);
@@ -169,7 +169,12 @@ __global__ __launch_bounds__(kThreads) void k_sample_f32(dsr_sample_args_t a) {
   DistOut d;
   int64_t n = 0;
   int why = 0;
-  const int st = f32_distribution(a, row, r, sh, flags, d, n, why);
+  int st = kHeadFull;
+  if (parts) {
+    st = f32_distribution_head(a, row, parts, r, sh, flags, d, n, why);
+    if (st == kHeadFull) __syncthreads();  // the records' pass is done with LDS
+  }
+  if (st == kHeadFull) st = f32_distribution(a, row, r, sh, flags, d, n, why);
   if (st >= 0) {
     const int32_t* kid = sh.t.kid;
     finish_row<RNG>(a, row, sh.t.kz, n, st, d, flags, sh.gen, [kid](int64_t j) { return (int64_t)kid[j]; });
@@ -903,7 +908,15 @@ static constexpr uint32_t kHintBits = DSR_HINT_WHOLE_SOME | DSR_HINT_WHOLE_ALL |
 
 static bool dtype_ok(int32_t d) { return d == DSR_BF16 || d == DSR_F32 || d == DSR_F64; }
 
-int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
+static int32_t sample_rows(const dsr_sample_args_t* args, const dsr_head_part_t* parts, void* stream);
+
+int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) { return sample_rows(args, nullptr, stream); }
+
+int32_t dsr_sample_rows_head(const dsr_sample_args_t* args, const dsr_head_part_t* parts, void* stream) {
+  return sample_rows(args, parts, stream);
+}
+
+static int32_t sample_rows(const dsr_sample_args_t* args, const dsr_head_part_t* parts, void* stream) {
   if (!args) return DSR_ERR_ARG;
   const dsr_sample_args_t& a = *args;
   const int64_t words = (a.vocab + 31) / 32;
@@ -953,8 +966,9 @@ int32_t dsr_sample_rows(const dsr_sample_args_t* args, void* stream) {
       hipLaunchKernelGGL(k_zero_probs, dim3((unsigned)(a.rows * chunks)), dim3(kZeroThreads), 0, s, a.out_probs_f32,
                          a.out_probs_f64, a.probs_ld, a.vocab, (int)chunks);
     }
-    if (a.rng_state) hipLaunchKernelGGL(k_sample_f32<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL(k_sample_f32<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a);
+    const dsr_head_part_t* hp = parts && f32_head_eligible(a) ? parts : nullptr;
+    if (a.rng_state) hipLaunchKernelGGL(k_sample_f32<true>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, hp);
+    else hipLaunchKernelGGL(k_sample_f32<false>, dim3((unsigned)a.rows), dim3(kThreads), 0, s, a, hp);
   } else if (split_path_eligible(a)) {
     const int smax = split_max_slices(a.rows);
     hipLaunchKernelGGL(k_split_select, dim3((unsigned)(a.rows * smax)), dim3(kThreads), 0, s, a, smax);

@@ -361,6 +361,17 @@ int32_t dsr_verify_drafts(const dsr_verify_args_t* args, void* stream);
  * has info bit 0 or 2. */
 int32_t dsr_vocab_head(const dsr_head_args_t* args, void* stream);
 
+/* dsr_sample_rows on FP32 logits written by dsr_vocab_head, with that call's
+ * records (`parts`, [rows, vocab / DSR_HEAD_TILE]): rows that the one-
+ * workgroup FP32 top-k path takes (DSR_HINT_TOPK_ALL, no history or bias
+ * table) and that carry no allow mask start from the records' per-tile
+ * maxima instead of a pass over the row, and read again only the tiles whose
+ * maximum reaches the k-th largest tile maximum (at most 256 tiles; more,
+ * or fewer finite tiles than k, and the row takes the full pass).  Results
+ * are dsr_sample_rows'; other batches are dsr_sample_rows itself.  The
+ * records must be those of these logits (the projection's own output). */
+int32_t dsr_sample_rows_head(const dsr_sample_args_t* args, const dsr_head_part_t* parts, void* stream);
+
 /* dsr_verify_drafts for FP32 logits written by dsr_vocab_head together with
  * their records: the verifier's per-row statistics come from the records
  * instead of a pass over the logits.  target_parts holds the records of the

@@ -242,3 +242,93 @@ def test_policy_tensors_off_the_device_are_refused():
     with pytest.raises(ValueError):   # two policies for four rows
         batch.sample_rows(torch.zeros(4, 512, dtype=torch.float32, device=DEV), one,
                           uniforms=torch.full((4,), 0.5, dtype=torch.float64, device=DEV))
+
+
+def _sample_pair(logits, pols, u, parts, **kw):
+    """The same rows sampled with and without the projection's records."""
+    pt = batch.policy_tensor(pols, DEV)
+    ud = torch.from_numpy(np.asarray(u, np.float64)).to(DEV)
+    a = batch.sample_rows(logits, pt, uniforms=ud, head_parts=parts, probs="f64", kept=True, **kw)
+    b = batch.sample_rows(logits, pt, uniforms=ud, probs="f64", kept=True, **kw)
+    torch.cuda.synchronize()
+    return a, b
+
+
+@pytest.mark.parametrize("rows,dim,vocab", [(6, 256, 129280), (16, 512, 8192), (3, 256, 1024)])
+def test_top_k_rows_from_the_records_match_the_plain_path_and_the_oracle(rows, dim, vocab):
+    """dsr_sample_rows_head: FP32 top-k rows start from the projection's
+    per-tile maxima.  Tokens, consumption, statuses, flags, kept bits and
+    float64 probabilities equal those of dsr_sample_rows on the same logits
+    bit for bit, and the oracle's on the host copy of the logits; rows whose
+    k exceeds the finite tiles or whose candidate tiles are too many take
+    the full pass in the same launch."""
+    x, w = head_inputs(71 + rows, rows, dim, vocab, scale=3.0)
+    res = batch.vocab_head(x.to(DEV), w.to(DEV))
+    logits = res.logits
+    host = logits.cpu().numpy()
+    rng = np.random.default_rng(5000 + vocab)
+    ks = [1, 3, 50, 200, 1000, 1024]
+    pols = []
+    for r in range(rows):
+        k = min(ks[r % len(ks)], vocab - 1)
+        pols.append(dict(temperature=[0.6, 1.0, 1.7][r % 3], top_k=k, top_p=[1.0, 0.9, 0.5][r % 3],
+                         min_p=0.02 if r % 4 == 3 else 0.0))
+    pols[0] = dict(temperature=0.0, top_k=5)
+    u = rng.random(rows)
+    a, b = _sample_pair(logits, pols, u, res.parts)
+    for f in ("tokens", "consumed", "status", "flags", "kept_bits"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    assert torch.equal(a.probs, b.probs)
+    # A top-k near the count of a small vocabulary's quad pairs may overflow
+    # the candidate lists and hand the row over, with or without records;
+    # smaller ones stay on the FP32 kernel.
+    fits = np.array([p["temperature"] == 0.0 or p["top_k"] <= vocab // 16 for p in pols])
+    assert ((a.flags.cpu().numpy() & N.FLAG_F32_TOPK) != 0)[fits].all()
+    tok = a.tokens.cpu().numpy()
+    for r in range(rows):
+        ref = O.sample_row(host[r], O.Policy(**pols[r]), float(u[r]))
+        assert int(tok[r]) == ref.token, r
+        np.testing.assert_allclose(a.probs[r].cpu().numpy(), ref.probs, rtol=1e-5, atol=1e-300)
+
+
+def test_records_with_masks_infinities_or_other_paths_change_nothing():
+    """A masked batch ignores the records; rows with -inf logits and rows
+    whose every value is -inf take the records' route or hand over as the
+    plain path does; device draws advance the same states."""
+    rows, dim, vocab = 4, 256, 4096
+    x, w = head_inputs(93, rows, dim, vocab)
+    res = batch.vocab_head(x.to(DEV), w.to(DEV))
+    logits = res.logits.clone()
+    logits[1, 100:300] = -float("inf")
+    logits[2, :] = -float("inf")
+    # The edited rows' records (maximum, first column holding it, flags),
+    # as dsr_vocab_head writes them, from the edited logits.
+    host = logits.cpu().numpy()
+    p = res.parts.cpu().numpy().reshape(rows, vocab // TILE, 4).copy()
+    for r in (1, 2):
+        t = host[r].reshape(-1, TILE)
+        for tl in range(t.shape[0]):
+            mx = t[tl].max()
+            fin = np.isfinite(t[tl]).any()
+            col = int(np.flatnonzero(t[tl] == mx)[0]) if fin else 0xFFFFFF
+            flags = (2 if fin else 0) | (4 if np.isneginf(t[tl]).any() else 0)
+            p[r, tl, 2] = np.array([mx], np.float32).view(np.int32)[0]
+            p[r, tl, 3] = np.array([flags | (col << 8)], np.uint32).view(np.int32)[0]
+    parts = torch.from_numpy(p).to(DEV)
+    pols = [dict(temperature=0.8, top_k=20, top_p=0.9)] * rows
+    u = np.random.default_rng(3).random(rows)
+    a, b = _sample_pair(logits, pols, u, parts)
+    for f in ("tokens", "consumed", "status", "flags", "kept_bits"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    assert torch.equal(a.probs, b.probs)
+    allow = torch.from_numpy(batch.pack_allow(np.random.default_rng(4).random((rows, vocab)) < 0.7).view(np.int32)).to(DEV)
+    a, b = _sample_pair(logits, pols, u, parts, allow_bits=allow)
+    for f in ("tokens", "consumed", "status", "flags"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f
+    gens = [np.random.default_rng(40 + r) for r in range(rows)]
+    s1, s2 = batch.pcg64_states(gens, DEV), batch.pcg64_states(gens, DEV)
+    pt = batch.policy_tensor(pols, DEV)
+    r1 = batch.sample_rows(logits, pt, rng_state=s1, head_parts=parts)
+    r2 = batch.sample_rows(logits, pt, rng_state=s2)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.tokens, r2.tokens) and torch.equal(s1, s2)
