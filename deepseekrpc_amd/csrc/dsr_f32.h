@@ -403,12 +403,153 @@ __device__ __forceinline__ uint32_t f32_tau16(F32Lists& t, int wave, int lane, u
   return tau16;
 }
 
+constexpr int kDecided = -4;      // f32_list_finish: the row's outputs are written
+constexpr int kWaveTailMax = 64;  // lists a single wave finishes (one candidate per lane)
+
+// Steps 9-13 and the draw (sampling.py:89-128) for a list of at most 64
+// candidates (t.cz / t.cid, nc entries, index order), by wave 0 alone with
+// one candidate per lane: the steps, float64 arithmetic and rounding-band
+// flags of f32_sorted_tail and finish_row, with wave reductions in place of
+// workgroup ones.  The candidates are ranked by (z desc, list position asc),
+// the reference's order, by comparing every pair.  Writes the row's outputs.
+__device__ __forceinline__ void f32_wave_tail(const dsr_sample_args_t& a, int64_t row, const RowSpec& r, F32Lists& t,
+                                              int nc, long long k, int64_t V, unsigned flags) {
+  if (wave_id() != 0) return;
+  const int l = lane_id();
+  const dsr_policy_t& p = r.pol;
+  const bool have = l < nc;
+  const double z0 = have ? t.cz[l] : -(double)INFINITY;
+  const unsigned long long key = have ? (unsigned long long)order_key(z0) : 0ull;
+  int rank = 0;
+  for (int j = 0; j < nc; ++j) {  // uniform
+    const unsigned long long kj = lane_value(key, j);
+    rank += (kj > key || (kj == key && j < l)) ? 1 : 0;
+  }
+  if (have) {
+    t.srt.xs[rank] = z0;
+    t.sp[rank] = l;
+  }
+  wave_lds_sync();
+  // Lane l holds sorted position l: top-k (sampling.py:89-91) keeps the
+  // first k with finite z.
+  const double z = have ? t.srt.xs[l] : -(double)INFINITY;
+  const int c = have ? t.sp[l] : 0;  // list position
+  const bool kept = have && l < k && z > -(double)INFINITY;
+  const int32_t tok = kept ? t.cid[c] : 0;
+  if (kept && r.kept_bits) atomicOr(&r.kept_bits[tok >> 5], 1u << (tok & 31));
+
+  // sampling.py:92-96
+  const double e = kept ? exp(z) : 0.0;
+  const double s1 = wave_sum(e);
+  double x;
+  if (p.min_p != 0.0) {
+    const double cut_p = p.min_p * (1.0 / s1);
+    const double tol = cut_p * 0x1p-49;
+    x = e / s1;
+    const bool close = x > 0.0 && fabs(x - cut_p) <= tol;
+    if (x < cut_p) x = 0.0;
+    if (__ballot(close)) flags |= DSR_FLAG_MARGIN;
+    const double s2 = wave_sum(x);
+    x = x / s2;
+  } else {
+    x = e / s1;
+  }
+  if (p.top_p < 1.0) {  // sampling.py:97-102, as f32_sorted_tail
+    long long tgt = (long long)(p.top_p * 0x1p60);
+    if (tgt == 0) tgt = 1;
+    const long long fx = x > 0.0 ? (long long)(x * 0x1p60) : 0ll;
+    const long long incl = wave_scan_dpp(fx);
+    const long long fex = incl - fx;
+    if (lane_value(incl, 63) >= tgt) {
+      const unsigned long long hit = __ballot(fx > 0 && fex < tgt && fex + fx >= tgt);
+      const double rt = lane_value(x, __ffsll((long long)hit) - 1);
+      const double A = wave_sum(x > rt ? x : 0.0);
+      const long long n_above = __popcll(__ballot(x > rt)), n_tie = __popcll(__ballot(x == rt));
+      bool close;
+      const long long keep = top_p_tie_keep(A, n_above, n_tie, rt, p.top_p, close);
+      if (close) flags |= DSR_FLAG_MARGIN;
+      int cutc = -1;
+      if (keep > 0) {
+        const int f = (int)n_above, lst = f + (int)n_tie - 1;
+        if (lane_value(z, f) == lane_value(z, lst)) {
+          cutc = (int)lane_value((uint32_t)c, f + (int)keep - 1);
+        } else {  // several z round to one probability: rank the group by list position
+          int rk = 0;
+          for (int q = f; q <= lst; ++q) rk += (int)lane_value((uint32_t)c, q) < c ? 1 : 0;
+          const unsigned long long hb = __ballot(l >= f && l <= lst && rk == (int)keep - 1);
+          cutc = (int)lane_value((uint32_t)c, __ffsll((long long)hb) - 1);
+        }
+      }
+      if (x < rt || (x == rt && c > cutc)) x = 0.0;
+    } else {
+      // The whole mass stays below top_p: nothing is removed.
+      const double tot = wave_sum(x);
+      if (fabs(tot - p.top_p) <= ((double)V + 16.0) * 0x1p-51) flags |= DSR_FLAG_MARGIN;
+    }
+  }
+
+  const double total = wave_sum(x);  // sampling.py:103-106
+  int st = (total > 0.0 && isfinite(total)) ? DSR_OK : DSR_E_NO_MASS;
+  int64_t token = -1;
+  int consumed = 0;
+  if (st == DSR_OK) {
+    x = x / total;
+    if (kept) {
+      if (r.probs_f32) r.probs_f32[tok] = (float)x;
+      if (r.probs_f64) r.probs_f64[tok] = x;
+    }
+    // The final probabilities by list position (index order) for the draw.
+    if (have) t.cz[c] = kept ? x : 0.0;
+    wave_lds_sync();
+    const double w = have ? t.cz[l] : 0.0;
+    const long long npos = __popcll(__ballot(w > 0.0));
+    const unsigned long long pos_l = __ballot(w > 0.0);
+    if (a.rng_state || a.uniforms) {
+      if (npos == 1) {
+        token = t.cid[__ffsll((long long)pos_l) - 1];  // sampling.py:120-122: no uniform is drawn
+      } else {
+        uint64_t next[4];
+        const double u = a.rng_state ? pcg64_random(a.rng_state + 4 * row, next) : a.uniforms[row];
+        if (!(u >= 0.0 && u < 1.0)) {
+          st = DSR_E_UNIFORM;
+        } else {
+          // categorical (sampling.py:126-128): the first index whose running
+          // sum exceeds u times the total, in index order.
+          const double tot2 = wave_sum(w);
+          const double thr = u * tot2;
+          const double tol = ((double)npos + 16.0) * 0x1p-51 * tot2;
+          const double cv = wave_scan_dpp(w), before = cv - w;
+          const unsigned long long cross = __ballot(w > 0.0 && cv > thr);
+          int owner;
+          if (cross) {
+            owner = __ffsll((long long)cross) - 1;
+            const double cvo = lane_value(cv, owner), bo = lane_value(before, owner);
+            if (cvo - thr <= tol || (bo > 0.0 && thr - bo <= tol)) flags |= DSR_FLAG_MARGIN;
+          } else {  // rounding left no crossing: the last positive entry
+            owner = 63 - __clzll((long long)pos_l);
+            flags |= DSR_FLAG_MARGIN;
+          }
+          token = t.cid[owner];
+          consumed = 1;
+        }
+        if (a.rng_state && l == 0) store_rng(a, row, next);
+      }
+    }
+  }
+  if (l == 0) {
+    a.out_token[row] = st == DSR_OK ? (int32_t)token : -1;
+    a.out_consumed[row] = (uint8_t)(st == DSR_OK ? consumed : 0);
+    a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = (uint8_t)flags;
+  }
+}
+
 // From the per-wave token lists (t.lv / t.li, wn entries in this wave) to
 // the row's decision: the row-wide list as float64 z = (v - max) / T, then
 // f32_sorted_tail, or radix_top_k and filter_tail when a bucket is too full.
-__device__ __forceinline__ int f32_list_finish(const RowSpec& r, F32Shared& shu, int wave, int lane, int wn, double M,
-                                               long long k, int64_t V, unsigned& flags, DistOut& out, int64_t& n,
-                                               int& why) {
+__device__ __forceinline__ int f32_list_finish(const dsr_sample_args_t& a, int64_t row, const RowSpec& r,
+                                               F32Shared& shu, int wave, int lane, int wn, double M, long long k,
+                                               int64_t V, unsigned& flags, DistOut& out, int64_t& n, int& why) {
   F32Lists& t = shu.t;
   GenShared& sh = shu.gen;
   const int tid = threadIdx.x;
@@ -436,6 +577,10 @@ __device__ __forceinline__ int f32_list_finish(const RowSpec& r, F32Shared& shu,
   }
   __syncthreads();
   const int64_t nc = total;
+  if (nc <= kWaveTailMax) {
+    f32_wave_tail(a, row, r, t, (int)nc, k, V, flags);
+    return kDecided;
+  }
 
   const int st = f32_sorted_tail(r, t, sh, nc, k, V, flags, out, n);
   if (st != kTailFallback) return st;
@@ -707,7 +852,7 @@ __device__ __forceinline__ int f32_distribution(const dsr_sample_args_t& a, int6
       }
     }
   }
-  return f32_list_finish(r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
+  return f32_list_finish(a, row, r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
 }
 
 
@@ -856,6 +1001,6 @@ __device__ __forceinline__ int f32_distribution_head(const dsr_sample_args_t& a,
       }
     }
   }
-  return f32_list_finish(r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
+  return f32_list_finish(a, row, r, shu, wave, lane, wn, M, k, V, flags, out, n, why);
 }
 }  // namespace dsr

@@ -175,6 +175,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_f32(dsr_sample_args_t a, co
     if (st == kHeadFull) __syncthreads();  // the records' pass is done with LDS
   }
   if (st == kHeadFull) st = f32_distribution(a, row, r, sh, flags, d, n, why);
+  if (st == kDecided) return;  // a short list's wave wrote the outputs
   if (st >= 0) {
     const int32_t* kid = sh.t.kid;
     finish_row<RNG>(a, row, sh.t.kz, n, st, d, flags, sh.gen, [kid](int64_t j) { return (int64_t)kid[j]; });

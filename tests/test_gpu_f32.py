@@ -175,19 +175,25 @@ def test_sorted_tail_edge_rows():
     """Rows whose float64 steps collapse distinct values: logits near 1e-30
     (every exp rounds to 1, so the top-p tie group holds tokens of different
     z, cut by index), a denormal temperature (every z but the maximum's is
-    -inf), and an exact two-way tie at the maximum under a tiny top-p."""
+    -inf), and an exact two-way tie at the maximum under a tiny top-p; both
+    tails (lists of at most 64 candidates finish in one wave, longer ones
+    in the workgroup's sorted tail)."""
     rng = np.random.default_rng(8706)
     V = 4096
-    x = rng.normal(0, 1, (6, V)).astype(np.float32)
+    x = rng.normal(0, 1, (8, V)).astype(np.float32)
     x[0] *= np.float32(1e-30)
     x[1] *= np.float32(1e-30)
+    x[6] *= np.float32(1e-30)
+    x[7] *= np.float32(1e-30)
     x[3, rng.choice(V, 2, replace=False)] = 9.0
     pols = [dict(temperature=1.0, top_k=100, top_p=0.37),
             dict(temperature=0.5, top_k=1000, top_p=0.999, min_p=0.5),
             dict(temperature=1e-320, top_k=50, top_p=0.9),
             dict(temperature=1.0, top_k=20, top_p=1e-9),
             dict(temperature=0.05, top_k=7, min_p=1e-3),
-            dict(temperature=2.0, top_k=1024, top_p=0.6)]
-    w = workloads.Workload("edges", "f32", x, pols, rng.random(6))
+            dict(temperature=2.0, top_k=1024, top_p=0.6),
+            dict(temperature=1.0, top_k=40, top_p=0.37),                 # short lists: one wave's tail
+            dict(temperature=0.9, top_k=60, top_p=0.8, min_p=0.5)]
+    w = workloads.Workload("edges", "f32", x, pols, rng.random(8))
     gpu = check(w, probs="f64")
     assert f32_path(gpu).all(), np.flatnonzero(~f32_path(gpu))
