@@ -21,16 +21,16 @@
 // band are reported with DSR_FLAG_MARGIN, and rows whose boundary order the
 // keys cannot certify are handed to the general path (reason in flags).
 //
-// Steps: (1) loads and the history's penalised-token bitmap; pass 1 over the
-// arriving chunks drops masked and penalised tokens from the key set and
-// checks for NaN/+inf; (2) the row maximum over keys and penalised values;
-// greedy rows end here; (3) the key-count histogram; (4) per 64-key block,
-// the masses of the present keys (thread t owns block t); penalised masses
-// are added to the block of their floor key; (5) the top-p boundary: the
+// Steps: (1) loads, issued in rounds, and the history's penalised-token
+// bitmap; pass 1 over the arriving chunks drops masked and penalised tokens
+// from the key set, fills the key-count histogram and checks for NaN/+inf;
+// (2) the row maximum over keys and penalised values; greedy rows end here;
+// (3) per 64-key block, the masses of the present keys; penalised masses
+// are added to the block of their floor key; (4) the top-p boundary: the
 // block, then the key (one wave), then inside the boundary key's bucket the
 // penalised values above its bf16 value and its tie group, resolved by value
 // and by index as the reference's stable sort does (sampling.py:97-102);
-// (6) the categorical draw (:118-128): per-wave kept mass, then the wave
+// (5) the categorical draw (:118-128): per-wave kept mass, then the wave
 // holding u * total walks its chunks in index order.
 #pragma once
 
@@ -233,15 +233,32 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const uint16_t*)a.logits + row * a.ld), (short)0, (int)(V * 2), 0x00020000);
+  // Every wave's small loads enter the CU's memory pipeline before any
+  // wave's row loads: the LDS set-up below waits only for them, and the
+  // first pass then takes each slot as it lands instead of starting after
+  // the whole row (a wave's small loads would otherwise queue behind the
+  // row loads of the waves issued before it).  No wait: a bare barrier at
+  // workgroup-uniform control flow.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // The row's slots are issued in rounds (the first kAhead now, then one
+  // per round with a barrier per round), as the top-k kernel issues them: a
+  // wave whose next instruction is a load waits until the CU's memory
+  // pipeline (about 40 KB in flight) takes it, so sixteen slots issued up
+  // front would hold every wave in its loads until the row had nearly
+  // landed, and the first pass could not start before then.
   uint4 d[kFastChunks];
-#pragma unroll
-  for (int j = 0; j < kFastChunks; ++j) {
+  auto issue = [&](int j) {
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
     const uint32_t c = (uint32_t)wave * CW + cw;
     const bool mine = cw < CW;
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)(mine ? c * 16u : 0x7FFFFFF0u), 0, 0);
     d[j] = make_uint4(v[0], v[1], v[2], v[3]);
-  }
+  };
+  constexpr int kAhead = 4;
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) issue(j);
   __builtin_amdgcn_sched_barrier(0);
   if (!policy_ok(pol)) return kHandPolicy;
   if (pol.top_k != 0 && pol.top_k < V) return kHandTopK;  // a top-k cut with history: the general path
@@ -282,9 +299,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // atomic contention on them later); raw NaN/+inf check; key max and min.
   uint32_t vmax_s = 0x80008000u, vmax_u = 0u, kmax = 0u, kmin = 0xFFFFFFFFu;
   const uint32_t dummy2 = (2u + (uint32_t)lane) * 0x00010001u;  // keys 2..65 hold no value
-#pragma unroll
-  for (int j = 0; j < kFastChunks; ++j) {
-    __builtin_amdgcn_sched_barrier(0);
+  auto pass1 = [&](int j) {
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
     const uint32_t c = (uint32_t)wave * CW + cw;
     // Slots past this wave's chunks or past the row were not loaded (they
@@ -303,8 +318,25 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       kmax = pk_max_u16(kmax, k);
       kmin = pk_min_u16(kmin, k | m4[q]);            // excluded -> 0xFFFF, neutral for the minimum
       w[q] = k | (m4[q] & dummy2);                   // excluded -> a per-lane key below the real ones
+      // The key-count histogram of the register-resident tokens, filled while
+      // the later slots stream in (excluded and dummy keys land below 128 and
+      // are ignored from here on; greedy rows never read it).
+      const uint32_t k0 = w[q] & 0xFFFFu, k1 = w[q] >> 16;
+      atomicAdd(&sh.big.cnt[k0 >> 1], 1u << ((k0 & 1u) << 4));
+      atomicAdd(&sh.big.cnt[k1 >> 1], 1u << ((k1 & 1u) << 4));
     }
     d[j] = make_uint4(w[0], w[1], w[2], w[3]);
+  };
+  // Round r issues slot r (r < 16) and runs the pass of slot r - kAhead.
+  // The barriers keep the waves' issues in step (workgroup-uniform control
+  // flow; nothing in LDS changes, so no fence).
+#pragma unroll
+  for (int r = kAhead; r < kFastChunks + kAhead; ++r) {
+    if (r < kFastChunks) issue(r);
+    __builtin_amdgcn_sched_barrier(0);
+    pass1(r - kAhead);
+    __builtin_amdgcn_sched_barrier(0);
+    if (r + 1 < kFastChunks) __builtin_amdgcn_s_barrier();
   }
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) asm volatile("" : "+v"(d[j].x), "+v"(d[j].y), "+v"(d[j].z), "+v"(d[j].w));
@@ -339,7 +371,9 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       const int64_t e = base + (int64_t)i * kThreads;
       ok[i] = e < pn && id[i] >= 0 && id[i] < V && prv[i] < id[i] && c[i] >= 0 && c[i] <= DSR_MAX_COUNT &&
               g[i] >= 0 && g[i] <= c[i];
-      raw[i] = ok[i] ? ((const uint16_t*)a.logits)[row * a.ld + id[i]] : 0u;
+      // Unbranched raw buffer loads (out of range reads 0), so that the
+      // batch's gathers are in flight together.
+      raw[i] = __builtin_amdgcn_raw_buffer_load_b16(rrs, ok[i] ? 2 * id[i] : 0x7FFFFFF0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kPenBatch; ++i) {
@@ -413,18 +447,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
   unsigned flags = 0;
 
-  // ---- key-count histogram of the register-resident tokens (excluded and
-  // dummy keys land below 128 and are ignored from here on).
-#pragma unroll
-  for (int j = 0; j < kFastChunks; ++j) {
-    const uint32_t w4[4] = {d[j].x, d[j].y, d[j].z, d[j].w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t k0 = w4[q] & 0xFFFFu, k1 = w4[q] >> 16;
-      atomicAdd(&sh.big.cnt[k0 >> 1], 1u << ((k0 & 1u) << 4));
-      atomicAdd(&sh.big.cnt[k1 >> 1], 1u << ((k1 & 1u) << 4));
-    }
-  }
+  // The key-count histogram was filled by the first pass.
   lds_barrier();
 
   // ---- masses of the present keys (sampling.py:86-96: exp((v - max) / T),
