@@ -225,6 +225,16 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     aw[i] = (a.allow_bits && w < nwords) ? a.allow_bits[row * a.allow_ld + w] : 0xFFFFFFFFu;
   }
   const double etv = kExp2Frac[lane];
+  // The row's uniform or PCG64 state, read with the small loads: the draw at
+  // the end then waits for no memory round trip.
+  uint64_t st_pre[4] = {0ull, 0ull, 0ull, 0ull};
+  double u_pre = 0.0;
+  if (RNG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_pre[i] = a.rng_state[4 * row + i];
+  } else if (a.uniforms) {
+    u_pre = a.uniforms[row];
+  }
   int32_t pid[kPenPre];
 #pragma unroll
   for (int i = 0; i < kPenPre; ++i) {
@@ -297,7 +307,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // ---- pass 1, chunk by chunk as the loads land: keys, with masked and
   // penalised tokens set to keys below every value's (2 + lane: no LDS
   // atomic contention on them later); raw NaN/+inf check; key max and min.
-  uint32_t vmax_s = 0x80008000u, vmax_u = 0u, kmax = 0u, kmin = 0xFFFFFFFFu;
+  uint32_t vmax_s = 0x80008000u, vmax_u = 0u, kmax = 0u;
   const uint32_t dummy2 = (2u + (uint32_t)lane) * 0x00010001u;  // keys 2..65 hold no value
   auto pass1 = [&](int j) {
     const uint32_t cw = (uint32_t)j * 64u + (uint32_t)lane;
@@ -316,7 +326,6 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
       vmax_u = pk_max_u16(vmax_u, w[q]);
       const uint32_t k = bf16x2_keys(w[q] | m4[q]);  // excluded -> key 0
       kmax = pk_max_u16(kmax, k);
-      kmin = pk_min_u16(kmin, k | m4[q]);            // excluded -> 0xFFFF, neutral for the minimum
       w[q] = k | (m4[q] & dummy2);                   // excluded -> a per-lane key below the real ones
       // The key-count histogram of the register-resident tokens, filled while
       // the later slots stream in (excluded and dummy keys land below 128 and
@@ -340,7 +349,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
 #pragma unroll
   for (int j = 0; j < kFastChunks; ++j) asm volatile("" : "+v"(d[j].x), "+v"(d[j].y), "+v"(d[j].z), "+v"(d[j].w));
-  asm volatile("" : "+v"(vmax_s), "+v"(vmax_u), "+v"(kmax), "+v"(kmin));
+  asm volatile("" : "+v"(vmax_s), "+v"(vmax_u), "+v"(kmax));
   __builtin_amdgcn_sched_barrier(0);
 
   // History validity (the general path reports any error in the reference's
@@ -404,15 +413,22 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   }
 
   // ---- row maximum over keys and penalised values; invalid rows hand over.
-  const uint32_t kmx = max(kmax & 0xFFFFu, kmax >> 16), kmn = min(kmin & 0xFFFFu, kmin >> 16);
+  const uint32_t kmx = max(kmax & 0xFFFFu, kmax >> 16);
   const uint32_t badv = (max((int)(short)(vmax_s & 0xFFFFu), (int)(short)(vmax_s >> 16)) >= 0x7F80 ||
                          max(vmax_u & 0xFFFFu, vmax_u >> 16) >= 0xFF81u || bad) ? 1u : 0u;
+  // One barrier for the key maximum (with the invalid flag), one more for
+  // the history's count total and value maximum when the row has a history
+  // (pn is uniform).
   const uint32_t red = bs.max((kmx << 1) | badv);
   const uint32_t Mk = red >> 1;
-  const long long csum_all = bs.sum(csum);
+  long long csum_all = 0;
+  double PM = -(double)INFINITY;
+  if (pn > 0) {
+    csum_all = csum;
+    PM = pmax;
+    bs.sum_max(csum_all, PM);
+  }
   if ((red & 1u) || csum_all > DSR_MAX_COUNT) return kHandInvalid;
-  const uint32_t Kmin = bs.min(kmn);
-  const double PM = bs.reduce(pmax, -(double)INFINITY, OpMax());
   const double Mv = Mk > kKeyNegInf ? bf16_key_value(Mk) : -(double)INFINITY;
   const double M = Mv > PM ? Mv : PM;
   if (!(M > -(double)INFINITY)) return kHandInvalid;  // every token masked or -inf: reported by the general path
@@ -472,7 +488,16 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
                  ((q4.z & 0xFFFFu) + (q4.z >> 16)) + ((q4.w & 0xFFFFu) + (q4.w >> 16));
       long long gm = 0;
       uint32_t gp = 0, gc = 0;
-      if ((q4.x | q4.y | q4.z | q4.w) != 0u && g >= 16u) {  // keys below 128 hold no value
+      const bool any = (q4.x | q4.y | q4.z | q4.w) != 0u && g >= 16u;  // keys below 128 hold no value
+      if (!__ballot(any)) {  // no key of the wave's 512 (most of them: the keys cluster)
+        if ((tid & 7) == 0) {
+          sh.mid.blk.bm[g >> 3] = 0;
+          sh.mid.blk.bp[g >> 3] = 0u;
+          sh.mid.blk.bc[g >> 3] = 0u;
+        }
+        continue;
+      }
+      if (any) {
 #pragma unroll 1
         for (int h = 0; h < 8; ++h) {
           const uint32_t wq = h < 4 ? (h < 2 ? q4.x : q4.y) : (h < 6 ? q4.z : q4.w);
@@ -914,14 +939,17 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     return false;
   };
   auto fetch_pk = [&](int64_t e) { return e >= 0 ? PenPk{Wp[e], a.pen_ids[o0 + e]} : PenPk{0ll, 0}; };
+  // The crossing slot's per-chunk penalised masses start at zero (the
+  // block sums sharing their LDS were last read before the mass table's
+  // barrier).
+  if (tid < 512) sh.mid.cm.pe[tid] = 0;
+  if (tid < 64) sh.mid.cm.pen[tid] = 0;
+  if (tid == 0) sh.bc_i[2] = 1;
   lds_barrier();
-  if (tid == 0) {
-    long long base = 0;
-    for (int w = 0; w < kWaves; ++w) base += sh.wtot[w];
-    sh.bc_l[1] = base;
-  }
-  lds_barrier();
-  if (sh.bc_l[1] != Sk) return kHandCapacity;  // the per-wave masses must add up to the kept total
+  // Every wave reads the 16 wave totals: their inclusive prefix on lanes 0..15.
+  const long long wtl = lane < kWaves ? sh.wtot[lane] : 0ll;
+  const long long wti = row_scan_dpp(wtl);
+  if (lane_value(wti, kWaves - 1) != Sk) return kHandCapacity;  // the per-wave masses must add up to the kept total
 
   if (dense) {
     // Kept probabilities mass / kept total in float64 (recomputed, not the
@@ -962,7 +990,7 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     return 0;
   }
   uint64_t rng_next[4];
-  const double u = RNG ? pcg64_random(a.rng_state + 4 * row, rng_next) : a.uniforms[row];
+  const double u = RNG ? pcg64_random(st_pre, rng_next) : u_pre;
   if (!(u >= 0.0 && u < 1.0)) {
     if (tid == 0) fast_write_result(a, row, DSR_E_UNIFORM, -1, 0, flags);
     return 0;
@@ -974,27 +1002,12 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
     flags |= DSR_FLAG_MARGIN;
   }
   flags = uni(flags);
-  // The wave holding thr, and the mass before it.
-  if (tid < 512) sh.mid.cm.pe[tid] = 0;
-  if (tid < 64) sh.mid.cm.pen[tid] = 0;
-  if (tid == 0) {
-    long long base = 0, obase = 0;
-    int ow = -1;
-    for (int w = 0; w < kWaves; ++w) {
-      if (ow < 0 && thr < base + sh.wtot[w]) {
-        ow = w;
-        obase = base;
-      }
-      base += sh.wtot[w];
-    }
-    sh.bc_i[0] = ow;
-    sh.bc_l[0] = obase;
-    sh.bc_i[2] = 1;
-  }
-  lds_barrier();
-  const int ow = uni(sh.bc_i[0]);
-  if (ow < 0) return kHandCapacity;  // unreachable: thr < Sk
-  const long long obase = uni(sh.bc_l[0]);
+  // The wave holding thr (the first whose inclusive total exceeds it), and
+  // the mass before it.
+  const unsigned long long owb = __ballot(lane < kWaves && thr < wti);
+  if (!owb) return kHandCapacity;  // unreachable: thr < Sk
+  const int ow = uni(__ffsll((long long)owb) - 1);
+  const long long obase = uni(lane_value(wti - wtl, ow));
   // The register slot of that wave holding thr, from its 16 slot masses in
   // order (every wave finds the same one).
   int js;
@@ -1016,16 +1029,18 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   // read, so the LDS-only barriers above order everything this pass needs.
   const int64_t elo = sh.elo[ow], ehi = sh.elo[ow + 1];
   const int64_t first = elo + (((int64_t)tid - elo) % kThreads + kThreads) % kThreads;
-  pen_batches<1>(ehi, first, fetch_pk, [&](int64_t, PenPk x) {
-    const uint32_t cid = (uint32_t)(x.id >> 3);
-    if (x.pk != 0 && cid >= cw0 && cid < cw0 + 64u && cid < (uint32_t)(ow + 1) * CW &&
-        pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
-      const long long fx = x.pk & ((1ll << 47) - 1);
-      atomicAdd((unsigned long long*)&sh.mid.cm.pen[cid - cw0], (unsigned long long)fx);
-      sh.mid.cm.pe[(cid - cw0) * 8u + (uint32_t)(x.id & 7)] = fx;  // one entry per token
-    }
-  });
-  lds_barrier();
+  if (ehi > elo) {  // uniform
+    pen_batches<1>(ehi, first, fetch_pk, [&](int64_t, PenPk x) {
+      const uint32_t cid = (uint32_t)(x.id >> 3);
+      if (x.pk != 0 && cid >= cw0 && cid < cw0 + 64u && cid < (uint32_t)(ow + 1) * CW &&
+          pen_kept((uint32_t)((unsigned long long)x.pk >> 48), x.id)) {
+        const long long fx = x.pk & ((1ll << 47) - 1);
+        atomicAdd((unsigned long long*)&sh.mid.cm.pen[cid - cw0], (unsigned long long)fx);
+        sh.mid.cm.pe[(cid - cw0) * 8u + (uint32_t)(x.id & 7)] = fx;  // one entry per token
+      }
+    });
+    lds_barrier();
+  }
   // The chunk of that slot holding thr (a scan over its 64 lanes), then that
   // lane walks its 8 tokens.
   if (wave == ow) {

@@ -171,6 +171,24 @@ class BlockSync {
   __device__ uint32_t min(uint32_t x) { return reduce(x, 0xFFFFFFFFu, OpMin()); }
   __device__ uint32_t sum(uint32_t x) { return reduce(x, 0u, OpSum()); }
 
+  // The sum of a 64-bit integer and the maximum of a double behind one barrier.
+  __device__ void sum_max(long long& s, double& m) {
+    const int p = next();
+    long long* si = s_.i[p];
+    double* sf = s_.f[p];
+    const long long ws = wave_reduce_dpp(s, OpSum());
+    const double wm = wave_reduce_dpp(m, OpMax());
+    if (lane_id() == 0) {
+      si[wave_id()] = ws;
+      sf[wave_id()] = wm;
+    }
+    lds_barrier();
+    const long long a = lane_id() < kWaves ? si[lane_id()] : 0ll;
+    const double b = lane_id() < kWaves ? sf[lane_id()] : -(double)INFINITY;
+    s = lane_value(row_reduce(a, OpSum()), 0);
+    m = lane_value(row_reduce(b, OpMax()), 0);
+  }
+
   // Exclusive prefix over threads in thread order, and the workgroup total.
   template <class T>
   __device__ T scan(T x, T& total) {
