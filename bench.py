@@ -29,7 +29,8 @@ Prints one JSON line: the throughput, the roofline of the step (algorithmic
 HBM bytes / HIP-event time of the launches on their stream, against 8 TB/s)
 and the CPU baseline: the float64 oracle (a restatement of the reference's
 NumPy sampler) timed on the host over a bounded sample of the same workload,
-on 16 worker processes (the GPU box's CPU share) and on one process alone.
+on 16 worker processes (the host's CPU share for one GPU) and on one process
+alone.
 """
 from __future__ import annotations
 
@@ -309,8 +310,9 @@ def _cpu_model():
     return "unknown"
 
 
-# Worker processes of the CPU baseline: the GPU box's CPU share for one GPU
-# (its process limits size pools by that share, not by os.cpu_count()).
+# Worker processes of the CPU baseline: the host's CPU share for one GPU
+# (pools are sized by that share, not by os.cpu_count(), which counts every
+# CPU of the machine).
 CPU_WORKERS = 16
 
 
