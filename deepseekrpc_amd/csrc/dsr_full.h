@@ -338,7 +338,8 @@ __device__ __forceinline__ int full_sample_row(const dsr_sample_args_t& a, int64
   };
   // Round r issues slot r (r < 16) and runs the pass of slot r - kAhead.
   // The barriers keep the waves' issues in step (workgroup-uniform control
-  // flow; nothing in LDS changes, so no fence).
+  // flow).  They carry no fence: the histogram's atomics are read only after
+  // the fenced barrier of the row maximum.
 #pragma unroll
   for (int r = kAhead; r < kFastChunks + kAhead; ++r) {
     if (r < kFastChunks) issue(r);
