@@ -633,8 +633,9 @@ def main():
                     help="also run a plain copy kernel over the batch's logit bytes (for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: rows are independent, and this "
-              "build measures the single-GPU kernel only", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: rows are independent, so each "
+              "GPU would run these kernels on its own share of the rows, and only one GPU's share is measured",
+              file=sys.stderr)
         sys.exit(2)
 
     from deepseekrpc_amd import workloads
